@@ -1,0 +1,179 @@
+/*
+ * yirage_hip.h -- C ABI of the MI355X-native `hip` backend for YiRage.
+ *
+ * Plain pointers and sizes only: no STL, no torch, no HIP types in the
+ * signatures (streams travel as `void*` holding a hipStream_t; NULL is the
+ * null stream).  Every entry point returns YR_OK (0) or a negative YR_E* code;
+ * yr_hip_last_error() returns the message of the last failure on the calling
+ * thread.  Device pointers must be 16-byte aligned.  All compute calls are
+ * stream-ordered and never synchronize the device.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the YiRage source tree).
+ */
+#ifndef YIRAGE_HIP_H_
+#define YIRAGE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ codes */
+#define YR_OK 0
+#define YR_E_INVALID (-1)     /* bad argument / unsupported shape */
+#define YR_E_HIP (-2)         /* HIP runtime error */
+#define YR_E_WORKSPACE (-3)   /* workspace too small */
+#define YR_E_NODEVICE (-4)    /* no usable gfx950 device */
+#define YR_E_GRAPH (-5)       /* malformed task graph */
+#define YR_E_TIMEOUT (-6)     /* persistent kernel watchdog fired */
+
+/* dtypes: values mirror yirage::type::DataType (include/yirage/type.h:84-120) */
+#define YR_DTYPE_F16 940
+#define YR_DTYPE_BF16 941
+#define YR_DTYPE_F32 950
+#define YR_DTYPE_I32 955
+#define YR_DTYPE_I64 965
+
+/* weight layouts of a linear / matmul operand */
+#define YR_W_NK 0 /* W[N][K]: torch Linear.weight, MPK linear task (tasks/ampere/linear.cuh:38-49) */
+#define YR_W_KN 1 /* W[K][N]: kernel-graph matmul X @ W (src/kernel/matmul.cc:73-96) */
+
+/* ------------------------------------------------------------------ status */
+/* Message of the last failure on this thread ("" if none). */
+const char* yr_hip_last_error(void);
+
+/* Library version string. */
+const char* yr_hip_version(void);
+
+typedef struct {
+  int device_id;
+  int num_compute_units;      /* CUs */
+  int compute_capability;     /* 950 for gfx950 */
+  int wavefront_size;         /* 64 */
+  size_t total_memory;        /* bytes of HBM */
+  size_t max_shared_memory;   /* LDS bytes per workgroup */
+  int clock_khz;
+  char arch_name[64];         /* e.g. "gfx950:sramecc+:xnack-" */
+} yr_device_info;
+
+/* Replaces BackendInterface::get_info / get_num_compute_units /
+ * get_compute_capability / get_max_shared_memory
+ * (include/yirage/backend/backend_interface.h:74,171,184,190). */
+int yr_hip_device_info(int device_id, yr_device_info* out);
+
+/* ------------------------------------------------------- synthetic data */
+/* Deterministic ~N(0, std) fill (Irwin-Hall of four 16-bit uniforms from a
+ * splitmix64 counter hash; bit-identical to the CPU generator).  Used to
+ * build random-init model weights on the device.  No reference counterpart
+ * (the reference draws torch.randn on the host). */
+int yr_hip_synth_fill(void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset, float stddev,
+                      void* stream);
+
+/* ------------------------------------------------------- fused operators */
+/* Workspace bytes a fused operator needs for the given shape (0 if none).
+ * The workspace must be zero-filled once when it is allocated; the kernels
+ * leave it zeroed again when they finish.  Replaces the buffer sizing of
+ * the generated program (python/yirage/kernel.py:393-402,411-421). */
+size_t yr_hip_rmsnorm_linear_workspace(int batch, int k, int n, int dtype, int w_layout);
+size_t yr_hip_gated_mlp_workspace(int batch, int k, int n, int dtype, int w_layout);
+
+/* out[b][n] = sum_k (x[b][k] * rsqrt(mean_k x[b]^2 + eps) * gamma[k]) * W(k, n)
+ * fp32 accumulate, out in `dtype`.  gamma may be NULL (no affine).
+ * Replaces the fused customized op found by superoptimize for
+ * matmul(rms_norm(X), W) (demo/reference_mugraphs/rms_norm.py:16-25,
+ * src/transpiler/transpile.cc:681-693) and the MPK task rmsnorm_linear
+ * (src/kernel/task_register.cc:126-168). */
+int yr_hip_rmsnorm_linear(const void* x, const void* gamma, const void* w, void* out, int batch, int k,
+                          int n, int dtype, int w_layout, float eps, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* out[b][n] = silu(sum_k x[b][k] W1(k,n)) * (sum_k x[b][k] W3(k,n)), fp32 math.
+ * Replaces the fused gated-MLP customized op
+ * (demo/reference_mugraphs/gated_mlp.py:75-86). */
+int yr_hip_gated_mlp(const void* x, const void* w1, const void* w3, void* out, int batch, int k, int n,
+                     int dtype, int w_layout, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[b][n] = sum_k x[b][k] W(k,n) (+ residual[b][n]), fp32 accumulate.
+ * Replaces the MPK linear / linear_with_residual tasks
+ * (tasks/ampere/linear_cutlass.cuh:34-475, task_register.cc:497-553). */
+int yr_hip_linear(const void* x, const void* w, const void* residual, void* out, int batch, int k,
+                  int n, int dtype, int w_layout, void* workspace, size_t workspace_bytes,
+                  void* stream);
+size_t yr_hip_linear_workspace(int batch, int k, int n, int dtype, int w_layout);
+
+/* Paged GQA decode, one query token per sequence.
+ * q[batch][hq][d]; k_cache/v_cache[num_pages][page_size][hkv][d];
+ * sequence b owns pages kv_indices[kv_indptr[b] .. kv_indptr[b+1]) and has
+ * kv_len[b] tokens; out[batch][hq][d] = softmax(q k^T / sqrt(d)) v with kv
+ * head h / (hq / hkv).  Replaces the attention part of the MPK paged
+ * attention task (tasks/ampere/multitoken_paged_attention_4_16.cuh:40-656)
+ * and the superoptimize GQA customized ops
+ * (demo/reference_mugraphs/group_query_attention.py:10-34). */
+size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv_len, int page_size);
+int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_cache,
+                            const int32_t* kv_indptr, const int32_t* kv_indices,
+                            const int32_t* kv_len, void* out, int batch, int hq, int hkv, int d,
+                            int page_size, int max_kv_len, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Causal (or full) GQA prefill attention, q[batch][seq][hq][d],
+ * k/v[batch][seq][hkv][d], out like q; fp32 softmax statistics, MFMA
+ * contractions.  Replaces the prefill path of the MPK attention task
+ * (multitoken_paged_attention_4_16.cuh:227-655 with seq_len == num_tokens). */
+int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, int batch, int seq,
+                       int hq, int hkv, int d, int causal, int dtype, void* stream);
+
+/* Row-wise argmax over the first n_valid of n columns of a 16-bit matrix,
+ * lowest index on ties; out is int64[rows].  Replaces argmax_partial /
+ * argmax_reduce (tasks/ampere/argmax.cuh:71-155). */
+int yr_hip_argmax(const void* x, int64_t* out, int rows, int n, int n_valid, int dtype, void* stream);
+
+/* ------------------------------------------------------- generic launcher */
+/* One fused operator by kind, with the shape of the reference's
+ * execute_mugraph(inputs, outputs, buffer, stream, profiler) launcher
+ * (python/yirage/kernel.py:22-72,411-421): inputs and outputs are arrays of
+ * device pointers, `params` holds the integer shape/attribute list of the op.
+ * op_kind / param layouts:
+ *   YR_OP_RMSNORM_LINEAR: in {x, gamma|NULL, w}, out {o};
+ *        params {batch, k, n, dtype, w_layout, eps_as_float_bits}
+ *   YR_OP_GATED_MLP:      in {x, w1, w3}, out {o};
+ *        params {batch, k, n, dtype, w_layout}
+ *   YR_OP_GQA_PREFILL:    in {q, k, v}, out {o};
+ *        params {batch, seq, hq, hkv, d, causal, dtype}
+ *   YR_OP_LINEAR:         in {x, w, residual|NULL}, out {o};
+ *        params {batch, k, n, dtype, w_layout} */
+#define YR_OP_RMSNORM_LINEAR 1
+#define YR_OP_GATED_MLP 2
+#define YR_OP_GQA_PREFILL 3
+#define YR_OP_LINEAR 4
+int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
+                     int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* ------------------------------------------------------- backend registry */
+/* Restates BackendRegistry / BackendInterface
+ * (include/yirage/backend/backend_registry.h:40-166,
+ *  include/yirage/backend/backend_interface.h:40-212) with the `hip`
+ * backend registered as BT_HIP.  Names/types follow
+ * src/backend/backend_utils.cc:27-87 plus "hip". */
+#define YR_BT_HIP 6
+#define YR_BT_CPU 10
+#define YR_BT_UNKNOWN 999
+int yr_backend_num_registered(void);
+/* writes the i-th registered backend name into buf; returns its type */
+int yr_backend_registered_name(int i, char* buf, size_t buf_len);
+int yr_backend_is_available(const char* name);
+int yr_backend_type_from_name(const char* name);
+/* default backend name by priority (hip first), "" if none available */
+int yr_backend_default(char* buf, size_t buf_len);
+/* BackendInterface::get_compile_flags() of a backend */
+int yr_backend_compile_flags(const char* name, char* buf, size_t buf_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YIRAGE_HIP_H_ */

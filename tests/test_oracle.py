@@ -1,0 +1,366 @@
+"""Pins the CPU oracle (oracle/yr_oracle.c) before anything is compared with it.
+
+Each check is independent of the oracle's own formula: library routines
+(numpy float16, torch bfloat16 / SDPA in float64), closed forms, invariants,
+brute force on tiny inputs, and the known-answer cases of the reference tests
+(tests/runtime_python/test_argmax.py:9-34, the RoPE restatement of
+tests/runtime_python/test_multitoken_paged_attention.py:21-37).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+
+rng = np.random.default_rng(1234)
+
+
+# ------------------------------------------------------------- conversions
+
+def test_f16_conversion_matches_numpy():
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = O.to_float(bits, "f16")
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite], ref[finite])
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * s for s in (1e-6, 1e-3, 1, 300, 7e4)])
+    x = np.concatenate([x, np.float32([0.0, -0.0, 65504, 65519.99, 65520, 2 ** -24, 2 ** -25, 3 * 2 ** -26])])
+    assert np.array_equal(O.from_float(x, "f16"), x.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_conversion_matches_torch():
+    x = np.concatenate([rng.standard_normal(300000).astype(np.float32) * s for s in (1e-30, 1e-3, 1, 1e30)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.from_float(x, "bf16"), ref)
+    bits = np.arange(65536, dtype=np.uint16)
+    got = O.to_float(bits, "bf16")
+    tr = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    ok = np.isfinite(tr)
+    assert np.array_equal(got[ok], tr[ok])
+
+
+def test_synth_moments_and_determinism():
+    a = O.synth((1 << 20,), "bf16", seed=7, std=0.02)
+    b = O.synth((1 << 20,), "bf16", seed=7, std=0.02)
+    c = O.synth((1 << 20,), "bf16", seed=8, std=0.02)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    f = O.to_float(a, "bf16").astype(np.float64)
+    assert abs(f.mean()) < 1e-4 and abs(f.std() - 0.02) < 2e-4
+    # offset addressing: a slice generated alone equals the slice of the whole
+    d = O.synth((1000,), "bf16", seed=7, std=0.02, offset=5000)
+    assert np.array_equal(d, a[5000:6000])
+
+
+# ------------------------------------------------------------- rmsnorm / linear
+
+def test_rmsnorm_closed_form_and_invariants():
+    x = rng.standard_normal((5, 64)).astype(np.float32)
+    w = rng.standard_normal(64).astype(np.float32)
+    got = O.rmsnorm(x, w, 1e-6)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    # scale invariance f(cx) = f(x) (eps -> 0)
+    np.testing.assert_allclose(O.rmsnorm(37.0 * x, w, 0.0), O.rmsnorm(x, w, 0.0), rtol=1e-6, atol=1e-6)
+    # constant rows with gamma = 1 -> +-1
+    c = np.full((2, 32), -3.5, np.float32)
+    np.testing.assert_allclose(O.rmsnorm(c, None, 0.0), -np.ones_like(c), rtol=1e-7)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_linear_brute_force_both_layouts(dt):
+    B, K, N = 3, 37, 19
+    x = rng.standard_normal((B, K)).astype(np.float32)
+    Wf = rng.standard_normal((N, K)).astype(np.float32)
+    Wb = O.from_float(Wf, dt)
+    Wv = O.to_float(Wb, dt).astype(np.float64)
+    res = rng.standard_normal((B, N)).astype(np.float32)
+    ref = np.zeros((B, N))
+    for b in range(B):
+        for n in range(N):
+            ref[b, n] = sum(float(x[b, k]) * Wv[n, k] for k in range(K)) + res[b, n]
+    np.testing.assert_allclose(O.linear(x, Wb, dt, O.W_NK, res), ref, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.linear(x, np.ascontiguousarray(Wb.T), dt, O.W_KN, res), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_linear_identity_and_one_hot():
+    K = 16
+    eye = O.from_float(np.eye(K, dtype=np.float32), "bf16")
+    x = O.round_to(rng.standard_normal((4, K)), "bf16")
+    np.testing.assert_array_equal(O.linear(x, eye, "bf16", O.W_KN), x)
+    W = O.from_float(rng.standard_normal((K, 9)).astype(np.float32), "f16")
+    oh = np.zeros((1, K), np.float32)
+    oh[0, 5] = 1.0
+    np.testing.assert_array_equal(O.linear(oh, W, "f16", O.W_KN)[0], O.to_float(W, "f16")[5])
+
+
+def test_rmsnorm_linear_matches_torch():
+    B, K, N = 4, 256, 64
+    x = O.round_to(rng.standard_normal((B, K)), "f16")
+    g = O.round_to(rng.standard_normal(K), "f16")
+    W = O.from_float(rng.standard_normal((K, N)) * 0.02, "f16")
+    xt = torch.from_numpy(x).double()
+    ref = (xt * torch.rsqrt(xt.pow(2).mean(-1, keepdim=True) + 1e-6) * torch.from_numpy(g).double()) @ \
+        torch.from_numpy(O.to_float(W, "f16")).double()
+    np.testing.assert_allclose(O.rmsnorm_linear(x, g, W, "f16", O.W_KN, 1e-6), ref.numpy(), rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------- gated MLP / silu_mul
+
+def test_gated_mlp_against_torch_and_special_cases():
+    B, K, N = 3, 128, 40
+    x = O.round_to(rng.standard_normal((B, K)), "bf16")
+    W1 = O.from_float(rng.standard_normal((K, N)) * 0.05, "bf16")
+    W3 = O.from_float(rng.standard_normal((K, N)) * 0.05, "bf16")
+    xt = torch.from_numpy(x).double()
+    g = xt @ torch.from_numpy(O.to_float(W1, "bf16")).double()
+    u = xt @ torch.from_numpy(O.to_float(W3, "bf16")).double()
+    ref = F.silu(g) * u
+    np.testing.assert_allclose(O.gated_mlp(x, W1, W3, "bf16"), ref.numpy(), rtol=1e-5, atol=1e-7)
+    zero = np.zeros_like(W3)
+    assert np.all(O.gated_mlp(x, W1, zero, "bf16") == 0)
+    # silu(0) = 0: zero input row gives zero output
+    x0 = x.copy()
+    x0[1] = 0
+    assert np.all(O.gated_mlp(x0, W1, W3, "bf16")[1] == 0)
+
+
+def test_silu_mul_rounding_matches_torch_bf16():
+    g = O.round_to(rng.standard_normal(10000) * 4, "bf16")
+    u = O.round_to(rng.standard_normal(10000) * 2, "bf16")
+    gt = torch.from_numpy(g).to(torch.bfloat16)
+    ut = torch.from_numpy(u).to(torch.bfloat16)
+    ref = (F.silu(gt.float()).to(torch.bfloat16) * ut).float().numpy()
+    np.testing.assert_array_equal(O.silu_mul(g, u, "bf16"), ref)
+    # large positive -> silu(x) ~ x
+    big = np.float32([30.0])
+    assert O.silu_mul(big, np.float32([1.0]), "bf16")[0] == 30.0
+
+
+# ------------------------------------------------------------- RoPE
+
+def _rope_tables(npos, D, base=500000.0):
+    inv = 1.0 / (base ** (np.arange(0, D, 2, dtype=np.float64) / D))
+    ang = np.outer(np.arange(npos), inv)
+    emb = np.concatenate([ang, ang], -1)
+    return O.round_to(np.cos(emb), "bf16"), O.round_to(np.sin(emb), "bf16")
+
+
+def test_rope_matches_reference_test_restatement():
+    D = 128
+    cos, sin = _rope_tables(64, D)
+    x = O.round_to(rng.standard_normal((4, D)), "bf16")
+    pos = 37
+    got = O.rope(x, cos[pos], sin[pos], "bf16")
+    xt = torch.from_numpy(x)
+    x1, x2 = xt[..., : D // 2], xt[..., D // 2:]
+    rot = torch.cat((-x2, x1), -1)
+    ref = (xt * torch.from_numpy(cos[pos]) + rot * torch.from_numpy(sin[pos])).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(got, ref)
+    # position 0 is the identity; rotation preserves the norm (up to rounding)
+    np.testing.assert_array_equal(O.rope(x, cos[0], sin[0], "bf16"), x)
+    np.testing.assert_allclose(np.linalg.norm(got, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-2)
+
+
+# ------------------------------------------------------------- attention
+
+def _sdpa(q, k, v, causal=False):
+    return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+
+def test_gqa_decode_paged_vs_sdpa_and_invariants():
+    B, Hq, Hkv, D, page = 3, 8, 2, 16, 4
+    lens = np.array([7, 12, 1], np.int32)
+    npg = (lens + page - 1) // page
+    P = int(npg.sum()) + 3
+    perm = rng.permutation(P).astype(np.int32)
+    indptr = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+    indices = perm[: indptr[-1]]
+    kc = O.from_float(rng.standard_normal((P, page, Hkv, D)), "f16")
+    vc = O.from_float(rng.standard_normal((P, page, Hkv, D)), "f16")
+    q = O.round_to(rng.standard_normal((B, Hq, D)), "f16")
+    got = O.gqa_decode_paged(q, kc, vc, "f16", indptr, indices, lens)
+    kf, vf = O.to_float(kc, "f16"), O.to_float(vc, "f16")
+    G = Hq // Hkv
+    for b in range(B):
+        pages = indices[indptr[b]:indptr[b + 1]]
+        K = kf[pages].reshape(-1, Hkv, D)[: lens[b]]
+        V = vf[pages].reshape(-1, Hkv, D)[: lens[b]]
+        Kt = torch.from_numpy(K).double().permute(1, 0, 2).repeat_interleave(G, 0)
+        Vt = torch.from_numpy(V).double().permute(1, 0, 2).repeat_interleave(G, 0)
+        ref = _sdpa(torch.from_numpy(q[b]).double()[:, None], Kt, Vt)[:, 0]
+        np.testing.assert_allclose(got[b], ref.numpy(), rtol=1e-5, atol=1e-6)
+    # KV length 1 -> output is V of that token (per kv head)
+    np.testing.assert_allclose(got[2].reshape(Hkv, G, D), np.repeat(vf[indices[indptr[2]], 0][:, None], G, 1), rtol=1e-6)
+
+
+def test_gqa_decode_equal_scores_mean_and_head_map():
+    B, Hq, Hkv, D, page = 1, 4, 2, 8, 4
+    kc = np.zeros((2, page, Hkv, D), np.uint16)  # all-zero keys -> equal scores
+    vf = rng.standard_normal((2, page, Hkv, D)).astype(np.float32)
+    vf[:, :, 1] += 100.0  # kv head 1 distinct from kv head 0
+    vc = O.from_float(vf, "bf16")
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    out = O.gqa_decode_paged(q, kc, vc, "bf16", np.int32([0, 2]), np.int32([1, 0]), np.int32([6]))
+    v = O.to_float(vc, "bf16")[[1, 0]].reshape(-1, Hkv, D)[:6]
+    np.testing.assert_allclose(out[0, 0], v[:, 0].mean(0), rtol=1e-6)
+    np.testing.assert_allclose(out[0, 1], v[:, 0].mean(0), rtol=1e-6)
+    np.testing.assert_allclose(out[0, 2], v[:, 1].mean(0), rtol=1e-6)  # q head 2 -> kv head 2 // 2 = 1
+    np.testing.assert_allclose(out[0, 3], v[:, 1].mean(0), rtol=1e-6)
+
+
+def test_gqa_decode_page_permutation_invariance():
+    Hq, Hkv, D, page = 4, 1, 8, 4
+    n = 11
+    kc = O.from_float(rng.standard_normal((3, page, Hkv, D)), "bf16")
+    vc = O.from_float(rng.standard_normal((3, page, Hkv, D)), "bf16")
+    q = rng.standard_normal((1, Hq, D)).astype(np.float32)
+    a = O.gqa_decode_paged(q, kc, vc, "bf16", np.int32([0, 3]), np.int32([0, 1, 2]), np.int32([n]))
+    perm = np.int32([2, 0, 1])
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc  # physical page i moves to slot perm[i]
+    b = O.gqa_decode_paged(q, kc2, vc2, "bf16", np.int32([0, 3]), perm, np.int32([n]))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_gqa_prefill_causal_vs_sdpa_and_row_subset():
+    B, S, Hq, Hkv, D = 2, 9, 4, 2, 16
+    q = rng.standard_normal((B, S, Hq, D)).astype(np.float32)
+    k = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((B, S, Hkv, D)).astype(np.float32)
+    got = O.gqa_prefill(q, k, v, causal=True)
+    G = Hq // Hkv
+    qt = torch.from_numpy(q).double().permute(0, 2, 1, 3)
+    kt = torch.from_numpy(k).double().permute(0, 2, 1, 3).repeat_interleave(G, 1)
+    vt = torch.from_numpy(v).double().permute(0, 2, 1, 3).repeat_interleave(G, 1)
+    ref = _sdpa(qt, kt, vt, causal=True).permute(0, 2, 1, 3)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-5, atol=1e-6)
+    # row 0 sees only key 0 -> equals v[:, 0]
+    np.testing.assert_allclose(got[:, 0], np.repeat(v[:, 0], G, axis=1), rtol=1e-6)
+    sub = O.gqa_prefill(q, k, v, causal=True, rows=[3, 8])
+    np.testing.assert_array_equal(sub[:, [3, 8]], got[:, [3, 8]])
+
+
+def test_paged_attention_task_rope_append_causal():
+    """MPK attention task: 2 requests, one prefill of 3 tokens into an empty
+    cache and one decode token on 5 cached tokens; compared with a torch
+    composition (rotate-half RoPE as in test_multitoken_paged_attention.py)."""
+    Hq, Hkv, D, page = 4, 2, 8, 4
+    G = Hq // Hkv
+    cos, sin = _rope_tables(16, D, base=10000.0)
+    P = 6
+    kc = O.from_float(rng.standard_normal((P, page, Hkv, D)), "bf16")
+    vc = O.from_float(rng.standard_normal((P, page, Hkv, D)), "bf16")
+    kc0, vc0 = kc.copy(), vc.copy()
+    qo = np.int32([0, 3, 4])
+    kv_indptr = np.int32([0, 1, 3])
+    kv_indices = np.int32([4, 2, 5])
+    lpl = np.int32([3, 2])  # request 1: seq_len = 4 + 2 = 6, 5 cached + 1 new
+    qkv = O.round_to(rng.standard_normal((4, (Hq + 2 * Hkv) * D)), "bf16")
+    out = O.paged_attention(qkv, Hq, Hkv, D, kc, vc, "bf16", qo, kv_indptr, kv_indices, lpl, cos, sin)
+
+    def rope_t(x, pos):
+        xt = torch.from_numpy(x)
+        rot = torch.cat((-xt[..., D // 2:], xt[..., : D // 2]), -1)
+        return (xt * torch.from_numpy(cos[pos]) + rot * torch.from_numpy(sin[pos])).to(torch.bfloat16).float()
+
+    kf0, vf0 = O.to_float(kc0, "bf16"), O.to_float(vc0, "bf16")
+    for r, (t0, t1, pages, seq) in enumerate([(0, 3, [4], 3), (3, 4, [2, 5], 6)]):
+        nt = t1 - t0
+        Kall = kf0[pages].reshape(-1, Hkv, D)[:seq].copy()
+        Vall = vf0[pages].reshape(-1, Hkv, D)[:seq].copy()
+        for j in range(nt):
+            pos = seq - nt + j
+            row = qkv[t0 + j].reshape(Hkv, G + 2, D)
+            Kall[pos] = rope_t(row[:, G], pos).numpy()
+            Vall[pos] = row[:, G + 1]
+        # appended cache contents
+        kcn = O.to_float(kc, "bf16")[pages].reshape(-1, Hkv, D)[:seq]
+        np.testing.assert_array_equal(kcn, Kall)
+        for j in range(nt):
+            pos = seq - nt + j
+            row = qkv[t0 + j].reshape(Hkv, G + 2, D)
+            for hk in range(Hkv):
+                qh = rope_t(row[hk, :G], pos).double()
+                Kt = torch.from_numpy(Kall[: pos + 1, hk]).double()
+                Vt = torch.from_numpy(Vall[: pos + 1, hk]).double()
+                ref = _sdpa(qh[:, None], Kt[None].expand(G, -1, -1), Vt[None].expand(G, -1, -1))[:, 0]
+                got = out[t0 + j].reshape(Hq, D)[hk * G:(hk + 1) * G]
+                np.testing.assert_allclose(got, ref.numpy(), rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------- argmax
+
+def test_argmax_planted_known_answer():
+    """tests/runtime_python/test_argmax.py:9-34: vocab 153600, one planted max per row."""
+    rows, V = 6, 153600
+    x = O.round_to(rng.standard_normal((rows, V)), "bf16")
+    idx = rng.integers(0, V, rows)
+    x[np.arange(rows), idx] = O.round_to(np.float32([65504.0]), "bf16")[0]
+    np.testing.assert_array_equal(O.argmax(x), idx)
+
+
+def test_argmax_ties_lowest_index_and_padding_mask():
+    x = np.zeros((2, 10), np.float32) - 1.0
+    x[0, [3, 7]] = 5.0
+    x[1, :] = -2.0
+    x[1, 8:] = 0.0  # padding columns: excluded by n_valid
+    np.testing.assert_array_equal(O.argmax(x, n_valid=8), [3, 0])
+    y = rng.standard_normal((5, 1000)).astype(np.float32)
+    np.testing.assert_array_equal(O.argmax(y), y.argmax(-1))
+
+
+# ------------------------------------------------------------- page manager
+
+def test_page_manager_hand_computed_prefill_then_decode():
+    """Prompt 100, page 64 -> 2 pages, last_page_len 36; after 28 decode
+    steps the sequence reaches 128 tokens and last_page_len reads 0
+    (persistent_kernel.cuh:250-251)."""
+    MSL = 256
+    tokens = np.zeros((1, MSL), np.int64)
+    tokens[0, :100] = np.arange(1, 101)
+    bm = O.BatchManager(max_requests=2, max_tokens=128, max_pages=8, page_size=64,
+                        tokens=tokens, prompt_lengths=np.int32([100]), eos=-5)
+    assert bm.prepare_next()
+    assert list(bm["qo_indptr"]) == [0, 100, 100]
+    assert list(bm["kv_indptr"]) == [0, 2, 2]
+    assert list(bm["kv_indices"][:2]) == [0, 1]
+    assert bm["last_page_len"][0] == 36
+    assert list(bm["input_tokens"][:100]) == list(range(1, 101))
+    for s in range(28):
+        bm["output_tokens"][: bm["qo_indptr"][1]] = 1000 + s
+        assert bm.prepare_next()
+        assert bm["qo_indptr"][1] == 1
+    # step = 100 + 27 = 127, one new token -> 128 tokens in 2 pages, last len 0
+    assert bm["step"][0] == 127
+    assert list(bm["kv_indptr"][:2]) == [0, 2]
+    assert bm["last_page_len"][0] == 0
+    bm["output_tokens"][0] = 7
+    assert bm.prepare_next()
+    assert list(bm["kv_indptr"][:2]) == [0, 3]           # third page allocated
+    assert list(bm["kv_indices"][:3]) == [0, 1, 2]
+    assert bm["last_page_len"][0] == 1
+    assert bm["tokens"][0, 100] == 1000 and bm["tokens"][0, 128] == 7
+
+
+def test_page_manager_eos_frees_pages_and_admits_next():
+    MSL = 64
+    tokens = np.zeros((3, MSL), np.int64)
+    tokens[:, :5] = 3
+    bm = O.BatchManager(max_requests=2, max_tokens=16, max_pages=4, page_size=8,
+                        tokens=tokens, prompt_lengths=np.int32([5, 5, 5]), eos=99)
+    assert bm.prepare_next()
+    assert list(bm["kv_indices"][:2]) == [0, 1]
+    bm["output_tokens"][:10] = 11
+    bm["output_tokens"][4] = 99  # request 0 emits EOS at its last prefill token
+    assert bm.prepare_next()
+    # request 0 finished: its page (0) went to the tail of the queue; request 1
+    # decodes with page 1; request 2 is admitted and takes the next free page (2)
+    assert list(bm["request_ids"]) == [1, 2]
+    assert list(bm["kv_indices"][:2]) == [1, 2]
+    assert bm["page_queue_tail"][0] == 5 and bm["page_queue"][0] == 0
+    # every live page index is distinct
+    live = bm["kv_indices"][: bm["kv_indptr"][2]]
+    assert len(set(live.tolist())) == len(live)

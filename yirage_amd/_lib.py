@@ -1,0 +1,94 @@
+"""ctypes binding of libyirage_hip.so (declared in include/yirage_hip.h).
+
+The library is built in-tree by yirage_amd.build; nothing here falls back to
+another implementation: a missing or stale library raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libyirage_hip.so")
+
+YR_OK = 0
+DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64 = 940, 941, 950, 955, 965
+W_NK, W_KN = 0, 1
+OP_RMSNORM_LINEAR, OP_GATED_MLP, OP_GQA_PREFILL, OP_LINEAR = 1, 2, 3, 4
+
+
+class YirageHipError(RuntimeError):
+    pass
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("device_id", ctypes.c_int),
+        ("num_compute_units", ctypes.c_int),
+        ("compute_capability", ctypes.c_int),
+        ("wavefront_size", ctypes.c_int),
+        ("total_memory", ctypes.c_size_t),
+        ("max_shared_memory", ctypes.c_size_t),
+        ("clock_khz", ctypes.c_int),
+        ("arch_name", ctypes.c_char * 64),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_U64 = ctypes.c_uint64
+
+# name -> (restype, argtypes); every symbol declared in include/yirage_hip.h
+SIGNATURES = {
+    "yr_hip_last_error": (ctypes.c_char_p, []),
+    "yr_hip_version": (ctypes.c_char_p, []),
+    "yr_hip_device_info": (_I, [_I, ctypes.POINTER(DeviceInfo)]),
+    "yr_hip_synth_fill": (_I, [_P, _SZ, _I, _U64, _U64, _F, _P]),
+    "yr_hip_rmsnorm_linear_workspace": (_SZ, [_I, _I, _I, _I, _I]),
+    "yr_hip_gated_mlp_workspace": (_SZ, [_I, _I, _I, _I, _I]),
+    "yr_hip_linear_workspace": (_SZ, [_I, _I, _I, _I, _I]),
+    "yr_hip_rmsnorm_linear": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
+    "yr_hip_gated_mlp": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "yr_hip_linear": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "yr_hip_gqa_decode_workspace": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "yr_hip_gqa_decode_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "yr_hip_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "yr_hip_argmax": (_I, [_P, _P, _I, _I, _I, _I, _P]),
+    "yr_hip_run_fused": (_I, [_I, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "yr_backend_num_registered": (_I, []),
+    "yr_backend_registered_name": (_I, [_I, ctypes.c_char_p, _SZ]),
+    "yr_backend_is_available": (_I, [ctypes.c_char_p]),
+    "yr_backend_type_from_name": (_I, [ctypes.c_char_p]),
+    "yr_backend_default": (_I, [ctypes.c_char_p, _SZ]),
+    "yr_backend_compile_flags": (_I, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the HIP backend library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise YirageHipError(
+                f"{LIB_PATH} not found: build it with `python -m yirage_amd.build` "
+                "(the hip backend has no fallback path)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().yr_hip_last_error().decode()
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != YR_OK:
+        raise YirageHipError(f"{what or 'yirage_hip'} failed ({rc}): {last_error()}")

@@ -1,0 +1,544 @@
+// GQA attention for gfx950: paged split-KV decode and causal prefill.
+//
+// Decode (HBM-bound, reads every cached K/V byte once):
+//   grid = (kv splits, kv heads, batch); one workgroup = 4 waves covers a
+//   chunk of DEC_CHUNK tokens of one (sequence, kv head) for all G = Hq/Hkv
+//   query heads of the group.  Q.K^T runs on MFMA 16x16x32 with the K rows as
+//   the B operand straight from HBM (16-byte loads, no LDS); P.V runs on VALU
+//   with lanes along head_dim.  Every wave keeps its own online-softmax state;
+//   the 4 waves merge in LDS, and splits merge through the workspace with the
+//   last-arriving workgroup (atomic ticket) writing the output.
+//
+// Prefill (MFMA-bound): flash attention, one workgroup per (64 query rows,
+//   q head, batch); K tiles and transposed V tiles are staged in LDS, S = Q K^T
+//   and O += P V both on MFMA 16x16x32, fp32 running max/sum per row.
+#include "yr_common.h"
+
+namespace yr {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- decode
+constexpr int DEC_WAVES = 4;
+constexpr int DEC_THREADS = DEC_WAVES * kWave;
+constexpr int DEC_TOK_PER_WAVE = 64;
+constexpr int DEC_CHUNK = DEC_WAVES * DEC_TOK_PER_WAVE;  // 256 tokens per workgroup
+
+struct DecodeArgs {
+  const uint16_t* q;       // [B][Hq][D]
+  const uint16_t* kc;      // [P][page][Hkv][D]
+  const uint16_t* vc;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* kv_len;
+  uint16_t* out;           // [B][Hq][D]
+  float* partial;          // [B][Hkv][splits][G][D + 2]
+  uint32_t* tickets;       // [B][Hkv]
+  int B, Hq, Hkv, page, splits;
+  float scale_log2;        // log2(e) / sqrt(D)
+};
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (DT == DT_F16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c,
+                                                  0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b),
+                                                   c, 0, 0, 0);
+  }
+}
+
+// D = 128, G <= 16
+template <int DT, int G>
+__global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
+  constexpr int D = 128;
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int len = a.kv_len[b];
+  const int c0 = split * DEC_CHUNK;            // first token of this chunk
+  const int pbase = a.kv_indptr[b];
+  const size_t tok_stride = (size_t)a.Hkv * D;  // elements between tokens in a page
+  const size_t page_stride = (size_t)a.page * tok_stride;
+
+  __shared__ float s_p[DEC_WAVES][G][DEC_TOK_PER_WAVE];
+  __shared__ float s_m[DEC_WAVES][G], s_l[DEC_WAVES][G];
+  __shared__ float s_o[DEC_WAVES][G][D];
+  __shared__ int s_last;
+
+  const int wt0 = c0 + wave * DEC_TOK_PER_WAVE;  // first token of this wave
+  auto tok_addr = [&](int t) -> size_t {
+    int pg = a.kv_indices[pbase + t / a.page];
+    return (size_t)pg * page_stride + (size_t)(t % a.page) * tok_stride + (size_t)hk * D;
+  };
+
+  // ---- issue K (MFMA B operand) and V (VALU) loads for the wave's 64 tokens
+  uint4 kf[4][4];  // [n-tile j][k-step s]
+  uint4 vf[16];    // token wt0 + lane/16 + 4i, dims (lane%16)*8 .. +8
+  {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int t = wt0 + 16 * j + (lane % 16);
+      bool ok = t < len;
+      size_t base = ok ? tok_addr(t) : 0;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        int d = 32 * s + (lane / 16) * 8;
+        kf[j][s] = ok ? ldg16(a.kc + base + d) : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      int t = wt0 + lane / 16 + 4 * i;
+      bool ok = t < len;
+      vf[i] = ok ? ldg16(a.vc + tok_addr(t) + (lane % 16) * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- Q as the MFMA A operand: row = head (lane%16 < G), k = d
+  uint4 qf[4];
+  {
+    int g = lane % 16;
+    const uint16_t* qrow = a.q + ((size_t)b * a.Hq + (size_t)hk * G + g) * D;
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+      qf[s] = g < G ? ldg16(qrow + 32 * s + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
+  }
+
+  // ---- scores: C[head][token] for 4 n-tiles of 16 tokens
+  f32x4 sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; s++) c = mfma16x16x32<DT>(qf[s], kf[j][s], c);
+    sc[j] = c;
+  }
+  // lane l holds rows 4*(l/16)+i, column l%16: head g = 4*(l/16)+i
+  float mloc[4], lloc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      int t = wt0 + 16 * j + (lane % 16);
+      float v = t < len ? sc[j][i] * a.scale_log2 : -INFINITY;
+      sc[j][i] = v;
+      m = fmaxf(m, v);
+    }
+    // max over the 16 lanes sharing l/16
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    float l = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float p = m == -INFINITY ? 0.f : exp2f(sc[j][i] - m);
+      sc[j][i] = p;
+      l += p;
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
+    mloc[i] = m;
+    lloc[i] = l;
+    int g = 4 * (lane / 16) + i;
+    if (g < G) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) s_p[wave][g][16 * j + (lane % 16)] = sc[j][i];
+      if ((lane % 16) == 0) {
+        s_m[wave][g] = m;
+        s_l[wave][g] = l;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- O = P V over the wave's tokens; lane: dims (lane%16)*8.., tokens lane/16 + 4i
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[g][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    int tl = lane / 16 + 4 * i;
+    uint32_t vw[4] = {vf[i].x, vf[i].y, vf[i].z, vf[i].w};
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = lo16<DT>(vw[e]);
+      v[2 * e + 1] = hi16<DT>(vw[e]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float p = s_p[wave][g][tl];
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[g][e] = fmaf(p, v[e], o[g][e]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float x = o[g][e];
+      x += __shfl_xor(x, 16, kWave);
+      x += __shfl_xor(x, 32, kWave);
+      o[g][e] = x;
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) s_o[wave][g][lane * 8 + e] = o[g][e];
+  }
+  __syncthreads();
+
+  // ---- merge the 4 waves: thread -> (g, d)
+  const int REC = D + 2;
+  float* rec_base = a.partial + (((size_t)b * a.Hkv + hk) * a.splits) * G * REC;
+  for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
+    int g = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; w++) M = fmaxf(M, s_m[w][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; w++) {
+      float f = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+      L += s_l[w][g] * f;
+      O += s_o[w][g][d] * f;
+    }
+    if (a.splits == 1) {
+      a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
+    } else {
+      float* rec = rec_base + ((size_t)split * G + g) * REC;
+      rec[d] = O;
+      if (d == 0) {
+        rec[D] = M;
+        rec[D + 1] = L;
+      }
+    }
+  }
+  if (a.splits == 1) return;
+
+  // ---- split merge by the last workgroup of this (b, hk)
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t old = atomicAdd(&a.tickets[b * a.Hkv + hk], 1u);
+    s_last = old == (uint32_t)(a.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
+    int g = idx / D, d = idx % D;
+    float M = -INFINITY;
+    for (int s = 0; s < a.splits; s++)
+      M = fmaxf(M, __builtin_nontemporal_load(rec_base + ((size_t)s * G + g) * REC + D));
+    float L = 0.f, O = 0.f;
+    for (int s = 0; s < a.splits; s++) {
+      const float* rec = rec_base + ((size_t)s * G + g) * REC;
+      float ms = __builtin_nontemporal_load(rec + D);
+      float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+      L += __builtin_nontemporal_load(rec + D + 1) * f;
+      O += __builtin_nontemporal_load(rec + d) * f;
+    }
+    a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
+  }
+  if (tid == 0) a.tickets[b * a.Hkv + hk] = 0u;
+}
+
+
+static int dec_splits(int max_len) { return (max_len + DEC_CHUNK - 1) / DEC_CHUNK; }
+
+// ---------------------------------------------------------------- prefill
+constexpr int PF_WAVES = 4;
+constexpr int PF_THREADS = PF_WAVES * kWave;
+constexpr int PF_QROWS = 16 * PF_WAVES;  // 64 query rows per workgroup
+constexpr int PF_KT = 64;                // kv tokens per tile
+
+struct PrefillArgs {
+  const uint16_t* q;  // [B][S][Hq][D]
+  const uint16_t* k;  // [B][S][Hkv][D]
+  const uint16_t* v;
+  uint16_t* o;
+  int B, S, Hq, Hkv, causal;
+  float scale_log2;
+};
+
+template <int DT>
+__global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) {
+  constexpr int D = 128;
+  // LDS: K tile [64 tok][128 d] (row pad 8 elems), V^T tile [128 d][64 tok] (pad 8)
+  constexpr int KP = D + 8, VP = PF_KT + 8;
+  __shared__ __align__(16) uint16_t sk[PF_KT * KP];
+  __shared__ __align__(16) uint16_t svt[D * VP];
+  __shared__ __align__(16) uint16_t sp[PF_WAVES][16 * (PF_KT + 8)];
+
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int G = a.Hq / a.Hkv, hk = h / G;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int q0 = qt * PF_QROWS + wave * 16;  // first query row of this wave
+  const size_t qstride = (size_t)a.Hq * D, kstride = (size_t)a.Hkv * D;
+
+  // Q fragments (A operand): row q0 + lane%16, d = 32 s + 8 (lane/16)
+  uint4 qf[4];
+  {
+    int r = q0 + lane % 16;
+    const uint16_t* qrow = a.q + ((size_t)b * a.S + r) * qstride + (size_t)h * D;
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+      qf[s] = r < a.S ? ldg16(qrow + 32 * s + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
+  }
+  f32x4 acc[8];  // O[16 rows][128 d] as 8 n-tiles of 16 d
+#pragma unroll
+  for (int n = 0; n < 8; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i[4], l_i[4];  // rows 4*(lane/16)+i of the wave's 16
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    m_i[i] = -INFINITY;
+    l_i[i] = 0.f;
+  }
+
+  const int wg_last_row = (qt + 1) * PF_QROWS - 1;
+  const int kv_end = a.causal ? min(a.S, wg_last_row + 1) : a.S;
+  for (int t0 = 0; t0 < kv_end; t0 += PF_KT) {
+    __syncthreads();
+    // stage K tile (row-major) and V tile (transposed) : 64 tok x 128 d each
+    for (int c = tid; c < PF_KT * (D / 8); c += PF_THREADS) {
+      int tr = c / (D / 8), dc = (c % (D / 8)) * 8;
+      int t = t0 + tr;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (t < a.S) {
+        size_t off = ((size_t)b * a.S + t) * kstride + (size_t)hk * D + dc;
+        kv = ldg16(a.k + off);
+        vv = ldg16(a.v + off);
+      }
+      *reinterpret_cast<uint4*>(&sk[tr * KP + dc]) = kv;
+      uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        svt[(dc + 2 * e) * VP + tr] = (uint16_t)(vw[e] & 0xffff);
+        svt[(dc + 2 * e + 1) * VP + tr] = (uint16_t)(vw[e] >> 16);
+      }
+    }
+    __syncthreads();
+    if (a.causal && t0 > q0 + 15) continue;  // whole tile masked for this wave
+
+    // S = Q K^T : 4 n-tiles of 16 tokens
+    f32x4 s4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        uint4 kb = *reinterpret_cast<const uint4*>(&sk[(16 * j + lane % 16) * KP + 32 * s + (lane / 16) * 8]);
+        c = mfma16x16x32<DT>(qf[s], kb, c);
+      }
+      s4[j] = c;
+    }
+    // online softmax per row (row = 4*(lane/16)+i, col = token 16 j + lane%16)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int r = q0 + 4 * (lane / 16) + i;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        int t = t0 + 16 * j + lane % 16;
+        bool ok = t < a.S && (!a.causal || t <= r);
+        float v = ok ? s4[j][i] * a.scale_log2 : -INFINITY;
+        s4[j][i] = v;
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+      float mnew = fmaxf(m_i[i], mx);
+      float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[i] - mnew);
+      float ls = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float p = mnew == -INFINITY ? 0.f : exp2f(s4[j][i] - mnew);
+        s4[j][i] = p;
+        ls += p;
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) ls += __shfl_xor(ls, o, kWave);
+      l_i[i] = l_i[i] * alpha + ls;
+      m_i[i] = mnew;
+#pragma unroll
+      for (int n = 0; n < 8; n++) acc[n][i] *= alpha;
+      // P (rounded to the input dtype) to LDS as [row][token]
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        sp[wave][(4 * (lane / 16) + i) * (PF_KT + 8) + 16 * j + lane % 16] = (uint16_t)st_elem<DT>(s4[j][i]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes of this wave done
+    __builtin_amdgcn_wave_barrier();
+    // O += P V : A = P[16 rows][32 tok] (lane: row lane%16, tok 8(lane/16)..), B = V[32 tok][16 d]
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      uint4 pa = *reinterpret_cast<const uint4*>(&sp[wave][(lane % 16) * (PF_KT + 8) + 32 * ks + (lane / 16) * 8]);
+#pragma unroll
+      for (int n = 0; n < 8; n++) {
+        uint4 vb = *reinterpret_cast<const uint4*>(&svt[(16 * n + lane % 16) * VP + 32 * ks + (lane / 16) * 8]);
+        acc[n] = mfma16x16x32<DT>(pa, vb, acc[n]);
+      }
+    }
+  }
+  // write O rows 4*(lane/16)+i, d = 16 n + lane%16
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int r = q0 + 4 * (lane / 16) + i;
+    if (r >= a.S) continue;
+    float inv = l_i[i] > 0.f ? 1.f / l_i[i] : 0.f;
+    uint16_t* orow = a.o + ((size_t)b * a.S + r) * qstride + (size_t)h * D;
+#pragma unroll
+    for (int n = 0; n < 8; n++) orow[16 * n + lane % 16] = (uint16_t)st_elem<DT>(acc[n][i] * inv);
+  }
+}
+
+// ---------------------------------------------------------------- argmax
+// One workgroup per row; lowest index wins ties.
+template <int DT>
+__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* x, int64_t* out, int n, int n_valid) {
+  const int row = blockIdx.x;
+  const uint16_t* xr = x + (size_t)row * n;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < n_valid; i += blockDim.x) {
+    float v = ld_elem<DT>(xr[i]);
+    if (v > best || (v == best && i < bi)) {
+      best = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(best, o, kWave);
+    int oi = __shfl_xor(bi, o, kWave);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  int w = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    sv[w] = best;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < (int)(blockDim.x / kWave); k++)
+      if (sv[k] > best || (sv[k] == best && si[k] < bi)) {
+        best = sv[k];
+        bi = si[k];
+      }
+    out[row] = bi == 0x7fffffff ? -1 : bi;
+  }
+}
+
+}  // namespace yr
+
+using namespace yr;
+
+extern "C" {
+
+size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv_len, int page_size) {
+  (void)page_size;
+  int sp = dec_splits(max_kv_len);
+  if (sp <= 1 || hkv <= 0) return 0;
+  int G = hq / hkv;
+  return kTicketBytes + (size_t)batch * hkv * sp * G * (d + 2) * sizeof(float);
+}
+
+int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
+                            const int32_t* kv_indices, const int32_t* kv_len, void* out, int batch, int hq,
+                            int hkv, int d, int page_size, int max_kv_len, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const char* nm = "yr_hip_gqa_decode_paged";
+  if (!q || !k_cache || !v_cache || !kv_indptr || !kv_indices || !kv_len || !out)
+    return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (batch <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: hq must be a multiple of hkv", nm);
+  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
+  int G = hq / hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return fail(YR_E_INVALID, "%s: group size %d", nm, G);
+  if (page_size <= 0) return fail(YR_E_INVALID, "%s: bad page size", nm);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  if (max_kv_len <= 0) return fail(YR_E_INVALID, "%s: max_kv_len must be > 0", nm);
+  if (batch * hkv > kMaxTickets) return fail(YR_E_INVALID, "%s: batch * hkv too large", nm);
+  size_t need = yr_hip_gqa_decode_workspace(batch, hq, hkv, d, max_kv_len, page_size);
+  if (need > workspace_bytes || (need && !workspace))
+    return fail(YR_E_WORKSPACE, "%s: workspace %zu < %zu", nm, workspace_bytes, need);
+  DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.kc = (const uint16_t*)k_cache;
+  a.vc = (const uint16_t*)v_cache;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_len = kv_len;
+  a.out = (uint16_t*)out;
+  a.B = batch;
+  a.Hq = hq;
+  a.Hkv = hkv;
+  a.page = page_size;
+  a.splits = dec_splits(max_kv_len);
+  a.tickets = (uint32_t*)workspace;
+  a.partial = need ? (float*)((char*)workspace + kTicketBytes) : nullptr;
+  a.scale_log2 = kLog2e / sqrtf((float)d);
+  dim3 grid(a.splits, hkv, batch);
+  hipStream_t st = (hipStream_t)stream;
+#define YR_DEC(G_)                                                                                        \
+  if (G == G_) {                                                                                          \
+    if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL((gqa_decode_kernel<DT_F16, G_>), grid, dim3(DEC_THREADS), 0, st, a); \
+    else hipLaunchKernelGGL((gqa_decode_kernel<DT_BF16, G_>), grid, dim3(DEC_THREADS), 0, st, a);         \
+  }
+  YR_DEC(1) YR_DEC(2) YR_DEC(4) YR_DEC(8) YR_DEC(16)
+#undef YR_DEC
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, int batch, int seq, int hq,
+                       int hkv, int d, int causal, int dtype, void* stream) {
+  const char* nm = "yr_hip_gqa_prefill";
+  if (!q || !k || !v || !out) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (batch <= 0 || seq <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: bad shape", nm);
+  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.o = (uint16_t*)out;
+  a.B = batch;
+  a.S = seq;
+  a.Hq = hq;
+  a.Hkv = hkv;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = kLog2e / sqrtf((float)d);
+  dim3 grid((seq + PF_QROWS - 1) / PF_QROWS, hq, batch);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL(gqa_prefill_kernel<DT_F16>, grid, dim3(PF_THREADS), 0, st, a);
+  else hipLaunchKernelGGL(gqa_prefill_kernel<DT_BF16>, grid, dim3(PF_THREADS), 0, st, a);
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+int yr_hip_argmax(const void* x, int64_t* out, int rows, int n, int n_valid, int dtype, void* stream) {
+  const char* nm = "yr_hip_argmax";
+  if (!x || !out) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (rows <= 0 || n <= 0 || n_valid <= 0 || n_valid > n) return fail(YR_E_INVALID, "%s: bad shape", nm);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == YR_DTYPE_F16)
+    hipLaunchKernelGGL(argmax_kernel<DT_F16>, dim3(rows), dim3(256), 0, st, (const uint16_t*)x, out, n, n_valid);
+  else if (dtype == YR_DTYPE_BF16)
+    hipLaunchKernelGGL(argmax_kernel<DT_BF16>, dim3(rows), dim3(256), 0, st, (const uint16_t*)x, out, n, n_valid);
+  else
+    return fail(YR_E_INVALID, "%s: dtype", nm);
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// Shared device/host helpers for the MI355X (gfx950, wave64) HIP backend.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/yirage_hip.h"
+
+namespace yr {
+
+constexpr int kWave = 64;
+
+typedef _Float16 half_t;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+// ----------------------------------------------------------------- dtype tags
+// DT_F16 / DT_BF16 select the 16-bit storage type; all math is fp32.
+enum : int { DT_F16 = YR_DTYPE_F16, DT_BF16 = YR_DTYPE_BF16 };
+
+// Workspace layout shared by every operator that needs one:
+//   [0, kTicketBytes)  u32 arrival tickets, all zero at rest (each operator
+//                      re-arms the tickets it used before it returns)
+//   [kTicketBytes, ..) fp32 scratch (split partials), contents undefined
+// A fixed ticket region means operators of different shapes can share one
+// workspace without their scratch ever overlapping a ticket.
+constexpr size_t kTicketBytes = 64 * 1024;
+constexpr int kMaxTickets = (int)(kTicketBytes / 4);
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) {
+  return __uint_as_float(b16 << 16);
+}
+
+// round-to-nearest-even f32 -> bf16 bits (NaN kept quiet)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
+  union { uint16_t u; _Float16 h; } c;
+  c.u = (uint16_t)h16;
+  return (float)c.h;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  union { uint16_t u; _Float16 h; } c;
+  c.h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+  return c.u;
+}
+
+template <int DT>
+__device__ __forceinline__ float ld_elem(uint32_t bits16) {
+  if constexpr (DT == DT_F16) return f16_bits_to_f32(bits16);
+  else return bf16_bits_to_f32(bits16);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t st_elem(float v) {
+  if constexpr (DT == DT_F16) return f32_to_f16_bits(v);
+  else return f32_to_bf16_bits(v);
+}
+
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  return ld_elem<DT>(st_elem<DT>(v));
+}
+
+// low / high 16-bit element of a packed dword
+template <int DT>
+__device__ __forceinline__ float lo16(uint32_t w) { return ld_elem<DT>(w & 0xffffu); }
+template <int DT>
+__device__ __forceinline__ float hi16(uint32_t w) { return ld_elem<DT>(w >> 16); }
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return st_elem<DT>(lo) | (st_elem<DT>(hi) << 16);
+}
+
+// fp32 += dot(a.xy, b.xy) on packed 16-bit pairs (v_dot2_f32_f16 / v_dot2_f32_bf16)
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == DT_F16) {
+    half2v ha = __builtin_bit_cast(half2v, a);
+    half2v hb = __builtin_bit_cast(half2v, b);
+    return __builtin_amdgcn_fdot2(ha, hb, c, false);
+  } else {
+    bf16x2v ha = __builtin_bit_cast(bf16x2v, a);
+    bf16x2v hb = __builtin_bit_cast(bf16x2v, b);
+    return __builtin_amdgcn_fdot2_f32_bf16(ha, hb, c, false);
+  }
+}
+
+// ----------------------------------------------------------------- wave ops
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// 128-bit global load that bypasses nothing special (cached); used for weights
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// streaming (non-temporal) 128-bit load for data read exactly once
+__device__ __forceinline__ uint4 ldg16_stream(const void* p) {
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+  uint4 r;
+  r.x = __builtin_nontemporal_load(&q->x);
+  r.y = __builtin_nontemporal_load(&q->y);
+  r.z = __builtin_nontemporal_load(&q->z);
+  r.w = __builtin_nontemporal_load(&q->w);
+  return r;
+}
+
+__device__ __forceinline__ float silu(float a) { return a / (1.0f + __expf(-a)); }
+
+}  // namespace yr
+
+// ----------------------------------------------------------------- host side
+namespace yr {
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+}  // namespace yr
+
+#define YR_CHECK_LAUNCH(what)                                    \
+  do {                                                           \
+    hipError_t _e = hipGetLastError();                           \
+    if (_e != hipSuccess) return yr::check_hip(_e, what);        \
+  } while (0)
