@@ -64,7 +64,6 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   __shared__ float s_p[DEC_WAVES][G][DEC_TOK_PER_WAVE];
   __shared__ float s_m[DEC_WAVES][G], s_l[DEC_WAVES][G];
   __shared__ float s_o[DEC_WAVES][G][D];
-  __shared__ int s_last;
 
   const int wt0 = c0 + wave * DEC_TOK_PER_WAVE;  // first token of this wave
   auto tok_addr = [&](int t) -> size_t {
@@ -211,41 +210,52 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
       a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
     } else {
       float* rec = rec_base + ((size_t)split * G + g) * REC;
-      rec[d] = O;
+      st_agent(rec + d, O);
       if (d == 0) {
-        rec[D] = M;
-        rec[D + 1] = L;
+        st_agent(rec + D, M);
+        st_agent(rec + D + 1, L);
       }
     }
   }
   if (a.splits == 1) return;
 
   // ---- split merge by the last workgroup of this (b, hk)
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t old = atomicAdd(&a.tickets[b * a.Hkv + hk], 1u);
-    s_last = old == (uint32_t)(a.splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(&a.tickets[b * a.Hkv + hk], a.splits)) return;
   for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
     int g = idx / D, d = idx % D;
-    float M = -INFINITY;
-    for (int s = 0; s < a.splits; s++)
-      M = fmaxf(M, __builtin_nontemporal_load(rec_base + ((size_t)s * G + g) * REC + D));
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < a.splits; s++) {
-      const float* rec = rec_base + ((size_t)s * G + g) * REC;
-      float ms = __builtin_nontemporal_load(rec + D);
-      float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-      L += __builtin_nontemporal_load(rec + D + 1) * f;
-      O += __builtin_nontemporal_load(rec + d) * f;
+    // one pass over the splits, 16 records in flight per round trip
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    for (int s0 = 0; s0 < a.splits; s0 += 16) {
+      float mv[16], lv[16], ov[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        if (s0 + u < a.splits) {
+          const float* rec = rec_base + ((size_t)(s0 + u) * G + g) * REC;
+          mv[u] = ld_agent(rec + D);
+          lv[u] = ld_agent(rec + D + 1);
+          ov[u] = ld_agent(rec + d);
+        } else {
+          mv[u] = -INFINITY;
+          lv[u] = 0.f;
+          ov[u] = 0.f;
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int u = 0; u < 16; u++) mb = fmaxf(mb, mv[u]);
+      float f0 = M == -INFINITY ? 0.f : exp2f(M - mb);
+      L *= f0;
+      O *= f0;
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        float f = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mb);
+        L += lv[u] * f;
+        O += ov[u] * f;
+      }
+      M = mb;
     }
     a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
   }
-  if (tid == 0) a.tickets[b * a.Hkv + hk] = 0u;
 }
 
 

@@ -49,7 +49,7 @@ template <int ROWS>
 constexpr int kn_rows_per_wg() { return KN_WAVES * 4 * ROWS; }
 
 template <int NMAT>
-__host__ __device__ constexpr int kn_rec(int nb) { return NMAT * nb * KN_COLS + nb; }
+__host__ __device__ constexpr int kn_rec(int nb) { return round_up4(NMAT * nb * KN_COLS + nb); }
 
 template <int DT, int NB, int NMAT, int EPI>
 __device__ __forceinline__ void tile_epilogue(const GemvArgs& a, const float* acc /*[NMAT][NB][128] in LDS*/,
@@ -77,30 +77,14 @@ template <int DT, int NB, int NMAT, int EPI>
 __device__ __forceinline__ void splitk_finish(const GemvArgs& a, float* red /*LDS, >= rec floats*/,
                                               int tile, int split, int col_base) {
   constexpr int REC = kn_rec<NMAT>(NB);
-  __shared__ int s_last;
   if (a.S == 1) {
     tile_epilogue<DT, NB, NMAT, EPI>(a, red, red + NMAT * NB * KN_COLS, col_base);
     return;
   }
-  float* rec = a.partial + ((size_t)tile * a.S + split) * REC;
-  for (int i = threadIdx.x; i < REC; i += blockDim.x) rec[i] = red[i];
-  __threadfence();
+  put_record(a.partial + ((size_t)tile * a.S + split) * REC, red, REC);
+  if (!arrive_last(&a.tickets[tile], a.S)) return;
+  sum_records(a.partial + (size_t)tile * a.S * REC, a.S, REC, red);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t old = atomicAdd(&a.tickets[tile], 1u);
-    s_last = (old == (uint32_t)(a.S - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* base = a.partial + (size_t)tile * a.S * REC;
-  for (int i = threadIdx.x; i < REC; i += blockDim.x) {
-    float v = 0.f;
-    for (int s = 0; s < a.S; s++) v += __builtin_nontemporal_load(base + (size_t)s * REC + i);
-    red[i] = v;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) a.tickets[tile] = 0u;  // re-arm for the next launch
   tile_epilogue<DT, NB, NMAT, EPI>(a, red, red + NMAT * NB * KN_COLS, col_base);
 }
 
@@ -110,7 +94,7 @@ __global__ __launch_bounds__(KN_THREADS) void gemv_kn_kernel(GemvArgs a) {
   constexpr int NPAIR = RPW / 2;
   __shared__ uint32_t xs[NPAIR * NB];            // packed (x[k], x[k+1]) per batch row
   __shared__ float ssl[8];
-  __shared__ float red[NMAT * NB * KN_COLS + NB];
+  __shared__ float red[kn_rec<NMAT>(NB)];
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -256,7 +240,7 @@ __device__ __forceinline__ void wave_reduce_nb(float (&v)[NB], int lane) {
 template <int DT, int NB, int NMAT, int EPI, int C, int TROWS>
 __global__ __launch_bounds__(NK_THREADS) void gemv_nk_kernel(GemvArgs a) {
   constexpr int KS = kWave * 8 * C;  // K elements per workgroup
-  __shared__ float red[NMAT * NB * TROWS + NB];
+  __shared__ float red[round_up4(NMAT * NB * TROWS + NB)];
   __shared__ float ssl[NK_WAVES];
 
   const int tid = threadIdx.x;
@@ -351,30 +335,14 @@ __global__ __launch_bounds__(NK_THREADS) void gemv_nk_kernel(GemvArgs a) {
   __syncthreads();
 
   // split-K combine (same ticket protocol as the KN kernel, tile width TROWS)
-  constexpr int REC = NMAT * NB * TROWS + NB;
-  __shared__ int s_last;
+  constexpr int REC = round_up4(NMAT * NB * TROWS + NB);
   const float* fin = red;
   __shared__ float sum[REC];
   if (a.S > 1) {
-    float* rec = a.partial + ((size_t)tile * a.S + split) * REC;
-    for (int i = tid; i < REC; i += NK_THREADS) rec[i] = red[i];
-    __threadfence();
+    put_record(a.partial + ((size_t)tile * a.S + split) * REC, red, REC);
+    if (!arrive_last(&a.tickets[tile], a.S)) return;
+    sum_records(a.partial + (size_t)tile * a.S * REC, a.S, REC, sum);
     __syncthreads();
-    if (tid == 0) {
-      uint32_t old = atomicAdd(&a.tickets[tile], 1u);
-      s_last = (old == (uint32_t)(a.S - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* base = a.partial + (size_t)tile * a.S * REC;
-    for (int i = tid; i < REC; i += NK_THREADS) {
-      float v = 0.f;
-      for (int s = 0; s < a.S; s++) v += __builtin_nontemporal_load(base + (size_t)s * REC + i);
-      sum[i] = v;
-    }
-    __syncthreads();
-    if (tid == 0) a.tickets[tile] = 0u;
     fin = sum;
   }
   for (int i = tid; i < NB * TROWS; i += NK_THREADS) {
@@ -411,12 +379,12 @@ static Plan plan_gemv(int B, int K, int N, int layout, int nmat) {
     int rpw = KN_WAVES * 4 * (nmat == 1 ? KN_ROWS_1 : KN_ROWS_2);
     p.tiles = (N + KN_COLS - 1) / KN_COLS;
     p.S = (K + rpw - 1) / rpw;
-    p.rec = nmat * nb * KN_COLS + nb;
+    p.rec = round_up4(nmat * nb * KN_COLS + nb);
   } else {
     int ks = kWave * 8 * (B == 1 ? NK_C1 : NK_C8);
     p.tiles = (N + NK_TROWS - 1) / NK_TROWS;
     p.S = (K + ks - 1) / ks;
-    p.rec = nmat * nb * NK_TROWS + nb;
+    p.rec = round_up4(nmat * nb * NK_TROWS + nb);
   }
   p.ws = 0;
   if (p.S > 1) p.ws = kTicketBytes + (size_t)p.tiles * p.S * p.rec * sizeof(float);

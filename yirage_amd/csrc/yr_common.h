@@ -126,6 +126,88 @@ __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
   return r;
 }
 
+// ---------------------------------------------------------------- cross-CU exchange
+// Split-K style exchange between workgroups of one launch without cache
+// maintenance: records are written with agent-scope (sc1) stores that go
+// past the XCD-local L2, completion is awaited (vmcnt 0) before the arrival
+// ticket is bumped, and the last arriving workgroup reads the records back
+// with agent-scope (sc1) loads.  No buffer_wbl2 / buffer_inv is issued, which
+// on gfx950 would walk the whole L2 of the XCD for every workgroup.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void st_agent4(float* p, float4 v) {
+  uint64_t lo = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
+  uint64_t hi = (uint64_t)__float_as_uint(v.z) | ((uint64_t)__float_as_uint(v.w) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ float4 ld_agent4(const float* p) {
+  uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t hi = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                     __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
+}
+
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Copy n floats (n % 4 == 0) from LDS to a record with agent-scope stores.
+__device__ __forceinline__ void put_record(float* rec, const float* src, int n) {
+  for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4)
+    st_agent4(rec + i, make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]));
+}
+
+// Every thread's agent stores complete, then one arrival on *ticket.
+// Returns true in every thread of the workgroup that arrived last (of n);
+// that workgroup re-arms the ticket to 0.
+__device__ __forceinline__ bool arrive_last(uint32_t* ticket, int n) {
+  __shared__ int s_last;
+  wait_vm();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (uint32_t)(n - 1);
+    if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+// Sum S records of `rec` floats (rec % 4 == 0) laid out back to back at
+// `base` into dst[0..rec), in record order s = 0..S-1 (deterministic).  Each
+// thread keeps up to 8 independent 16-byte loads in flight, so the S records
+// cost ceil(S / 8) memory round trips instead of S.
+__device__ __forceinline__ void sum_records(const float* base, int S, int rec, float* dst) {
+  for (int i = threadIdx.x * 4; i < rec; i += blockDim.x * 4) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = ld_agent4(base + (size_t)(s + u) * rec + i);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+      }
+    }
+    for (; s < S; s++) {
+      float4 v = ld_agent4(base + (size_t)s * rec + i);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    dst[i] = acc.x; dst[i + 1] = acc.y; dst[i + 2] = acc.z; dst[i + 3] = acc.w;
+  }
+}
+
+__host__ __device__ constexpr int round_up4(int x) { return (x + 3) & ~3; }
+
 __device__ __forceinline__ float silu(float a) { return a / (1.0f + __expf(-a)); }
 
 }  // namespace yr
