@@ -153,6 +153,65 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* ------------------------------------------------------- persistent kernel */
+/* Task graph of the persistent megakernel, built on the host (no GPU needed).
+ * `json` describes the workers, tensors (name -> device pointer, dims,
+ * dtype) and the ordered op list; see yirage_amd/persistent_kernel.py for the
+ * producer.  Replaces Graph::generate_task_graph / register_mugraph /
+ * sanity_check (src/kernel/runtime.cc:161-600,1416-1449). */
+typedef struct yr_pk_graph yr_pk_graph;
+typedef struct yr_pk_handle yr_pk_handle;
+int yr_pk_graph_build(const char* json, yr_pk_graph** out);
+void yr_pk_graph_free(yr_pk_graph* graph);
+/* info[0..7] = ops, tasks, events, workers, tickets, scratch floats, longest queue, 0 */
+int yr_pk_graph_info(const yr_pk_graph* graph, int64_t* info, int n);
+/* rec[0..9] = op, task type, wait event, wait count, trigger event, row0, rows, i0, i1, i2 */
+int yr_pk_graph_task(const yr_pk_graph* graph, int task, int64_t* rec, int n);
+/* CPU replay of the queue/event protocol with random interleavings over
+ * `epochs` launches, then (race_window > 0) a proof that every conflicting
+ * tensor access pair within race_window ops is ordered.  YR_OK or
+ * YR_E_GRAPH with the finding in `report`.  Mirrors sanity_check
+ * (src/kernel/runtime.cc:540-600). */
+int yr_pk_graph_simulate(const yr_pk_graph* graph, uint64_t seed, int epochs, int race_window, char* report,
+                         size_t report_len);
+/* The task graph in the reference's task_graph.json vocabulary
+ * (all_tasks / all_events / first_tasks, runtime.cc:847-1318). */
+int yr_pk_graph_export_json(const yr_pk_graph* graph, char* buf, size_t buf_len, size_t* needed);
+
+/* Device pointers of the reference's meta tensors, in the order of
+ * python/yirage/persistent_kernel.py:1291-1301. */
+typedef struct {
+  int32_t* step;
+  int64_t* tokens;
+  int64_t* input_tokens;
+  int64_t* output_tokens;
+  int32_t* num_new_tokens;
+  int32_t* prompt_lengths;
+  int32_t* qo_indptr;
+  int32_t* paged_kv_indptr;
+  int32_t* paged_kv_indices;
+  int32_t* paged_kv_last_page_len;
+} yr_pk_meta;
+
+/* Uploads a built graph to the current device (cooperative launch of one
+ * workgroup per worker).  Replaces init_persistent_kernel
+ * (persistent_kernel.cuh:1036-1249); unlike it, state lives in the handle so
+ * several persistent kernels can coexist. */
+int yr_pk_create(const yr_pk_graph* graph, const yr_pk_meta* meta, yr_pk_handle** out);
+/* Offline batch state (page queue, request slots) reset, as init_kernel
+ * (persistent_kernel.cuh:107-132). */
+int yr_pk_init_batch(yr_pk_handle* handle, void* stream);
+/* One pass over the task graph (one decode/extend step).  Replaces
+ * launch_persistent_kernel (persistent_kernel.cuh:1253-1318). */
+int yr_pk_launch(yr_pk_handle* handle, void* stream);
+/* Polls a dependency may spin before the watchdog flags an error. */
+int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
+/* Synchronous read of the status words; YR_E_TIMEOUT after a watchdog exit. */
+int yr_pk_status(yr_pk_handle* handle, int* status4);
+int yr_pk_reset_status(yr_pk_handle* handle);
+/* Replaces finalize_persistent_kernel (persistent_kernel.cuh:1320-1363). */
+void yr_pk_destroy(yr_pk_handle* handle);
+
 /* ------------------------------------------------------- backend registry */
 /* Restates BackendRegistry / BackendInterface
  * (include/yirage/backend/backend_registry.h:40-166,

@@ -21,6 +21,13 @@ class YirageHipError(RuntimeError):
     pass
 
 
+class PKMeta(ctypes.Structure):
+    """yr_pk_meta: device pointers of the reference's meta tensors."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "step", "tokens", "input_tokens", "output_tokens", "num_new_tokens", "prompt_lengths",
+        "qo_indptr", "paged_kv_indptr", "paged_kv_indices", "paged_kv_last_page_len")]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [
         ("device_id", ctypes.c_int),
@@ -57,6 +64,19 @@ SIGNATURES = {
     "yr_hip_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "yr_hip_argmax": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "yr_hip_run_fused": (_I, [_I, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "yr_pk_graph_build": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "yr_pk_graph_free": (None, [_P]),
+    "yr_pk_graph_info": (_I, [_P, ctypes.POINTER(ctypes.c_int64), _I]),
+    "yr_pk_graph_task": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int64), _I]),
+    "yr_pk_graph_simulate": (_I, [_P, _U64, _I, _I, ctypes.c_char_p, _SZ]),
+    "yr_pk_graph_export_json": (_I, [_P, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)]),
+    "yr_pk_create": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "yr_pk_init_batch": (_I, [_P, _P]),
+    "yr_pk_launch": (_I, [_P, _P]),
+    "yr_pk_set_spin_limit": (_I, [_P, ctypes.c_longlong]),
+    "yr_pk_status": (_I, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "yr_pk_reset_status": (_I, [_P]),
+    "yr_pk_destroy": (None, [_P]),
     "yr_backend_num_registered": (_I, []),
     "yr_backend_registered_name": (_I, [_I, ctypes.c_char_p, _SZ]),
     "yr_backend_is_available": (_I, [ctypes.c_char_p]),

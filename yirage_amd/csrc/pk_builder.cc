@@ -1,0 +1,672 @@
+// Host-side task-graph builder, CPU protocol simulator and race checker for
+// the persistent megakernel.
+//
+// Restates the reference's task-graph construction (src/kernel/runtime.cc:
+// 161-538 register_mugraph, 540-600 sanity_check, 847-1318 JSON schema)
+// for this backend's op set:
+//   * each op ("layer") expands into tasks covering disjoint output ranges;
+//   * consecutive ops are joined by events: a barrier event (all producer
+//     tasks) or, when a paged-attention op consumes the QKV projection,
+//     one event per kv-head group (the reference's gcd partitioning,
+//     runtime.cc:53-159, specialised to that edge);
+//   * tasks go to per-worker queues in op order (round-robin with a rotating
+//     start), which with co-resident workers makes the schedule deadlock-free.
+// The simulator replays the queue/event protocol on the CPU with random
+// interleavings; the race checker proves that every pair of conflicting
+// tensor accesses is ordered by the event graph.
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <random>
+#include <set>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "json_min.h"
+#include "pk_builder.h"
+
+namespace yr {
+namespace pk {
+
+static int dtype_bytes(int dt) {
+  switch (dt) {
+    case YR_DTYPE_F16: case YR_DTYPE_BF16: return 2;
+    case YR_DTYPE_F32: case YR_DTYPE_I32: return 4;
+    case YR_DTYPE_I64: return 8;
+  }
+  return 0;
+}
+
+struct Seg {
+  int tensor;
+  int64_t row0, rows;
+};
+
+static std::vector<Seg> read_segments(Graph& g, const json::Value& v) {
+  std::vector<Seg> segs;
+  if (v.kind == json::Value::Str) {
+    int t = g.tensor_id(v.s());
+    segs.push_back({t, 0, g.tensors[t].dims[0]});
+    return segs;
+  }
+  for (size_t i = 0; i < v.size(); i++) {
+    const json::Value& s = v[i];
+    int t = g.tensor_id(s[0].s());
+    Seg sg{t, s[1].i64(), s[2].i64()};
+    if (sg.row0 < 0 || sg.row0 + sg.rows > g.tensors[t].dims[0])
+      throw std::runtime_error("weight segment out of range for tensor " + g.tensors[t].name);
+    segs.push_back(sg);
+  }
+  return segs;
+}
+
+// Device address of virtual weight rows [r, r + n) (must lie in one segment).
+static const uint16_t* seg_rows(Graph& g, const std::vector<Seg>& segs, int64_t r, int64_t n, int64_t K) {
+  int64_t base = 0;
+  for (auto& s : segs) {
+    if (r >= base && r < base + s.rows) {
+      if (r + n > base + s.rows)
+        throw std::runtime_error("task rows straddle two weight segments; choose rows_per_task dividing the segments");
+      const Tensor& t = g.tensors[s.tensor];
+      if (t.dims.size() != 2 || t.dims[1] != K) throw std::runtime_error("weight " + t.name + " is not [rows, K]");
+      return (const uint16_t*)(t.ptr + (uint64_t)((s.row0 + (r - base)) * K * 2));
+    }
+    base += s.rows;
+  }
+  throw std::runtime_error("task rows beyond the weight segments");
+}
+
+static int64_t seg_total(const std::vector<Seg>& segs) {
+  int64_t n = 0;
+  for (auto& s : segs) n += s.rows;
+  return n;
+}
+
+int Graph::tensor_id(const std::string& name) const {
+  auto it = tensor_index.find(name);
+  if (it == tensor_index.end()) throw std::runtime_error("unknown tensor '" + name + "'");
+  return it->second;
+}
+
+const Tensor& Graph::t(const std::string& name) const { return tensors[tensor_id(name)]; }
+
+static void need_dtype(const Tensor& t, int dt, const char* what) {
+  if (t.dtype != dt) throw std::runtime_error(std::string(what) + ": tensor " + t.name + " has the wrong dtype");
+}
+
+static int ptr_tensor(Graph& g, const json::Value& op, const char* key, bool optional = false) {
+  if (!op.has(key)) {
+    if (optional) return -1;
+    throw std::runtime_error(std::string("op is missing '") + key + "'");
+  }
+  return g.tensor_id(op[key].s());
+}
+
+void Graph::build(const char* text) {
+  json::Value root = json::parse(text);
+  num_workers = (int)root["num_workers"].i64(0);
+  if (num_workers <= 0 || num_workers > 4096) throw std::runtime_error("num_workers must be in 1..4096");
+  cfg.max_tokens = (int)root["max_tokens"].i64(1);
+  cfg.max_requests = (int)root["max_requests"].i64(1);
+  cfg.page_size = (int)root["page_size"].i64(64);
+  cfg.max_pages = (int)root["max_pages"].i64(0);
+  cfg.max_seq_len = (int)root["max_seq_len"].i64(0);
+  cfg.total_requests = (int)root["total_requests"].i64(cfg.max_requests);
+  cfg.eos_token_id = root["eos_token_id"].i64(-1);
+
+  const json::Value& tv = root["tensors"];
+  if (tv.kind != json::Value::Obj) throw std::runtime_error("'tensors' must be an object");
+  for (auto& kv : tv.obj) {
+    Tensor t;
+    t.name = kv.first;
+    t.ptr = (uint64_t)kv.second["ptr"].f64();
+    for (size_t i = 0; i < kv.second["dims"].size(); i++) t.dims.push_back(kv.second["dims"][i].i64());
+    t.dtype = (int)kv.second["dtype"].i64();
+    if (!dtype_bytes(t.dtype)) throw std::runtime_error("tensor " + t.name + ": unsupported dtype");
+    tensor_index[t.name] = (int)tensors.size();
+    tensors.push_back(t);
+  }
+  const json::Value& mv = root["meta"];
+  if (mv.kind == json::Value::Obj)
+    for (auto& kv : mv.obj) meta_names[kv.first] = kv.second.s();
+
+  const json::Value& opsv = root["ops"];
+  if (opsv.kind != json::Value::Arr || opsv.size() == 0) throw std::runtime_error("'ops' must be a non-empty array");
+  int ticket_next = 0;
+  int64_t scratch_next = 0;
+  for (size_t oi = 0; oi < opsv.size(); oi++) {
+    const json::Value& o = opsv[oi];
+    const std::string type = o["type"].s();
+    OpDesc d;
+    memset(&d, 0, sizeof(d));
+    OpInfo info;
+    info.name = type;
+    int first_task = (int)tasks.size();
+    auto add_task = [&](TaskDesc td) {
+      td.op = (int)ops.size();
+      td.wait_event = -1;
+      td.trigger_event = -1;
+      tasks.push_back(td);
+    };
+    if (type == "embed") {
+      d.type = TASK_EMBED;
+      int tok = ptr_tensor(*this, o, "tokens"), tab = ptr_tensor(*this, o, "table"), out = ptr_tensor(*this, o, "out");
+      need_dtype(tensors[tok], YR_DTYPE_I64, "embed tokens");
+      const Tensor& T = tensors[tab];
+      d.K = (int)T.dims[1];
+      d.N = d.K;
+      d.vocab = (int)T.dims[0];
+      d.out_ld = (int)tensors[out].dims[1];
+      d.max_tokens = cfg.max_tokens;
+      d.tokens_in = (const int64_t*)tensors[tok].ptr;
+      d.table = (const uint16_t*)T.ptr;
+      d.out = (uint16_t*)tensors[out].ptr;
+      int nt = (int)o["tasks"].i64(1);
+      int per = (d.N + nt - 1) / nt;
+      per = (per + 7) & ~7;
+      for (int r = 0; r < d.N; r += per) {
+        TaskDesc td;
+        memset(&td, 0, sizeof(td));
+        td.row0 = r;
+        td.rows = std::min(per, d.N - r);
+        add_task(td);
+      }
+      info.writes.push_back({out, 0, d.N, 1});
+    } else if (type == "linear" || type == "rmsnorm_linear" || type == "rmsnorm_linear_silu" ||
+               type == "rmsnorm_linear_argmax") {
+      bool norm = type != "linear";
+      bool silu = type == "rmsnorm_linear_silu";
+      bool amax = type == "rmsnorm_linear_argmax";
+      d.type = type == "linear" ? TASK_LINEAR : silu ? TASK_RMSNORM_LINEAR_SILU
+                                             : amax ? TASK_RMSNORM_LINEAR_ARGMAX : TASK_RMSNORM_LINEAR;
+      int x = ptr_tensor(*this, o, "x"), out = ptr_tensor(*this, o, "out");
+      const Tensor& X = tensors[x];
+      need_dtype(X, YR_DTYPE_BF16, "linear x");
+      d.K = (int)X.dims[1];
+      d.x_ld = d.K;
+      d.x = (const uint16_t*)X.ptr;
+      d.max_tokens = cfg.max_tokens;
+      if (X.dims[0] < cfg.max_tokens) throw std::runtime_error("activation rows < max_tokens");
+      std::vector<Seg> segs = read_segments(*this, o["weight"]);
+      int64_t wrows = seg_total(segs);
+      int group = (int)o["group"].i64(0);
+      d.N = silu ? (int)(wrows / 2) : (int)wrows;
+      if (silu && (group <= 0 || wrows % (2 * group))) throw std::runtime_error("silu op: bad 'group'");
+      const Tensor& OT = tensors[out];
+      d.out_ld = (int)OT.dims[1];
+      int col0 = (int)o["out_col0"].i64(0);
+      if (col0 + d.N > d.out_ld) throw std::runtime_error("linear output columns exceed the out tensor");
+      d.out = (uint16_t*)(OT.ptr + (uint64_t)col0 * 2);
+      if (norm) {
+        int nw = ptr_tensor(*this, o, "norm");
+        d.norm = (const uint16_t*)tensors[nw].ptr;
+        d.eps = (float)o["eps"].f64(1e-6);
+        info.reads.push_back({nw, 0, d.K});
+      }
+      int res = ptr_tensor(*this, o, "residual", true);
+      if (res >= 0) {
+        d.flags |= OPF_RESIDUAL;
+        d.residual = (const uint16_t*)tensors[res].ptr;
+        d.res_ld = (int)tensors[res].dims[1];
+        info.reads.push_back({res, 0, d.N, 1});
+      }
+      if (amax) {
+        int to = ptr_tensor(*this, o, "tokens_out");
+        need_dtype(tensors[to], YR_DTYPE_I64, "argmax tokens_out");
+        d.tokens_out = (int64_t*)tensors[to].ptr;
+        d.vocab = (int)o["vocab"].i64(d.N);
+        info.writes.push_back({to, 0, 1});
+      }
+      int rpt = (int)o["rows_per_task"].i64(16);
+      if (rpt <= 0) throw std::runtime_error("rows_per_task must be > 0");
+      if (silu && group % rpt) throw std::runtime_error("silu op: rows_per_task must divide 'group'");
+      int ntasks = (d.N + rpt - 1) / rpt;
+      int ordinal = 0;
+      for (int r = 0; r < d.N; r += rpt) {
+        TaskDesc td;
+        memset(&td, 0, sizeof(td));
+        td.row0 = r;
+        td.rows = std::min(rpt, d.N - r);
+        if (silu) {
+          int64_t gi = r / group, j = r % group;
+          td.w0 = seg_rows(*this, segs, gi * 2 * group + j, td.rows, d.K);
+          td.w1 = seg_rows(*this, segs, gi * 2 * group + group + j, td.rows, d.K);
+        } else {
+          td.w0 = seg_rows(*this, segs, r, td.rows, d.K);
+        }
+        td.i0 = ordinal++;
+        td.i1 = ntasks;
+        add_task(td);
+      }
+      if (amax) {
+        d.ticket_base = ticket_next;
+        ticket_next += 1;
+        d.scratch_off = (int)scratch_next;
+        scratch_next += (int64_t)ntasks * cfg.max_tokens * 2;
+      }
+      info.reads.push_back({x, 0, d.K});
+      info.writes.push_back({out, col0, col0 + d.N, 1});
+    } else if (type == "attention") {
+      d.type = TASK_ATTENTION;
+      int qkv = ptr_tensor(*this, o, "qkv"), out = ptr_tensor(*this, o, "out");
+      int kc = ptr_tensor(*this, o, "k_cache"), vc = ptr_tensor(*this, o, "v_cache");
+      d.num_q_heads = (int)o["num_q_heads"].i64();
+      d.num_kv_heads = (int)o["num_kv_heads"].i64();
+      d.head_dim = (int)o["head_dim"].i64(128);
+      d.splits = (int)o["splits"].i64(1);
+      d.page_size = cfg.page_size;
+      if (d.head_dim != 128) throw std::runtime_error("attention: head_dim must be 128");
+      if (d.num_kv_heads <= 0 || d.num_q_heads % d.num_kv_heads) throw std::runtime_error("attention: bad heads");
+      int G = d.num_q_heads / d.num_kv_heads;
+      if (G > 16) throw std::runtime_error("attention: group size > 16");
+      if (d.splits <= 0 || d.splits > 256) throw std::runtime_error("attention: splits must be 1..256");
+      const Tensor& Q = tensors[qkv];
+      d.qkv_ld = (int)Q.dims[1];
+      if (d.qkv_ld != (d.num_q_heads + 2 * d.num_kv_heads) * d.head_dim)
+        throw std::runtime_error("attention: qkv width must be (Hq + 2 Hkv) * head_dim");
+      d.x = (const uint16_t*)Q.ptr;
+      d.out = (uint16_t*)tensors[out].ptr;
+      d.out_ld = (int)tensors[out].dims[1];
+      const Tensor& KC = tensors[kc];
+      if (KC.dims.size() != 4 || KC.dims[1] != cfg.page_size || KC.dims[2] != d.num_kv_heads || KC.dims[3] != d.head_dim)
+        throw std::runtime_error("attention: cache must be [pages, page_size, Hkv, head_dim]");
+      d.k_cache = (uint16_t*)KC.ptr;
+      d.v_cache = (uint16_t*)tensors[vc].ptr;
+      int ct = ptr_tensor(*this, o, "cos", true), st = ptr_tensor(*this, o, "sin", true);
+      d.cos_t = ct >= 0 ? (const uint16_t*)tensors[ct].ptr : nullptr;
+      d.sin_t = st >= 0 ? (const uint16_t*)tensors[st].ptr : nullptr;
+      d.max_tokens = cfg.max_tokens;
+      d.ticket_base = ticket_next;
+      ticket_next += cfg.max_requests * d.num_kv_heads;
+      d.scratch_off = (int)scratch_next;
+      scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * kAttnRecFloats;
+      for (int r = 0; r < cfg.max_requests; r++)
+        for (int h = 0; h < d.num_kv_heads; h++)
+          for (int s = 0; s < d.splits; s++) {
+            TaskDesc td;
+            memset(&td, 0, sizeof(td));
+            td.i0 = r;
+            td.i1 = h;
+            td.i2 = s;
+            td.row0 = h * (G + 2) * d.head_dim;
+            td.rows = (G + 2) * d.head_dim;
+            add_task(td);
+          }
+      info.reads.push_back({qkv, 0, d.qkv_ld, 2});
+      info.writes.push_back({out, 0, d.num_q_heads * d.head_dim, 2});
+      info.kv_group_width = (G + 2) * d.head_dim;
+      info.kv_groups = d.num_kv_heads;
+      info.group_reads_qkv = qkv;
+    } else if (type == "prepare_batch") {
+      d.type = TASK_PREPARE_BATCH;
+      TaskDesc td;
+      memset(&td, 0, sizeof(td));
+      add_task(td);
+      info.writes.push_back({-2, 0, 1});  // batch metadata
+    } else {
+      throw std::runtime_error("unknown op type '" + type + "'");
+    }
+    info.first_task = first_task;
+    info.num_tasks = (int)tasks.size() - first_task;
+    if (info.num_tasks == 0) throw std::runtime_error("op '" + type + "' produced no tasks");
+    ops.push_back(d);
+    op_info.push_back(info);
+  }
+  num_tickets = ticket_next;
+  scratch_floats = scratch_next;
+  if (num_tickets > 16384) throw std::runtime_error("too many arrival tickets");
+  // every op reads the batch metadata written by prepare_batch
+  for (auto& oi : op_info)
+    if (!(oi.writes.size() && oi.writes[0].tensor == -2)) oi.reads.push_back({-2, 0, 1});
+  make_events();
+  assign_workers();
+}
+
+void Graph::make_events() {
+  events.clear();
+  for (size_t i = 1; i < ops.size(); i++) {
+    OpInfo& prod = op_info[i - 1];
+    OpInfo& cons = op_info[i];
+    bool grouped = false;
+    if (ops[i].type == TASK_ATTENTION && prod.writes.size() && prod.writes[0].tensor == cons.group_reads_qkv) {
+      // producer tasks must each fall inside one kv group of the qkv tensor
+      grouped = true;
+      int W = cons.kv_group_width;
+      int col0 = prod.writes[0].c0;
+      for (int t = prod.first_task; t < prod.first_task + prod.num_tasks; t++) {
+        int a = col0 + tasks[t].row0, b = a + tasks[t].rows - 1;
+        if (a / W != b / W) { grouped = false; break; }
+      }
+    }
+    if (grouped) {
+      int W = cons.kv_group_width;
+      int col0 = prod.writes[0].c0;
+      int base = (int)events.size();
+      for (int g = 0; g < cons.kv_groups; g++) events.push_back(EventInfo{0, (int)i});
+      for (int t = prod.first_task; t < prod.first_task + prod.num_tasks; t++) {
+        int g = (col0 + tasks[t].row0) / W;
+        tasks[t].trigger_event = base + g;
+        events[base + g].num_triggers++;
+      }
+      for (int t = cons.first_task; t < cons.first_task + cons.num_tasks; t++) {
+        int g = tasks[t].i1;
+        if (events[base + g].num_triggers == 0) throw std::runtime_error("kv group without producer tasks");
+        tasks[t].wait_event = base + g;
+        tasks[t].wait_count = events[base + g].num_triggers;
+      }
+    } else {
+      int e = (int)events.size();
+      events.push_back(EventInfo{prod.num_tasks, (int)i});
+      for (int t = prod.first_task; t < prod.first_task + prod.num_tasks; t++) tasks[t].trigger_event = e;
+      for (int t = cons.first_task; t < cons.first_task + cons.num_tasks; t++) {
+        tasks[t].wait_event = e;
+        tasks[t].wait_count = prod.num_tasks;
+      }
+    }
+  }
+}
+
+void Graph::assign_workers() {
+  queues.assign(num_workers, {});
+  int start = 0;
+  for (auto& oi : op_info) {
+    for (int j = 0; j < oi.num_tasks; j++) queues[(start + j) % num_workers].push_back(oi.first_task + j);
+    start = (start + oi.num_tasks) % num_workers;
+  }
+}
+
+// ------------------------------------------------------------------ simulator
+std::string Graph::simulate(uint64_t seed, int epochs) const {
+  std::mt19937_64 rng(seed);
+  std::vector<int64_t> counters(events.size(), 0);
+  std::vector<int> executed(tasks.size(), 0);
+  for (int ep = 1; ep <= epochs; ep++) {
+    std::vector<size_t> pos(num_workers, 0);
+    size_t remaining = tasks.size();
+    std::vector<int> ready;
+    while (remaining) {
+      ready.clear();
+      for (int w = 0; w < num_workers; w++) {
+        if (pos[w] >= queues[w].size()) continue;
+        const TaskDesc& t = tasks[queues[w][pos[w]]];
+        if (t.wait_event < 0 || counters[t.wait_event] >= (int64_t)t.wait_count * ep) ready.push_back(w);
+      }
+      if (ready.empty()) {
+        std::ostringstream os;
+        os << "deadlock in epoch " << ep << " with " << remaining << " tasks left";
+        for (int w = 0; w < num_workers; w++)
+          if (pos[w] < queues[w].size()) {
+            const TaskDesc& t = tasks[queues[w][pos[w]]];
+            os << "; worker " << w << " blocked on task " << queues[w][pos[w]] << " (event " << t.wait_event
+               << ": " << counters[t.wait_event] << "/" << (int64_t)t.wait_count * ep << ")";
+            break;
+          }
+        return os.str();
+      }
+      int w = ready[rng() % ready.size()];
+      int tid = queues[w][pos[w]++];
+      executed[tid]++;
+      if (tasks[tid].trigger_event >= 0) {
+        counters[tasks[tid].trigger_event]++;
+        if (counters[tasks[tid].trigger_event] > (int64_t)events[tasks[tid].trigger_event].num_triggers * ep)
+          return "event over-triggered: " + std::to_string(tasks[tid].trigger_event);
+      }
+      remaining--;
+    }
+    for (size_t e = 0; e < events.size(); e++)
+      if (counters[e] != (int64_t)events[e].num_triggers * ep)
+        return "event " + std::to_string(e) + " did not reach its trigger count";
+  }
+  for (size_t t = 0; t < tasks.size(); t++)
+    if (executed[t] != epochs) return "task " + std::to_string(t) + " executed " + std::to_string(executed[t]) + " times";
+  return "";
+}
+
+// ------------------------------------------------------------------ races
+// For every pair of ops (a, b), a < b, whose tasks touch overlapping columns
+// of one tensor with at least one write, every conflicting task pair must be
+// ordered: b's task transitively waits for a's task through the events, or
+// both run on the same worker with a first.  Reachability is propagated as
+// per-task bitsets over the tasks of op a, within a window of ops.
+std::string Graph::check_races(int window) const {
+  auto overlap = [](const Access& x, const Access& y) {
+    return x.tensor == y.tensor && x.c0 < y.c1 && y.c0 < x.c1;
+  };
+  // per-task access ranges (attention tasks touch one kv group; linear tasks
+  // their own output columns)
+  auto task_access = [&](int op, int t, std::vector<Access>& rd, std::vector<Access>& wr) {
+    const OpInfo& oi = op_info[op];
+    const TaskDesc& td = tasks[t];
+    const OpDesc& od = ops[op];
+    int G = od.type == TASK_ATTENTION ? od.num_q_heads / od.num_kv_heads : 0;
+    auto fix = [&](std::vector<Access>& v, bool is_write) {
+      for (auto& a : v) {
+        if (a.scope == 1) {          // own output columns (base + row0 .. + rows)
+          int base = a.c0;
+          a.c0 = base + td.row0;
+          a.c1 = a.c0 + td.rows;
+        } else if (a.scope == 2) {   // kv-head group
+          if (is_write) {
+            a.c0 = td.i1 * G * od.head_dim;
+            a.c1 = a.c0 + G * od.head_dim;
+          } else {
+            a.c0 = td.row0;
+            a.c1 = td.row0 + td.rows;
+          }
+        }
+      }
+    };
+    rd = oi.reads;
+    wr = oi.writes;
+    fix(rd, false);
+    fix(wr, true);
+  };
+  // worker position of every task
+  std::vector<int> worker(tasks.size()), qpos(tasks.size());
+  for (int w = 0; w < num_workers; w++)
+    for (size_t i = 0; i < queues[w].size(); i++) {
+      worker[queues[w][i]] = w;
+      qpos[queues[w][i]] = (int)i;
+    }
+  // producers of each event
+  std::vector<std::vector<int>> producers(events.size());
+  for (size_t t = 0; t < tasks.size(); t++)
+    if (tasks[t].trigger_event >= 0) producers[tasks[t].trigger_event].push_back((int)t);
+
+  int nops = (int)ops.size();
+  int64_t checked = 0;
+  for (int a = 0; a < nops; a++) {
+    const OpInfo& A = op_info[a];
+    // reach[t] (t in ops a+1 .. a+window): bitset over A's tasks already done
+    int last = std::min(nops - 1, a + window);
+    int na = A.num_tasks;
+    int words = (na + 63) / 64;
+    std::vector<std::vector<uint64_t>> reach(tasks.size());
+    auto get = [&](int t) -> std::vector<uint64_t>& {
+      if (reach[t].empty()) reach[t].assign(words, 0);
+      return reach[t];
+    };
+    for (int b = a + 1; b <= last; b++) {
+      const OpInfo& B = op_info[b];
+      for (int t = B.first_task; t < B.first_task + B.num_tasks; t++) {
+        std::vector<uint64_t>& r = get(t);
+        if (qpos[t] > 0) {  // the worker's previous task finished first
+          int p = queues[worker[t]][qpos[t] - 1];
+          if (p >= A.first_task && p < A.first_task + na) {
+            int k = p - A.first_task;
+            r[k / 64] |= 1ull << (k % 64);
+          } else if (!reach[p].empty()) {
+            for (int i = 0; i < words; i++) r[i] |= reach[p][i];
+          }
+        }
+        int e = tasks[t].wait_event;
+        if (e >= 0)
+          for (int p : producers[e]) {
+            if (p >= A.first_task && p < A.first_task + na) {
+              int k = p - A.first_task;
+              r[k / 64] |= 1ull << (k % 64);
+            } else if (!reach[p].empty()) {
+              for (int i = 0; i < words; i++) r[i] |= reach[p][i];
+            }
+          }
+      }
+      // conflicts between op a and op b
+      std::vector<Access> ra, wa, rb, wb;
+      for (int tb = B.first_task; tb < B.first_task + B.num_tasks; tb++) {
+        task_access(b, tb, rb, wb);
+        for (int ta = A.first_task; ta < A.first_task + na; ta++) {
+          task_access(a, ta, ra, wa);
+          bool conflict = false;
+          for (auto& x : wa) {
+            for (auto& y : rb) conflict |= overlap(x, y);
+            for (auto& y : wb) conflict |= overlap(x, y);
+          }
+          for (auto& x : ra)
+            for (auto& y : wb) conflict |= overlap(x, y);
+          if (!conflict) continue;
+          checked++;
+          int k = ta - A.first_task;
+          bool ordered = (reach[tb][k / 64] >> (k % 64)) & 1;
+          ordered |= worker[ta] == worker[tb] && qpos[ta] < qpos[tb];
+          if (!ordered) {
+            std::ostringstream os;
+            os << "race: task " << ta << " (op " << a << " " << A.name << ") and task " << tb << " (op " << b << " "
+               << B.name << ") conflict but are not ordered";
+            return os.str();
+          }
+        }
+      }
+    }
+  }
+  (void)checked;
+  return "";
+}
+
+// ------------------------------------------------------------------ export
+// Task graph in the reference's JSON vocabulary (runtime.cc:847-1318):
+// all_tasks / all_events / first_tasks.
+std::string Graph::export_json() const {
+  static const char* names[] = {"nop", "embedding", "linear", "rmsnorm_linear", "rmsnorm_linear_silu_mul",
+                                "paged_attention", "rmsnorm_linear_argmax", "prepare_next_batch"};
+  std::ostringstream os;
+  os << "{\"all_tasks\":[";
+  for (size_t i = 0; i < tasks.size(); i++) {
+    const TaskDesc& t = tasks[i];
+    if (i) os << ",";
+    os << "{\"task_type\":\"" << names[ops[t.op].type] << "\",\"op\":" << t.op << ",\"trigger_event\":"
+       << t.trigger_event << ",\"dependent_event\":" << t.wait_event << ",\"row0\":" << t.row0 << ",\"rows\":" << t.rows
+       << ",\"request_id\":" << (ops[t.op].type == TASK_ATTENTION ? t.i0 : -1) << "}";
+  }
+  os << "],\"all_events\":[";
+  for (size_t e = 0; e < events.size(); e++) {
+    if (e) os << ",";
+    int first = -1, last = -1;
+    for (int t = op_info[events[e].consumer_op].first_task;
+         t < op_info[events[e].consumer_op].first_task + op_info[events[e].consumer_op].num_tasks; t++)
+      if (tasks[t].wait_event == (int)e) {
+        if (first < 0) first = t;
+        last = t;
+      }
+    os << "{\"event_type\":\"EVENT_LAUNCH_TASKS\",\"num_triggers\":" << events[e].num_triggers
+       << ",\"first_task_id\":" << first << ",\"last_task_id\":" << last + 1 << "}";
+  }
+  os << "],\"first_tasks\":[";
+  bool firstw = true;
+  for (int t = 0; t < op_info[0].num_tasks; t++) {
+    os << (firstw ? "" : ",") << t;
+    firstw = false;
+  }
+  os << "],\"num_workers\":" << num_workers << "}";
+  return os.str();
+}
+
+}  // namespace pk
+}  // namespace yr
+
+// ------------------------------------------------------------------ C ABI
+using yr::pk::Graph;
+
+extern "C" {
+
+int yr_pk_graph_build(const char* json_text, yr_pk_graph** out) {
+  if (!json_text || !out) return yr::fail(YR_E_INVALID, "yr_pk_graph_build: null argument");
+  *out = nullptr;
+  Graph* g = new Graph();
+  try {
+    g->build(json_text);
+  } catch (std::exception& e) {
+    delete g;
+    return yr::fail(YR_E_GRAPH, "task graph: %s", e.what());
+  }
+  *out = reinterpret_cast<yr_pk_graph*>(g);
+  return YR_OK;
+}
+
+void yr_pk_graph_free(yr_pk_graph* g) { delete reinterpret_cast<Graph*>(g); }
+
+int yr_pk_graph_info(const yr_pk_graph* gp, int64_t* info, int n) {
+  const Graph* g = reinterpret_cast<const Graph*>(gp);
+  if (!g || !info || n < 8) return yr::fail(YR_E_INVALID, "yr_pk_graph_info: bad arguments");
+  size_t maxq = 0;
+  for (auto& q : g->queues) maxq = std::max(maxq, q.size());
+  info[0] = (int64_t)g->ops.size();
+  info[1] = (int64_t)g->tasks.size();
+  info[2] = (int64_t)g->events.size();
+  info[3] = g->num_workers;
+  info[4] = g->num_tickets;
+  info[5] = g->scratch_floats;
+  info[6] = (int64_t)maxq;
+  info[7] = 0;
+  return YR_OK;
+}
+
+int yr_pk_graph_task(const yr_pk_graph* gp, int task, int64_t* rec, int n) {
+  const Graph* g = reinterpret_cast<const Graph*>(gp);
+  if (!g || !rec || n < 10 || task < 0 || task >= (int)g->tasks.size())
+    return yr::fail(YR_E_INVALID, "yr_pk_graph_task: bad arguments");
+  const yr::pk::TaskDesc& t = g->tasks[task];
+  rec[0] = t.op;
+  rec[1] = g->ops[t.op].type;
+  rec[2] = t.wait_event;
+  rec[3] = t.wait_count;
+  rec[4] = t.trigger_event;
+  rec[5] = t.row0;
+  rec[6] = t.rows;
+  rec[7] = t.i0;
+  rec[8] = t.i1;
+  rec[9] = t.i2;
+  return YR_OK;
+}
+
+int yr_pk_graph_simulate(const yr_pk_graph* gp, uint64_t seed, int epochs, int race_window, char* report,
+                         size_t report_len) {
+  const Graph* g = reinterpret_cast<const Graph*>(gp);
+  if (!g) return yr::fail(YR_E_INVALID, "yr_pk_graph_simulate: null graph");
+  std::string r = g->simulate(seed, epochs > 0 ? epochs : 1);
+  if (r.empty() && race_window > 0) r = g->check_races(race_window);
+  if (report && report_len) {
+    size_t k = std::min(report_len - 1, r.size());
+    memcpy(report, r.data(), k);
+    report[k] = 0;
+  }
+  return r.empty() ? YR_OK : yr::fail(YR_E_GRAPH, "%s", r.c_str());
+}
+
+int yr_pk_graph_export_json(const yr_pk_graph* gp, char* buf, size_t buf_len, size_t* needed) {
+  const Graph* g = reinterpret_cast<const Graph*>(gp);
+  if (!g) return yr::fail(YR_E_INVALID, "yr_pk_graph_export_json: null graph");
+  std::string s = g->export_json();
+  if (needed) *needed = s.size() + 1;
+  if (buf && buf_len) {
+    size_t k = std::min(buf_len - 1, s.size());
+    memcpy(buf, s.data(), k);
+    buf[k] = 0;
+    if (buf_len < s.size() + 1) return yr::fail(YR_E_INVALID, "buffer too small");
+  }
+  return YR_OK;
+}
+
+}  // extern "C"

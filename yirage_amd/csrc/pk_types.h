@@ -1,0 +1,111 @@
+// Task-graph records shared by the host builder (pk_builder.cc) and the
+// persistent megakernel (pk_kernel.hip).  Plain PODs, identical layout on
+// host and device.
+//
+// Restates the runtime ABI of include/yirage/persistent_kernel/
+// runtime_header.h:47-269 (TaskDesc / EventDesc / RuntimeConfig) for this
+// backend: a task carries one wait event and one trigger event; event
+// counters are monotonic across launches (a wait is satisfied when the
+// counter reaches num_triggers * epoch, as in the reference's
+// num_triggers * iteration rule, persistent_kernel.cuh:582-604).
+#pragma once
+#include <stdint.h>
+
+namespace yr {
+namespace pk {
+
+enum TaskType : int {
+  TASK_NOP = 0,
+  TASK_EMBED = 1,            // tasks/ampere/embedding.cuh:42-72
+  TASK_LINEAR = 2,           // linear / linear_with_residual (linear_cutlass.cuh)
+  TASK_RMSNORM_LINEAR = 3,   // rmsnorm (rmsnorm.cuh:76-128) fused into linear
+  TASK_RMSNORM_LINEAR_SILU = 4,  // + silu_mul (silu_mul.cuh:31-40) on [gate | up] rows
+  TASK_ATTENTION = 5,        // multitoken_paged_attention_4_16.cuh:40-656 (decode / short extend)
+  TASK_RMSNORM_LINEAR_ARGMAX = 6,  // LM head + argmax_partial/reduce (argmax.cuh:71-155)
+  TASK_PREPARE_BATCH = 7,    // prepare_next_batch (persistent_kernel.cuh:169-322)
+};
+
+enum OpFlags : int {
+  OPF_RESIDUAL = 1,          // out = residual + x W^T
+};
+
+// One per op (layer call).  Pointers are device addresses.
+struct OpDesc {
+  int type;
+  int flags;
+  int K;              // reduction dim (hidden / intermediate)
+  int N;              // output columns of the whole op
+  int x_ld, out_ld, res_ld;
+  int max_tokens;     // rows of the activation buffers
+  float eps;
+  // attention
+  int num_q_heads, num_kv_heads, head_dim, page_size, splits, qkv_ld;
+  int ticket_base;    // first arrival ticket used by this op
+  int vocab;          // argmax: valid columns (<= N)
+  int scratch_off;    // float offset of this op's scratch records
+  int pad0;
+  const uint16_t* x;        // activations in
+  const uint16_t* norm;     // RMSNorm weight
+  uint16_t* out;            // activations out (column 0 of the op)
+  const uint16_t* residual;
+  uint16_t* k_cache;        // [pages][page][Hkv][D]
+  uint16_t* v_cache;
+  const uint16_t* cos_t;    // [pos][D]
+  const uint16_t* sin_t;
+  const int64_t* tokens_in; // embed: token ids [max_tokens]
+  const uint16_t* table;    // embed: [vocab][hidden]
+  int64_t* tokens_out;      // argmax: output token ids [max_tokens]
+};
+
+// One per task (workgroup-sized unit of work).
+struct TaskDesc {
+  int op;             // index into OpDesc[]
+  int wait_event;     // -1: none
+  int wait_count;     // num_triggers of wait_event (per epoch)
+  int trigger_event;  // -1: none
+  int row0, rows;     // output rows / columns covered [row0, row0 + rows)
+  int i0, i1;         // attention: request, kv head; argmax: task ordinal
+  int i2, i3;         // attention: split index; argmax: number of tasks
+  int pad0, pad1;
+  const uint16_t* w0; // weight rows of this task (gate rows for the SiLU op)
+  const uint16_t* w1; // up rows for the SiLU op
+};
+
+// Batch / page manager state (persistent_kernel.cuh:107-132,169-322).
+struct BatchMeta {
+  int* step;              // [total_requests]
+  int64_t* tokens;        // [total_requests][max_seq_len]
+  int64_t* input_tokens;  // [max_tokens]
+  int64_t* output_tokens; // [max_tokens]
+  int* num_new_tokens;    // [total_requests] (unused by offline mode)
+  int* prompt_lengths;    // [total_requests]
+  int* qo_indptr;         // [max_requests + 1]
+  int* kv_indptr;         // [max_requests + 1]
+  int* kv_indices;        // [max_pages]
+  int* last_page_len;     // [max_requests]
+  int* request_ids;       // [max_requests]
+  int* next_request_id;   // [1]
+  int* page_queue;        // [max_pages]
+  int* page_queue_head;   // [1]
+  int* page_queue_tail;   // [1]
+  int* status;            // [4]: [0] watchdog flag, [1] batch non-empty, [2] failing task, [3] spare
+  int max_requests, max_tokens, max_pages, page_size, max_seq_len, total_requests;
+  int64_t eos_token_id;
+};
+
+struct KernelArgs {
+  const OpDesc* ops;
+  const TaskDesc* tasks;
+  const int* queue_offsets;  // [num_workers + 1]
+  const int* queue;          // task ids, worker-major
+  uint32_t* events;          // monotonic counters
+  uint32_t* tickets;         // arrival tickets (zero at rest)
+  float* scratch;            // split records
+  BatchMeta meta;
+  uint32_t epoch;            // 1, 2, 3, ... per launch
+  int num_workers;
+  long long spin_limit;      // watchdog: polls before a wait gives up
+};
+
+}  // namespace pk
+}  // namespace yr

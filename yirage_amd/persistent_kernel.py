@@ -1,0 +1,405 @@
+"""PersistentKernel for the `hip` backend.
+
+Mirrors python/yirage/persistent_kernel.py:217-1347 of the reference: the
+same constructor arguments and meta tensors, attach_input / new_tensor /
+fuse_tensors / shuffle_tensors, the *_layer builders, compile() and
+__call__().  compile() runs a fusion pass over the recorded layers
+(rmsnorm -> linear becomes one rmsnorm_linear task; a [gate | up] linear
+followed by silu_mul becomes one task with a SiLU-mul epilogue; the LM-head
+linear followed by argmax_partial / argmax_reduce becomes one task with an
+argmax epilogue), serialises the op list to JSON and hands it to the C++
+task-graph builder in libyirage_hip.so, which emits per-worker queues and
+events for the gfx950 megakernel.  No code is generated or compiled at run
+time.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from ._lib import YirageHipError, check, lib
+
+valid_persistent_kernel_modes = {"offline", "online", "onepass"}
+
+# dtype tags (include/yirage/type.h:84-120 values)
+float16, bfloat16, float32, int32, int64 = (_lib.DTYPE_F16, _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_I32,
+                                            _lib.DTYPE_I64)
+_TORCH2DT = {torch.float16: float16, torch.bfloat16: bfloat16, torch.float32: float32, torch.int32: int32,
+             torch.int64: int64}
+_DT2TORCH = {v: k for k, v in _TORCH2DT.items()}
+
+
+@dataclass(eq=False)
+class DTensor:
+    """A kernel-graph tensor: a name, a shape and (once bound) device memory.
+    Shuffled / fused tensors are views over row segments of their sources."""
+    name: str
+    dims: tuple
+    dtype: int
+    tensor: torch.Tensor | None = None
+    segments: list = field(default_factory=list)   # [(DTensor, row0, rows)] for views
+    group: int = 0                                  # rows per source chunk of a shuffle
+
+    @property
+    def num_dims(self) -> int:
+        return len(self.dims)
+
+    def dim(self, i: int) -> int:
+        return self.dims[i]
+
+
+def get_configurations_from_gpu(rank: int = 0):
+    """(num_workers, num_schedulers).  One worker per CU; the hip backend has
+    no scheduler workgroups (python/yirage/utils.py:31-57 sizes both for
+    NVIDIA parts)."""
+    props = torch.cuda.get_device_properties(rank)
+    return props.multi_processor_count, 0
+
+
+class PersistentKernel:
+    def __init__(self, mode: str, world_size: int, mpi_rank: int, num_workers: int, num_local_schedulers: int,
+                 num_remote_schedulers: int, max_seq_length: int, max_num_batched_requests: int,
+                 max_num_batched_tokens: int, max_num_pages: int, page_size: int, eos_token_id: int,
+                 meta_tensors: dict, profiler_tensor: torch.Tensor | None = None, trace_name: str = "",
+                 spec_decode_config=None, use_cutlass_kernel: bool = False):
+        if mode not in valid_persistent_kernel_modes:
+            raise ValueError(f"Invalid persistent kernel mode: {mode}")
+        if world_size != 1:
+            raise YirageHipError("hip backend: the persistent kernel runs on one GPU (world_size must be 1)")
+        if spec_decode_config is not None:
+            raise YirageHipError("hip backend: speculative decoding is not supported")
+        if max_num_batched_tokens > 8:
+            raise YirageHipError("hip backend: max_num_batched_tokens must be <= 8")
+        self.mode = mode
+        self.world_size = world_size
+        self.mpi_rank = mpi_rank
+        self.num_workers = num_workers
+        self.num_local_schedulers = num_local_schedulers
+        self.num_remote_schedulers = num_remote_schedulers
+        self.max_seq_length = max_seq_length
+        self.max_num_batched_requests = max_num_batched_requests
+        self.max_num_batched_tokens = max_num_batched_tokens
+        self.max_num_pages = max_num_pages
+        self.page_size = page_size
+        self.eos_token_id = eos_token_id
+        self.meta_tensors = meta_tensors
+        self.profiler_tensor = profiler_tensor
+        self.trace_name = trace_name
+        self.total_num_requests = meta_tensors["tokens"].shape[0]
+        assert self.max_seq_length == meta_tensors["tokens"].shape[1]
+        assert meta_tensors["qo_indptr_buffer"].shape == (max_num_batched_requests + 1,)
+        assert meta_tensors["paged_kv_indptr_buffer"].shape == (max_num_batched_requests + 1,)
+        assert meta_tensors["paged_kv_indices_buffer"].shape == (max_num_pages,)
+        assert meta_tensors["paged_kv_last_page_len_buffer"].shape == (max_num_batched_requests,)
+        self._tensors: dict[str, DTensor] = {}
+        self._layers: list[dict] = []
+        self._owned: list[torch.Tensor] = []
+        self._graph = None
+        self._handle = None
+        self._is_compiled = False
+        self.__finalized__ = False
+        self.ops: list[dict] = []
+
+    # ------------------------------------------------------------ tensors
+    def _register(self, t: DTensor) -> DTensor:
+        if t.name in self._tensors:
+            raise YirageHipError(f"duplicate tensor name {t.name}")
+        self._tensors[t.name] = t
+        return t
+
+    def attach_input(self, torch_tensor: torch.Tensor, name: str = None) -> DTensor:
+        assert name is not None
+        dims = tuple(torch_tensor.shape)
+        strides = torch_tensor.stride()
+        for d in range(len(dims) - 1):
+            assert strides[d] == strides[d + 1] * dims[d + 1], "row-major tensors only"
+        if torch_tensor.dtype not in _TORCH2DT:
+            raise YirageHipError(f"unsupported dtype {torch_tensor.dtype}")
+        return self._register(DTensor(name, dims, _TORCH2DT[torch_tensor.dtype], torch_tensor))
+
+    def new_tensor(self, dims: tuple, strides: tuple = None, dtype: int = bfloat16, name: str = None,
+                   io_category: str = "cuda_tensor") -> DTensor:
+        assert name is not None
+        if io_category not in ("cuda_tensor", "nvshmem_tensor"):
+            raise RuntimeError(f"Invalid io_category: {io_category}")
+        t = torch.zeros(dims, dtype=_DT2TORCH[dtype], device=self.meta_tensors["qo_indptr_buffer"].device)
+        self._owned.append(t)
+        return self._register(DTensor(name, tuple(dims), dtype, t))
+
+    def _view(self, inputs, num_groups: int, name: str, shuffled: bool) -> DTensor:
+        rows = [t.dim(0) for t in inputs]
+        for t in inputs:
+            assert t.num_dims == 2 and t.dim(1) == inputs[0].dim(1)
+            assert t.dim(0) % num_groups == 0
+        segs = []
+        if shuffled:
+            # group g: rows g*r_i/num_groups .. of every input in turn (runtime.cc:804-842)
+            for g in range(num_groups):
+                for t, r in zip(inputs, rows):
+                    c = r // num_groups
+                    segs.append((t, g * c, c))
+        else:
+            for t, r in zip(inputs, rows):
+                segs.append((t, 0, r))
+        v = DTensor(name, (sum(rows), inputs[0].dim(1)), inputs[0].dtype, None, segs, rows[0] // num_groups)
+        return self._register(v)
+
+    def fuse_tensors(self, inputs: list, fused_dim: int, num_groups: int, name: str = None) -> DTensor:
+        assert fused_dim == 0
+        return self._view(inputs, num_groups, name, shuffled=False)
+
+    def shuffle_tensors(self, inputs: list, shuffled_dim: int, num_groups: int, name: str = None) -> DTensor:
+        assert shuffled_dim == 0
+        return self._view(inputs, num_groups, name, shuffled=True)
+
+    # ------------------------------------------------------------ layers
+    def _add(self, kind, **kw):
+        self._layers.append(dict(kind=kind, **kw))
+
+    def embed_layer(self, input: DTensor, weight: DTensor, output: DTensor, grid_dim: tuple, block_dim: tuple,
+                    input_source: int = 0):
+        self._add("embed", input=input, weight=weight, output=output)
+
+    def rmsnorm_layer(self, input: DTensor, weight: DTensor, output: DTensor, grid_dim: tuple, block_dim: tuple):
+        assert input.num_dims == 2 and output.num_dims == 2
+        self._add("rmsnorm", input=input, weight=weight, output=output)
+
+    def rmsnorm_linear_layer(self, input: DTensor, weight_norm: DTensor, weight_linear: DTensor, output: DTensor,
+                             grid_dim: tuple, block_dim: tuple):
+        self._add("rmsnorm_linear", input=input, norm=weight_norm, weight=weight_linear, output=output)
+
+    def linear_layer(self, input: DTensor, weight: DTensor, output: DTensor, grid_dim: tuple, block_dim: tuple):
+        self._add("linear", input=input, weight=weight, output=output, residual=None)
+
+    def linear_with_residual_layer(self, input: DTensor, weight: DTensor, residual: DTensor, output: DTensor,
+                                   grid_dim: tuple, block_dim: tuple):
+        self._add("linear", input=input, weight=weight, output=output, residual=residual)
+
+    def silu_mul_layer(self, input: DTensor, output: DTensor, grid_dim: tuple, block_dim: tuple):
+        self._add("silu_mul", input=input, output=output)
+
+    def paged_attention_layer(self, input: DTensor, k_cache: DTensor, v_cache: DTensor, q_norm: DTensor,
+                              k_norm: DTensor, cos_pos_embed: DTensor, sin_pos_embed: DTensor, output: DTensor,
+                              grid_dim: tuple, block_dim: tuple):
+        if q_norm is not None or k_norm is not None:
+            raise YirageHipError("hip backend: qk-norm in paged attention is not supported")
+        assert k_cache.dim(0) == self.max_num_pages and k_cache.dim(1) == self.page_size
+        self._add("attention", input=input, k_cache=k_cache, v_cache=v_cache, cos=cos_pos_embed,
+                  sin=sin_pos_embed, output=output, num_q_heads=output.dim(1) // k_cache.dim(3),
+                  num_kv_heads=k_cache.dim(2), head_dim=k_cache.dim(3))
+
+    def argmax_partial_layer(self, input: DTensor, output: tuple, grid_dim: tuple, block_dim: tuple):
+        self._add("argmax_partial", input=input, output=output)
+
+    def argmax_reduce_layer(self, input: tuple, output: DTensor, grid_dim: tuple, block_dim: tuple):
+        self._add("argmax_reduce", input=input, output=output)
+
+    def argmax_layer(self, input: DTensor, output: DTensor, grid_dim: tuple, block_dim: tuple):
+        self._add("argmax_partial", input=input, output=None)
+        self._add("argmax_reduce", input=None, output=output)
+
+    def prepare_batch_layer(self):
+        """Append the on-device batch/page manager (prepare_next_batch of
+        persistent_kernel.cuh:169-322) as the last task of the graph."""
+        self._add("prepare_batch")
+
+    # ------------------------------------------------------------ fusion + JSON
+    def _segments(self, w: DTensor):
+        return [(s.name, r0, n) for (s, r0, n) in w.segments] if w.segments else [(w.name, 0, w.dim(0))]
+
+    @staticmethod
+    def _rows_per_task(n_rows: int, num_workers: int, gran: int, max_rows: int | None = None) -> int:
+        """Even rows per task dividing `gran`, minimising the per-worker
+        makespan ceil(tasks / workers) * rows (ties -> fewer tasks)."""
+        best = None
+        cands = [r for r in range(2, gran + 1, 2) if gran % r == 0] if gran else \
+            list(range(2, n_rows + 2, 2))
+        for r in cands:
+            if max_rows and r > max_rows:
+                continue
+            tasks = -(-n_rows // r)
+            span = -(-tasks // num_workers) * r
+            key = (span, tasks)
+            if best is None or key < best[0]:
+                best = (key, r)
+        if best is None:
+            raise YirageHipError(f"no valid rows-per-task for {n_rows} rows (granularity {gran})")
+        return best[1]
+
+    def _fuse(self):
+        L = self._layers
+        consumers = {}
+        for i, l in enumerate(L):
+            for k in ("input", "norm", "residual"):
+                v = l.get(k)
+                if isinstance(v, DTensor):
+                    consumers.setdefault(v.name, []).append(i)
+        ops = []
+        i = 0
+        W = self.num_workers
+        while i < len(L):
+            l = L[i]
+            k = l["kind"]
+            nxt = L[i + 1] if i + 1 < len(L) else None
+            if k == "embed":
+                ops.append(dict(type="embed", tokens=l["input"].name, table=l["weight"].name,
+                                out=l["output"].name, tasks=max(1, l["weight"].dim(1) // 512)))
+                i += 1
+                continue
+            if k == "rmsnorm":
+                if not (nxt and nxt["kind"] == "linear" and nxt["input"] is l["output"] and nxt["residual"] is None):
+                    raise YirageHipError("hip backend: rmsnorm_layer must feed a linear_layer (fused into one task)")
+                l = dict(kind="rmsnorm_linear", input=l["input"], norm=l["weight"], weight=nxt["weight"],
+                         output=nxt["output"])
+                i += 1
+                nxt = L[i + 1] if i + 1 < len(L) else None
+                k = "rmsnorm_linear"
+            if k in ("rmsnorm_linear", "linear"):
+                w = l["weight"]
+                K = w.dim(1)
+                op = dict(x=l["input"].name, weight=self._segments(w), out=l["output"].name)
+                if k == "rmsnorm_linear":
+                    op.update(type="rmsnorm_linear", norm=l["norm"].name, eps=1e-6)
+                else:
+                    op.update(type="linear")
+                    if l.get("residual") is not None:
+                        op["residual"] = l["residual"].name
+                seg_rows = [n for (_, _, n) in op["weight"]]
+                gran = math.gcd(*seg_rows)
+                tm8 = self.max_num_batched_tokens > 1
+                max_rows = 16 if (tm8 and K > 4096) else None
+                if nxt and nxt["kind"] == "silu_mul" and nxt["input"] is l["output"]:
+                    if k != "rmsnorm_linear" or not w.segments or len(set(s.name for s, _, _ in w.segments)) != 2:
+                        raise YirageHipError("hip backend: silu_mul must follow an rmsnorm+linear over shuffled "
+                                             "[gate, up] weights")
+                    op["type"] = "rmsnorm_linear_silu"
+                    op["group"] = w.group
+                    op["out"] = nxt["output"].name
+                    op["rows_per_task"] = self._rows_per_task(w.dim(0) // 2, W, w.group, max_rows)
+                    i += 2
+                elif nxt and nxt["kind"] == "argmax_partial" and nxt["input"] is l["output"]:
+                    red = L[i + 2] if i + 2 < len(L) else None
+                    if not red or red["kind"] != "argmax_reduce":
+                        raise YirageHipError("argmax_partial_layer must be followed by argmax_reduce_layer")
+                    if k != "rmsnorm_linear":
+                        raise YirageHipError("hip backend: argmax must follow the final rmsnorm+linear")
+                    op["type"] = "rmsnorm_linear_argmax"
+                    op["tokens_out"] = red["output"].name
+                    op["vocab"] = int(getattr(self, "vocab_size", None) or w.dim(0))
+                    op["rows_per_task"] = self._rows_per_task(w.dim(0), W, 0, max_rows)
+                    i += 3
+                else:
+                    op["rows_per_task"] = self._rows_per_task(w.dim(0), W, gran, max_rows)
+                    i += 1
+                ops.append(op)
+                continue
+            if k == "attention":
+                per = self.max_num_batched_requests * l["num_kv_heads"]
+                splits = max(1, min(256, W // per))
+                ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
+                                v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
+                                sin=l["sin"].name if l["sin"] is not None else None, out=l["output"].name,
+                                num_q_heads=l["num_q_heads"], num_kv_heads=l["num_kv_heads"],
+                                head_dim=l["head_dim"], splits=splits))
+                i += 1
+                continue
+            if k == "prepare_batch":
+                ops.append(dict(type="prepare_batch"))
+                i += 1
+                continue
+            raise YirageHipError(f"hip backend: layer '{k}' cannot be scheduled here (no fusion partner)")
+        return ops
+
+    def _graph_json(self) -> str:
+        tensors = {}
+        for t in self._tensors.values():
+            if t.tensor is not None:
+                ptr = 0 if t.tensor.device.type == "meta" else t.tensor.data_ptr()
+                tensors[t.name] = dict(ptr=ptr, dims=list(t.dims), dtype=t.dtype)
+        return json.dumps(dict(
+            num_workers=self.num_workers, max_tokens=self.max_num_batched_tokens,
+            max_requests=self.max_num_batched_requests, page_size=self.page_size, max_pages=self.max_num_pages,
+            max_seq_len=self.max_seq_length, total_requests=self.total_num_requests,
+            eos_token_id=int(self.eos_token_id), tensors=tensors, ops=self.ops))
+
+    # ------------------------------------------------------------ compile / run
+    def compile(self, **kwargs):
+        assert not self._is_compiled
+        self.ops = self._fuse()
+        g = ctypes.c_void_p()
+        check(lib().yr_pk_graph_build(self._graph_json().encode(), ctypes.byref(g)), "task graph build")
+        self._graph = g
+        if kwargs.get("verify", True):
+            rep = ctypes.create_string_buffer(1024)
+            check(lib().yr_pk_graph_simulate(g, 1234, 2, kwargs.get("race_window", 8), rep, 1024),
+                  "task graph simulation")
+        if kwargs.get("build_only", False):
+            # graph construction and verification only (no device resources)
+            self._is_compiled = False
+            return
+        mt = self.meta_tensors
+        m = _lib.PKMeta()
+        for field_name, key in (("step", "step"), ("tokens", "tokens"), ("input_tokens", "input_tokens"),
+                                ("output_tokens", "output_tokens"), ("num_new_tokens", "num_new_tokens"),
+                                ("prompt_lengths", "prompt_lengths"), ("qo_indptr", "qo_indptr_buffer"),
+                                ("paged_kv_indptr", "paged_kv_indptr_buffer"),
+                                ("paged_kv_indices", "paged_kv_indices_buffer"),
+                                ("paged_kv_last_page_len", "paged_kv_last_page_len_buffer")):
+            t = mt.get(key)
+            setattr(m, field_name, t.data_ptr() if t is not None else None)
+        self._meta = m
+        h = ctypes.c_void_p()
+        check(lib().yr_pk_create(g, ctypes.byref(m), ctypes.byref(h)), "persistent kernel create")
+        self._handle = h
+        if any(o["type"] == "prepare_batch" for o in self.ops):
+            check(lib().yr_pk_init_batch(h, self._stream()), "init batch")
+        self._is_compiled = True
+
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def __call__(self, **kwargs):
+        if not self._is_compiled:
+            raise YirageHipError("PersistentKernel: call compile() first")
+        check(lib().yr_pk_launch(self._handle, self._stream()), "persistent kernel launch")
+
+    def status(self):
+        st = (ctypes.c_int * 4)()
+        rc = lib().yr_pk_status(self._handle, st)
+        return rc, list(st)
+
+    def graph_info(self) -> dict:
+        info = (ctypes.c_int64 * 8)()
+        check(lib().yr_pk_graph_info(self._graph, info, 8), "graph info")
+        keys = ("ops", "tasks", "events", "workers", "tickets", "scratch_floats", "max_queue")
+        return dict(zip(keys, list(info)[:7]))
+
+    def export_task_graph(self) -> str:
+        need = ctypes.c_size_t()
+        check(lib().yr_pk_graph_export_json(self._graph, None, 0, ctypes.byref(need)), "export")
+        buf = ctypes.create_string_buffer(need.value)
+        check(lib().yr_pk_graph_export_json(self._graph, buf, need.value, None), "export")
+        return buf.value.decode()
+
+    def __del__(self):
+        try:
+            if not getattr(self, "__finalized__", True):
+                self.finalize()
+        except Exception:
+            pass  # interpreter shutdown: the library may already be unloaded
+
+    def finalize(self):
+        if self.__finalized__:
+            return
+        if self._handle is not None:
+            lib().yr_pk_destroy(self._handle)
+            self._handle = None
+        if self._graph is not None:
+            lib().yr_pk_graph_free(self._graph)
+            self._graph = None
+        self.__finalized__ = True
