@@ -1,0 +1,250 @@
+"""Benchmark of the hip backend on one MI355X.
+
+Headline (BASELINE.json metric): latency of one Llama-3-8B-shaped decode step
+at batch 1 (32 layers, hidden 4096, GQA 32/8, head_dim 128, MLP 14336, vocab
+128256, bf16 random-init weights, KV length 4096 in 64-token pages behind a
+random page table), run as one persistent-megakernel launch per step.  The
+fused operators of BASELINE configs 1-4 and the batch-8 step are reported in
+the same JSON line under "fused_ops" / "decode_b8".
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-fused] [--no-cpu]
+
+Prints exactly one JSON line on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def _events_time(torch, fn, iters: int) -> float:
+    """Average milliseconds per call of fn (launches on torch's current stream)."""
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def _graph_time(torch, fn, per_graph: int = 20, replays: int = 5) -> float:
+    """Average ms per call with launch overhead removed: `per_graph` calls are
+    captured in one HIP graph and replayed."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for _ in range(per_graph):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    return _events_time(torch, g.replay, replays) / per_graph
+
+
+def bench_fused(torch):
+    import yirage_amd.fused as F
+
+    dev = "cuda"
+    gen = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+
+    def rnd(shape, std, dtype):
+        return (torch.randn(shape, generator=gen, device=dev) * std).to(dtype)
+
+    # config 1: RMSNorm + linear, X[8,4096] f16, W[4096,4096] (K x N)
+    x = rnd((8, 4096), 1.0, torch.float16)
+    g = torch.ones(4096, dtype=torch.float16, device=dev)
+    w = rnd((4096, 4096), 0.02, torch.float16)
+    o = torch.empty((8, 4096), dtype=torch.float16, device=dev)
+    ms = _graph_time(torch, lambda: F.rmsnorm_linear(x, g, w, eps=1e-6, out=o))
+    b = 33_693_696
+    out["rmsnorm_linear_b8"] = dict(us=ms * 1e3, gbs=b / ms / 1e6, frac_hbm=b / ms / 1e6 / HBM_PEAK_GBS)
+    # config 2a / 2b: gated MLP W1, W3 [4096, 14336] bf16
+    w1 = rnd((4096, 14336), 0.02, torch.bfloat16)
+    w3 = rnd((4096, 14336), 0.02, torch.bfloat16)
+    for B, b in ((8, 235_175_936), (128, 239_599_616)):
+        xb = rnd((B, 4096), 1.0, torch.bfloat16)
+        ob = torch.empty((B, 14336), dtype=torch.bfloat16, device=dev)
+        ms = _graph_time(torch, lambda: F.gated_mlp(xb, w1, w3, out=ob), per_graph=10 if B > 8 else 20)
+        flops = 4.0 * B * 4096 * 14336
+        out[f"gated_mlp_b{B}"] = dict(us=ms * 1e3, gbs=b / ms / 1e6, frac_hbm=b / ms / 1e6 / HBM_PEAK_GBS,
+                                      tflops=flops / ms / 1e9)
+    del w1, w3
+    # config 3: paged GQA decode, B=8, 32/8 heads, d=128, KV 4096 f16, 64-token pages
+    B, Hq, Hkv, D, L, page = 8, 32, 8, 128, 4096, 64
+    P = B * L // page
+    kc = rnd((P, page, Hkv, D), 1.0, torch.float16)
+    vc = rnd((P, page, Hkv, D), 1.0, torch.float16)
+    idx = torch.randperm(P, generator=gen, device=dev).to(torch.int32)
+    indptr = (torch.arange(B + 1, device=dev) * (L // page)).to(torch.int32)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    q = rnd((B, Hq, D), 1.0, torch.float16)
+    oq = torch.empty_like(q)
+    ms = _graph_time(torch, lambda: F.gqa_decode_paged(q, kc, vc, indptr, idx, lens, max_kv_len=L, out=oq))
+    b = 2 * B * L * Hkv * D * 2 + 2 * B * Hq * D * 2 + (B + 1 + P) * 4
+    out["gqa_decode_b8"] = dict(us=ms * 1e3, gbs=b / ms / 1e6, frac_hbm=b / ms / 1e6 / HBM_PEAK_GBS)
+    del kc, vc
+    # config 4: causal GQA prefill, S=2048, 32/8 heads, d=128 bf16
+    S = 2048
+    qq = rnd((1, S, 32, 128), 1.0, torch.bfloat16)
+    kk = rnd((1, S, 8, 128), 1.0, torch.bfloat16)
+    vv = rnd((1, S, 8, 128), 1.0, torch.bfloat16)
+    oo = torch.empty_like(qq)
+    ms = _graph_time(torch, lambda: F.gqa_prefill(qq, kk, vv, causal=True, out=oo), per_graph=10)
+    flops = 4.0 * 128 * 32 * S * (S + 1) / 2
+    out["gqa_prefill_s2048"] = dict(us=ms * 1e3, tflops=flops / ms / 1e9,
+                                    frac_mfma=flops / ms / 1e9 / MFMA_BF16_PEAK_TFS)
+    for v in out.values():
+        for k in list(v):
+            v[k] = round(v[k], 4)
+    return out
+
+
+def cpu_baseline(sample_layers: int = 2):
+    """The CPU oracle (oracle/yr_oracle.c, double accumulation, OpenMP) timed
+    on a bounded sample of the same decode step: `sample_layers` full decoder
+    layers at batch 1 plus the LM head, scaled to 32 layers."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from yirage_amd.llama import LLAMA3_8B as cfg, page_table, rope_tables, tensor_seed, weight_shapes
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_num_threads(threads)
+    bf = "bf16"
+    G, D, kv_len, page = cfg.num_q_heads // cfg.num_kv_heads, cfg.head_dim, 4096, 64
+    indptr, indices, pool = page_table(1, kv_len, page, 7)
+    cos, sin = rope_tables(kv_len + 8, D, cfg.rope_theta)
+    cos, sin = cos.float().numpy(), sin.float().numpy()
+    qo = np.array([0, 1], np.int32)
+    lpl = np.array([kv_len % page], np.int32)
+    ones = np.ones(cfg.hidden, np.float32)
+    x = O.round_to(np.random.default_rng(0).standard_normal((1, cfg.hidden)), bf)
+    elapsed = 0.0
+    for layer in range(sample_layers):
+        W = {n: O.synth(s, bf, tensor_seed(0, layer, n), 0.02) for n, s in weight_shapes(cfg).items()}
+        rows = []
+        for g in range(cfg.num_kv_heads):
+            rows += [W["wq"][g * G * D:(g + 1) * G * D], W["wk"][g * D:(g + 1) * D], W["wv"][g * D:(g + 1) * D]]
+        wqkv = np.ascontiguousarray(np.concatenate(rows, 0))
+        kc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(0, layer, "kc"), 1.0)
+        vc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(0, layer, "vc"), 1.0)
+        t0 = time.perf_counter()
+        xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
+        qkv = O.round_to(O.linear(xn, wqkv, bf, O.W_NK), bf)
+        att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, kc, vc, bf, qo, indptr,
+                                           indices, lpl, cos, sin), bf)
+        h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
+        hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
+        m = O.silu_mul(O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf),
+                       O.round_to(O.linear(hn, W["wu"], bf, O.W_NK), bf), bf)
+        x = O.round_to(O.linear(m, W["wd"], bf, O.W_NK, residual=h), bf)
+        elapsed += time.perf_counter() - t0
+        del W, kc, vc
+    lm = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(0, 0, "lm_head"), 0.02)
+    t0 = time.perf_counter()
+    logits = O.round_to(O.linear(O.round_to(O.rmsnorm(x, ones, cfg.eps), bf), lm, bf, O.W_NK), bf)
+    O.argmax(logits)
+    t_lm = time.perf_counter() - t0
+    step_ms = (elapsed / sample_layers * cfg.num_layers + t_lm) * 1e3
+    return dict(value=round(step_ms, 2), unit="ms", cores=threads, kind="port",
+                sample=f"{sample_layers} of 32 decoder layers + LM head/argmax at batch 1 (kv 4096), "
+                       f"layer time scaled x32; weight generation excluded")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-b8", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the hip backend's persistent kernel is single-GPU; "
+              "see DESIGN.md for how the path would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from yirage_amd.llama import LLAMA3_8B, LlamaDecodeModel
+
+    torch.cuda.set_device(0)
+    model = LlamaDecodeModel(LLAMA3_8B, batch=1, kv_len=4096, seed=0)
+    model.set_input_tokens([128000])
+    for _ in range(args.warmup):
+        model.step()
+    torch.cuda.synchronize()
+    rc, st = model.pk.status()
+    if rc != 0:
+        raise SystemExit(f"persistent kernel status {st}")
+    ms = _events_time(torch, model.step, args.steps)
+    rc, st = model.pk.status()
+    if rc != 0:
+        raise SystemExit(f"persistent kernel status {st}")
+    step_bytes = model.weight_bytes() + model.kv_bytes()
+    achieved = step_bytes / ms / 1e6
+    info = model.pk.graph_info()
+    del model
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.no_b8:
+        m8 = LlamaDecodeModel(LLAMA3_8B, batch=8, kv_len=4096, seed=0)
+        m8.set_input_tokens([128000] * 8)
+        for _ in range(max(1, args.warmup)):
+            m8.step()
+        ms8 = _events_time(torch, m8.step, max(5, args.steps // 2))
+        b8 = m8.weight_bytes() + m8.kv_bytes()
+        extra["decode_b8"] = dict(ms=round(ms8, 4), gbs=round(b8 / ms8 / 1e6, 1),
+                                  frac_hbm=round(b8 / ms8 / 1e6 / HBM_PEAK_GBS, 4),
+                                  tokens_per_s=round(8 / ms8 * 1e3, 1))
+        del m8
+        torch.cuda.empty_cache()
+    if not args.no_fused:
+        extra["fused_ops"] = bench_fused(torch)
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": "fused-op latency (µs) & % HBM peak; 8B-shape decode step latency, batch 1",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights ~N(0,0.02), KV cache ~N(0,1), seeded)",
+        "config": {"workload": "llama3-8b-shape decode step, batch 1, kv 4096, persistent kernel",
+                   "layers": 32, "hidden": 4096, "heads": "32/8", "head_dim": 128, "mlp": 14336,
+                   "vocab": 128256, "page_size": 64, "parallelism": "single GPU",
+                   "tasks_per_step": info["tasks"], "workers": info["workers"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": step_bytes},
+        "tokens_per_s": round(1e3 / ms, 2),
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
