@@ -206,6 +206,12 @@ int yr_pk_init_batch(yr_pk_handle* handle, void* stream);
 int yr_pk_launch(yr_pk_handle* handle, void* stream);
 /* Polls a dependency may spin before the watchdog flags an error. */
 int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
+/* Per-task timestamps (10 ns device clock) into buffer[task][8] =
+ * {start, inputs ready, end, worker, activations staged, compute done,
+ * outputs published, 0}; NULL disables.  Replaces the
+ * YPK_ENABLE_PROFILING ring buffer (persistent_kernel.cuh:473-480,608-635,
+ * profiler.h:90-158). */
+int yr_pk_set_profiler(yr_pk_handle* handle, uint64_t* buffer, size_t entries);
 /* Synchronous read of the status words; YR_E_TIMEOUT after a watchdog exit. */
 int yr_pk_status(yr_pk_handle* handle, int* status4);
 int yr_pk_reset_status(yr_pk_handle* handle);

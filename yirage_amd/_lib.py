@@ -75,6 +75,7 @@ SIGNATURES = {
     "yr_pk_launch": (_I, [_P, _P]),
     "yr_pk_set_spin_limit": (_I, [_P, ctypes.c_longlong]),
     "yr_pk_status": (_I, [_P, ctypes.POINTER(ctypes.c_int)]),
+    "yr_pk_set_profiler": (_I, [_P, _P, _SZ]),
     "yr_pk_reset_status": (_I, [_P]),
     "yr_pk_destroy": (None, [_P]),
     "yr_backend_num_registered": (_I, []),

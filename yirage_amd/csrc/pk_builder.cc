@@ -79,6 +79,16 @@ static const uint16_t* seg_rows(Graph& g, const std::vector<Seg>& segs, int64_t 
   throw std::runtime_error("task rows beyond the weight segments");
 }
 
+// Rows left in the segment that holds virtual row r.
+static int64_t seg_remaining(const std::vector<Seg>& segs, int64_t r) {
+  int64_t base = 0;
+  for (auto& s : segs) {
+    if (r >= base && r < base + s.rows) return base + s.rows - r;
+    base += s.rows;
+  }
+  throw std::runtime_error("row beyond the weight segments");
+}
+
 static int64_t seg_total(const std::vector<Seg>& segs) {
   int64_t n = 0;
   for (auto& s : segs) n += s.rows;
@@ -221,7 +231,13 @@ void Graph::build(const char* text) {
         info.writes.push_back({to, 0, 1});
       }
       int rpt = (int)o["rows_per_task"].i64(16);
-      if (rpt <= 0) throw std::runtime_error("rows_per_task must be > 0");
+      if (rpt <= 0 || rpt % 2) throw std::runtime_error("rows_per_task must be even and > 0");
+      if (rpt * cfg.max_tokens > 4096) throw std::runtime_error("rows_per_task x max_tokens must be <= 4096");
+      if (col0 % 2 || d.out_ld % 2) throw std::runtime_error("linear output columns must be even-aligned");
+      if (norm && (cfg.max_tokens == 1 ? d.K > 32768 : d.K > 4096))
+        throw std::runtime_error("rmsnorm input too wide for the staged activation block");
+      if (cfg.max_tokens > 1 && d.K > 4096 && rpt > 7 * 3 * (silu ? 1 : 1))
+        throw std::runtime_error("batch > 1 with K > 4096: rows_per_task must be <= 21");
       if (silu && group % rpt) throw std::runtime_error("silu op: rows_per_task must divide 'group'");
       int ntasks = (d.N + rpt - 1) / rpt;
       int ordinal = 0;
@@ -235,7 +251,17 @@ void Graph::build(const char* text) {
           td.w0 = seg_rows(*this, segs, gi * 2 * group + j, td.rows, d.K);
           td.w1 = seg_rows(*this, segs, gi * 2 * group + group + j, td.rows, d.K);
         } else {
-          td.w0 = seg_rows(*this, segs, r, td.rows, d.K);
+          // a task may straddle one segment boundary (e.g. the q/k rows of a
+          // per-kv-group shuffled QKV weight): rows [0, split_row) from w0
+          int64_t in_first = seg_remaining(segs, r);
+          if (in_first >= td.rows) {
+            td.w0 = seg_rows(*this, segs, r, td.rows, d.K);
+            td.split_row = td.rows;
+          } else {
+            td.w0 = seg_rows(*this, segs, r, in_first, d.K);
+            td.w1 = seg_rows(*this, segs, r + in_first, td.rows - in_first, d.K);
+            td.split_row = (int)in_first;
+          }
         }
         td.i0 = ordinal++;
         td.i1 = ntasks;
@@ -257,6 +283,9 @@ void Graph::build(const char* text) {
       d.num_kv_heads = (int)o["num_kv_heads"].i64();
       d.head_dim = (int)o["head_dim"].i64(128);
       d.splits = (int)o["splits"].i64(1);
+      // a split holds at most 7 compute waves x 64 cached positions
+      int min_splits = (cfg.max_seq_len + 447) / 448;
+      if (d.splits < min_splits) d.splits = min_splits;
       d.page_size = cfg.page_size;
       if (d.head_dim != 128) throw std::runtime_error("attention: head_dim must be 128");
       if (d.num_kv_heads <= 0 || d.num_q_heads % d.num_kv_heads) throw std::runtime_error("attention: bad heads");

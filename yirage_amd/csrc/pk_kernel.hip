@@ -35,7 +35,10 @@ struct Shared {
   float red[PK_WAVES * 16 * 2];   // small reductions
   float attn_p[PK_WAVES][16][64]; // attention probabilities per wave
   float attn_ml[PK_WAVES][16][2];
-  int flag;
+  TaskDesc tq[256];               // this worker's first 256 task descriptors
+  int flag;                       // last wait succeeded (0 after a watchdog exit)
+  int last_op;                    // op whose activations are staged in xs (-1: none)
+  int last_T;
 };
 
 // ------------------------------------------------------------ protocol
@@ -45,9 +48,16 @@ __device__ __forceinline__ bool aborted(const KernelArgs& a) {
 
 // Whole-workgroup wait until events[e] >= wait_count * epoch.  Returns false
 // when the watchdog fired here or elsewhere.
+__device__ __forceinline__ uint64_t now_10ns() { return __builtin_amdgcn_s_memrealtime(); }
+
+constexpr int POLL_T = (PK_WAVES - 1) * kWave;  // first lane of the sync wave (no weight loads)
+
 __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  if (t.wait_event < 0) return true;
-  if (threadIdx.x == 0) {
+  if (t.wait_event < 0) {
+    if (a.profile && threadIdx.x == POLL_T) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    return true;
+  }
+  if (threadIdx.x == POLL_T) {
     const uint32_t need = (uint32_t)t.wait_count * a.epoch;
     long long spins = 0;
     int ok = 1;
@@ -63,6 +73,7 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
       }
       __builtin_amdgcn_s_sleep(2);
     }
+    if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
   }
   __syncthreads();
@@ -73,7 +84,7 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
 __device__ void signal_event(const KernelArgs& a, const TaskDesc& t) {
   wait_vm();
   __syncthreads();
-  if (threadIdx.x == 0 && t.trigger_event >= 0)
+  if (threadIdx.x == POLL_T && t.trigger_event >= 0)
     __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -117,40 +128,58 @@ __device__ void task_embed(const KernelArgs& a, const TaskDesc& t, int task_id, 
 }
 
 // ------------------------------------------------------------ GEMV family
-// Each lane owns 16-byte chunks (lane + 64 j) of a 4096-element sub-block;
-// a stage is RI rows x NM matrices x 8 chunks = 16 loads per lane.
+// Workgroup roles: waves 0..CW-1 stream weights and do the dot products; the
+// sync wave (wave CW) never loads weights, so its dependency polls and
+// activation loads never wait (vmcnt is in order) behind weight traffic.
+//   compute waves: issue stage 0 -> [X] -> stages (prefetch k+1, compute k)
+//                  -> row sums to LDS -> [O]
+//   sync wave:     poll the event -> stage activations (+RMSNorm) -> [X]
+//                  -> [O] -> epilogue, stores, publish
+// Between [O] of task i and [X] of task i+1 the compute waves already have
+// task i+1's first stage in flight while the sync wave publishes task i and
+// waits for task i+1's inputs.
 enum { EPI_LIN = 0, EPI_NORM = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+constexpr int CW = PK_WAVES - 1;           // compute waves
+constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
 
-template <int TM, int NM, int RI>
+// A stage holds NM x RI rows x NCH chunks of 16 bytes per lane (NM*RI*NCH = 8
+// loads): a sub-block of SB = NCH * 512 elements of every row in the stage.
+// Eight loads per lane keep ~57 KB per CU in flight, about bandwidth x
+// latency; deeper prefetch only lengthens the CU's memory queue in front of
+// the latency-critical polls and activation loads.
+template <int NM, int RI, int NCH>
 struct Stage {
-  uint4 w[NM][RI][8];
+  uint4 w[NM][RI][NCH];
 };
 
-template <int TM, int NM, int RI>
-__device__ __forceinline__ void load_stage(Stage<TM, NM, RI>& s, const TaskDesc& t, int K, int wave, int lane,
+template <int NM, int RI, int NCH>
+__device__ __forceinline__ void load_stage(Stage<NM, RI, NCH>& s, const TaskDesc& t, int K, int wave, int lane,
                                            int group, int sb, int R) {
 #pragma unroll
   for (int m = 0; m < NM; m++) {
-    const uint16_t* W = m == 0 ? t.w0 : t.w1;
 #pragma unroll
     for (int r = 0; r < RI; r++) {
-      int row = wave + PK_WAVES * (group * RI + r);
+      int row = wave + CW * (group * RI + r);
+      // SiLU op: matrix m = gate / up; linear op: row split across two segments
+      const uint16_t* W;
+      if (NM == 2) W = (m == 0 ? t.w0 : t.w1) + (size_t)row * K;
+      else W = row < t.split_row ? t.w0 + (size_t)row * K : t.w1 + (size_t)(row - t.split_row) * K;
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        int k = sb * 4096 + (lane + 64 * j) * 8;
-        if (row < R && k < K) s.w[m][r][j] = ldg16(W + (size_t)row * K + k);
+      for (int j = 0; j < NCH; j++) {
+        int k = sb * (NCH * 512) + (lane + 64 * j) * 8;
+        if (row < R && k < K) s.w[m][r][j] = ldg16(W + k);
         else s.w[m][r][j] = make_uint4(0, 0, 0, 0);
       }
     }
   }
 }
 
-template <int TM, int NM, int RI>
-__device__ __forceinline__ void compute_stage(const Stage<TM, NM, RI>& s, const Shared& sm, int KB, int kb_off,
+template <int TM, int NM, int RI, int NCH>
+__device__ __forceinline__ void compute_stage(const Stage<NM, RI, NCH>& s, const Shared& sm, int KB, int kb_off,
                                               int sb, int K, int lane, float (&acc)[NM][RI][TM]) {
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    int kl = sb * 4096 + (lane + 64 * j) * 8 - kb_off;  // element offset inside the staged block
+  for (int j = 0; j < NCH; j++) {
+    int kl = sb * (NCH * 512) + (lane + 64 * j) * 8 - kb_off;  // element offset inside the staged block
     if (kb_off + kl >= K) continue;
     uint4 xv[TM];
 #pragma unroll
@@ -173,26 +202,51 @@ __device__ __forceinline__ void compute_stage(const Stage<TM, NM, RI>& s, const 
   }
 }
 
-// Stage activations [T][kb_off .. kb_off + KB) into LDS, applying RMSNorm
+// Sync wave: activations [T][kb_off .. kb_off + KB) into LDS (agent-scope
+// loads, 16 per lane in flight), RMSNorm applied when NORM
 // (x * (rsqrt(mean(x^2) + eps) * w), rounded to bf16 as rmsnorm.cuh:120-124).
+// RMSNorm weights of one sync-wave lane (K <= 4096): loaded before the poll,
+// since they never depend on the event.
+struct NormRegs {
+  uint4 g[8];
+};
+
+__device__ __forceinline__ void load_norm(NormRegs& nr, const OpDesc& op, int lane) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    int c = (lane + kWave * j) * 8;
+    nr.g[j] = c < op.K ? ldg16(op.norm + c) : make_uint4(0, 0, 0, 0);
+  }
+}
+
 template <int TM, bool NORM>
-__device__ void stage_x(const KernelArgs& a, const OpDesc& op, int T, int KB, int kb_off, Shared& sm) {
+__device__ __forceinline__ void stage_x_sync(const OpDesc& op, int T, int KB, int kb_off, Shared& sm, const NormRegs& nr,
+                                             bool have_nr) {
+  const int lane = threadIdx.x - SYNC_T0;
   const int K = op.K;
   const int n8 = KB / 8;
-  for (int i = threadIdx.x; i < TM * n8; i += PK_THREADS) {
-    int b = i / n8, c = (i % n8) * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (b < T && kb_off + c < K) v = ld_agent_u128(op.x + (size_t)b * op.x_ld + kb_off + c);
-    *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = v;
+  const int total = TM * n8;
+  for (int i0 = 0; i0 < total; i0 += kWave * 16) {
+    uint4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      int i = i0 + u * kWave + lane;
+      int b = i / n8, c = (i % n8) * 8;
+      v[u] = (i < total && b < T && kb_off + c < K) ? ld_agent_u128(op.x + (size_t)b * op.x_ld + kb_off + c)
+                                                     : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      int i = i0 + u * kWave + lane;
+      if (i < total) *reinterpret_cast<uint4*>(&sm.xs[(i / n8) * KB + (i % n8) * 8]) = v[u];
+    }
   }
-  __syncthreads();
   if constexpr (NORM) {
-    // sum of squares per token: wave b handles token b
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    if (wave < TM) {
+    // K <= KB here (checked at build): one pass per token
+    for (int b = 0; b < TM; b++) {
       float ss = 0.f;
       for (int c = lane * 8; c < K; c += kWave * 8) {
-        uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[wave * KB + c]);
+        uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
         uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -201,49 +255,111 @@ __device__ void stage_x(const KernelArgs& a, const OpDesc& op, int T, int KB, in
         }
       }
       ss = wave_sum(ss);
-      if (lane == 0) sm.red[wave] = rsqrtf(ss / (float)K + op.eps);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < TM * n8; i += PK_THREADS) {
-      int b = i / n8, c = (i % n8) * 8;
-      if (b >= T || c >= K) continue;
-      float r = sm.red[b];
-      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
-      uint4 g = ldg16(op.norm + c);
-      uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w}, o[4];
+      float r = rsqrtf(ss / (float)K + op.eps);
+      if (b >= T) continue;
+      auto norm_chunk = [&](int c, uint4 g) __attribute__((always_inline)) {
+        uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
+        uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w}, o[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float lo = lo16<DT_BF16>(xv[e]) * (r * lo16<DT_BF16>(gv[e]));
-        float hi = hi16<DT_BF16>(xv[e]) * (r * hi16<DT_BF16>(gv[e]));
-        o[e] = pack2<DT_BF16>(lo, hi);
+        for (int e = 0; e < 4; e++) {
+          float lo = lo16<DT_BF16>(xv[e]) * (r * lo16<DT_BF16>(gv[e]));
+          float hi = hi16<DT_BF16>(xv[e]) * (r * hi16<DT_BF16>(gv[e]));
+          o[e] = pack2<DT_BF16>(lo, hi);
+        }
+        *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = make_uint4(o[0], o[1], o[2], o[3]);
+      };
+      if (have_nr) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          int c = (lane + kWave * j) * 8;
+          if (c < K) norm_chunk(c, nr.g[j]);
+        }
+      } else {
+        for (int c = lane * 8; c < K; c += kWave * 8) norm_chunk(c, ldg16(op.norm + c));
       }
-      *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    __syncthreads();
   }
+}
+
+// Sync wave: one-lane event poll (the watchdog exits through sm.flag).
+__device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  if (threadIdx.x == SYNC_T0) {
+    int ok = 1;
+    if (t.wait_event >= 0) {
+      const uint32_t need = (uint32_t)t.wait_count * a.epoch;
+      long long spins = 0;
+      for (;;) {
+        uint32_t v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int32_t)(v - need) >= 0) break;
+        if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
+        if (++spins > a.spin_limit) {
+          __hip_atomic_store(a.meta.status + 2, task_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    sm.flag = ok;
+  }
+  __builtin_amdgcn_wave_barrier();
+  return __shfl(sm.flag, 0, kWave) != 0;
 }
 
 template <int TM, int EPI>
 __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   constexpr int NM = EPI == EPI_SILU ? 2 : 1;
-  constexpr int RI = (NM == 2 || TM > 1) ? 1 : 2;  // rows per stage (16 or 8 loads per lane)
+  constexpr int RI = 1;
+  constexpr int NCH = 8 / NM;          // chunks per lane per matrix per stage
+  constexpr int SB = NCH * 512;        // elements per sub-block
   constexpr bool NORM = EPI != EPI_LIN;
   const OpDesc& op = a.ops[t.op];
   const int K = op.K, R = t.rows;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  // wave index as a scalar: role branches are wave-uniform, so the register
+  // live ranges of the sync and compute paths do not overlap
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const bool is_sync = wave == CW;
   const int KB = TM == 1 ? K : (K < 4096 ? K : 4096);   // staged activation block
   const int nkb = (K + KB - 1) / KB;
-  const int nsb = (KB + 4095) / 4096;                     // sub-blocks per staged block
-  const int nrows_w = wave < R ? (R - wave + PK_WAVES - 1) / PK_WAVES : 0;
+  const int nsb = (KB + SB - 1) / SB;                     // sub-blocks per staged block
+  float* outs = reinterpret_cast<float*>(sm.outs);       // [T][R] fp32 row sums (SiLU: products)
+  const bool same_op = sm.last_op == t.op && nkb == 1;   // inputs of this op already staged
+
+  if (is_sync) {
+    // ---------------- sync wave: inputs
+    int T = sm.last_T;
+    if (!same_op) {
+      NormRegs nr;
+      const bool pre = NORM && K <= 4096;
+      if (pre) load_norm(nr, op, lane);
+      bool ok = poll_event_sync(a, t, task_id, sm);
+      if (ok) {
+        T = active_tokens(a, op);
+        stage_x_sync<TM, NORM>(op, T, KB, 0, sm, nr, pre);
+      }
+    } else if (a.profile && lane == 0) {
+      a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    }
+    if (lane == 0) {
+      sm.last_T = T;
+      sm.last_op = nkb == 1 ? t.op : -1;
+    }
+  }
+  // compute waves: first stage in flight before the inputs are ready
+  const int nrows_w = (!is_sync && wave < R) ? (R - wave + CW - 1) / CW : 0;
   const int ngroups = (nrows_w + RI - 1) / RI;
+  Stage<NM, RI, NCH> cur, nxt;
+  if (ngroups > 0) load_stage<NM, RI, NCH>(cur, t, K, wave, lane, 0, 0, R);
+  __syncthreads();  // [X]: activations block 0 staged
+  if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+  if (!sm.flag) return;
+  const int T = sm.last_T;
 
-  // prefetch the first stage of weights before waiting for the inputs
-  Stage<TM, NM, RI> cur, nxt;
-  if (ngroups > 0) load_stage<TM, NM, RI>(cur, t, K, wave, lane, 0, 0, R);
-  if (!wait_event(a, t, task_id, sm)) return;
-  const int T = active_tokens(a, op);
-
-  constexpr int GMAX = 2;  // row groups kept live across staged blocks (K > KB)
+  // row groups kept live across staged blocks: only a plain linear can have
+  // K > KB (RMSNorm ops stage all of K, the builder checks it)
+  constexpr int GMAX = NORM ? 1 : 3;
   float acc_keep[GMAX][NM][RI][TM];
 #pragma unroll
   for (int g = 0; g < GMAX; g++)
@@ -254,44 +370,44 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
 #pragma unroll
         for (int b = 0; b < TM; b++) acc_keep[g][m][r][b] = 0.f;
 
-  auto finish_group = [&](int g, float (&acc)[NM][RI][TM]) {
+  auto finish_group = [&](int g, float (&acc)[NM][RI][TM]) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < RI; r++) {
-      int row = wave + PK_WAVES * (g * RI + r);
+      int row = wave + CW * (g * RI + r);
 #pragma unroll
       for (int b = 0; b < TM; b++) {
         float v0 = wave_sum(acc[0][r][b]);
         float v1 = NM == 2 ? wave_sum(acc[NM - 1][r][b]) : 0.f;
         if (lane == 0 && row < R && b < T) {
-          float o;
+          float o = v0;
           if constexpr (EPI == EPI_SILU) {
             // silu_mul.cuh:31-40 on the bf16 gate/up results
             float gt = round_to<DT_BF16>(v0), up = round_to<DT_BF16>(v1);
             o = round_to<DT_BF16>(gt / (1.0f + expf(-gt))) * up;
-          } else {
-            o = v0;
-            if (op.flags & OPF_RESIDUAL) {
-              uint32_t rw = ld_agent_u32(op.residual + (size_t)b * op.res_ld + ((t.row0 + row) & ~1));
-              o += (t.row0 + row) & 1 ? hi16<DT_BF16>(rw) : lo16<DT_BF16>(rw);
-            }
           }
-          sm.outs[b * R + row] = (uint16_t)st_elem<DT_BF16>(o);
+          outs[b * R + row] = o;
         }
       }
     }
   };
 
   for (int kb = 0; kb < nkb; kb++) {
-    if (kb) __syncthreads();
-    stage_x<TM, NORM>(a, op, T, KB, kb * KB, sm);
+    if (kb) {
+      __syncthreads();  // compute waves are done with block kb-1
+      if (is_sync) {
+        NormRegs none;
+        stage_x_sync<TM, false>(op, T, KB, kb * KB, sm, none, false);
+      }
+      __syncthreads();  // block kb staged
+    }
+    if (is_sync) continue;
     const int nst = ngroups * nsb;
     for (int st = 0; st < nst; st++) {
       int g = st / nsb, sb = kb * nsb + st % nsb;
-      // prefetch the next stage (next sub-block / row group / staged block)
       int st2 = st + 1, kb2 = kb;
       if (st2 == nst) { st2 = 0; kb2 = kb + 1; }
       bool has_next = kb2 < nkb && ngroups > 0;
-      if (has_next) load_stage<TM, NM, RI>(nxt, t, K, wave, lane, st2 / nsb, kb2 * nsb + st2 % nsb, R);
+      if (has_next) load_stage<NM, RI, NCH>(nxt, t, K, wave, lane, st2 / nsb, kb2 * nsb + st2 % nsb, R);
       float acc[NM][RI][TM];
       if (nkb > 1) {
 #pragma unroll
@@ -318,7 +434,7 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
 #pragma unroll
             for (int b = 0; b < TM; b++) acc[m][r][b] = acc_keep[0][m][r][b];
       }
-      compute_stage<TM, NM, RI>(cur, sm, KB, kb * KB, sb, K, lane, acc);
+      compute_stage<TM, NM, RI, NCH>(cur, sm, KB, kb * KB, sb, K, lane, acc);
       bool last_sb = st % nsb == nsb - 1;
       if (nkb > 1) {
 #pragma unroll
@@ -344,24 +460,36 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
       if (has_next) cur = nxt;
     }
   }
-  __syncthreads();
+  __syncthreads();  // [O]: row sums of every compute wave are in LDS
+  if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
+  if (!is_sync) return;
 
-  // write the task's output slice (bf16 pairs, agent scope)
-  for (int i = threadIdx.x; i < T * (R / 2); i += PK_THREADS) {
+  // ---------------- sync wave: epilogue, stores, publish
+  for (int i = lane; i < T * (R / 2); i += kWave) {
     int b = i / (R / 2), p = i % (R / 2);
-    uint32_t v = (uint32_t)sm.outs[b * R + 2 * p] | ((uint32_t)sm.outs[b * R + 2 * p + 1] << 16);
-    st_agent_u32(op.out + (size_t)b * op.out_ld + t.row0 + 2 * p, v);
+    float v0 = outs[b * R + 2 * p], v1 = outs[b * R + 2 * p + 1];
+    if (EPI != EPI_SILU && (op.flags & OPF_RESIDUAL)) {
+      uint32_t rw = ld_agent_u32(op.residual + (size_t)b * op.res_ld + t.row0 + 2 * p);
+      v0 += lo16<DT_BF16>(rw);
+      v1 += hi16<DT_BF16>(rw);
+    }
+    uint32_t packed = pack2<DT_BF16>(v0, v1);
+    st_agent_u32(op.out + (size_t)b * op.out_ld + t.row0 + 2 * p, packed);
+    if (EPI == EPI_ARGMAX) {
+      outs[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
+      outs[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
+    }
   }
-
   if constexpr (EPI == EPI_ARGMAX) {
     // local (value, index) maximum per token over this task's valid rows;
     // lowest index wins ties (torch.argmax semantics)
+    __builtin_amdgcn_wave_barrier();
     const int lim = op.vocab - t.row0 < R ? op.vocab - t.row0 : R;
     for (int b = 0; b < T; b++) {
       float best = -INFINITY;
       int bi = 0x7fffffff;
-      for (int i = threadIdx.x; i < lim; i += PK_THREADS) {
-        float v = ld_elem<DT_BF16>(sm.outs[b * R + i]);
+      for (int i = lane; i < lim; i += kWave) {
+        float v = outs[b * R + i];
         if (v > best || (v == best && i < bi)) { best = v; bi = i; }
       }
 #pragma unroll
@@ -371,26 +499,21 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
         if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
       }
       if (lane == 0) {
-        sm.red[wave * 2] = best;
-        sm.red[wave * 2 + 1] = __int_as_float(bi);
-      }
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        for (int w = 1; w < PK_WAVES; w++) {
-          float ov = sm.red[w * 2];
-          int oi = __float_as_int(sm.red[w * 2 + 1]);
-          if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
-        }
         float* rec = a.scratch + op.scratch_off + ((size_t)t.i0 * op.max_tokens + b) * 2;
         st_agent(rec, best);
         st_agent(rec + 1, __int_as_float(bi == 0x7fffffff ? -1 : t.row0 + bi));
       }
-      __syncthreads();
     }
-    if (arrive_last(&a.tickets[op.ticket_base], t.i1)) {
-      // reduce all tasks' records; task order = column order, so the first
-      // strictly greater value keeps the lowest index on ties
-      for (int b = wave; b < T; b += PK_WAVES) {
+    wait_vm();
+    int last = 0;
+    if (lane == 0)
+      last = __hip_atomic_fetch_add(&a.tickets[op.ticket_base], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(t.i1 - 1);
+    last = __shfl(last, 0, kWave);
+    if (last) {
+      if (lane == 0) __hip_atomic_store(&a.tickets[op.ticket_base], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // reduce every task's record; task order = column order
+      for (int b = 0; b < T; b++) {
         float best = -INFINITY;
         int bi = 0x7fffffff;
         for (int k = lane; k < t.i1; k += kWave) {
@@ -412,7 +535,10 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
       }
     }
   }
-  signal_event(a, t);
+  wait_vm();
+  if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
+  if (lane == 0 && t.trigger_event >= 0)
+    __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------ attention
@@ -453,7 +579,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
   constexpr int D = 128;
   const int r = t.i0, h = t.i1, s = t.i2, S = op.splits;
   const int G = op.num_q_heads / op.num_kv_heads;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const BatchMeta& m = a.meta;
   // request geometry (the page table is written by the host or by the
   // previous launch's prepare_batch task)
@@ -468,7 +594,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
   const int c1 = (s + 1) * chunk < base ? (s + 1) * chunk : base;
   const bool last = s == S - 1;
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
-  auto cache_off = [&](int pos) -> size_t {
+  auto cache_off = [&](int pos) __attribute__((always_inline)) -> size_t {
     int pg = m.kv_indices[pb + pos / op.page_size];
     return ((size_t)pg * op.page_size + pos % op.page_size) * tok_stride + (size_t)h * D;
   };
@@ -478,7 +604,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
   const int nblk = (c1 - c0 + 63) / 64;
   // prefetch the first block of this wave before waiting
   uint4 kf[4][4], vf[16];
-  auto load_block = [&](int blk) {
+  auto load_block = [&](int blk) __attribute__((always_inline)) {
     int p0 = c0 + blk * 64;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -494,14 +620,14 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
       vf[i] = p < c1 ? ldg16(op.v_cache + cache_off(p) + (lane % 16) * 8) : make_uint4(0, 0, 0, 0);
     }
   };
-  if (nt > 0 && wave < nblk) load_block(wave);
+  if (nt > 0 && wave < nblk && wave < CW) load_block(wave);
 
   if (!wait_event(a, t, task_id, sm)) return;
   if (nt <= 0) {
     signal_event(a, t);
     return;
   }
-  if (nt * G > 16) {  // more query rows than one MFMA row block: unsupported here
+  if (nt * G > 16 || nblk > CW) {  // beyond one MFMA row block / one block per wave
     if (threadIdx.x == 0) {
       __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -532,7 +658,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
     for (int e = 0; e < 8; e++) o_acc[rr][e] = 0.f;
 
   // process one 64-position block held in kf/vf; mask(p_local, row) -> visible
-  auto process = [&](int p0, int npos, bool causal_new) {
+  auto process = [&](int p0, int npos, bool causal_new) __attribute__((always_inline)) {
     f32x4 sc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -600,10 +726,9 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
     __builtin_amdgcn_wave_barrier();
   };
 
-  for (int blk = wave; blk < nblk; blk += PK_WAVES) {
-    process(c0 + blk * 64, (c1 - c0) - blk * 64 < 64 ? (c1 - c0) - blk * 64 : 64, false);
-    if (blk + PK_WAVES < nblk) load_block(blk + PK_WAVES);
-  }
+  // one 64-position block per compute wave (the builder sizes splits so that
+  // a split never holds more than CW * 64 cached positions)
+  if (wave < nblk && wave < CW) process(c0 + wave * 64, (c1 - c0) - wave * 64 < 64 ? (c1 - c0) - wave * 64 : 64, false);
 
   // new tokens (last split, wave 0): k/v from qkv, RoPE on k, append to cache
   if (last && wave == 0) {
@@ -800,11 +925,39 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
   __shared__ Shared sm;
   const int w = blockIdx.x;
   const int q0 = a.queue_offsets[w], q1 = a.queue_offsets[w + 1];
+  // this worker's task descriptors move to LDS, 256 at a time
+  auto load_descs = [&](int first) __attribute__((always_inline)) {
+    const int n = q1 - first < 256 ? q1 - first : 256;
+    const int words = (int)(sizeof(TaskDesc) / 4);
+    for (int i = threadIdx.x; i < n * words; i += PK_THREADS) {
+      int k = i / words, e = i % words;
+      reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = reinterpret_cast<const uint32_t*>(&a.tasks[a.queue[first + k]])[e];
+    }
+  };
+  load_descs(q0);
+  if (threadIdx.x == 0) {
+    sm.flag = 1;
+    sm.last_op = -1;
+    sm.last_T = 0;
+  }
+  __syncthreads();
   for (int q = q0; q < q1; q++) {
+    if (q > q0 && (q - q0) % 256 == 0) {
+      __syncthreads();
+      load_descs(q);
+      __syncthreads();
+    }
     const int tid = a.queue[q];
-    const TaskDesc t = a.tasks[tid];
+    const TaskDesc& t = sm.tq[(q - q0) % 256];
     const OpDesc& op = a.ops[t.op];
+    if (a.profile && threadIdx.x == 0) {
+      a.profile[(size_t)tid * 8] = now_10ns();
+      a.profile[(size_t)tid * 8 + 3] = (uint64_t)w;
+    }
     const int tm8 = op.max_tokens > 1;
+    const bool gemv = op.type == TASK_LINEAR || op.type == TASK_RMSNORM_LINEAR ||
+                      op.type == TASK_RMSNORM_LINEAR_SILU || op.type == TASK_RMSNORM_LINEAR_ARGMAX;
+    if (!gemv && threadIdx.x == 0) sm.last_op = -1;  // attention / embed / batch tasks reuse xs
     switch (op.type) {
       case TASK_EMBED: task_embed(a, t, tid, sm); break;
       case TASK_LINEAR:
@@ -829,8 +982,13 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       case TASK_PREPARE_BATCH: task_prepare(a, t, tid, sm); break;
       default: break;
     }
-    __syncthreads();
-    if (aborted(a)) break;
+    // GEMV tasks need no trailing barrier: the next task's first LDS access
+    // comes after its own [X] barrier, which the sync wave reaches only after
+    // publishing this task, so the compute waves run ahead and put the next
+    // task's weights in flight meanwhile
+    if (!gemv) __syncthreads();
+    if (a.profile && threadIdx.x == 0) a.profile[(size_t)tid * 8 + 2] = now_10ns();
+    if (!sm.flag) break;  // a dependency never arrived: leave the queue
   }
 }
 
@@ -868,6 +1026,7 @@ struct Handle {
   BatchMeta meta;
   uint32_t epoch = 0;
   long long spin_limit = 1ll << 26;
+  uint64_t* profile = nullptr;
 };
 
 }  // namespace pk
@@ -998,6 +1157,7 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream) {
   a.epoch = h->epoch;
   a.num_workers = h->num_workers;
   a.spin_limit = h->spin_limit;
+  a.profile = h->profile;
   void* args[] = {&a};
   hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
                                             dim3(PK_THREADS), args, 0, st);
@@ -1012,13 +1172,24 @@ int yr_pk_set_spin_limit(yr_pk_handle* hp, long long polls) {
   return YR_OK;
 }
 
+int yr_pk_set_profiler(yr_pk_handle* hp, uint64_t* buffer, size_t entries) {
+  Handle* h = reinterpret_cast<Handle*>(hp);
+  if (!h) return fail(YR_E_INVALID, "yr_pk_set_profiler: null handle");
+  if (buffer && entries < h->n_tasks * 8)
+    return fail(YR_E_INVALID, "yr_pk_set_profiler: buffer needs %zu entries", h->n_tasks * 8);
+  h->profile = buffer;
+  return YR_OK;
+}
+
 int yr_pk_status(yr_pk_handle* hp, int* status4) {
   Handle* h = reinterpret_cast<Handle*>(hp);
   if (!h || !status4) return fail(YR_E_INVALID, "yr_pk_status: bad arguments");
   hipError_t e = hipMemcpy(status4, h->d_status, sizeof(int) * 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return check_hip(e, "yr_pk_status");
   if (status4[0]) return fail(YR_E_TIMEOUT, "persistent kernel watchdog fired waiting in task %d", status4[2]);
-  if (status4[3]) return fail(YR_E_INVALID, "attention task %d: more than 16 query rows per kv head", status4[3] - 1);
+  if (status4[3])
+    return fail(YR_E_INVALID, "attention task %d: more than 16 query rows per kv head or 512 positions per split",
+                status4[3] - 1);
   return YR_OK;
 }
 

@@ -66,9 +66,10 @@ struct TaskDesc {
   int row0, rows;     // output rows / columns covered [row0, row0 + rows)
   int i0, i1;         // attention: request, kv head; argmax: task ordinal
   int i2, i3;         // attention: split index; argmax: number of tasks
-  int pad0, pad1;
+  int split_row;      // linear: rows [0, split_row) come from w0, the rest from w1
+  int pad1;
   const uint16_t* w0; // weight rows of this task (gate rows for the SiLU op)
-  const uint16_t* w1; // up rows for the SiLU op
+  const uint16_t* w1; // up rows for the SiLU op; second weight segment of a linear task
 };
 
 // Batch / page manager state (persistent_kernel.cuh:107-132,169-322).
@@ -102,6 +103,7 @@ struct KernelArgs {
   uint32_t* tickets;         // arrival tickets (zero at rest)
   float* scratch;            // split records
   BatchMeta meta;
+  uint64_t* profile;         // optional [num_tasks][4]: start, inputs ready, end, worker
   uint32_t epoch;            // 1, 2, 3, ... per launch
   int num_workers;
   long long spin_limit;      // watchdog: polls before a wait gives up

@@ -44,6 +44,7 @@ class DTensor:
     tensor: torch.Tensor | None = None
     segments: list = field(default_factory=list)   # [(DTensor, row0, rows)] for views
     group: int = 0                                  # rows per source chunk of a shuffle
+    ngroups: int = 1                                # number of shuffle groups
 
     @property
     def num_dims(self) -> int:
@@ -146,7 +147,8 @@ class PersistentKernel:
         else:
             for t, r in zip(inputs, rows):
                 segs.append((t, 0, r))
-        v = DTensor(name, (sum(rows), inputs[0].dim(1)), inputs[0].dtype, None, segs, rows[0] // num_groups)
+        v = DTensor(name, (sum(rows), inputs[0].dim(1)), inputs[0].dtype, None, segs, rows[0] // num_groups,
+                    num_groups if shuffled else 1)
         return self._register(v)
 
     def fuse_tensors(self, inputs: list, fused_dim: int, num_groups: int, name: str = None) -> DTensor:
@@ -270,7 +272,14 @@ class PersistentKernel:
                     if l.get("residual") is not None:
                         op["residual"] = l["residual"].name
                 seg_rows = [n for (_, _, n) in op["weight"]]
-                gran = math.gcd(*seg_rows)
+                # a task may straddle one weight-segment boundary: rows per task
+                # <= the smallest segment and dividing the shuffle group (so no
+                # task crosses a kv-head group of a QKV projection)
+                if w.segments:
+                    gran = w.dim(0) // w.ngroups
+                    max_seg = min(seg_rows)
+                else:
+                    gran, max_seg = 0, None
                 tm8 = self.max_num_batched_tokens > 1
                 max_rows = 16 if (tm8 and K > 4096) else None
                 if nxt and nxt["kind"] == "silu_mul" and nxt["input"] is l["output"]:
@@ -294,7 +303,8 @@ class PersistentKernel:
                     op["rows_per_task"] = self._rows_per_task(w.dim(0), W, 0, max_rows)
                     i += 3
                 else:
-                    op["rows_per_task"] = self._rows_per_task(w.dim(0), W, gran, max_rows)
+                    lim = min(x for x in (max_rows, max_seg) if x) if (max_rows or max_seg) else None
+                    op["rows_per_task"] = self._rows_per_task(w.dim(0), W, gran, lim)
                     i += 1
                 ops.append(op)
                 continue
@@ -367,6 +377,32 @@ class PersistentKernel:
         if not self._is_compiled:
             raise YirageHipError("PersistentKernel: call compile() first")
         check(lib().yr_pk_launch(self._handle, self._stream()), "persistent kernel launch")
+
+    def enable_profiler(self, enable: bool = True):
+        """Per-task device timestamps; read them with profile()."""
+        if enable:
+            n = self.graph_info()["tasks"] * 8
+            self._prof = torch.zeros(n, dtype=torch.int64, device="cuda")
+            check(lib().yr_pk_set_profiler(self._handle, ctypes.c_void_p(self._prof.data_ptr()), n), "profiler")
+        else:
+            check(lib().yr_pk_set_profiler(self._handle, None, 0), "profiler")
+            self._prof = None
+
+    def profile(self):
+        """[tasks, 8] int64 numpy array (10 ns ticks): start, inputs ready, end, worker,
+        activations staged, compute done, outputs published (GEMV tasks), 0."""
+        return self._prof.view(-1, 8).cpu().numpy()
+
+    def task_table(self):
+        """[tasks, 10] int64: op, type, wait event, wait count, trigger event, row0, rows, i0, i1, i2."""
+        n = self.graph_info()["tasks"]
+        rec = (ctypes.c_int64 * 10)()
+        import numpy as np
+        out = np.zeros((n, 10), np.int64)
+        for t in range(n):
+            check(lib().yr_pk_graph_task(self._graph, t, rec, 10), "task")
+            out[t] = list(rec)
+        return out
 
     def status(self):
         st = (ctypes.c_int * 4)()
