@@ -207,8 +207,11 @@ int yr_pk_launch(yr_pk_handle* handle, void* stream);
 /* Polls a dependency may spin before the watchdog flags an error. */
 int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
 /* Per-task timestamps (10 ns device clock) into buffer[task][8] =
- * {start, inputs ready, end, worker, activations staged, compute done,
- * outputs published, 0}; NULL disables.  Replaces the
+ * {start, inputs ready, end, worker, s4, s5, s6, s7}; NULL disables.
+ * GEMV tasks: s4 activations staged, s5 compute done, s6 outputs published.
+ * Attention tasks: s5 request geometry read, s4 page ids read, s7 first K/V
+ * block landed (profiling waits for it), s6 split merge done (merging task
+ * only).  Replaces the
  * YPK_ENABLE_PROFILING ring buffer (persistent_kernel.cuh:473-480,608-635,
  * profiler.h:90-158). */
 int yr_pk_set_profiler(yr_pk_handle* handle, uint64_t* buffer, size_t entries);

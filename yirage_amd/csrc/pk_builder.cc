@@ -300,6 +300,7 @@ void Graph::build(const char* text) {
       d.out = (uint16_t*)tensors[out].ptr;
       d.out_ld = (int)tensors[out].dims[1];
       const Tensor& KC = tensors[kc];
+      if (cfg.page_size != 64) throw std::runtime_error("attention: page_size must be 64");
       if (KC.dims.size() != 4 || KC.dims[1] != cfg.page_size || KC.dims[2] != d.num_kv_heads || KC.dims[3] != d.head_dim)
         throw std::runtime_error("attention: cache must be [pages, page_size, Hkv, head_dim]");
       d.k_cache = (uint16_t*)KC.ptr;

@@ -27,11 +27,11 @@ namespace pk {
 constexpr int PK_WAVES = 8;
 constexpr int PK_THREADS = PK_WAVES * kWave;
 constexpr int XS_ELEMS = 32768;   // staged activation elements (64 KiB)
-constexpr int OUT_ELEMS = 8192;   // staged task outputs (16 KiB)
+constexpr int OUT_ELEMS = 16384;  // GEMV partial-sum slots (32 KiB as float)
 
 struct Shared {
   uint16_t xs[XS_ELEMS];          // activations (bf16), [token][KB]
-  uint16_t outs[OUT_ELEMS];       // task outputs (bf16), [token][rows]
+  uint16_t outs[OUT_ELEMS];       // GEMV partial-sum slots (float)
   float red[PK_WAVES * 16 * 2];   // small reductions
   float attn_p[PK_WAVES][16][64]; // attention probabilities per wave
   float attn_ml[PK_WAVES][16][2];
@@ -39,7 +39,23 @@ struct Shared {
   int flag;                       // last wait succeeded (0 after a watchdog exit)
   int last_op;                    // op whose activations are staged in xs (-1: none)
   int last_T;
+  KernelArgs args;                // this launch's arguments, for the task functions
 };
+
+// One workgroup per CU: the worker's LDS, addressed directly by the task
+// functions (which are separate functions, so that each task type gets its
+// own register allocation, and read their arguments from here instead of
+// through generic pointers).
+__shared__ Shared g_sm;
+
+// The op table is read-only for a whole launch: reading it through the
+// constant address space lets uniform field loads become scalar loads, which
+// never queue behind (or wait for) the vector memory traffic of a task.
+using OpRef = const __attribute__((address_space(4))) OpDesc&;
+__device__ __forceinline__ OpRef op_of(const KernelArgs& a, int i) {
+  return reinterpret_cast<const __attribute__((address_space(4))) OpDesc*>(
+      reinterpret_cast<uintptr_t>(a.ops))[i];
+}
 
 // ------------------------------------------------------------ protocol
 __device__ __forceinline__ bool aborted(const KernelArgs& a) {
@@ -71,7 +87,7 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
         ok = 0;
         break;
       }
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(16);
     }
     if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
@@ -106,14 +122,14 @@ __device__ __forceinline__ void st_agent_u128(void* p, uint4 v) {
   __hip_atomic_store(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ int active_tokens(const KernelArgs& a, const OpDesc& op) {
+__device__ __forceinline__ int active_tokens(const KernelArgs& a, OpRef op) {
   int n = (int)ld_agent_u32(a.meta.qo_indptr + a.meta.max_requests);
   return n < op.max_tokens ? n : op.max_tokens;
 }
 
 // ------------------------------------------------------------ embedding
-__device__ void task_embed(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  const OpDesc& op = a.ops[t.op];
+__device__ __forceinline__ void task_embed(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  OpRef op = op_of(a, t.op);
   if (!wait_event(a, t, task_id, sm)) return;
   const int T = active_tokens(a, op);
   for (int b = 0; b < T; b++) {
@@ -127,91 +143,112 @@ __device__ void task_embed(const KernelArgs& a, const TaskDesc& t, int task_id, 
   signal_event(a, t);
 }
 
+// Geometry of attention task (request r, split s): new tokens [t0, t0+nt),
+// pages [pb, pb+np) of the page table, cached positions [0, base), of which
+// this split reads [c0, c1).
+constexpr int kPage = 64;  // KV page size in positions (the builder accepts only this)
+
+struct AttnGeom {
+  int t0, nt, pb, np, base, c0, c1;
+};
+
+__device__ __forceinline__ AttnGeom attn_geom(const BatchMeta& m, OpRef op, int r, int s) {
+  AttnGeom g;
+  const int S = op.splits;
+  g.t0 = m.qo_indptr[r];
+  g.nt = m.qo_indptr[r + 1] - g.t0;
+  g.pb = m.kv_indptr[r];
+  g.np = m.kv_indptr[r + 1] - g.pb;
+  const int lpl = m.last_page_len[r];
+  const int seq = g.nt > 0 ? (g.np - 1) * kPage + (lpl == 0 ? kPage : lpl) : 0;
+  g.base = seq - g.nt;
+  int chunk = (g.base + S - 1) / S;
+  chunk = (chunk + 15) & ~15;
+  g.c0 = s * chunk < g.base ? s * chunk : g.base;
+  g.c1 = (s + 1) * chunk < g.base ? (s + 1) * chunk : g.base;
+  return g;
+}
+
 // ------------------------------------------------------------ GEMV family
 // Workgroup roles: waves 0..CW-1 stream weights and do the dot products; the
 // sync wave (wave CW) never loads weights, so its dependency polls and
 // activation loads never wait (vmcnt is in order) behind weight traffic.
-//   compute waves: issue stage 0 -> [X] -> stages (prefetch k+1, compute k)
-//                  -> row sums to LDS -> [O]
+//   compute waves: RING weight loads in flight -> [X] -> stream the unit range
+//                  (consume one 1 KiB unit, issue the next) -> [O]
 //   sync wave:     poll the event -> stage activations (+RMSNorm) -> [X]
 //                  -> [O] -> epilogue, stores, publish
-// Between [O] of task i and [X] of task i+1 the compute waves already have
-// task i+1's first stage in flight while the sync wave publishes task i and
-// waits for task i+1's inputs.
+// Work is cut into units of 512 elements of one weight row (one 16-byte load
+// per lane).  The RT x NC units of a staged block are split into CW equal
+// contiguous row-major ranges, one per compute wave, so every wave streams the
+// same number of bytes whatever the row count.  A wave keeps fp32 partial sums
+// for its current row and adds them into LDS slot (row + wave) when the row
+// (or its range) ends; (row, wave) pairs of one split never collide on a slot,
+// and the epilogue adds a row's slots in wave order, so results do not depend
+// on timing.  The code is kept loop-shaped and small on purpose: every task
+// type runs its straight-line code once per task, and on gfx950 fetching
+// instructions that fell out of the instruction cache costs more than the
+// arithmetic it saves to unroll them.
 enum { EPI_LIN = 0, EPI_NORM = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 constexpr int CW = PK_WAVES - 1;           // compute waves
 constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
+constexpr int RING = 8;                    // weight loads in flight per compute lane (56 KiB per CU)
+constexpr int kCpolSC1 = 16;               // buffer cache policy: agent-coherent (sc1)
 
-// A stage holds NM x RI rows x NCH chunks of 16 bytes per lane (NM*RI*NCH = 8
-// loads): a sub-block of SB = NCH * 512 elements of every row in the stage.
-// Eight loads per lane keep ~57 KB per CU in flight, about bandwidth x
-// latency; deeper prefetch only lengthens the CU's memory queue in front of
-// the latency-critical polls and activation loads.
-template <int NM, int RI, int NCH>
-struct Stage {
-  uint4 w[NM][RI][NCH];
-};
+// 128-bit agent-coherent loads of activations written by other CUs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld_sc1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSC1));
+}
 
-template <int NM, int RI, int NCH>
-__device__ __forceinline__ void load_stage(Stage<NM, RI, NCH>& s, const TaskDesc& t, int K, int wave, int lane,
-                                           int group, int sb, int R) {
+// Sync wave: rows [0, TM) of elements [k0, k0 + KB) of op.x into xs[b][KB];
+// rows b >= T are zero.  16 loads per lane in flight.
+template <int TM>
+__device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared& sm, int lane) {
+  // groups of 64 chunks (one 16-byte load per lane): group m is row m / k,
+  // chunks (m % k) * 64 + lane.  Row and group offsets are wave-uniform, so
+  // a load is one buffer load at (lane * 16 + scalar offset), and groups past
+  // the end load from beyond the buffer (zero, no memory access) into a junk
+  // LDS line: the unrolled batch has no branches.
+  const int k = KB >> 9, total = TM * k;
+  const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));  // rows >= T read as zero
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
+  const uint32_t vo = lane * 16;
+  const int row_bytes = op.x_ld * 2;
+  uint16_t* const junk = reinterpret_cast<uint16_t*>(sm.red);
+  constexpr int NB = TM == 1 ? 16 : 32;  // loads per lane in flight
+  for (int g = 0; g < total; g += NB) {
+    const int mb0 = g / k, mc0 = g - mb0 * k;
+    uint4 v[NB];
+    int rb = mb0 * row_bytes + k0 * 2, co = mc0 * 1024;
 #pragma unroll
-  for (int m = 0; m < NM; m++) {
+    for (int u = 0; u < NB; u++) {
+      const int off = g + u < total ? rb + co : 0x7ffffff0;
+      v[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, off, kCpolSC1));
+      co += 1024;
+      if (co == k * 1024) { co = 0; rb += row_bytes; }
+    }
+    int xb = mb0 * KB + mc0 * 512;
+    int xc = mc0;
 #pragma unroll
-    for (int r = 0; r < RI; r++) {
-      int row = wave + CW * (group * RI + r);
-      // SiLU op: matrix m = gate / up; linear op: row split across two segments
-      const uint16_t* W;
-      if (NM == 2) W = (m == 0 ? t.w0 : t.w1) + (size_t)row * K;
-      else W = row < t.split_row ? t.w0 + (size_t)row * K : t.w1 + (size_t)(row - t.split_row) * K;
-#pragma unroll
-      for (int j = 0; j < NCH; j++) {
-        int k = sb * (NCH * 512) + (lane + 64 * j) * 8;
-        if (row < R && k < K) s.w[m][r][j] = ldg16(W + k);
-        else s.w[m][r][j] = make_uint4(0, 0, 0, 0);
-      }
+    for (int u = 0; u < NB; u++) {
+      uint16_t* dst = g + u < total ? sm.xs + xb : junk;
+      *reinterpret_cast<uint4*>(dst + lane * 8) = v[u];
+      xb += 512;
+      if (++xc == k) { xc = 0; xb += KB - k * 512; }
     }
   }
 }
 
-template <int TM, int NM, int RI, int NCH>
-__device__ __forceinline__ void compute_stage(const Stage<NM, RI, NCH>& s, const Shared& sm, int KB, int kb_off,
-                                              int sb, int K, int lane, float (&acc)[NM][RI][TM]) {
-#pragma unroll
-  for (int j = 0; j < NCH; j++) {
-    int kl = sb * (NCH * 512) + (lane + 64 * j) * 8 - kb_off;  // element offset inside the staged block
-    if (kb_off + kl >= K) continue;
-    uint4 xv[TM];
-#pragma unroll
-    for (int b = 0; b < TM; b++) xv[b] = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + kl]);
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int r = 0; r < RI; r++) {
-        const uint4 w = s.w[m][r][j];
-#pragma unroll
-        for (int b = 0; b < TM; b++) {
-          float v = acc[m][r][b];
-          v = dot2<DT_BF16>(w.x, xv[b].x, v);
-          v = dot2<DT_BF16>(w.y, xv[b].y, v);
-          v = dot2<DT_BF16>(w.z, xv[b].z, v);
-          v = dot2<DT_BF16>(w.w, xv[b].w, v);
-          acc[m][r][b] = v;
-        }
-      }
-  }
-}
-
-// Sync wave: activations [T][kb_off .. kb_off + KB) into LDS (agent-scope
-// loads, 16 per lane in flight), RMSNorm applied when NORM
-// (x * (rsqrt(mean(x^2) + eps) * w), rounded to bf16 as rmsnorm.cuh:120-124).
-// RMSNorm weights of one sync-wave lane (K <= 4096): loaded before the poll,
-// since they never depend on the event.
+// RMSNorm weights of one sync-wave lane for K <= 4096, loaded before the poll
+// (they never depend on the event).
 struct NormRegs {
   uint4 g[8];
 };
 
-__device__ __forceinline__ void load_norm(NormRegs& nr, const OpDesc& op, int lane) {
+__device__ __forceinline__ void load_norm(NormRegs& nr, OpRef op, int lane) {
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     int c = (lane + kWave * j) * 8;
@@ -219,64 +256,44 @@ __device__ __forceinline__ void load_norm(NormRegs& nr, const OpDesc& op, int la
   }
 }
 
-template <int TM, bool NORM>
-__device__ __forceinline__ void stage_x_sync(const OpDesc& op, int T, int KB, int kb_off, Shared& sm, const NormRegs& nr,
-                                             bool have_nr) {
-  const int lane = threadIdx.x - SYNC_T0;
+// Sync wave, after staging all of K: x * (rsqrt(mean(x^2) + eps) * w) rounded
+// to bf16 (rmsnorm.cuh:120-124), in place.
+__device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, const NormRegs& nr, bool have_nr,
+                                       int lane) {
   const int K = op.K;
-  const int n8 = KB / 8;
-  const int total = TM * n8;
-  for (int i0 = 0; i0 < total; i0 += kWave * 16) {
-    uint4 v[16];
+  for (int b = 0; b < T; b++) {
+    float ss = 0.f;
+    for (int c = lane * 8; c < K; c += kWave * 8) {
+      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
+      uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int u = 0; u < 16; u++) {
-      int i = i0 + u * kWave + lane;
-      int b = i / n8, c = (i % n8) * 8;
-      v[u] = (i < total && b < T && kb_off + c < K) ? ld_agent_u128(op.x + (size_t)b * op.x_ld + kb_off + c)
-                                                     : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < 16; u++) {
-      int i = i0 + u * kWave + lane;
-      if (i < total) *reinterpret_cast<uint4*>(&sm.xs[(i / n8) * KB + (i % n8) * 8]) = v[u];
-    }
-  }
-  if constexpr (NORM) {
-    // K <= KB here (checked at build): one pass per token
-    for (int b = 0; b < TM; b++) {
-      float ss = 0.f;
-      for (int c = lane * 8; c < K; c += kWave * 8) {
-        uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
-        uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
-          ss += lo * lo + hi * hi;
-        }
+      for (int e = 0; e < 4; e++) {
+        float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
+        ss += lo * lo + hi * hi;
       }
-      ss = wave_sum(ss);
-      float r = rsqrtf(ss / (float)K + op.eps);
-      if (b >= T) continue;
-      auto norm_chunk = [&](int c, uint4 g) __attribute__((always_inline)) {
-        uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
-        uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w}, o[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          float lo = lo16<DT_BF16>(xv[e]) * (r * lo16<DT_BF16>(gv[e]));
-          float hi = hi16<DT_BF16>(xv[e]) * (r * hi16<DT_BF16>(gv[e]));
-          o[e] = pack2<DT_BF16>(lo, hi);
-        }
-        *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = make_uint4(o[0], o[1], o[2], o[3]);
-      };
+    }
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)K + op.eps);
+    for (int j = 0; lane * 8 + j * kWave * 8 < K; j++) {
+      const int c = (lane + kWave * j) * 8;
+      uint4 g;
       if (have_nr) {
+        g = nr.g[0];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          int c = (lane + kWave * j) * 8;
-          if (c < K) norm_chunk(c, nr.g[j]);
-        }
+        for (int q = 1; q < 8; q++)
+          if (j == q) g = nr.g[q];
       } else {
-        for (int c = lane * 8; c < K; c += kWave * 8) norm_chunk(c, ldg16(op.norm + c));
+        g = ldg16(op.norm + c);
       }
+      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
+      uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w}, o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float lo = lo16<DT_BF16>(xv[e]) * (r * lo16<DT_BF16>(gv[e]));
+        float hi = hi16<DT_BF16>(xv[e]) * (r * hi16<DT_BF16>(gv[e]));
+        o[e] = pack2<DT_BF16>(lo, hi);
+      }
+      *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
@@ -308,176 +325,225 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
   return __shfl(sm.flag, 0, kWave) != 0;
 }
 
+// Sum over the 64 lanes with DPP row operations (a handful of instructions,
+// no LDS crossbar); the result is read from the last lane.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_term(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_term<0xb1>(v);         // quad_perm [1,0,3,2]
+  v += dpp_term<0x4e>(v);         // quad_perm [2,3,0,1]
+  v += dpp_term<0x141>(v);        // row_half_mirror: 8-lane sums
+  v += dpp_term<0x140>(v);        // row_mirror: 16-lane sums in every lane
+  v += dpp_term<0x142, 0xa>(v);   // row_bcast:15 -> rows 1, 3
+  v += dpp_term<0x143, 0xc>(v);   // row_bcast:31 -> rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Adds a compute wave's per-token partial sums into its LDS slot and clears
+// them: a plain wave sum for one token; a reduce-scatter (10 shuffles) for 8.
+template <int TM>
+__device__ __forceinline__ void flush_acc(float (&acc)[TM], float* slot, int lane) {
+  if constexpr (TM == 1) {
+    const float v = wave_sum_dpp(acc[0]);
+    if (lane == 0) slot[0] += v;
+    acc[0] = 0.f;
+  } else {
+    static_assert(TM == 8, "token tiles of 1 or 8");
+    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8;
+    float a4[4], a2[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) a4[i] = (h32 ? acc[i + 4] : acc[i]) + __shfl_xor(h32 ? acc[i] : acc[i + 4], 32, kWave);
+#pragma unroll
+    for (int i = 0; i < 2; i++) a2[i] = (h16 ? a4[i + 2] : a4[i]) + __shfl_xor(h16 ? a4[i] : a4[i + 2], 16, kWave);
+    float v = (h8 ? a2[1] : a2[0]) + __shfl_xor(h8 ? a2[0] : a2[1], 8, kWave);
+    v += __shfl_xor(v, 4, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    v += __shfl_xor(v, 1, kWave);
+    if ((lane & 7) == 0) slot[(h32 ? 4 : 0) + (h16 ? 2 : 0) + (h8 ? 1 : 0)] += v;
+#pragma unroll
+    for (int i = 0; i < TM; i++) acc[i] = 0.f;
+  }
+}
+
+// Number of staged K blocks: the fewest equal blocks of whole 512-element
+// chunks whose activations fit the staging buffer.
+__device__ __forceinline__ int gemv_blocks(int NC, int TM) {
+  const int maxc = (XS_ELEMS / TM) >> 9;
+  int nkb = (NC + maxc - 1) / maxc;
+  while (NC % nkb) nkb++;
+  return nkb;
+}
+
 template <int TM, int EPI>
-__device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  constexpr int NM = EPI == EPI_SILU ? 2 : 1;
-  constexpr int RI = 1;
-  constexpr int NCH = 8 / NM;          // chunks per lane per matrix per stage
-  constexpr int SB = NCH * 512;        // elements per sub-block
+__device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  constexpr bool SILU = EPI == EPI_SILU;
   constexpr bool NORM = EPI != EPI_LIN;
-  const OpDesc& op = a.ops[t.op];
+  OpRef op = op_of(a, t.op);
   const int K = op.K, R = t.rows;
-  // wave index as a scalar: role branches are wave-uniform, so the register
-  // live ranges of the sync and compute paths do not overlap
+  const int RT = SILU ? 2 * R : R;                 // weight rows streamed
+  const int seg = SILU ? R : t.split_row;          // rows [0, seg) from w0, the rest from w1
+  const int NC = K >> 9;                           // 512-element chunks per row
+  const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM);
+  const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
+  const int U = RT * NCB;                          // units per block
+  // wave index as a scalar: role branches are wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const bool is_sync = wave == CW;
-  const int KB = TM == 1 ? K : (K < 4096 ? K : 4096);   // staged activation block
-  const int nkb = (K + KB - 1) / KB;
-  const int nsb = (KB + SB - 1) / SB;                     // sub-blocks per staged block
-  float* outs = reinterpret_cast<float*>(sm.outs);       // [T][R] fp32 row sums (SiLU: products)
-  const bool same_op = sm.last_op == t.op && nkb == 1;   // inputs of this op already staged
+  float* slots = reinterpret_cast<float*>(sm.outs);  // [(RT + CW) slots][TM]
+
+  // this compute wave's unit range (the same in every block)
+  const int u0 = (wave * U) / CW, u1 = ((wave + 1) * U) / CW;
+  const int n = is_sync ? 0 : u1 - u0, total = n * nkb;
+  const int row0 = u0 / NCB, c00 = u0 - row0 * NCB;
+  // load cursor: unit l_i of the wave's stream, at row l_row, chunk l_c;
+  // lrow points at lane's element of chunk 0 of that row in the current block
+  const uint16_t* const w1b = t.w1 + lane * 8;
+  auto row_ptr = [&](int row, int kb) __attribute__((always_inline)) -> const uint16_t* {
+    return (row < seg ? t.w0 + (size_t)row * K : t.w1 + (size_t)(row - seg) * K) + (size_t)kb * KB + lane * 8;
+  };
+  int l_i = 0, l_ib = 0, l_kb = 0, l_row = row0, l_c = c00;
+  const uint16_t* lrow = row_ptr(row0, 0);
+  uint4 ring[RING];
+  auto issue = [&](uint4& dst) __attribute__((always_inline)) {
+    if (l_i < total) {
+      dst = ldg16(lrow + (l_c << 9));
+      l_i++;
+      if (++l_c == NCB) {
+        l_c = 0;
+        l_row++;
+        lrow = l_row == seg ? w1b + (size_t)l_kb * KB : lrow + K;
+      }
+      if (TM > 1 && ++l_ib == n) {
+        l_ib = 0;
+        l_kb++;
+        l_row = row0;
+        l_c = c00;
+        lrow = row_ptr(row0, l_kb);
+      }
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < RING; s++) issue(ring[s]);
 
   if (is_sync) {
     // ---------------- sync wave: inputs
+    const bool same_op = sm.last_op == t.op && nkb == 1;  // this op's inputs are already staged
     int T = sm.last_T;
     if (!same_op) {
       NormRegs nr;
       const bool pre = NORM && K <= 4096;
       if (pre) load_norm(nr, op, lane);
-      bool ok = poll_event_sync(a, t, task_id, sm);
-      if (ok) {
+      if (poll_event_sync(a, t, task_id, sm)) {
         T = active_tokens(a, op);
-        stage_x_sync<TM, NORM>(op, T, KB, 0, sm, nr, pre);
+        stage_x<TM>(op, T, KB, 0, sm, lane);
+        if (NORM) norm_x(op, T, KB, sm, nr, pre, lane);
       }
     } else if (a.profile && lane == 0) {
       a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     }
+    for (int i = lane; i < (RT + CW) * TM; i += kWave) slots[i] = 0.f;
     if (lane == 0) {
       sm.last_T = T;
       sm.last_op = nkb == 1 ? t.op : -1;
     }
   }
-  // compute waves: first stage in flight before the inputs are ready
-  const int nrows_w = (!is_sync && wave < R) ? (R - wave + CW - 1) / CW : 0;
-  const int ngroups = (nrows_w + RI - 1) / RI;
-  Stage<NM, RI, NCH> cur, nxt;
-  if (ngroups > 0) load_stage<NM, RI, NCH>(cur, t, K, wave, lane, 0, 0, R);
-  __syncthreads();  // [X]: activations block 0 staged
+  __syncthreads();  // [X]: block 0 staged, slots cleared
   if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
 
-  // row groups kept live across staged blocks: only a plain linear can have
-  // K > KB (RMSNorm ops stage all of K, the builder checks it)
-  constexpr int GMAX = NORM ? 1 : 3;
-  float acc_keep[GMAX][NM][RI][TM];
+  if (is_sync) {
+    for (int kb = 1; kb < nkb; kb++) {
+      __syncthreads();  // compute waves are done with block kb - 1
+      stage_x<TM>(op, T, KB, kb * KB, sm, lane);
+      __syncthreads();  // block kb staged
+    }
+  } else if (n == 0) {
+    for (int kb = 1; kb < nkb; kb++) {
+      __syncthreads();
+      __syncthreads();
+    }
+  } else {
+    // ---------------- compute waves: stream the unit range
+    float acc[TM];
 #pragma unroll
-  for (int g = 0; g < GMAX; g++)
+    for (int b = 0; b < TM; b++) acc[b] = 0.f;
+    int row = row0, c = c00, ib = 0;
+    for (int g0 = 0; g0 < total; g0 += RING) {
 #pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int r = 0; r < RI; r++)
-#pragma unroll
-        for (int b = 0; b < TM; b++) acc_keep[g][m][r][b] = 0.f;
-
-  auto finish_group = [&](int g, float (&acc)[NM][RI][TM]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < RI; r++) {
-      int row = wave + CW * (g * RI + r);
-#pragma unroll
-      for (int b = 0; b < TM; b++) {
-        float v0 = wave_sum(acc[0][r][b]);
-        float v1 = NM == 2 ? wave_sum(acc[NM - 1][r][b]) : 0.f;
-        if (lane == 0 && row < R && b < T) {
-          float o = v0;
-          if constexpr (EPI == EPI_SILU) {
-            // silu_mul.cuh:31-40 on the bf16 gate/up results
-            float gt = round_to<DT_BF16>(v0), up = round_to<DT_BF16>(v1);
-            o = round_to<DT_BF16>(gt / (1.0f + expf(-gt))) * up;
+      for (int s = 0; s < RING; s++) {
+        if (g0 + s < total) {
+          if (TM > 1 && ib == n) {  // next staged block
+            ib = 0;
+            row = row0;
+            c = c00;
+            __syncthreads();
+            __syncthreads();
           }
-          outs[b * R + row] = o;
+          const uint4 w = ring[s];
+          issue(ring[s]);
+          const uint16_t* xb = sm.xs + (c << 9) + lane * 8;
+#pragma unroll
+          for (int b = 0; b < TM; b++) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xb + b * KB);
+            float v = acc[b];
+            v = dot2<DT_BF16>(w.x, xv.x, v);
+            v = dot2<DT_BF16>(w.y, xv.y, v);
+            v = dot2<DT_BF16>(w.z, xv.z, v);
+            v = dot2<DT_BF16>(w.w, xv.w, v);
+            acc[b] = v;
+          }
+          ++ib;
+          if (++c == NCB || ib == n) {
+            flush_acc<TM>(acc, slots + (row + wave) * TM, lane);
+            if (c == NCB) {
+              c = 0;
+              row++;
+            }
+          }
         }
       }
     }
-  };
-
-  for (int kb = 0; kb < nkb; kb++) {
-    if (kb) {
-      __syncthreads();  // compute waves are done with block kb-1
-      if (is_sync) {
-        NormRegs none;
-        stage_x_sync<TM, false>(op, T, KB, kb * KB, sm, none, false);
-      }
-      __syncthreads();  // block kb staged
-    }
-    if (is_sync) continue;
-    const int nst = ngroups * nsb;
-    for (int st = 0; st < nst; st++) {
-      int g = st / nsb, sb = kb * nsb + st % nsb;
-      int st2 = st + 1, kb2 = kb;
-      if (st2 == nst) { st2 = 0; kb2 = kb + 1; }
-      bool has_next = kb2 < nkb && ngroups > 0;
-      if (has_next) load_stage<NM, RI, NCH>(nxt, t, K, wave, lane, st2 / nsb, kb2 * nsb + st2 % nsb, R);
-      float acc[NM][RI][TM];
-      if (nkb > 1) {
-#pragma unroll
-        for (int gg = 0; gg < GMAX; gg++)
-          if (gg == g)
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-              for (int r = 0; r < RI; r++)
-#pragma unroll
-                for (int b = 0; b < TM; b++) acc[m][r][b] = acc_keep[gg][m][r][b];
-      } else if (st % nsb == 0) {
-#pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-          for (int r = 0; r < RI; r++)
-#pragma unroll
-            for (int b = 0; b < TM; b++) acc[m][r][b] = 0.f;
-      } else {
-#pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-          for (int r = 0; r < RI; r++)
-#pragma unroll
-            for (int b = 0; b < TM; b++) acc[m][r][b] = acc_keep[0][m][r][b];
-      }
-      compute_stage<TM, NM, RI, NCH>(cur, sm, KB, kb * KB, sb, K, lane, acc);
-      bool last_sb = st % nsb == nsb - 1;
-      if (nkb > 1) {
-#pragma unroll
-        for (int gg = 0; gg < GMAX; gg++)
-          if (gg == g)
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-              for (int r = 0; r < RI; r++)
-#pragma unroll
-                for (int b = 0; b < TM; b++) acc_keep[gg][m][r][b] = acc[m][r][b];
-        if (kb == nkb - 1 && last_sb) finish_group(g, acc);
-      } else if (last_sb) {
-        finish_group(g, acc);
-      } else {
-#pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-          for (int r = 0; r < RI; r++)
-#pragma unroll
-            for (int b = 0; b < TM; b++) acc_keep[0][m][r][b] = acc[m][r][b];
-      }
-      if (has_next) cur = nxt;
-    }
   }
-  __syncthreads();  // [O]: row sums of every compute wave are in LDS
+  __syncthreads();  // [O]: every partial sum is in its slot
   if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
   if (!is_sync) return;
 
   // ---------------- sync wave: epilogue, stores, publish
-  for (int i = lane; i < T * (R / 2); i += kWave) {
-    int b = i / (R / 2), p = i % (R / 2);
-    float v0 = outs[b * R + 2 * p], v1 = outs[b * R + 2 * p + 1];
-    if (EPI != EPI_SILU && (op.flags & OPF_RESIDUAL)) {
-      uint32_t rw = ld_agent_u32(op.residual + (size_t)b * op.res_ld + t.row0 + 2 * p);
-      v0 += lo16<DT_BF16>(rw);
-      v1 += hi16<DT_BF16>(rw);
-    }
-    uint32_t packed = pack2<DT_BF16>(v0, v1);
-    st_agent_u32(op.out + (size_t)b * op.out_ld + t.row0 + 2 * p, packed);
-    if (EPI == EPI_ARGMAX) {
-      outs[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
-      outs[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
+  // value of weight row j for token b: its slots, in wave order
+  auto rowval = [&](int j, int b) __attribute__((always_inline)) -> float {
+    const int wlo = ((j * NCB + 1) * CW - 1) / U, whi = ((j * NCB + NCB) * CW - 1) / U;
+    float v = 0.f;
+    for (int w = wlo; w <= whi; w++) v += slots[(j + w) * TM + b];
+    return v;
+  };
+  float* vals = &sm.attn_p[0][0][0];  // argmax: bf16-rounded logits [T][R]
+  for (int b = 0; b < T; b++) {
+    for (int p = lane; p < R / 2; p += kWave) {
+      float v0, v1;
+      if constexpr (SILU) {
+        // silu_mul.cuh:31-40 on the bf16 gate/up results
+        float g0 = round_to<DT_BF16>(rowval(2 * p, b)), g1 = round_to<DT_BF16>(rowval(2 * p + 1, b));
+        float x0 = round_to<DT_BF16>(rowval(R + 2 * p, b)), x1 = round_to<DT_BF16>(rowval(R + 2 * p + 1, b));
+        v0 = round_to<DT_BF16>(g0 / (1.0f + expf(-g0))) * x0;
+        v1 = round_to<DT_BF16>(g1 / (1.0f + expf(-g1))) * x1;
+      } else {
+        v0 = rowval(2 * p, b);
+        v1 = rowval(2 * p + 1, b);
+        if (op.flags & OPF_RESIDUAL) {
+          uint32_t rw = ld_agent_u32(op.residual + (size_t)b * op.res_ld + t.row0 + 2 * p);
+          v0 += lo16<DT_BF16>(rw);
+          v1 += hi16<DT_BF16>(rw);
+        }
+      }
+      const uint32_t packed = pack2<DT_BF16>(v0, v1);
+      st_agent_u32(op.out + (size_t)b * op.out_ld + t.row0 + 2 * p, packed);
+      if (EPI == EPI_ARGMAX) {
+        vals[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
+        vals[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
+      }
     }
   }
   if constexpr (EPI == EPI_ARGMAX) {
@@ -489,7 +555,7 @@ __device__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, S
       float best = -INFINITY;
       int bi = 0x7fffffff;
       for (int i = lane; i < lim; i += kWave) {
-        float v = outs[b * R + i];
+        float v = vals[b * R + i];
         if (v > best || (v == best && i < bi)) { best = v; bi = i; }
       }
 #pragma unroll
@@ -554,7 +620,7 @@ __device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
 
 // RoPE (rotate-half, rotary_embedding.cuh:22-81) of elements d .. d+7 of one
 // head vector `src` at position pos, rounded to bf16, packed.
-__device__ __forceinline__ uint4 rope8(const uint16_t* src, int d, int D, const OpDesc& op, int pos) {
+__device__ __forceinline__ uint4 rope8(const uint16_t* src, int d, int D, OpRef op, int pos) {
   uint4 x = ld_agent_u128(src + d);
   if (!op.cos_t) return x;
   int half = D / 2;
@@ -574,8 +640,8 @@ __device__ __forceinline__ uint4 rope8(const uint16_t* src, int d, int D, const 
 }
 
 template <int RMAX>
-__device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  const OpDesc& op = a.ops[t.op];
+__device__ __forceinline__ void task_attention_body(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  OpRef op = op_of(a, t.op);
   constexpr int D = 128;
   const int r = t.i0, h = t.i1, s = t.i2, S = op.splits;
   const int G = op.num_q_heads / op.num_kv_heads;
@@ -583,20 +649,17 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
   const BatchMeta& m = a.meta;
   // request geometry (the page table is written by the host or by the
   // previous launch's prepare_batch task)
-  const int t0 = m.qo_indptr[r], nt = m.qo_indptr[r + 1] - t0;
-  const int pb = m.kv_indptr[r], np = m.kv_indptr[r + 1] - pb;
-  const int lpl = m.last_page_len[r];
-  const int seq = nt > 0 ? (np - 1) * op.page_size + (lpl == 0 ? op.page_size : lpl) : 0;
-  const int base = seq - nt;
-  int chunk = (base + S - 1) / S;
-  chunk = (chunk + 15) & ~15;
-  const int c0 = s * chunk < base ? s * chunk : base;
-  const int c1 = (s + 1) * chunk < base ? (s + 1) * chunk : base;
+  const AttnGeom gm = attn_geom(m, op, r, s);
+  const int t0 = gm.t0, nt = gm.nt, pb = gm.pb, np = gm.np, base = gm.base, c0 = gm.c0, c1 = gm.c1;
+  if (a.profile && wave == 0) {
+    wait_vm();
+    if (lane == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
+  }
   const bool last = s == S - 1;
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
   auto cache_off = [&](int pos) __attribute__((always_inline)) -> size_t {
-    int pg = m.kv_indices[pb + pos / op.page_size];
-    return ((size_t)pg * op.page_size + pos % op.page_size) * tok_stride + (size_t)h * D;
+    int pg = m.kv_indices[pb + pos / kPage];
+    return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
   };
   const float scale = 1.4426950408889634f / sqrtf((float)D);
 
@@ -605,22 +668,43 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
   // prefetch the first block of this wave before waiting
   uint4 kf[4][4], vf[16];
   auto load_block = [&](int blk) __attribute__((always_inline)) {
-    int p0 = c0 + blk * 64;
+    // a 64-position block spans at most two pages (the builder fixes the page
+    // at kPage positions).  Both page ids are read first, so no K/V load waits
+    // on them; positions past c1 are clamped to c1 - 1 (finite data whose
+    // scores are masked), so the 32 loads issue without branches.
+    const int p0 = c0 + blk * 64;
+    const int pg0 = p0 / kPage;
+    const int idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
+    const int idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
+    if (a.profile && wave == 0) {
+      wait_vm();
+      if (lane == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+    }
+    const size_t page_elems = (size_t)kPage * tok_stride;
+    const uint16_t* kA = op.k_cache + (size_t)idA * page_elems + (size_t)h * D;
+    const uint16_t* kB = op.k_cache + (size_t)idB * page_elems + (size_t)h * D;
+    const uint16_t* vA = op.v_cache + (size_t)idA * page_elems + (size_t)h * D;
+    const uint16_t* vB = op.v_cache + (size_t)idB * page_elems + (size_t)h * D;
+    const int plast = c1 - 1 - pg0 * kPage;  // last valid in-window offset
+    const int pw0 = p0 - pg0 * kPage;        // window offset of p0
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      int p = p0 + 16 * j + lane % 16;
-      bool ok = p < c1;
-      size_t off = ok ? cache_off(p) : 0;
+      int o = min(pw0 + 16 * j + lane % 16, plast);
+      const uint16_t* src = (o >= kPage ? kB : kA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane / 16) * 8;
 #pragma unroll
-      for (int q = 0; q < 4; q++) kf[j][q] = ok ? ldg16(op.k_cache + off + 32 * q + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
+      for (int q = 0; q < 4; q++) kf[j][q] = ldg16(src + 32 * q);
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      int p = p0 + lane / 16 + 4 * i;
-      vf[i] = p < c1 ? ldg16(op.v_cache + cache_off(p) + (lane % 16) * 8) : make_uint4(0, 0, 0, 0);
+      int o = min(pw0 + lane / 16 + 4 * i, plast);
+      vf[i] = ldg16((o >= kPage ? vB : vA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane % 16) * 8);
     }
   };
   if (nt > 0 && wave < nblk && wave < CW) load_block(wave);
+  if (a.profile && wave == 0) {
+    wait_vm();
+    if (lane == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
+  }
 
   if (!wait_event(a, t, task_id, sm)) return;
   if (nt <= 0) {
@@ -805,7 +889,8 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
       st_agent(rec + rr * (D + 2) + D + 1, L);
     }
   }
-  if (arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S)) {
+  const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
+  if (merge) {
     for (int idx = threadIdx.x; idx < rows * (D / 2); idx += PK_THREADS) {
       int rr = idx / (D / 2), d = (idx % (D / 2)) * 2;
       // online merge over the splits, 8 records in flight per round trip
@@ -841,6 +926,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
       st_agent_u32(op.out + (size_t)(t0 + j) * op.out_ld + (size_t)(h * G + g) * D + d,
                    pack2<DT_BF16>(O0 * inv, O1 * inv));
     }
+    if (a.profile && threadIdx.x == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   }
   signal_event(a, t);
 }
@@ -848,7 +934,7 @@ __device__ void task_attention(const KernelArgs& a, const TaskDesc& t, int task_
 // ------------------------------------------------------------ batch manager
 // Offline-mode prepare_next_batch (persistent_kernel.cuh:169-322), run by one
 // thread; integer logic identical to the CPU restatement in the oracle.
-__device__ void task_prepare(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+__device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (!wait_event(a, t, task_id, sm)) return;
   if (threadIdx.x == 0) {
     const BatchMeta& s = a.meta;
@@ -921,8 +1007,45 @@ __device__ void task_prepare(const KernelArgs& a, const TaskDesc& t, int task_id
 }
 
 // ------------------------------------------------------------ kernel
+// ------------------------------------------------------------ task entry points
+// Each task type is its own function: the worker loop calls it with the
+// descriptor's LDS slot; the descriptor is copied into scalar registers here.
+__device__ __forceinline__ TaskDesc task_at(int slot) {
+  TaskDesc t;
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(&g_sm.tq[__builtin_amdgcn_readfirstlane(slot)]);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&t);
+#pragma unroll
+  for (int e = 0; e < (int)(sizeof(TaskDesc) / 4); e++) dst[e] = __builtin_amdgcn_readfirstlane(src[e]);
+  return t;
+}
+
+template <int TM, int EPI>
+__device__ __forceinline__ void run_gemv(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_gemv<TM, EPI>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
+template <int RMAX>
+__device__ __forceinline__ void run_attention(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_attention_body<RMAX>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
+// the multi-token variant (rare on the decode path, heavy register use) stays
+// out of line so that it cannot push the hot paths into spilling
+__device__ __attribute__((noinline)) void run_attention_large(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_attention_body<16>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
+__device__ __forceinline__ void run_embed(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_embed(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
+__device__ __forceinline__ void run_prepare(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_prepare(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
+
 __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) {
-  __shared__ Shared sm;
+  Shared& sm = g_sm;
   const int w = blockIdx.x;
   const int q0 = a.queue_offsets[w], q1 = a.queue_offsets[w + 1];
   // this worker's task descriptors move to LDS, 256 at a time
@@ -936,6 +1059,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
   };
   load_descs(q0);
   if (threadIdx.x == 0) {
+    sm.args = a;
     sm.flag = 1;
     sm.last_op = -1;
     sm.last_T = 0;
@@ -947,39 +1071,44 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       load_descs(q);
       __syncthreads();
     }
-    const int tid = a.queue[q];
-    const TaskDesc& t = sm.tq[(q - q0) % 256];
-    const OpDesc& op = a.ops[t.op];
+    const int tid = __builtin_amdgcn_readfirstlane(a.queue[q]);
+    const int slot = (q - q0) % 256;
+    OpRef op = op_of(a, sm.tq[slot].op);
     if (a.profile && threadIdx.x == 0) {
       a.profile[(size_t)tid * 8] = now_10ns();
       a.profile[(size_t)tid * 8 + 3] = (uint64_t)w;
     }
-    const int tm8 = op.max_tokens > 1;
-    const bool gemv = op.type == TASK_LINEAR || op.type == TASK_RMSNORM_LINEAR ||
-                      op.type == TASK_RMSNORM_LINEAR_SILU || op.type == TASK_RMSNORM_LINEAR_ARGMAX;
+    const int type = op.type;
+    const bool tm8 = op.max_tokens > 1;
+    const bool gemv = type == TASK_LINEAR || type == TASK_RMSNORM_LINEAR || type == TASK_RMSNORM_LINEAR_SILU ||
+                      type == TASK_RMSNORM_LINEAR_ARGMAX;
     if (!gemv && threadIdx.x == 0) sm.last_op = -1;  // attention / embed / batch tasks reuse xs
-    switch (op.type) {
-      case TASK_EMBED: task_embed(a, t, tid, sm); break;
+    switch (type) {
+      case TASK_EMBED: run_embed(slot, tid); break;
       case TASK_LINEAR:
-        if (tm8) task_gemv<8, EPI_LIN>(a, t, tid, sm); else task_gemv<1, EPI_LIN>(a, t, tid, sm);
+        if (tm8) run_gemv<8, EPI_LIN>(slot, tid); else run_gemv<1, EPI_LIN>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR:
-        if (tm8) task_gemv<8, EPI_NORM>(a, t, tid, sm); else task_gemv<1, EPI_NORM>(a, t, tid, sm);
+        if (tm8) run_gemv<8, EPI_NORM>(slot, tid); else run_gemv<1, EPI_NORM>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_SILU:
-        if (tm8) task_gemv<8, EPI_SILU>(a, t, tid, sm); else task_gemv<1, EPI_SILU>(a, t, tid, sm);
+        if (tm8) run_gemv<8, EPI_SILU>(slot, tid); else run_gemv<1, EPI_SILU>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_ARGMAX:
-        if (tm8) task_gemv<8, EPI_ARGMAX>(a, t, tid, sm); else task_gemv<1, EPI_ARGMAX>(a, t, tid, sm);
+        if (tm8) run_gemv<8, EPI_ARGMAX>(slot, tid); else run_gemv<1, EPI_ARGMAX>(slot, tid);
         break;
       case TASK_ATTENTION: {
-        const int r = t.i0;
-        const int nt = a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r];
-        if (nt * (op.num_q_heads / op.num_kv_heads) <= 4) task_attention<4>(a, t, tid, sm);
-        else task_attention<16>(a, t, tid, sm);
+        // query rows per kv head: nt * G (one MFMA row block of 4 or 16)
+        const int G = op.num_q_heads / op.num_kv_heads;
+        bool small = op.max_tokens * G <= 4;
+        if (!small) {
+          const int r = sm.tq[slot].i0;
+          small = (a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r]) * G <= 4;
+        }
+        if (small) run_attention<4>(slot, tid); else run_attention_large(slot, tid);
         break;
       }
-      case TASK_PREPARE_BATCH: task_prepare(a, t, tid, sm); break;
+      case TASK_PREPARE_BATCH: run_prepare(slot, tid); break;
       default: break;
     }
     // GEMV tasks need no trailing barrier: the next task's first LDS access

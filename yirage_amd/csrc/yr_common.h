@@ -35,13 +35,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) {
   return __uint_as_float(b16 << 16);
 }
 
-// round-to-nearest-even f32 -> bf16 bits (NaN kept quiet)
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// round-to-nearest-even f32 -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950)
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  bf16x2_cvt v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return f32x2_to_bf16x2_bits(f, 0.f) & 0xffffu; }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
   union { uint16_t u; _Float16 h; } c;
@@ -80,7 +80,8 @@ __device__ __forceinline__ float hi16(uint32_t w) { return ld_elem<DT>(w >> 16);
 
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return st_elem<DT>(lo) | (st_elem<DT>(hi) << 16);
+  if constexpr (DT == DT_BF16) return f32x2_to_bf16x2_bits(lo, hi);
+  else return st_elem<DT>(lo) | (st_elem<DT>(hi) << 16);
 }
 
 // fp32 += dot(a.xy, b.xy) on packed 16-bit pairs (v_dot2_f32_f16 / v_dot2_f32_bf16)
