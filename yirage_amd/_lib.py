@@ -9,7 +9,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libyirage_hip.so")
+# YIRAGE_HIP_LIB points at another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("YIRAGE_HIP_LIB") or os.path.join(_HERE, "libyirage_hip.so")
 
 YR_OK = 0
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64 = 940, 941, 950, 955, 965

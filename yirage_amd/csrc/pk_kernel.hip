@@ -13,6 +13,7 @@
 //    stores completed (vmcnt 0);
 //  * a bounded spin (watchdog) turns a lost dependency into an error flag the
 //    host reads back instead of a hang.
+#include <stdlib.h>
 #include <string.h>
 
 #include <vector>
@@ -57,6 +58,16 @@ __device__ __forceinline__ OpRef op_of(const KernelArgs& a, int i) {
       reinterpret_cast<uintptr_t>(a.ops))[i];
 }
 
+// Thread index behind an empty volatile asm: values derived from it are
+// recomputed inside each task instead of being hoisted out of the worker loop
+// (hoisted lane addresses stay live across every task and push the kernel
+// into scratch spills, and a spill reload is a full memory round trip).
+__device__ __forceinline__ int tix() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // ------------------------------------------------------------ protocol
 __device__ __forceinline__ bool aborted(const KernelArgs& a) {
   return __hip_atomic_load(a.meta.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -70,10 +81,10 @@ constexpr int POLL_T = (PK_WAVES - 1) * kWave;  // first lane of the sync wave (
 
 __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (t.wait_event < 0) {
-    if (a.profile && threadIdx.x == POLL_T) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    if (a.profile && tix() == POLL_T) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     return true;
   }
-  if (threadIdx.x == POLL_T) {
+  if (tix() == POLL_T) {
     const uint32_t need = (uint32_t)t.wait_count * a.epoch;
     long long spins = 0;
     int ok = 1;
@@ -100,7 +111,7 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
 __device__ void signal_event(const KernelArgs& a, const TaskDesc& t) {
   wait_vm();
   __syncthreads();
-  if (threadIdx.x == POLL_T && t.trigger_event >= 0)
+  if (tix() == POLL_T && t.trigger_event >= 0)
     __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -138,7 +149,7 @@ __device__ __forceinline__ void task_embed(const KernelArgs& a, const TaskDesc& 
     if (tok >= (uint64_t)op.vocab) tok = 0;  // out-of-range ids read row 0
     const uint16_t* src = op.table + tok * (uint64_t)op.K + t.row0;
     uint16_t* dst = op.out + (size_t)b * op.out_ld + t.row0;
-    for (int i = threadIdx.x * 8; i < t.rows; i += PK_THREADS * 8) st_agent_u128(dst + i, ldg16(src + i));
+    for (int i = tix() * 8; i < t.rows; i += PK_THREADS * 8) st_agent_u128(dst + i, ldg16(src + i));
   }
   signal_event(a, t);
 }
@@ -191,7 +202,10 @@ __device__ __forceinline__ AttnGeom attn_geom(const BatchMeta& m, OpRef op, int 
 enum { EPI_LIN = 0, EPI_NORM = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 constexpr int CW = PK_WAVES - 1;           // compute waves
 constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
-constexpr int RING = 8;                    // weight loads in flight per compute lane (56 KiB per CU)
+#ifndef YR_PK_RING
+#define YR_PK_RING 8
+#endif
+constexpr int RING = YR_PK_RING;           // weight loads in flight per compute lane (RING * 7 KiB per CU)
 constexpr int kCpolSC1 = 16;               // buffer cache policy: agent-coherent (sc1)
 
 // 128-bit agent-coherent loads of activations written by other CUs.
@@ -300,13 +314,19 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
 
 // Sync wave: one-lane event poll (the watchdog exits through sm.flag).
 __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  if (threadIdx.x == SYNC_T0) {
+  if (tix() == SYNC_T0) {
     int ok = 1;
     if (t.wait_event >= 0) {
       const uint32_t need = (uint32_t)t.wait_count * a.epoch;
       long long spins = 0;
+      const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(a.events, 0, 0x7fffffff, 0x00020000);
       for (;;) {
-        uint32_t v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t v;
+        if (a.dbg == 6) v = __hip_atomic_fetch_or(&a.events[t.wait_event], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else if (a.dbg == 7) v = __builtin_amdgcn_raw_buffer_load_b32(er, t.wait_event * 4, 0, 17);
+        else if (a.dbg == 8) v = __builtin_amdgcn_raw_buffer_load_b32(er, t.wait_event * 4, 0, 19);
+        else v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (spins == 0 && a.profile) a.profile[(size_t)task_id * 8 + 7] = now_10ns() | ((uint64_t)((need - v) & 0xfffffu) << 44);
         if ((int32_t)(v - need) >= 0) break;
         if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
         if (++spins > a.spin_limit) {
@@ -315,7 +335,10 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
           ok = 0;
           break;
         }
-        __builtin_amdgcn_s_sleep(2);
+        if (a.dbg == 1) __builtin_amdgcn_s_sleep(16);
+        else if (a.dbg == 2) __builtin_amdgcn_s_sleep(64);
+        else if (a.dbg == 3) { __builtin_amdgcn_s_sleep(127); __builtin_amdgcn_s_sleep(127); }
+        else __builtin_amdgcn_s_sleep(2);
       }
     }
     if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
@@ -389,7 +412,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
   const int U = RT * NCB;                          // units per block
   // wave index as a scalar: role branches are wave-uniform
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tix() / kWave), lane = tix() % kWave;
   const bool is_sync = wave == CW;
   float* slots = reinterpret_cast<float*>(sm.outs);  // [(RT + CW) slots][TM]
 
@@ -424,8 +447,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
   };
+  if (a.dbg != 4) {
 #pragma unroll
-  for (int s = 0; s < RING; s++) issue(ring[s]);
+    for (int s = 0; s < RING; s++) issue(ring[s]);
+  }
 
   if (is_sync) {
     // ---------------- sync wave: inputs
@@ -450,9 +475,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   }
   __syncthreads();  // [X]: block 0 staged, slots cleared
-  if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+  if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
+  if (a.dbg == 4) {
+#pragma unroll
+    for (int s = 0; s < RING; s++) issue(ring[s]);
+  }
 
   if (is_sync) {
     for (int kb = 1; kb < nkb; kb++) {
@@ -508,7 +537,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   }
   __syncthreads();  // [O]: every partial sum is in its slot
-  if (a.profile && threadIdx.x == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
+  if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
   if (!is_sync) return;
 
   // ---------------- sync wave: epilogue, stores, publish
@@ -603,8 +632,14 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   }
   wait_vm();
   if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
-  if (lane == 0 && t.trigger_event >= 0)
-    __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0 && t.trigger_event >= 0) {
+    if (a.dbg == 5) {
+      uint32_t old = __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (a.profile) a.profile[(size_t)task_id * 8 + 3] = now_10ns() + (old & 1) * 0;
+    } else {
+      __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ------------------------------------------------------------ attention
@@ -618,25 +653,49 @@ __device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
                                                  0, 0, 0);
 }
 
-// RoPE (rotate-half, rotary_embedding.cuh:22-81) of elements d .. d+7 of one
-// head vector `src` at position pos, rounded to bf16, packed.
-__device__ __forceinline__ uint4 rope8(const uint16_t* src, int d, int D, OpRef op, int pos) {
-  uint4 x = ld_agent_u128(src + d);
-  if (!op.cos_t) return x;
-  int half = D / 2;
-  int dp = d < half ? d + half : d - half;
-  uint4 y = ld_agent_u128(src + dp);
-  uint4 c = ldg16(op.cos_t + (size_t)pos * D + d), s = ldg16(op.sin_t + (size_t)pos * D + d);
-  uint32_t xv[4] = {x.x, x.y, x.z, x.w}, yv[4] = {y.x, y.y, y.z, y.w}, cv[4] = {c.x, c.y, c.z, c.w},
-           sv[4] = {s.x, s.y, s.z, s.w}, o[4];
-  float sg = d < half ? -1.f : 1.f;
+// RoPE (rotate-half, rotary_embedding.cuh:22-81) of one head vector held as
+// four 8-element chunks per lane: chunk q covers d = 32 q + 8 (lane / 16).
+// The rotate-half partner of chunk q (d +- D/2) is chunk (q + 2) % 4 of the
+// same lane, so one load per chunk suffices.  Loads and arithmetic are split
+// so that a wave can have several vectors in flight before it waits.
+struct RopeVec {
+  uint4 x[4], c[4], s[4];
+};
+// cos/sin rows of position pos (no dependency on the task's inputs)
+__device__ __forceinline__ void rope_load_tab(RopeVec& v, int D, OpRef op, int pos, bool ok, int lane) {
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    float lo = lo16<DT_BF16>(xv[e]) * lo16<DT_BF16>(cv[e]) + sg * lo16<DT_BF16>(yv[e]) * lo16<DT_BF16>(sv[e]);
-    float hi = hi16<DT_BF16>(xv[e]) * hi16<DT_BF16>(cv[e]) + sg * hi16<DT_BF16>(yv[e]) * hi16<DT_BF16>(sv[e]);
-    o[e] = pack2<DT_BF16>(lo, hi);
+  for (int q = 0; q < 4; q++) {
+    const int d = 32 * q + (lane / 16) * 8;
+    if (op.cos_t) {
+      v.c[q] = ok ? ldg16(op.cos_t + (size_t)pos * D + d) : make_uint4(0, 0, 0, 0);
+      v.s[q] = ok ? ldg16(op.sin_t + (size_t)pos * D + d) : make_uint4(0, 0, 0, 0);
+    }
   }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+// the head vector itself (written by another CU)
+__device__ __forceinline__ void rope_load_x(RopeVec& v, const uint16_t* src, bool ok, int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) v.x[q] = ok ? ld_agent_u128(src + 32 * q + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
+}
+__device__ __forceinline__ void rope_apply(const RopeVec& v, uint4 (&out)[4], OpRef op) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (!op.cos_t) {
+      out[q] = v.x[q];
+      continue;
+    }
+    const uint4 x = v.x[q], y = v.x[(q + 2) & 3], c = v.c[q], sn = v.s[q];
+    uint32_t xv[4] = {x.x, x.y, x.z, x.w}, yv[4] = {y.x, y.y, y.z, y.w}, cv[4] = {c.x, c.y, c.z, c.w},
+             sv[4] = {sn.x, sn.y, sn.z, sn.w}, o[4];
+    const float sg = q < 2 ? -1.f : 1.f;  // first half: x cos - x[d + D/2] sin
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float lo = lo16<DT_BF16>(xv[e]) * lo16<DT_BF16>(cv[e]) + sg * lo16<DT_BF16>(yv[e]) * lo16<DT_BF16>(sv[e]);
+      float hi = hi16<DT_BF16>(xv[e]) * hi16<DT_BF16>(cv[e]) + sg * hi16<DT_BF16>(yv[e]) * hi16<DT_BF16>(sv[e]);
+      o[e] = pack2<DT_BF16>(lo, hi);
+    }
+    out[q] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 template <int RMAX>
@@ -645,7 +704,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   constexpr int D = 128;
   const int r = t.i0, h = t.i1, s = t.i2, S = op.splits;
   const int G = op.num_q_heads / op.num_kv_heads;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tix() / kWave), lane = tix() % kWave;
   const BatchMeta& m = a.meta;
   // request geometry (the page table is written by the host or by the
   // previous launch's prepare_batch task)
@@ -657,10 +716,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   }
   const bool last = s == S - 1;
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
-  auto cache_off = [&](int pos) __attribute__((always_inline)) -> size_t {
-    int pg = m.kv_indices[pb + pos / kPage];
-    return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
-  };
   const float scale = 1.4426950408889634f / sqrtf((float)D);
 
   // cached positions: blocks of 64 per wave (wave w: blocks w, w + 8, ...)
@@ -701,6 +756,13 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   };
   if (nt > 0 && wave < nblk && wave < CW) load_block(wave);
+  // the page of new token lane % 16 (sync wave of the last split) does not
+  // depend on the QKV results either
+  const bool newtok = last && wave == CW;
+  const int qrow = lane % 16, qj = qrow / G, qg = qrow % G;
+  const bool qok = qrow < nt * G;
+  int pg_tok = 0;
+  if (newtok && qrow < nt) pg_tok = m.kv_indices[pb + (base + qrow) / kPage];
   if (a.profile && wave == 0) {
     wait_vm();
     if (lane == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
@@ -712,7 +774,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     return;
   }
   if (nt * G > 16 || nblk > CW) {  // beyond one MFMA row block / one block per wave
-    if (threadIdx.x == 0) {
+    if (tix() == 0) {
       __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     signal_event(a, t);
@@ -720,17 +782,51 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   }
   const uint16_t* qkv = op.x + (size_t)t0 * op.qkv_ld + (size_t)h * (G + 2) * D;
 
-  // Q fragments: row = j * G + g, k = d
+  // Q fragments: row = j * G + g, k = d.  In the last split the sync wave
+  // (which holds no cached block) also takes the new tokens: their k/v loads
+  // go out together with its q loads, and it processes them while the
+  // compute waves process the cached blocks.
   uint4 qf[4];
   {
-    int row = lane % 16, j = row / G, g = row % G;
-    bool ok = row < nt * G;
+    RopeVec qin;
+    rope_load_x(qin, qkv + (size_t)qj * op.qkv_ld + (size_t)qg * D, qok, lane);
+    rope_load_tab(qin, D, op, base + qj, qok, lane);
+    if (newtok) {
+      // new token i = lane % 16 (k, MFMA B layout) / lane / 16 + 4 i2 (v)
+      const int i = lane % 16;
+      const bool kok = i < nt;
+      RopeVec kin;
+      rope_load_x(kin, qkv + (size_t)i * op.qkv_ld + (size_t)G * D, kok, lane);
+      rope_load_tab(kin, D, op, base + i, kok, lane);
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-      qf[q] = ok ? rope8(qkv + (size_t)j * op.qkv_ld + (size_t)g * D, 32 * q + (lane / 16) * 8, D, op, base + j)
-                 : make_uint4(0, 0, 0, 0);
+      for (int i2 = 0; i2 < 16; i2++) {
+        const int iv = lane / 16 + 4 * i2;
+        vf[i2] = iv < nt ? ld_agent_u128(qkv + (size_t)iv * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
+                         : make_uint4(0, 0, 0, 0);
+      }
+      rope_apply(kin, kf[0], op);
+      auto tok_off = [&](int pg, int pos) __attribute__((always_inline)) -> size_t {
+        return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
+      };
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        kf[1][q] = kf[2][q] = kf[3][q] = make_uint4(0, 0, 0, 0);
+        if (kok) *reinterpret_cast<uint4*>(op.k_cache + tok_off(pg_tok, base + i) + 32 * q + (lane / 16) * 8) = kf[0][q];
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < 16; i2++) {
+        const int iv = lane / 16 + 4 * i2;
+        const int pgv = __shfl(pg_tok, iv & 15, kWave);
+        if (iv < nt) *reinterpret_cast<uint4*>(op.v_cache + tok_off(pgv, base + iv) + (lane % 16) * 8) = vf[i2];
+      }
+    }
+    rope_apply(qin, qf, op);
   }
 
+  if (a.dbg == 9 && a.profile && wave == 0) {
+    wait_vm();
+    if (lane == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+  }
   // per-wave online softmax state for rows 4*(lane/16)+i
   float m_i[4], l_i[4];
   float o_acc[RMAX][8];  // [query row][8 dims of this lane's d-chunk]
@@ -783,6 +879,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    if (a.dbg == 9 && a.profile && wave == 0 && lane == 0) a.profile[(size_t)task_id * 8 + 3] = now_10ns();
     // O[row][d] = O * alpha + sum_p P[row][p] V[p][d]; lane: d-chunk lane%16, positions lane/16 + 4i
 #pragma unroll
     for (int rr = 0; rr < RMAX; rr++) {
@@ -814,32 +911,10 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   // a split never holds more than CW * 64 cached positions)
   if (wave < nblk && wave < CW) process(c0 + wave * 64, (c1 - c0) - wave * 64 < 64 ? (c1 - c0) - wave * 64 : 64, false);
 
-  // new tokens (last split, wave 0): k/v from qkv, RoPE on k, append to cache
-  if (last && wave == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      int i = 16 * j + lane % 16;
-      bool ok = j == 0 && i < nt;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        int d = 32 * q + (lane / 16) * 8;
-        uint4 kv = ok ? rope8(qkv + (size_t)i * op.qkv_ld + (size_t)G * D, d, D, op, base + i) : make_uint4(0, 0, 0, 0);
-        kf[j][q] = kv;
-        if (ok) *reinterpret_cast<uint4*>(op.k_cache + cache_off(base + i) + d) = kv;
-      }
-    }
-#pragma unroll
-    for (int i2 = 0; i2 < 16; i2++) {
-      int i = lane / 16 + 4 * i2;
-      bool ok = i < nt;
-      uint4 vv = ok ? ld_agent_u128(qkv + (size_t)i * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
-                    : make_uint4(0, 0, 0, 0);
-      vf[i2] = vv;
-      if (ok) *reinterpret_cast<uint4*>(op.v_cache + cache_off(base + i) + (lane % 16) * 8) = vv;
-    }
-    process(base, nt, true);
-  }
+  // new tokens: causal block on the sync wave of the last split
+  if (newtok) process(base, nt, true);
 
+  if (a.dbg == 9 && a.profile && wave == 0 && lane == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
   // sum o over the 4 lane groups (positions lane/16 + 4 i), then merge the
   // 8 waves: per row, (m, l) in LDS, o through LDS (xs reused as float)
 #pragma unroll
@@ -871,7 +946,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   const int rows = nt * G;
   float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * kAttnRecFloats;
   float* rec = rec_base + (size_t)s * kAttnRecFloats;
-  for (int idx = threadIdx.x; idx < rows * D; idx += PK_THREADS) {
+  for (int idx = tix(); idx < rows * D; idx += PK_THREADS) {
     int rr = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
@@ -889,44 +964,79 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       st_agent(rec + rr * (D + 2) + D + 1, L);
     }
   }
+  if (a.dbg == 9 && a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
   const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
+  if (a.dbg == 9 && a.profile && tix() == 0 && !merge) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   if (merge) {
-    for (int idx = threadIdx.x; idx < rows * (D / 2); idx += PK_THREADS) {
-      int rr = idx / (D / 2), d = (idx % (D / 2)) * 2;
-      // online merge over the splits, 8 records in flight per round trip
-      float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
-      for (int s0 = 0; s0 < S; s0 += 8) {
-        float mv[8], lv[8], o0[8], o1[8];
+    // Online-softmax merge of the S split records in one memory round trip:
+    // every (m, l) pair and every o chunk is loaded before anything waits.
+    // Thread -> (unit = query row x 4-float d chunk, lane j of P); lane j
+    // takes splits j, j + P, ...; the P partial states combine through LDS.
+    float* ml = reinterpret_cast<float*>(sm.xs);           // [S][rows][2] (m, l)
+    float* part = ml + 2 * kAttnRecRows * 256;             // [unit][P][6]: M, L, o0..o3
+    const int units = rows * (D / 4);
+    const int P = PK_THREADS / units;                      // >= 1 (rows <= 16)
+    const int tid = tix();
+    for (int i = tid; i < rows * S; i += PK_THREADS) {
+      const float* rc = rec_base + (size_t)(i / rows) * kAttnRecFloats + (i % rows) * (D + 2) + D;
+      ml[2 * i] = ld_agent(rc);
+      ml[2 * i + 1] = ld_agent(rc + 1);
+    }
+    const int u = tid / P, j = tid % P;
+    const int rr = u / (D / 4), d4 = (u % (D / 4)) * 4;
+    const bool act = u < units;
+    float4 ob[8];
+    const int ns = act ? (S - j + P - 1) / P : 0;           // splits of this thread
+    // first batch of o chunks in flight with the (m, l) loads
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-          if (s0 + u < S) {
-            const float* rc = rec_base + (size_t)(s0 + u) * kAttnRecFloats + rr * (D + 2);
-            mv[u] = ld_agent(rc + D);
-            lv[u] = ld_agent(rc + D + 1);
-            o0[u] = ld_agent(rc + d);
-            o1[u] = ld_agent(rc + d + 1);
-          } else {
-            mv[u] = -INFINITY; lv[u] = 0.f; o0[u] = 0.f; o1[u] = 0.f;
+    for (int q = 0; q < 8; q++)
+      ob[q] = q < ns ? ld_agent4(rec_base + (size_t)(j + q * P) * kAttnRecFloats + rr * (D + 2) + d4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    __syncthreads();
+    float M = -INFINITY, L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (act) {
+      for (int s2 = j; s2 < S; s2 += P) M = fmaxf(M, ml[2 * (s2 * rows + rr)]);
+      for (int q0 = 0; q0 < ns; q0 += 8) {
+        if (q0 > 0) {
+#pragma unroll
+          for (int q = 0; q < 8; q++)
+            ob[q] = q0 + q < ns ? ld_agent4(rec_base + (size_t)(j + (q0 + q) * P) * kAttnRecFloats + rr * (D + 2) + d4)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          if (q0 + q < ns) {
+            const int s2 = j + (q0 + q) * P;
+            const float ms = ml[2 * (s2 * rows + rr)];
+            const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            L += ml[2 * (s2 * rows + rr) + 1] * f;
+            O.x += ob[q].x * f; O.y += ob[q].y * f; O.z += ob[q].z * f; O.w += ob[q].w * f;
           }
         }
-        float mb = M;
-#pragma unroll
-        for (int u = 0; u < 8; u++) mb = fmaxf(mb, mv[u]);
-        float f0 = M == -INFINITY ? 0.f : exp2f(M - mb);
-        L *= f0; O0 *= f0; O1 *= f0;
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          float f = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mb);
-          L += lv[u] * f; O0 += o0[u] * f; O1 += o1[u] * f;
-        }
-        M = mb;
       }
-      float inv = L > 0.f ? 1.f / L : 0.f;
-      int j = rr / G, g = rr % G;
-      st_agent_u32(op.out + (size_t)(t0 + j) * op.out_ld + (size_t)(h * G + g) * D + d,
-                   pack2<DT_BF16>(O0 * inv, O1 * inv));
+      float* pp = part + (size_t)(u * P + j) * 6;
+      pp[0] = M; pp[1] = L; pp[2] = O.x; pp[3] = O.y; pp[4] = O.z; pp[5] = O.w;
     }
-    if (a.profile && threadIdx.x == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
+    __syncthreads();
+    if (act && j == 0) {
+      const float* pp = part + (size_t)u * P * 6;
+      float Mt = -INFINITY;
+      for (int q = 0; q < P; q++) Mt = fmaxf(Mt, pp[q * 6]);
+      float Lt = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+      for (int q = 0; q < P; q++) {
+        const float f = pp[q * 6] == -INFINITY ? 0.f : exp2f(pp[q * 6] - Mt);
+        Lt += pp[q * 6 + 1] * f;
+        o0 += pp[q * 6 + 2] * f; o1 += pp[q * 6 + 3] * f; o2 += pp[q * 6 + 4] * f; o3 += pp[q * 6 + 5] * f;
+      }
+      const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+      const int jt = rr / G, g = rr % G;
+      uint16_t* dst = op.out + (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
+      const uint32_t lo = pack2<DT_BF16>(o0 * inv, o1 * inv), hi = pack2<DT_BF16>(o2 * inv, o3 * inv);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), (uint64_t)lo | ((uint64_t)hi << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   }
   signal_event(a, t);
 }
@@ -936,7 +1046,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
 // thread; integer logic identical to the CPU restatement in the oracle.
 __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (!wait_event(a, t, task_id, sm)) return;
-  if (threadIdx.x == 0) {
+  if (tix() == 0) {
     const BatchMeta& s = a.meta;
     const int MR = s.max_requests, MT = s.max_tokens, MP = s.max_pages, PS = s.page_size, MSL = s.max_seq_len;
     int head = *s.page_queue_head, tail = *s.page_queue_tail;
@@ -1287,6 +1397,7 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream) {
   a.num_workers = h->num_workers;
   a.spin_limit = h->spin_limit;
   a.profile = h->profile;
+  a.dbg = getenv("YR_PK_DBG") ? atoi(getenv("YR_PK_DBG")) : 0;
   void* args[] = {&a};
   hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
                                             dim3(PK_THREADS), args, 0, st);

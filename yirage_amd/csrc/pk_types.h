@@ -107,6 +107,7 @@ struct KernelArgs {
   uint32_t epoch;            // 1, 2, 3, ... per launch
   int num_workers;
   long long spin_limit;      // watchdog: polls before a wait gives up
+  int dbg;
 };
 
 }  // namespace pk
