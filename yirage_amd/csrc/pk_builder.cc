@@ -135,7 +135,13 @@ void Graph::build(const char* text) {
     t.ptr = (uint64_t)kv.second["ptr"].f64();
     for (size_t i = 0; i < kv.second["dims"].size(); i++) t.dims.push_back(kv.second["dims"][i].i64());
     t.dtype = (int)kv.second["dtype"].i64();
+    t.ll = kv.second.has("ll") && kv.second["ll"].i64(0) != 0;
     if (!dtype_bytes(t.dtype)) throw std::runtime_error("tensor " + t.name + ": unsupported dtype");
+    if (t.ll) {
+      if (t.dtype != YR_DTYPE_BF16 || t.dims.size() != 2 || t.dims[1] % 4)
+        throw std::runtime_error("link tensor " + t.name + " must be 2-D bf16 with columns % 4 == 0");
+      link_buffers.push_back({t.ptr, (uint64_t)(t.dims[0] * t.dims[1] * 4)});
+    }
     tensor_index[t.name] = (int)tensors.size();
     tensors.push_back(t);
   }
@@ -147,6 +153,16 @@ void Graph::build(const char* text) {
   if (opsv.kind != json::Value::Arr || opsv.size() == 0) throw std::runtime_error("'ops' must be a non-empty array");
   int ticket_next = 0;
   int64_t scratch_next = 0;
+  if (opsv.size() > (size_t)kMaxLinkOps) throw std::runtime_error("too many ops for the link-tensor tag");
+  // op that last wrote each link tensor (readers check its tag)
+  std::vector<int> link_writer(tensors.size(), -1);
+  auto link_read = [&](int tensor, int& src) -> bool {
+    if (!tensors[tensor].ll) return false;
+    if (link_writer[tensor] < 0)
+      throw std::runtime_error("link tensor " + tensors[tensor].name + " is read before any op writes it");
+    src = link_writer[tensor];
+    return true;
+  };
   for (size_t oi = 0; oi < opsv.size(); oi++) {
     const json::Value& o = opsv[oi];
     const std::string type = o["type"].s();
@@ -174,6 +190,10 @@ void Graph::build(const char* text) {
       d.tokens_in = (const int64_t*)tensors[tok].ptr;
       d.table = (const uint16_t*)T.ptr;
       d.out = (uint16_t*)tensors[out].ptr;
+      if (tensors[out].ll) {
+        d.flags |= OPF_OUT_LL;
+        link_writer[out] = (int)ops.size();
+      }
       int nt = (int)o["tasks"].i64(1);
       int per = (d.N + nt - 1) / nt;
       per = (per + 7) & ~7;
@@ -198,6 +218,7 @@ void Graph::build(const char* text) {
       d.K = (int)X.dims[1];
       d.x_ld = d.K;
       d.x = (const uint16_t*)X.ptr;
+      if (link_read(x, d.x_src)) d.flags |= OPF_X_LL;
       d.max_tokens = cfg.max_tokens;
       if (X.dims[0] < cfg.max_tokens) throw std::runtime_error("activation rows < max_tokens");
       std::vector<Seg> segs = read_segments(*this, o["weight"]);
@@ -209,7 +230,8 @@ void Graph::build(const char* text) {
       d.out_ld = (int)OT.dims[1];
       int col0 = (int)o["out_col0"].i64(0);
       if (col0 + d.N > d.out_ld) throw std::runtime_error("linear output columns exceed the out tensor");
-      d.out = (uint16_t*)(OT.ptr + (uint64_t)col0 * 2);
+      d.out = (uint16_t*)(OT.ptr + (uint64_t)col0 * (OT.ll ? 4 : 2));
+      if (OT.ll && amax) throw std::runtime_error("argmax logits must be a plain tensor");
       if (norm) {
         int nw = ptr_tensor(*this, o, "norm");
         d.norm = (const uint16_t*)tensors[nw].ptr;
@@ -219,6 +241,7 @@ void Graph::build(const char* text) {
       int res = ptr_tensor(*this, o, "residual", true);
       if (res >= 0) {
         d.flags |= OPF_RESIDUAL;
+        if (link_read(res, d.res_src)) d.flags |= OPF_RES_LL;
         d.residual = (const uint16_t*)tensors[res].ptr;
         d.res_ld = (int)tensors[res].dims[1];
         info.reads.push_back({res, 0, d.N, 1});
@@ -275,6 +298,10 @@ void Graph::build(const char* text) {
       }
       info.reads.push_back({x, 0, d.K});
       info.writes.push_back({out, col0, col0 + d.N, 1});
+      if (OT.ll) {
+        d.flags |= OPF_OUT_LL;
+        link_writer[out] = (int)ops.size();
+      }
     } else if (type == "attention") {
       d.type = TASK_ATTENTION;
       int qkv = ptr_tensor(*this, o, "qkv"), out = ptr_tensor(*this, o, "out");
@@ -297,8 +324,13 @@ void Graph::build(const char* text) {
       if (d.qkv_ld != (d.num_q_heads + 2 * d.num_kv_heads) * d.head_dim)
         throw std::runtime_error("attention: qkv width must be (Hq + 2 Hkv) * head_dim");
       d.x = (const uint16_t*)Q.ptr;
+      if (link_read(qkv, d.x_src)) d.flags |= OPF_X_LL;
       d.out = (uint16_t*)tensors[out].ptr;
       d.out_ld = (int)tensors[out].dims[1];
+      if (tensors[out].ll) {
+        d.flags |= OPF_OUT_LL;
+        link_writer[out] = (int)ops.size();
+      }
       const Tensor& KC = tensors[kc];
       if (cfg.page_size != 64) throw std::runtime_error("attention: page_size must be 64");
       if (KC.dims.size() != 4 || KC.dims[1] != cfg.page_size || KC.dims[2] != d.num_kv_heads || KC.dims[3] != d.head_dim)

@@ -21,6 +21,7 @@ struct Tensor {
   uint64_t ptr = 0;
   std::vector<int64_t> dims;
   int dtype = 0;
+  bool ll = false;  // link tensor: [rows][cols] tagged words, 4 bytes per element
 };
 
 // Column range [c0, c1) of a tensor (all rows).  scope: 0 = whole op range,
@@ -61,6 +62,7 @@ struct Graph {
   std::vector<std::vector<int>> queues;
   int num_tickets = 0;
   int64_t scratch_floats = 0;
+  std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // (device address, bytes), cleared on epoch re-base
 
   void build(const char* json_text);
   int tensor_id(const std::string& name) const;

@@ -13,7 +13,6 @@
 //    stores completed (vmcnt 0);
 //  * a bounded spin (watchdog) turns a lost dependency into an error flag the
 //    host reads back instead of a hang.
-#include <stdlib.h>
 #include <string.h>
 
 #include <vector>
@@ -108,8 +107,10 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
 }
 
 // Publish completion: every thread's stores are complete, then one arrival.
-__device__ void signal_event(const KernelArgs& a, const TaskDesc& t) {
-  wait_vm();
+// Outputs that are link tensors need not be complete: their readers check
+// tags, so only the other stores of the task are waited for.
+__device__ void signal_event(const KernelArgs& a, const TaskDesc& t, bool link_out = false) {
+  if (!link_out) wait_vm();
   __syncthreads();
   if (tix() == POLL_T && t.trigger_event >= 0)
     __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -133,6 +134,79 @@ __device__ __forceinline__ void st_agent_u128(void* p, uint4 v) {
   __hip_atomic_store(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+
+// ------------------------------------------------------------ link tensors
+__device__ __forceinline__ uint32_t link_tag(const KernelArgs& a, int op) {
+  return (a.epoch << kLinkOpBits) | (uint32_t)op;
+}
+// store the bf16 pair `pair` at (even) element `e` of a link tensor
+__device__ __forceinline__ void link_store(uint16_t* base, size_t e, uint32_t pair, uint32_t tag) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(base) + e / 2, (uint64_t)pair | ((uint64_t)tag << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A word that still carries another tag is re-read until it matches; the
+// spin shares the watchdog of event waits.  Returns false after a timeout /
+// abort (the caller's data is then garbage, and the status flag is set).
+__device__ __forceinline__ bool link_spin(const KernelArgs& a, const uint64_t* w, uint32_t tag, uint64_t& v) {
+  long long spins = 0;
+  for (;;) {
+    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)(v >> 32) == tag) return true;
+    if ((spins & 255) == 255 && aborted(a)) return false;
+    if (++spins > a.spin_limit) {
+      __hip_atomic_store(a.meta.status + 2, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+// the bf16 pair at (even) element e, waiting for this launch's producer
+__device__ __forceinline__ uint32_t link_load(const KernelArgs& a, const uint16_t* base, size_t e, uint32_t tag) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(base) + e / 2;
+  uint64_t v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((uint32_t)(v >> 32) != tag) link_spin(a, w, tag, v);
+  return (uint32_t)v;
+}
+// Eight elements (e % 8 == 0) of a link tensor as two 16-byte loads; issue
+// several with link8_issue before completing any with link8_take.
+struct Link8 {
+  uint4 w0, w1;  // words (pair, tag) x 2 each
+};
+__device__ __forceinline__ Link8 link8_issue(const uint16_t* base, size_t e) {
+  const uint16_t* p = base + 2 * e;  // 4 bytes per element
+  Link8 r;
+  r.w0 = ld_agent_u128(p);
+  r.w1 = ld_agent_u128(p + 8);
+  return r;
+}
+__device__ __forceinline__ bool link8_ok(const Link8& r, uint32_t tag) {
+  return r.w0.y == tag && r.w0.w == tag && r.w1.y == tag && r.w1.w == tag;
+}
+__device__ __forceinline__ uint4 link8_data(const Link8& r) { return make_uint4(r.w0.x, r.w0.z, r.w1.x, r.w1.z); }
+// One step of a wave-level retry loop over stale link words: false once the
+// watchdog fired or the launch was aborted (status flag set).
+__device__ __forceinline__ bool link_retry(const KernelArgs& a, long long& spins) {
+  if ((spins & 255) == 255 && aborted(a)) return false;
+  if (++spins > a.spin_limit) {
+    __hip_atomic_store(a.meta.status + 2, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
+  }
+  __builtin_amdgcn_s_sleep(2);
+  return true;
+}
+// eight elements of either kind of tensor (plain: one agent-coherent load)
+__device__ __forceinline__ Link8 act8_issue(bool link, const uint16_t* base, size_t e) {
+  if (link) return link8_issue(base, e);
+  Link8 r;
+  r.w0 = ld_agent_u128(base + e);
+  r.w1 = make_uint4(0, 0, 0, 0);
+  return r;
+}
+__device__ __forceinline__ bool act8_ok(bool link, const Link8& r, uint32_t tag) { return !link || link8_ok(r, tag); }
+__device__ __forceinline__ uint4 act8_data(bool link, const Link8& r) { return link ? link8_data(r) : r.w0; }
+
 __device__ __forceinline__ int active_tokens(const KernelArgs& a, OpRef op) {
   int n = (int)ld_agent_u32(a.meta.qo_indptr + a.meta.max_requests);
   return n < op.max_tokens ? n : op.max_tokens;
@@ -148,10 +222,22 @@ __device__ __forceinline__ void task_embed(const KernelArgs& a, const TaskDesc& 
                                                __HIP_MEMORY_SCOPE_AGENT);
     if (tok >= (uint64_t)op.vocab) tok = 0;  // out-of-range ids read row 0
     const uint16_t* src = op.table + tok * (uint64_t)op.K + t.row0;
-    uint16_t* dst = op.out + (size_t)b * op.out_ld + t.row0;
-    for (int i = tix() * 8; i < t.rows; i += PK_THREADS * 8) st_agent_u128(dst + i, ldg16(src + i));
+    if (op.flags & OPF_OUT_LL) {
+      const uint32_t tag = link_tag(a, t.op);
+      const size_t e0 = (size_t)b * op.out_ld + t.row0;
+      for (int i = tix() * 8; i < t.rows; i += PK_THREADS * 8) {
+        const uint4 v = ldg16(src + i);
+        link_store(op.out, e0 + i, v.x, tag);
+        link_store(op.out, e0 + i + 2, v.y, tag);
+        link_store(op.out, e0 + i + 4, v.z, tag);
+        link_store(op.out, e0 + i + 6, v.w, tag);
+      }
+    } else {
+      uint16_t* dst = op.out + (size_t)b * op.out_ld + t.row0;
+      for (int i = tix() * 8; i < t.rows; i += PK_THREADS * 8) st_agent_u128(dst + i, ldg16(src + i));
+    }
   }
-  signal_event(a, t);
+  signal_event(a, t, (op.flags & OPF_OUT_LL) != 0);
 }
 
 // Geometry of attention task (request r, split s): new tokens [t0, t0+nt),
@@ -256,6 +342,39 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
   }
 }
 
+// Sync wave, link-tensor input (batch-1 graphs only): elements [k0, k0 + KB)
+// of row 0 of op.x into xs[0][KB].  A lane loads chunks of four elements (one
+// 16-byte buffer load = two tagged words, each single-copy atomic), 24 chunks
+// in flight; a batch is re-read until every word carries the tag of this
+// launch's producing op.
+__device__ __forceinline__ void stage_x_link(const KernelArgs& a, OpRef op, int KB, int k0, Shared& sm, int lane) {
+  const uint32_t tag = link_tag(a, op.x_src);
+  const int total = KB >> 2;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x) + 2 * k0, 0, total * 16, 0x00020000);
+  constexpr int NB = 24;
+  for (int g0 = 0; g0 < total; g0 += kWave * NB) {
+    uint4 v[NB];
+    long long spins = 0;
+    for (;;) {
+#pragma unroll
+      for (int u = 0; u < NB; u++)  // chunks past the end read as zero
+        v[u] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(g0 + u * kWave + lane) * 16u, 0, kCpolSC1));
+      bool stale = false;
+#pragma unroll
+      for (int u = 0; u < NB; u++)
+        if (g0 + u * kWave + lane < total) stale |= v[u].y != tag || v[u].w != tag;
+      if (!__any(stale) || !link_retry(a, spins)) break;
+    }
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+      const int c = g0 + u * kWave + lane;
+      if (c < total) *reinterpret_cast<uint2*>(sm.xs + c * 4) = make_uint2(v[u].x, v[u].z);
+    }
+  }
+}
+
 // RMSNorm weights of one sync-wave lane for K <= 4096, loaded before the poll
 // (they never depend on the event).
 struct NormRegs {
@@ -319,13 +438,8 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
     if (t.wait_event >= 0) {
       const uint32_t need = (uint32_t)t.wait_count * a.epoch;
       long long spins = 0;
-      const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(a.events, 0, 0x7fffffff, 0x00020000);
       for (;;) {
-        uint32_t v;
-        if (a.dbg == 6) v = __hip_atomic_fetch_or(&a.events[t.wait_event], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else if (a.dbg == 7) v = __builtin_amdgcn_raw_buffer_load_b32(er, t.wait_event * 4, 0, 17);
-        else if (a.dbg == 8) v = __builtin_amdgcn_raw_buffer_load_b32(er, t.wait_event * 4, 0, 19);
-        else v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (spins == 0 && a.profile) a.profile[(size_t)task_id * 8 + 7] = now_10ns() | ((uint64_t)((need - v) & 0xfffffu) << 44);
         if ((int32_t)(v - need) >= 0) break;
         if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
@@ -335,17 +449,14 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
           ok = 0;
           break;
         }
-        if (a.dbg == 1) __builtin_amdgcn_s_sleep(16);
-        else if (a.dbg == 2) __builtin_amdgcn_s_sleep(64);
-        else if (a.dbg == 3) { __builtin_amdgcn_s_sleep(127); __builtin_amdgcn_s_sleep(127); }
-        else __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(2);
       }
     }
     if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
   }
   __builtin_amdgcn_wave_barrier();
-  return __shfl(sm.flag, 0, kWave) != 0;
+  return __builtin_amdgcn_readfirstlane(sm.flag) != 0;  // lane 0 wrote it; LDS ops of a wave are in order
 }
 
 // Sum over the 64 lanes with DPP row operations (a handful of instructions,
@@ -447,10 +558,8 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
   };
-  if (a.dbg != 4) {
 #pragma unroll
-    for (int s = 0; s < RING; s++) issue(ring[s]);
-  }
+  for (int s = 0; s < RING; s++) issue(ring[s]);
 
   if (is_sync) {
     // ---------------- sync wave: inputs
@@ -460,9 +569,12 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       NormRegs nr;
       const bool pre = NORM && K <= 4096;
       if (pre) load_norm(nr, op, lane);
-      if (poll_event_sync(a, t, task_id, sm)) {
+      // a link input is validated word by word: no event poll (measured
+      // faster than polling the producers' counter first)
+      if ((op.flags & OPF_X_LL) || poll_event_sync(a, t, task_id, sm)) {
         T = active_tokens(a, op);
-        stage_x<TM>(op, T, KB, 0, sm, lane);
+        if (TM == 1 && (op.flags & OPF_X_LL)) stage_x_link(a, op, KB, 0, sm, lane);
+        else stage_x<TM>(op, T, KB, 0, sm, lane);
         if (NORM) norm_x(op, T, KB, sm, nr, pre, lane);
       }
     } else if (a.profile && lane == 0) {
@@ -478,15 +590,12 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
-  if (a.dbg == 4) {
-#pragma unroll
-    for (int s = 0; s < RING; s++) issue(ring[s]);
-  }
 
   if (is_sync) {
     for (int kb = 1; kb < nkb; kb++) {
       __syncthreads();  // compute waves are done with block kb - 1
-      stage_x<TM>(op, T, KB, kb * KB, sm, lane);
+      if (TM == 1 && (op.flags & OPF_X_LL)) stage_x_link(a, op, KB, kb * KB, sm, lane);
+      else stage_x<TM>(op, T, KB, kb * KB, sm, lane);
       __syncthreads();  // block kb staged
     }
   } else if (n == 0) {
@@ -562,13 +671,17 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         v0 = rowval(2 * p, b);
         v1 = rowval(2 * p + 1, b);
         if (op.flags & OPF_RESIDUAL) {
-          uint32_t rw = ld_agent_u32(op.residual + (size_t)b * op.res_ld + t.row0 + 2 * p);
+          const size_t re = (size_t)b * op.res_ld + t.row0 + 2 * p;
+          const uint32_t rw = op.flags & OPF_RES_LL ? link_load(a, op.residual, re, link_tag(a, op.res_src))
+                                                    : ld_agent_u32(op.residual + re);
           v0 += lo16<DT_BF16>(rw);
           v1 += hi16<DT_BF16>(rw);
         }
       }
       const uint32_t packed = pack2<DT_BF16>(v0, v1);
-      st_agent_u32(op.out + (size_t)b * op.out_ld + t.row0 + 2 * p, packed);
+      const size_t oe = (size_t)b * op.out_ld + t.row0 + 2 * p;
+      if (op.flags & OPF_OUT_LL) link_store(op.out, oe, packed, link_tag(a, t.op));
+      else st_agent_u32(op.out + oe, packed);
       if (EPI == EPI_ARGMAX) {
         vals[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
         vals[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
@@ -630,15 +743,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
   }
-  wait_vm();
+  if (!(op.flags & OPF_OUT_LL)) wait_vm();  // link outputs are checked by their readers
   if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   if (lane == 0 && t.trigger_event >= 0) {
-    if (a.dbg == 5) {
-      uint32_t old = __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (a.profile) a.profile[(size_t)task_id * 8 + 3] = now_10ns() + (old & 1) * 0;
-    } else {
-      __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -671,11 +779,6 @@ __device__ __forceinline__ void rope_load_tab(RopeVec& v, int D, OpRef op, int p
       v.s[q] = ok ? ldg16(op.sin_t + (size_t)pos * D + d) : make_uint4(0, 0, 0, 0);
     }
   }
-}
-// the head vector itself (written by another CU)
-__device__ __forceinline__ void rope_load_x(RopeVec& v, const uint16_t* src, bool ok, int lane) {
-#pragma unroll
-  for (int q = 0; q < 4; q++) v.x[q] = ok ? ld_agent_u128(src + 32 * q + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
 }
 __device__ __forceinline__ void rope_apply(const RopeVec& v, uint4 (&out)[4], OpRef op) {
 #pragma unroll
@@ -768,7 +871,8 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     if (lane == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
   }
 
-  if (!wait_event(a, t, task_id, sm)) return;
+  // a link-tensor qkv is validated word by word below: no event wait
+  if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
   if (nt <= 0) {
     signal_event(a, t);
     return;
@@ -780,7 +884,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     signal_event(a, t);
     return;
   }
-  const uint16_t* qkv = op.x + (size_t)t0 * op.qkv_ld + (size_t)h * (G + 2) * D;
 
   // Q fragments: row = j * G + g, k = d.  In the last split the sync wave
   // (which holds no cached block) also takes the new tokens: their k/v loads
@@ -788,22 +891,62 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   // compute waves process the cached blocks.
   uint4 qf[4];
   {
+    // element offsets into qkv (plain or link tensor): row t0 + j, head column
+    const bool lk = (op.flags & OPF_X_LL) != 0;
+    const uint32_t xtag = lk ? link_tag(a, op.x_src) : 0u;
+    const size_t e_grp = (size_t)t0 * op.qkv_ld + (size_t)h * (G + 2) * D;
+    const size_t e_q = e_grp + (size_t)qj * op.qkv_ld + (size_t)qg * D;
+    const Link8 z8 = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    // The sync wave of the last split holds no cached block, so the raw
+    // words of the new tokens' k / v land in its kf / vf registers.
+    Link8 qr[4];
+    long long spins = 0;
+    for (;;) {  // all loads in flight at once; re-read if any word is stale
+#pragma unroll
+      for (int q = 0; q < 4; q++) qr[q] = qok ? act8_issue(lk, op.x, e_q + 32 * q + (lane / 16) * 8) : z8;
+      bool stale = false;
+#pragma unroll
+      for (int q = 0; q < 4; q++) stale |= qok && !act8_ok(lk, qr[q], xtag);
+      if (newtok) {
+        // new token i = lane % 16 (k, MFMA B layout) / lane / 16 + 4 i2 (v);
+        // nt * G <= 16 keeps every new v row below i2 = 4
+        const int i = lane % 16;
+        const size_t e_k = e_grp + (size_t)i * op.qkv_ld + (size_t)G * D;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const Link8 r = i < nt ? act8_issue(lk, op.x, e_k + 32 * q + (lane / 16) * 8) : z8;
+          kf[1][q] = r.w0;
+          kf[2][q] = r.w1;
+          stale |= i < nt && !act8_ok(lk, r, xtag);
+        }
+#pragma unroll
+        for (int i2 = 0; i2 < 4; i2++) {
+          const int iv = lane / 16 + 4 * i2;
+          const Link8 r =
+              iv < nt ? act8_issue(lk, op.x, e_grp + (size_t)iv * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
+                      : z8;
+          vf[4 + i2] = r.w0;
+          vf[8 + i2] = r.w1;
+          stale |= iv < nt && !act8_ok(lk, r, xtag);
+        }
+      }
+      if (!__any(stale) || !link_retry(a, spins)) break;
+    }
     RopeVec qin;
-    rope_load_x(qin, qkv + (size_t)qj * op.qkv_ld + (size_t)qg * D, qok, lane);
     rope_load_tab(qin, D, op, base + qj, qok, lane);
+#pragma unroll
+    for (int q = 0; q < 4; q++) qin.x[q] = act8_data(lk, qr[q]);
     if (newtok) {
-      // new token i = lane % 16 (k, MFMA B layout) / lane / 16 + 4 i2 (v)
       const int i = lane % 16;
       const bool kok = i < nt;
       RopeVec kin;
-      rope_load_x(kin, qkv + (size_t)i * op.qkv_ld + (size_t)G * D, kok, lane);
       rope_load_tab(kin, D, op, base + i, kok, lane);
 #pragma unroll
-      for (int i2 = 0; i2 < 16; i2++) {
-        const int iv = lane / 16 + 4 * i2;
-        vf[i2] = iv < nt ? ld_agent_u128(qkv + (size_t)iv * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
-                         : make_uint4(0, 0, 0, 0);
-      }
+      for (int q = 0; q < 4; q++) kin.x[q] = act8_data(lk, Link8{kf[1][q], kf[2][q]});
+#pragma unroll
+      for (int i2 = 0; i2 < 4; i2++) vf[i2] = act8_data(lk, Link8{vf[4 + i2], vf[8 + i2]});
+#pragma unroll
+      for (int i2 = 4; i2 < 16; i2++) vf[i2] = make_uint4(0, 0, 0, 0);
       rope_apply(kin, kf[0], op);
       auto tok_off = [&](int pg, int pos) __attribute__((always_inline)) -> size_t {
         return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
@@ -814,7 +957,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         if (kok) *reinterpret_cast<uint4*>(op.k_cache + tok_off(pg_tok, base + i) + 32 * q + (lane / 16) * 8) = kf[0][q];
       }
 #pragma unroll
-      for (int i2 = 0; i2 < 16; i2++) {
+      for (int i2 = 0; i2 < 4; i2++) {
         const int iv = lane / 16 + 4 * i2;
         const int pgv = __shfl(pg_tok, iv & 15, kWave);
         if (iv < nt) *reinterpret_cast<uint4*>(op.v_cache + tok_off(pgv, base + iv) + (lane % 16) * 8) = vf[i2];
@@ -823,10 +966,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     rope_apply(qin, qf, op);
   }
 
-  if (a.dbg == 9 && a.profile && wave == 0) {
-    wait_vm();
-    if (lane == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
-  }
   // per-wave online softmax state for rows 4*(lane/16)+i
   float m_i[4], l_i[4];
   float o_acc[RMAX][8];  // [query row][8 dims of this lane's d-chunk]
@@ -879,7 +1018,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    if (a.dbg == 9 && a.profile && wave == 0 && lane == 0) a.profile[(size_t)task_id * 8 + 3] = now_10ns();
     // O[row][d] = O * alpha + sum_p P[row][p] V[p][d]; lane: d-chunk lane%16, positions lane/16 + 4i
 #pragma unroll
     for (int rr = 0; rr < RMAX; rr++) {
@@ -914,7 +1052,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   // new tokens: causal block on the sync wave of the last split
   if (newtok) process(base, nt, true);
 
-  if (a.dbg == 9 && a.profile && wave == 0 && lane == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
   // sum o over the 4 lane groups (positions lane/16 + 4 i), then merge the
   // 8 waves: per row, (m, l) in LDS, o through LDS (xs reused as float)
 #pragma unroll
@@ -964,9 +1101,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       st_agent(rec + rr * (D + 2) + D + 1, L);
     }
   }
-  if (a.dbg == 9 && a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
   const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
-  if (a.dbg == 9 && a.profile && tix() == 0 && !merge) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   if (merge) {
     // Online-softmax merge of the S split records in one memory round trip:
     // every (m, l) pair and every o chunk is loaded before anything waits.
@@ -1031,14 +1166,20 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       }
       const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
       const int jt = rr / G, g = rr % G;
-      uint16_t* dst = op.out + (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
+      const size_t oe = (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
       const uint32_t lo = pack2<DT_BF16>(o0 * inv, o1 * inv), hi = pack2<DT_BF16>(o2 * inv, o3 * inv);
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), (uint64_t)lo | ((uint64_t)hi << 32), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      if (op.flags & OPF_OUT_LL) {
+        const uint32_t otag = link_tag(a, t.op);
+        link_store(op.out, oe, lo, otag);
+        link_store(op.out, oe + 2, hi, otag);
+      } else {
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(op.out + oe), (uint64_t)lo | ((uint64_t)hi << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   }
-  signal_event(a, t);
+  signal_event(a, t, (op.flags & OPF_OUT_LL) != 0);
 }
 
 // ------------------------------------------------------------ batch manager
@@ -1266,7 +1407,18 @@ struct Handle {
   uint32_t epoch = 0;
   long long spin_limit = 1ll << 26;
   uint64_t* profile = nullptr;
+  std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // tags restart with the epochs: cleared then
 };
+
+// Zero every link tensor (their tags embed the epoch, which restarts at 0).
+static int clear_links(Handle* h, hipStream_t st) {
+  for (auto& lb : h->link_buffers) {
+    hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(lb.first),
+                       (size_t)(lb.second / 4), 0u);
+    YR_CHECK_LAUNCH("pk_fill_u32_kernel (link tensors)");
+  }
+  return YR_OK;
+}
 
 }  // namespace pk
 }  // namespace yr
@@ -1299,6 +1451,7 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   h->n_ops = g->ops.size();
   h->n_tasks = g->tasks.size();
   h->n_events = g->events.size();
+  h->link_buffers = g->link_buffers;
   // queues flattened
   std::vector<int> qoff(g->num_workers + 1, 0), queue;
   for (int w = 0; w < g->num_workers; w++) {
@@ -1381,6 +1534,8 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream) {
   if (h->epoch >= (1u << 20)) {
     hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(64), dim3(256), 0, st, h->d_events, h->n_events, 0u);
     YR_CHECK_LAUNCH("pk_fill_u32_kernel");
+    int rc = clear_links(h, st);
+    if (rc != YR_OK) return rc;
     h->epoch = 0;
   }
   h->epoch++;
@@ -1397,7 +1552,6 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream) {
   a.num_workers = h->num_workers;
   a.spin_limit = h->spin_limit;
   a.profile = h->profile;
-  a.dbg = getenv("YR_PK_DBG") ? atoi(getenv("YR_PK_DBG")) : 0;
   void* args[] = {&a};
   hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
                                             dim3(PK_THREADS), args, 0, st);
@@ -1439,6 +1593,9 @@ int yr_pk_reset_status(yr_pk_handle* hp) {
   // clear the flags and re-base the counters (a watchdog exit leaves them short)
   if (hipMemset(h->d_status, 0, sizeof(int) * 4) != hipSuccess) return fail(YR_E_HIP, "reset status");
   if (hipMemset(h->d_events, 0, sizeof(uint32_t) * h->n_events) != hipSuccess) return fail(YR_E_HIP, "reset events");
+  int rc = clear_links(h, nullptr);
+  if (rc != YR_OK) return rc;
+  if (hipDeviceSynchronize() != hipSuccess) return fail(YR_E_HIP, "reset status: synchronize");
   h->epoch = 0;
   return YR_OK;
 }

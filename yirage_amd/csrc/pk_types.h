@@ -27,7 +27,17 @@ enum TaskType : int {
 
 enum OpFlags : int {
   OPF_RESIDUAL = 1,          // out = residual + x W^T
+  OPF_X_LL = 2,              // x (qkv for attention) is a link tensor written by op x_src
+  OPF_RES_LL = 4,            // residual is a link tensor written by op res_src
+  OPF_OUT_LL = 8,            // out is a link tensor
 };
+
+// Link tensors: activations passed between CUs inside one launch are stored
+// as 8-byte words {bf16 pair (low 32 bits), tag (high 32 bits)}, one 64-bit
+// store each (single-copy atomic).  tag = epoch << kLinkOpBits | producing op,
+// so a reader accepts a word only if this launch's producer wrote it.
+constexpr int kLinkOpBits = 10;
+constexpr int kMaxLinkOps = 1 << kLinkOpBits;
 
 // One per op (layer call).  Pointers are device addresses.
 struct OpDesc {
@@ -43,6 +53,8 @@ struct OpDesc {
   int ticket_base;    // first arrival ticket used by this op
   int vocab;          // argmax: valid columns (<= N)
   int scratch_off;    // float offset of this op's scratch records
+  int x_src;          // op that wrote x (OPF_X_LL)
+  int res_src;        // op that wrote the residual (OPF_RES_LL)
   int pad0;
   const uint16_t* x;        // activations in
   const uint16_t* norm;     // RMSNorm weight
@@ -107,7 +119,6 @@ struct KernelArgs {
   uint32_t epoch;            // 1, 2, 3, ... per launch
   int num_workers;
   long long spin_limit;      // watchdog: polls before a wait gives up
-  int dbg;
 };
 
 }  // namespace pk

@@ -45,6 +45,7 @@ class DTensor:
     segments: list = field(default_factory=list)   # [(DTensor, row0, rows)] for views
     group: int = 0                                  # rows per source chunk of a shuffle
     ngroups: int = 1                                # number of shuffle groups
+    ll: bool = False                                # stored as tagged words (see _link_tensors)
 
     @property
     def num_dims(self) -> int:
@@ -325,12 +326,39 @@ class PersistentKernel:
             raise YirageHipError(f"hip backend: layer '{k}' cannot be scheduled here (no fusion partner)")
         return ops
 
+    _LINK_PRODUCERS = ("embed", "rmsnorm_linear", "linear", "rmsnorm_linear_silu", "attention")
+
+    def _link_tensors(self):
+        """Intermediate activations passed between tasks on different CUs are
+        stored as 8-byte words {two bf16 values, 32-bit tag}: a consumer checks
+        each word's tag against the producing op of this launch instead of
+        waiting for the producer to confirm that its stores completed.  These
+        are the kernel-owned tensors (new_tensor) written by embed / linear /
+        attention ops; the logits of the argmax op stay plain bf16.  Storage is
+        re-allocated here at twice the bf16 size.  Batch-1 graphs only."""
+        if self.max_num_batched_tokens > 1:
+            # every task re-reads all token rows of its input: at batch > 1
+            # the doubled bytes cost more than the confirmation they replace
+            return
+        owned = {id(t) for t in self._owned}
+        for op in self.ops:
+            if op["type"] not in self._LINK_PRODUCERS:
+                continue
+            t = self._tensors[op["out"]]
+            if t.ll or t.tensor is None or id(t.tensor) not in owned or t.num_dims != 2 or t.dtype != bfloat16:
+                continue
+            buf = torch.zeros((t.dim(0), 2 * t.dim(1)), dtype=torch.bfloat16, device=t.tensor.device)
+            self._owned[[id(x) for x in self._owned].index(id(t.tensor))] = buf
+            owned.add(id(buf))
+            t.tensor = buf
+            t.ll = True
+
     def _graph_json(self) -> str:
         tensors = {}
         for t in self._tensors.values():
             if t.tensor is not None:
                 ptr = 0 if t.tensor.device.type == "meta" else t.tensor.data_ptr()
-                tensors[t.name] = dict(ptr=ptr, dims=list(t.dims), dtype=t.dtype)
+                tensors[t.name] = dict(ptr=ptr, dims=list(t.dims), dtype=t.dtype, ll=int(t.ll))
         return json.dumps(dict(
             num_workers=self.num_workers, max_tokens=self.max_num_batched_tokens,
             max_requests=self.max_num_batched_requests, page_size=self.page_size, max_pages=self.max_num_pages,
@@ -341,6 +369,7 @@ class PersistentKernel:
     def compile(self, **kwargs):
         assert not self._is_compiled
         self.ops = self._fuse()
+        self._link_tensors()
         g = ctypes.c_void_p()
         check(lib().yr_pk_graph_build(self._graph_json().encode(), ctypes.byref(g)), "task graph build")
         self._graph = g
