@@ -104,18 +104,20 @@ def test_gated_mlp_batch128_column_sample():
     _close(out[:, cols], ref, "gated_mlp_b128")
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_linear_with_residual(dtype):
+@pytest.mark.parametrize("dtype,layout", [(torch.float16, 0), (torch.bfloat16, 0), (torch.bfloat16, 1),
+                                          (torch.float16, 1)])
+def test_linear_with_residual(dtype, layout):
     import yirage_amd.fused as F
 
+    print(f"case linear+residual {dtype} layout={layout}", flush=True)
     g = torch.Generator().manual_seed(0)
-    B, K, N = 4, 4096, 1024
+    B, K, N = 4, 4096, 1040
     x = _randn((B, K), 1.0, dtype, g)
-    w = _randn((N, K), 0.02, dtype, g)
+    w = _randn((N, K) if layout == 0 else (K, N), 0.02, dtype, g)
     r = _randn((B, N), 1.0, dtype, g)
-    out = F.linear(x.cuda(), w.cuda(), residual=r.cuda())
+    out = F.linear(x.cuda(), w.cuda(), residual=r.cuda(), w_layout=layout)
     torch.cuda.synchronize()
-    ref = O.linear(_f(x), _bits(w), DT[dtype], O.W_NK, _f(r))
+    ref = O.linear(_f(x), _bits(w), DT[dtype], O.W_NK if layout == 0 else O.W_KN, _f(r))
     _close(out, ref, "linear+residual")
 
 

@@ -20,6 +20,12 @@
 
 namespace yr {
 
+// K x N weights go to the MFMA kernels of skinny.hip
+size_t skinny_kn_workspace(int B, int K, int N, int nmat);
+int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
+              const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
+              void* ws, size_t ws_bytes, hipStream_t st, const char* name);
+
 enum : int { EPI_LINEAR = 0, EPI_RMSNORM = 1, EPI_GATED = 2 };
 
 struct GemvArgs {
@@ -416,6 +422,9 @@ static int run_gemv(GemvArgs a, int dtype, int layout, void* ws, size_t ws_bytes
   if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype must be f16/bf16", name);
   if (layout != YR_W_KN && layout != YR_W_NK) return fail(YR_E_INVALID, "%s: bad weight layout", name);
   if (!a.x || !a.w0 || !a.out || (NMAT == 2 && !a.w1)) return fail(YR_E_INVALID, "%s: null pointer", name);
+  if (layout == YR_W_KN)
+    return skinny_kn(a.x, a.gamma, a.w0, a.w1, a.residual, a.out, a.B, a.K, a.N, a.eps, dtype, NMAT, EPI, ws,
+                     ws_bytes, st, name);
   // every batch chunk of <= 8 rows gets its own plan; the workspace must hold
   // the largest one
   size_t need = 0;
@@ -464,6 +473,7 @@ using namespace yr;
 extern "C" {
 
 static size_t ws_for(int batch, int k, int n, int w_layout, int nmat) {
+  if (w_layout == YR_W_KN) return skinny_kn_workspace(batch, k, n, nmat);
   size_t need = 0;
   for (int b0 = 0; b0 < batch; b0 += 8) {
     size_t w = plan_gemv(batch - b0 < 8 ? batch - b0 : 8, k, n, w_layout, nmat).ws;

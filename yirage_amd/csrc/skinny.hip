@@ -1,0 +1,388 @@
+// Skinny GEMMs with the weight in K x N layout (X[B][K] @ W[K][N], W row-major
+// with columns contiguous) on MFMA for gfx950: RMSNorm+linear, gated MLP
+// (SiLU(X W1) * (X W3)) and linear(+residual).
+//
+// The MFMA B operand wants eight consecutive k of one column per lane, the
+// transpose of how W sits in memory.  Weight tiles therefore go to LDS
+// unchanged (rows of 16 columns) and come back through ds_read_b64_tr_b16:
+// within a 16-lane group, lane i element e of the result is element i % 4 of
+// the 64-bit row that lane 4e + i / 4 addressed.  Lane j = 4e + q of group g
+// addresses row 8g + e (+4 for the second read), columns 4q..4q+3, so lane i
+// receives column i, rows 8g..8g+7: exactly its B fragment.
+//
+// Work split (stream-K): the (16-column tile, K chunk) units are dealt out in
+// equal contiguous ranges to one persistent workgroup per CU.  A tile that
+// straddles two ranges is finished by the last of its workgroups to arrive
+// (arrival ticket; partial tiles as fp32 records, summed in workgroup order,
+// so results do not depend on timing).  Workgroups are renumbered so that the
+// four tiles sharing one 128-byte weight line run on one XCD (workgroup i runs
+// on XCD i % 8): the line is fetched from HBM into that XCD's L2 once.
+#include <type_traits>
+
+#include "yr_common.h"
+
+namespace yr {
+namespace sk {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+enum : int { EPI_LINEAR = 0, EPI_RMSNORM = 1, EPI_GATED = 2 };
+
+struct Args {
+  const uint16_t* x;         // [B][K]
+  const uint16_t* gamma;     // [K] (RMSNorm) or null
+  const uint16_t* w0;        // [K][N]
+  const uint16_t* w1;        // [K][N] (gated: W3)
+  const uint16_t* residual;  // [B][N] or null
+  uint16_t* out;             // [B][N]
+  float* partial;            // records of partial tiles: [workgroup][2][rec]
+  uint32_t* tickets;         // [tiles], zero at rest
+  int B, K, N;
+  float eps;
+  int kch;                   // K chunks (units) per tile
+  int units;                 // tiles * kch
+};
+
+// Unit range [lo(v), lo(v + 1)) of virtual workgroup v; the virtual workgroup
+// that owns unit u.
+__device__ __forceinline__ int unit_lo(int v, int U, int G) { return (int)(((long long)v * U) / G); }
+__device__ __forceinline__ int owner_of(int u, int U, int G) { return (int)(((long long)(u + 1) * G - 1) / U); }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// B fragment of a 32 x 16 block of a row-major [rows][ld] bf16/f16 tile in
+// LDS whose first row is `row0`.
+__device__ __forceinline__ uint4 b_frag(const uint16_t* tile, int ld, int row0, int lane) {
+  const int g = lane >> 4, j = lane & 15, e = j >> 2, q = j & 3;
+  const uint16_t* p0 = tile + (row0 + 8 * g + e) * ld + 4 * q;
+  const uint16_t* p1 = p0 + 4 * ld;
+  auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
+    return reinterpret_cast<const lds_v4i16*>(
+        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+            reinterpret_cast<uintptr_t>(p)));
+  };
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p0)));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p1)));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+  return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
+                                                  0, 0);
+}
+
+// 16-byte loads through a buffer descriptor: an offset at or past `bytes`
+// returns zero without a memory access, so bounds checks need no branch (a
+// branch per load would also make the compiler wait for every outstanding
+// load where a count would do).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+constexpr uint32_t kOob = 0xfffffff0u;  // offset that is out of range for every buffer
+
+// x * gamma, element-wise on 8 packed values, rounded to the storage type
+// (the normalised activation the reference feeds its matmul)
+template <int DT>
+__device__ __forceinline__ uint4 scale8(uint4 x, uint4 g) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, gv[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    o[i] = pack2<DT>(lo16<DT>(xv[i]) * lo16<DT>(gv[i]), hi16<DT>(xv[i]) * hi16<DT>(gv[i]));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <int DT>
+__device__ __forceinline__ float sumsq8(uint4 x) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float lo = lo16<DT>(xv[i]), hi = hi16<DT>(xv[i]);
+    s += lo * lo + hi * hi;
+  }
+  return s;
+}
+
+// Epilogue of one output element from its full fp32 sums.
+template <int DT, int EPI>
+__device__ __forceinline__ void store_out(const Args& a, int b, int n, float v0, float v1, float ss) {
+  float v = v0;
+  if constexpr (EPI == EPI_RMSNORM) v *= rsqrtf(ss / (float)a.K + a.eps);
+  else if constexpr (EPI == EPI_GATED) v = silu(v0) * v1;
+  if (a.residual) v += ld_elem<DT>(a.residual[(size_t)b * a.N + n]);
+  a.out[(size_t)b * a.N + n] = (uint16_t)st_elem<DT>(v);
+}
+
+// ---------------------------------------------------------------- B <= 16
+// Tiles are TW columns wide (16, 32 or 64: NB = TW / 16 MFMA column blocks).
+// Every wave streams its own share of the weights: a k step is 32 rows x TW
+// columns of each matrix, NB 16-byte loads per lane per matrix (a load
+// instruction covers 512 / TW rows of TW * 2 contiguous bytes), written to a
+// wave-private LDS slot and read straight back as MFMA B fragments (LDS
+// operations of one wave execute in order, so no barrier is involved).  A
+// register ring keeps RING steps (weights, A fragment, gamma) in flight per
+// wave, across unit and tile boundaries; only the end of a tile synchronises
+// the workgroup, to add the waves' C tiles.
+//
+// Unit = KC rows of one tile; wave w takes steps [w SPW, (w+1) SPW) of every
+// unit in its workgroup's range.
+template <int DT, int NMAT, int EPI, int TW, int KC>
+__global__ __launch_bounds__(kThreads, 1) void sk16_kernel(Args a) {
+  constexpr int NB = TW / 16;                  // MFMA column blocks per tile
+  constexpr int RPL = 512 / TW;                // rows per wave load instruction
+  constexpr int SPW = KC / kWaves / 32;        // k steps per wave per unit
+  constexpr int RING = NB * NMAT >= 8 ? 2 : NB * NMAT >= 4 ? 16 / (NB * NMAT) : 8;  // steps in flight (8-16 KiB per wave)
+  constexpr bool NORM = EPI == EPI_RMSNORM;
+  constexpr int CT = NMAT * 16 * TW;           // C tile floats (all matrices)
+  constexpr int REC = CT + 16;                 // + row sums of squares
+  static_assert(SPW >= 1 && KC % (kWaves * 32) == 0, "unit must give every wave whole k steps");
+  // wave-private: one step; the next step's stores follow this step's reads
+  // in the wave's in-order LDS queue
+  __shared__ __attribute__((aligned(16))) uint16_t slot[kWaves][NMAT][32 * TW];
+  __shared__ float red[kWaves][REC];
+  __shared__ float fin[REC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, U = a.units, KCH = a.kch;
+  // XCD-grouped order when G % 8 == 0; the host launches G <= U workgroups,
+  // so every range holds at least one unit
+  const int v = G & 7 ? (int)blockIdx.x : (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int ub = unit_lo(v, U, G), ue = unit_lo(v + 1, U, G);
+  const int nsteps = (ue - ub) * SPW;  // this wave's steps
+
+  const __amdgpu_buffer_rsrc_t rw0 = rsrc(a.w0, (uint32_t)((size_t)a.K * a.N * 2));
+  const __amdgpu_buffer_rsrc_t rw1 = rsrc(NMAT == 2 ? a.w1 : a.w0, (uint32_t)((size_t)a.K * a.N * 2));
+  const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)((size_t)a.B * a.K * 2));
+  const __amdgpu_buffer_rsrc_t rg = rsrc(a.gamma, a.gamma ? (uint32_t)(a.K * 2) : 0u);
+  const int arow = lane & 15;
+  // weight load p of a step: lane -> row p RPL + lane / (TW / 8), columns 8 (lane % (TW / 8)) ..
+  const int wrow = lane / (TW / 8), wcol = 8 * (lane % (TW / 8));
+
+  struct Step {
+    uint4 w[NMAT][NB];
+    uint4 x;
+    uint4 g;
+  };
+  // step i of this wave -> unit ub + i / SPW, rows k0 + 32 (wave SPW + i % SPW)
+  auto issue = [&](Step& st, int i) __attribute__((always_inline)) {
+    const int u = ub + i / SPW, t = u / KCH;
+    const int kb = (u - t * KCH) * KC + 32 * (wave * SPW + i % SPW);  // first row of the step
+    const bool ok = i < nsteps;
+    const int n = t * TW + wcol;
+#pragma unroll
+    for (int p = 0; p < NB; p++) {
+      const int kw = kb + p * RPL + wrow;
+      const uint32_t woff = ok && kw < a.K && n < a.N ? (uint32_t)(((size_t)kw * a.N + n) * 2) : kOob;
+      st.w[0][p] = bload16(rw0, woff);
+      if constexpr (NMAT == 2) st.w[1][p] = bload16(rw1, woff);
+    }
+    const int kx = kb + 8 * (lane >> 4);
+    st.x = bload16(rx, ok && kx < a.K && arow < a.B ? (uint32_t)(((size_t)arow * a.K + kx) * 2) : kOob);
+    if constexpr (NORM) st.g = bload16(rg, ok && kx < a.K ? (uint32_t)(kx * 2) : kOob);
+  };
+
+  f32x4 acc[NMAT][NB];
+#pragma unroll
+  for (int m = 0; m < NMAT; m++)
+#pragma unroll
+    for (int q = 0; q < NB; q++) acc[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;  // this lane's sum of squares of x row lane % 16 (RMSNorm)
+
+  // end of tile t within this workgroup's range: add the waves' C tiles (and
+  // RMSNorm row sums of squares), then emit it or combine it across workgroups
+  auto finish_tile = [&](int t) __attribute__((always_inline)) {
+    // C block q of this wave: lane holds rows 4 (lane / 16) + i, column 16 q + lane % 16
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+      for (int q = 0; q < NB; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          red[wave][m * 16 * TW + (4 * (lane >> 4) + i) * TW + 16 * q + (lane & 15)] = acc[m][q][i];
+    if constexpr (NORM) {
+      float s2 = ss + __shfl_xor(ss, 16, kWave);
+      s2 += __shfl_xor(s2, 32, kWave);
+      if (lane < 16) red[wave][CT + lane] = s2;
+    }
+    __syncthreads();
+    for (int i = tid; i < REC; i += kThreads) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; w++) sum += red[w][i];
+      fin[i] = sum;
+    }
+    __syncthreads();
+    const int tu0 = t * KCH, tu1 = tu0 + KCH;  // units of tile t
+    const int n0 = t * TW;
+    bool emit = true;
+    if (tu0 < ub || tu1 > ue) {
+      // partial tile: record slot (v, side), then the last contributor sums
+      const int side = ub >= tu0 ? 0 : 1;  // 0: tile t is this range's first tile
+      float* rec = a.partial + ((size_t)v * 2 + side) * REC;
+      for (int i = tid * 4; i < REC; i += kThreads * 4)
+        st_agent4(rec + i, make_float4(fin[i], fin[i + 1], fin[i + 2], fin[i + 3]));
+      const int c0 = owner_of(tu0, U, G), c1 = owner_of(tu1 - 1, U, G);
+      emit = arrive_last(&a.tickets[t], c1 - c0 + 1);
+      if (emit) {
+        for (int i = tid * 4; i < REC; i += kThreads * 4) {
+          float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int c = c0; c <= c1; c++) {
+            const int cside = unit_lo(c, U, G) >= tu0 ? 0 : 1;
+            const float4 r = ld_agent4(a.partial + ((size_t)c * 2 + cside) * REC + i);
+            sum.x += r.x; sum.y += r.y; sum.z += r.z; sum.w += r.w;
+          }
+          fin[i] = sum.x; fin[i + 1] = sum.y; fin[i + 2] = sum.z; fin[i + 3] = sum.w;
+        }
+        __syncthreads();
+      }
+    }
+    if (emit) {
+      for (int i = tid; i < a.B * TW; i += kThreads) {
+        const int b = i / TW, col = i % TW, n = n0 + col;
+        if (n < a.N)
+          store_out<DT, EPI>(a, b, n, fin[b * TW + col], NMAT == 2 ? fin[16 * TW + b * TW + col] : 0.f,
+                             NORM ? fin[CT + b] : 0.f);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+      for (int q = 0; q < NB; q++) acc[m][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ss = 0.f;
+    __syncthreads();  // red / fin are reused by the next tile
+  };
+
+  Step ring[RING];
+#pragma unroll
+  for (int j = 0; j < RING; j++) issue(ring[j], j);
+  // consume step i from ring slot i % RING (compile-time within the unrolled
+  // block), then put step i + RING in flight in the same registers.  Steps
+  // past the end load zeros (out-of-range offsets), so the body runs without
+  // a branch around its loads; only the tile end is conditional.
+  for (int i0 = 0; i0 < nsteps; i0 += RING) {
+#pragma unroll
+    for (int j = 0; j < RING; j++) {
+      const int i = i0 + j;
+      Step& st = ring[j];
+#pragma unroll
+      for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int p = 0; p < NB; p++)
+          *reinterpret_cast<uint4*>(slot[wave][m] + (p * RPL + wrow) * TW + wcol) = st.w[m][p];
+      uint4 xa = st.x;
+      if constexpr (NORM) {
+        ss += sumsq8<DT>(xa);
+        if (a.gamma) xa = scale8<DT>(xa, st.g);  // no gamma: x as is
+      }
+#pragma unroll
+      for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int q = 0; q < NB; q++)
+          acc[m][q] = mfma16<DT>(xa, b_frag(slot[wave][m] + 16 * q, TW, 0, lane), acc[m][q]);
+      issue(st, i + RING);
+      const int u = ub + i / SPW;
+      if (i < nsteps && i % SPW == SPW - 1 && (u == ue - 1 || (u + 1) % KCH == 0)) finish_tile(u / KCH);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+constexpr int kGrid = 256;  // persistent workgroups (one per CU of an MI355X); a multiple of 8
+constexpr int kTW = 64;     // tile width (columns)
+constexpr int kKC = 1024;   // K rows per unit
+
+struct Plan {
+  int tw, kc, kch, units, tiles;
+  size_t ws;
+};
+
+// 64-column tiles: every weight row segment a wave loads is one whole
+// 128-byte line (narrower tiles leave the other parts of a line to other
+// workgroups, which measured slower even with no cross-workgroup sums).
+inline Plan plan16(int K, int N, int nmat) {
+  Plan p;
+  p.tw = kTW;
+  p.kc = kKC;
+  p.tiles = (N + p.tw - 1) / p.tw;
+  p.kch = (K + p.kc - 1) / p.kc;
+  p.units = p.tiles * p.kch;
+  const int rec = nmat * 16 * kTW + 16;
+  p.ws = kTicketBytes + (size_t)kGrid * 2 * rec * sizeof(float);
+  return p;
+}
+
+}  // namespace sk
+}  // namespace yr
+
+namespace yr {
+
+using namespace sk;
+
+size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
+  (void)B;
+  return plan16(K, N, nmat).ws;
+}
+
+// Persistent grid: kGrid workgroups, fewer (a multiple of 8 when possible)
+// when there are fewer units, so that no workgroup's range is empty.
+static int grid_for(int units) { return units >= kGrid ? kGrid : units >= 8 ? units & ~7 : units; }
+
+template <int DT, int NMAT, int EPI>
+static void launch16(const Args& a, int tw, hipStream_t st) {
+  const dim3 grid(grid_for(a.units)), block(kThreads);
+  (void)tw;
+  hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC>), grid, block, 0, st, a);
+}
+
+// X[B][K] @ W[K][N] (+ fused epilogue) for any B: passes of up to 16 rows.
+int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
+              const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
+              void* ws, size_t ws_bytes, hipStream_t st, const char* name) {
+  const Plan p = plan16(K, N, nmat);
+  if (p.ws > ws_bytes || !ws) return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, p.ws);
+  if (p.tiles > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
+  if ((size_t)K * N * 2 >= kOob || (size_t)B * K * 2 >= kOob)
+    return fail(YR_E_INVALID, "%s: operands must be < 4 GiB (32-bit buffer offsets)", name);
+  for (int b0 = 0; b0 < B; b0 += 16) {
+    Args a = {};
+    a.x = x + (size_t)b0 * K;
+    a.gamma = gamma;
+    a.w0 = w0;
+    a.w1 = w1;
+    a.residual = residual ? residual + (size_t)b0 * N : nullptr;
+    a.out = out + (size_t)b0 * N;
+    a.partial = (float*)((char*)ws + kTicketBytes);
+    a.tickets = (uint32_t*)ws;
+    a.B = B - b0 < 16 ? B - b0 : 16;
+    a.K = K;
+    a.N = N;
+    a.eps = eps;
+    a.kch = p.kch;
+    a.units = p.units;
+    const bool bf = dtype == YR_DTYPE_BF16;
+#define YR_SK(DTV, NM, EP) launch16<DTV, NM, EP>(a, p.tw, st)
+    if (nmat == 2) {
+      if (bf) YR_SK(DT_BF16, 2, EPI_GATED); else YR_SK(DT_F16, 2, EPI_GATED);
+    } else if (epi == EPI_RMSNORM) {
+      if (bf) YR_SK(DT_BF16, 1, EPI_RMSNORM); else YR_SK(DT_F16, 1, EPI_RMSNORM);
+    } else {
+      if (bf) YR_SK(DT_BF16, 1, EPI_LINEAR); else YR_SK(DT_F16, 1, EPI_LINEAR);
+    }
+#undef YR_SK
+    YR_CHECK_LAUNCH(name);
+  }
+  return YR_OK;
+}
+
+}  // namespace yr
