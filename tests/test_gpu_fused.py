@@ -38,7 +38,8 @@ def _close(got: torch.Tensor, ref: np.ndarray, what: str):
 
 
 @pytest.mark.parametrize("B,K,N,layout", [(8, 4096, 4096, 1), (3, 1024, 776, 1), (1, 4096, 4096, 0),
-                                          (8, 4096, 6144, 0), (5, 14336, 4096, 0), (20, 512, 256, 1)])
+                                          (8, 4096, 6144, 0), (5, 14336, 4096, 0), (20, 512, 256, 1),
+                                          (37, 1024, 200, 1), (128, 4096, 4096, 1)])
 def test_rmsnorm_linear(B, K, N, layout):
     import yirage_amd.fused as F
 
@@ -72,7 +73,7 @@ def test_rmsnorm_linear_config1_gamma_one():
 
 
 @pytest.mark.parametrize("B,K,N,layout", [(8, 4096, 14336, 1), (2, 2048, 520, 1), (8, 4096, 2048, 0),
-                                          (1, 4096, 14336, 0)])
+                                          (1, 4096, 14336, 0), (130, 1024, 520, 1)])
 def test_gated_mlp(B, K, N, layout):
     import yirage_amd.fused as F
 
@@ -104,14 +105,14 @@ def test_gated_mlp_batch128_column_sample():
     _close(out[:, cols], ref, "gated_mlp_b128")
 
 
-@pytest.mark.parametrize("dtype,layout", [(torch.float16, 0), (torch.bfloat16, 0), (torch.bfloat16, 1),
-                                          (torch.float16, 1)])
-def test_linear_with_residual(dtype, layout):
+@pytest.mark.parametrize("dtype,layout,B", [(torch.float16, 0, 4), (torch.bfloat16, 0, 4), (torch.bfloat16, 1, 4),
+                                            (torch.float16, 1, 4), (torch.bfloat16, 1, 40)])
+def test_linear_with_residual(dtype, layout, B):
     import yirage_amd.fused as F
 
-    print(f"case linear+residual {dtype} layout={layout}", flush=True)
+    print(f"case linear+residual {dtype} layout={layout} B={B}", flush=True)
     g = torch.Generator().manual_seed(0)
-    B, K, N = 4, 4096, 1040
+    K, N = 4096, 1040
     x = _randn((B, K), 1.0, dtype, g)
     w = _randn((N, K) if layout == 0 else (K, N), 0.02, dtype, g)
     r = _randn((B, N), 1.0, dtype, g)

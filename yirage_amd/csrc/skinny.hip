@@ -297,6 +297,176 @@ __global__ __launch_bounds__(kThreads, 1) void sk16_kernel(Args a) {
   }
 }
 
+// ---------------------------------------------------------------- B <= 128
+// A GEMM tile: all 128 rows x 64 columns of each matrix over one K split.
+// Chunks of 64 K rows of W (64 x 64 per matrix) and x (128 x 64) go through
+// registers (CHQ chunks in flight per thread) into a double-buffered LDS
+// stage; wave w owns rows 32 (w % 4) .. +32 and columns 32 (w / 4) .. +32
+// (2 x 2 MFMA blocks per matrix), A fragments by ds_read_b128, B fragments
+// by transposing reads.  Splits of one tile add up through fp32 records and
+// an arrival ticket (in split order).
+template <int DT, int NMAT, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
+  constexpr int TW = 64, KS = 64, MB = 128;
+  constexpr int LDW = TW + 8, LDX = KS + 8;   // padded LDS rows (fewer bank conflicts)
+  constexpr int CHQ = 4;                      // chunks in flight
+  constexpr bool NORM = EPI == EPI_RMSNORM;
+  __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][KS * LDW];
+  __shared__ __attribute__((aligned(16))) uint16_t xl[2][MB * LDX];
+  __shared__ float ssl[MB];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int splits = a.kch;                   // K splits per tile
+  const int t = blockIdx.x / splits, sp = blockIdx.x % splits;
+  const int kper = (((a.K + splits - 1) / splits) + KS - 1) / KS * KS;  // rows per split (whole chunks)
+  const int kbeg = sp * kper, kend = min(a.K, kbeg + kper);
+  const int nchunks = kend > kbeg ? (kend - kbeg + KS - 1) / KS : 0;
+  const int n0 = t * TW;
+
+  const __amdgpu_buffer_rsrc_t rw0 = rsrc(a.w0, (uint32_t)((size_t)a.K * a.N * 2));
+  const __amdgpu_buffer_rsrc_t rw1 = rsrc(NMAT == 2 ? a.w1 : a.w0, (uint32_t)((size_t)a.K * a.N * 2));
+  const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)((size_t)a.B * a.K * 2));
+  const __amdgpu_buffer_rsrc_t rg = rsrc(a.gamma, a.gamma ? (uint32_t)(a.K * 2) : 0u);
+  // this thread's chunk pieces: W row tid / 8, columns 8 (tid % 8); x rows
+  // tid / 8 and tid / 8 + 64, k 8 (tid % 8)
+  const int wr_ = tid >> 3, wc = 8 * (tid & 7);
+  const int xr0 = tid >> 3, xk = 8 * (tid & 7);
+
+  struct Chunk {
+    uint4 w[NMAT];
+    uint4 x[2];
+    uint4 g;
+  };
+  auto issue = [&](Chunk& c, int ci) __attribute__((always_inline)) {
+    const int k0 = kbeg + ci * KS;
+    const bool ok = ci < nchunks;
+    const int kw = k0 + wr_, n = n0 + wc;
+    const uint32_t woff = ok && kw < kend && n < a.N ? (uint32_t)(((size_t)kw * a.N + n) * 2) : kOob;
+    c.w[0] = bload16(rw0, woff);
+    if constexpr (NMAT == 2) c.w[1] = bload16(rw1, woff);
+    const int kx = k0 + xk;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int r = xr0 + 64 * h;
+      c.x[h] = bload16(rx, ok && kx < kend && r < a.B ? (uint32_t)(((size_t)r * a.K + kx) * 2) : kOob);
+    }
+    if constexpr (NORM) c.g = bload16(rg, ok && kx < kend ? (uint32_t)(kx * 2) : kOob);
+  };
+
+  f32x4 acc[NMAT][2][2];
+#pragma unroll
+  for (int m = 0; m < NMAT; m++)
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[m][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss0 = 0.f, ss1 = 0.f;  // RMSNorm: sums of squares of x rows xr0, xr0 + 64 (this thread's k)
+  const int mg = wave & 3, ng = wave >> 2;
+
+  Chunk ring[CHQ];
+#pragma unroll
+  for (int j = 0; j < CHQ; j++) issue(ring[j], j);
+  for (int c0 = 0; c0 < nchunks; c0 += CHQ) {
+#pragma unroll
+    for (int j = 0; j < CHQ; j++) {
+      const int ci = c0 + j, lb = j & 1;
+      Chunk& c = ring[j];
+      // stage chunk ci (x scaled by gamma for RMSNorm, row sums first)
+#pragma unroll
+      for (int m = 0; m < NMAT; m++) *reinterpret_cast<uint4*>(&wl[lb][m][wr_ * LDW + wc]) = c.w[m];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint4 xv = c.x[h];
+        if constexpr (NORM) {
+          (h ? ss1 : ss0) += sumsq8<DT>(xv);
+          if (a.gamma) xv = scale8<DT>(xv, c.g);
+        }
+        *reinterpret_cast<uint4*>(&xl[lb][(xr0 + 64 * h) * LDX + xk]) = xv;
+      }
+      __syncthreads();
+      issue(c, ci + CHQ);
+#pragma unroll
+      for (int ks = 0; ks < KS / 32; ks++) {
+        uint4 af[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+          af[i] = *reinterpret_cast<const uint4*>(&xl[lb][(32 * mg + 16 * i + (lane & 15)) * LDX + 32 * ks + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+          for (int j2 = 0; j2 < 2; j2++) {
+            const uint4 bf = b_frag(&wl[lb][m][32 * ng + 16 * j2], LDW, 32 * ks, lane);
+#pragma unroll
+            for (int i = 0; i < 2; i++) acc[m][i][j2] = mfma16<DT>(af[i], bf, acc[m][i][j2]);
+          }
+      }
+    }
+  }
+  // per-row sums of squares of this split (the 8 threads of a row are lanes
+  // 8 r .. 8 r + 7 of one wave)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) {
+      ss0 += __shfl_xor(ss0, o, kWave);
+      ss1 += __shfl_xor(ss1, o, kWave);
+    }
+    if ((tid & 7) == 0) {
+      ssl[xr0] = ss0;
+      ssl[xr0 + 64] = ss1;
+    }
+  }
+  __syncthreads();
+  // C element (matrix m, block i, j2, reg q) of this lane: row 32 mg + 16 i +
+  // 4 (lane / 16) + q, column 32 ng + 16 j2 + lane % 16
+  if (splits > 1) {
+    // record [split][matrix][128][64] + row sums; the last split sums them
+    constexpr int REC = NMAT * MB * TW + MB;
+    float* rec = a.partial + ((size_t)t * splits + sp) * REC;
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j2 = 0; j2 < 2; j2++)
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            st_agent(rec + m * MB * TW + (32 * mg + 16 * i + 4 * (lane >> 4) + q) * TW + 32 * ng + 16 * j2 + (lane & 15),
+                     acc[m][i][j2][q]);
+    if (NORM && tid < MB) st_agent(rec + NMAT * MB * TW + tid, ssl[tid]);
+    if (!arrive_last(&a.tickets[t], splits)) return;
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j2 = 0; j2 < 2; j2++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int off = m * MB * TW + (32 * mg + 16 * i + 4 * (lane >> 4) + q) * TW + 32 * ng + 16 * j2 + (lane & 15);
+            float sum = 0.f;
+            for (int s2 = 0; s2 < splits; s2++) sum += ld_agent(a.partial + ((size_t)t * splits + s2) * REC + off);
+            acc[m][i][j2][q] = sum;
+          }
+    if (NORM && tid < MB) {
+      float sum = 0.f;
+      for (int s2 = 0; s2 < splits; s2++) sum += ld_agent(a.partial + ((size_t)t * splits + s2) * REC + NMAT * MB * TW + tid);
+      ssl[tid] = sum;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j2 = 0; j2 < 2; j2++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int b = 32 * mg + 16 * i + 4 * (lane >> 4) + q, n = n0 + 32 * ng + 16 * j2 + (lane & 15);
+        if (b < a.B && n < a.N)
+          store_out<DT, EPI>(a, b, n, acc[0][i][j2][q], NMAT == 2 ? acc[NMAT - 1][i][j2][q] : 0.f,
+                             NORM ? ssl[b] : 0.f);
+      }
+}
+
 // ---------------------------------------------------------------- host side
 constexpr int kGrid = 256;  // persistent workgroups (one per CU of an MI355X); a multiple of 8
 constexpr int kTW = 64;     // tile width (columns)
@@ -329,11 +499,6 @@ namespace yr {
 
 using namespace sk;
 
-size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
-  (void)B;
-  return plan16(K, N, nmat).ws;
-}
-
 // Persistent grid: kGrid workgroups, fewer (a multiple of 8 when possible)
 // when there are fewer units, so that no workgroup's range is empty.
 static int grid_for(int units) { return units >= kGrid ? kGrid : units >= 8 ? units & ~7 : units; }
@@ -345,16 +510,52 @@ static void launch16(const Args& a, int tw, hipStream_t st) {
   hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC>), grid, block, 0, st, a);
 }
 
-// X[B][K] @ W[K][N] (+ fused epilogue) for any B: passes of up to 16 rows.
+// Splits of K per 64-column tile so that tiles x splits fills the CUs.
+inline Plan plan128(int K, int N, int nmat) {
+  Plan p;
+  p.tw = 64;
+  p.tiles = (N + 63) / 64;
+  int s = kGrid / p.tiles;
+  const int maxs = (K + 63) / 64;
+  s = s < 1 ? 1 : s > maxs ? maxs : s > 16 ? 16 : s;
+  p.kch = s;
+  p.kc = 0;
+  p.units = p.tiles * s;
+  const int rec = nmat * 128 * 64 + 128;
+  p.ws = s > 1 ? kTicketBytes + (size_t)p.units * rec * sizeof(float) : 0;
+  return p;
+}
+
+template <int DT, int NMAT, int EPI>
+static void launch128(const Args& a, hipStream_t st) {
+  hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI>), dim3(a.units), dim3(kThreads), 0, st, a);
+}
+
+size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
+  size_t need = 0;
+  for (int b0 = 0; b0 < B; b0 += 128) {
+    const size_t w = B - b0 > 16 ? plan128(K, N, nmat).ws : plan16(K, N, nmat).ws;
+    if (w > need) need = w;
+  }
+  return need;
+}
+
+// X[B][K] @ W[K][N] (+ fused epilogue) for any B: passes of up to 128 rows
+// (the batch-128 GEMM kernel above 16 rows, the skinny kernel below).
 int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
               const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
               void* ws, size_t ws_bytes, hipStream_t st, const char* name) {
-  const Plan p = plan16(K, N, nmat);
-  if (p.ws > ws_bytes || !ws) return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, p.ws);
-  if (p.tiles > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
+  const size_t need = skinny_kn_workspace(B, K, N, nmat);
+  if (need > ws_bytes || (need && !ws))
+    return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, need);
+  if ((N + 63) / 64 > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
   if ((size_t)K * N * 2 >= kOob || (size_t)B * K * 2 >= kOob)
     return fail(YR_E_INVALID, "%s: operands must be < 4 GiB (32-bit buffer offsets)", name);
-  for (int b0 = 0; b0 < B; b0 += 16) {
+  const bool bf = dtype == YR_DTYPE_BF16;
+  for (int b0 = 0; b0 < B; b0 += 128) {
+    const int rows = B - b0 < 128 ? B - b0 : 128;
+    const bool big = rows > 16;
+    const Plan p = big ? plan128(K, N, nmat) : plan16(K, N, nmat);
     Args a = {};
     a.x = x + (size_t)b0 * K;
     a.gamma = gamma;
@@ -364,14 +565,13 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
     a.out = out + (size_t)b0 * N;
     a.partial = (float*)((char*)ws + kTicketBytes);
     a.tickets = (uint32_t*)ws;
-    a.B = B - b0 < 16 ? B - b0 : 16;
+    a.B = rows;
     a.K = K;
     a.N = N;
     a.eps = eps;
     a.kch = p.kch;
     a.units = p.units;
-    const bool bf = dtype == YR_DTYPE_BF16;
-#define YR_SK(DTV, NM, EP) launch16<DTV, NM, EP>(a, p.tw, st)
+#define YR_SK(DTV, NM, EP) (big ? launch128<DTV, NM, EP>(a, st) : launch16<DTV, NM, EP>(a, p.tw, st))
     if (nmat == 2) {
       if (bf) YR_SK(DT_BF16, 2, EPI_GATED); else YR_SK(DT_F16, 2, EPI_GATED);
     } else if (epi == EPI_RMSNORM) {
