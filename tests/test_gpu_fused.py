@@ -137,6 +137,9 @@ def _paged_cache(B, L, Hkv, D, page, dtype, gen, pool_extra=0):
     (2, 32, 8, 1000, 64, torch.bfloat16),    # ragged tail
     (3, 8, 8, 300, 16, torch.float16),       # MHA, small pages
     (1, 16, 2, 64, 64, torch.bfloat16),      # single split
+    (2, 32, 2, 2000, 1, torch.bfloat16),     # G = 16, one token per page
+    (1, 64, 8, 777, 32, torch.float16),      # G = 8
+    (40, 32, 8, 200, 16, torch.float16),     # batch * kv heads >= CUs: one split each
 ])
 def test_gqa_decode_paged(B, Hq, Hkv, L, page, dtype):
     import yirage_amd.fused as F
@@ -149,8 +152,11 @@ def test_gqa_decode_paged(B, Hq, Hkv, L, page, dtype):
     lens = torch.full((B,), L, dtype=torch.int32)
     if B > 1:
         lens[-1] = max(1, L - 37)  # ragged lengths inside one batch
-    out = F.gqa_decode_paged(q.cuda(), kc.cuda(), vc.cuda(), indptr.cuda(), indices.cuda(), lens.cuda(), max_kv_len=L)
+    args = (q.cuda(), kc.cuda(), vc.cuda(), indptr.cuda(), indices.cuda(), lens.cuda())
+    out = F.gqa_decode_paged(*args, max_kv_len=L)
+    again = F.gqa_decode_paged(*args, max_kv_len=L)  # tickets re-armed: same bits
     torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
     ref = O.gqa_decode_paged(_f(q), _bits(kc), _bits(vc), DT[dtype], indptr.numpy(), indices.numpy(), lens.numpy())
     _close(out, ref, "gqa_decode")
 

@@ -1,13 +1,14 @@
 // GQA attention for gfx950: paged split-KV decode and causal prefill.
 //
 // Decode (HBM-bound, reads every cached K/V byte once):
-//   grid = (kv splits, kv heads, batch); one workgroup = 4 waves covers a
-//   chunk of DEC_CHUNK tokens of one (sequence, kv head) for all G = Hq/Hkv
-//   query heads of the group.  Q.K^T runs on MFMA 16x16x32 with the K rows as
-//   the B operand straight from HBM (16-byte loads, no LDS); P.V runs on VALU
-//   with lanes along head_dim.  Every wave keeps its own online-softmax state;
-//   the 4 waves merge in LDS, and splits merge through the workspace with the
-//   last-arriving workgroup (atomic ticket) writing the output.
+//   grid = (kv splits, kv heads, batch), about one workgroup per CU; one
+//   workgroup = 8 waves covers a chunk of tokens of one (sequence, kv head)
+//   for all G = Hq/Hkv query heads of the group.  Q.K^T runs on MFMA 16x16x32
+//   with the K rows as the B operand straight from HBM (16-byte loads, no
+//   LDS); P.V runs on VALU with lanes along head_dim.  Every wave streams its
+//   own 32-token blocks with an online softmax; the 8 waves merge in LDS, and
+//   splits merge through the workspace with the last-arriving workgroup
+//   (atomic ticket) writing the output.
 //
 // Prefill (MFMA-bound): flash attention, one workgroup per (64 query rows,
 //   q head, batch); K tiles and transposed V tiles are staged in LDS, S = Q K^T
@@ -19,10 +20,18 @@ namespace yr {
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- decode
-constexpr int DEC_WAVES = 4;
+// Streaming split-KV decode: grid = (splits, kv heads, batch) with about one
+// workgroup per CU in total; a workgroup (8 waves) owns `chunk` tokens of one
+// (sequence, kv head).  Its page ids are staged in LDS first, so no K/V load
+// waits on a page-table load.  Wave w streams 32-token blocks w, w + 8, ...
+// with RING blocks in flight (K as MFMA B fragments, V along head_dim), keeps
+// an online softmax per head row, and the 8 waves then the splits merge
+// (splits through fp32 records, the last workgroup to arrive writing out).
+constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * kWave;
-constexpr int DEC_TOK_PER_WAVE = 64;
-constexpr int DEC_CHUNK = DEC_WAVES * DEC_TOK_PER_WAVE;  // 256 tokens per workgroup
+constexpr int DEC_BLK = 32;        // tokens per wave block
+constexpr int DEC_MAXPG = 4096;    // page ids staged per workgroup
+constexpr int DEC_TARGET_WG = 256; // workgroups to aim for (one per CU)
 
 struct DecodeArgs {
   const uint16_t* q;       // [B][Hq][D]
@@ -34,7 +43,7 @@ struct DecodeArgs {
   uint16_t* out;           // [B][Hq][D]
   float* partial;          // [B][Hkv][splits][G][D + 2]
   uint32_t* tickets;       // [B][Hkv]
-  int B, Hq, Hkv, page, splits;
+  int B, Hq, Hkv, page, splits, chunk;
   float scale_log2;        // log2(e) / sqrt(D)
 };
 
@@ -53,127 +62,153 @@ __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
 template <int DT, int G>
 __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = 128;
+  constexpr int RING = G <= 8 ? 2 : 1;  // blocks in flight per wave
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int len = a.kv_len[b];
-  const int c0 = split * DEC_CHUNK;            // first token of this chunk
-  const int pbase = a.kv_indptr[b];
+  const int c0 = split * a.chunk, c1 = min(len, c0 + a.chunk);
   const size_t tok_stride = (size_t)a.Hkv * D;  // elements between tokens in a page
-  const size_t page_stride = (size_t)a.page * tok_stride;
 
-  __shared__ float s_p[DEC_WAVES][G][DEC_TOK_PER_WAVE];
+  __shared__ int s_pg[DEC_MAXPG];
+  __shared__ float s_p[DEC_WAVES][G][DEC_BLK];
+  __shared__ float s_alpha[DEC_WAVES][G];
   __shared__ float s_m[DEC_WAVES][G], s_l[DEC_WAVES][G];
   __shared__ float s_o[DEC_WAVES][G][D];
 
-  const int wt0 = c0 + wave * DEC_TOK_PER_WAVE;  // first token of this wave
-  auto tok_addr = [&](int t) -> size_t {
-    int pg = a.kv_indices[pbase + t / a.page];
-    return (size_t)pg * page_stride + (size_t)(t % a.page) * tok_stride + (size_t)hk * D;
-  };
-
-  // ---- issue K (MFMA B operand) and V (VALU) loads for the wave's 64 tokens
-  uint4 kf[4][4];  // [n-tile j][k-step s]
-  uint4 vf[16];    // token wt0 + lane/16 + 4i, dims (lane%16)*8 .. +8
-  {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      int t = wt0 + 16 * j + (lane % 16);
-      bool ok = t < len;
-      size_t base = ok ? tok_addr(t) : 0;
-#pragma unroll
-      for (int s = 0; s < 4; s++) {
-        int d = 32 * s + (lane / 16) * 8;
-        kf[j][s] = ok ? ldg16(a.kc + base + d) : make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      int t = wt0 + lane / 16 + 4 * i;
-      bool ok = t < len;
-      vf[i] = ok ? ldg16(a.vc + tok_addr(t) + (lane % 16) * 8) : make_uint4(0, 0, 0, 0);
-    }
-  }
-
+  // ---- page ids of this split
+  const int pg0 = c0 / a.page;
+  const int npg = c1 > c0 ? (c1 - 1) / a.page - pg0 + 1 : 0;
+  const int pbase = a.kv_indptr[b];
+  for (int i = tid; i < npg; i += DEC_THREADS) s_pg[i] = a.kv_indices[pbase + pg0 + i];
   // ---- Q as the MFMA A operand: row = head (lane%16 < G), k = d
   uint4 qf[4];
   {
-    int g = lane % 16;
-    const uint16_t* qrow = a.q + ((size_t)b * a.Hq + (size_t)hk * G + g) * D;
+    const int g = lane % 16;
+    const uint16_t* qrow = a.q + ((size_t)b * a.Hq + (size_t)hk * G + (g < G ? g : 0)) * D;
 #pragma unroll
-    for (int s = 0; s < 4; s++)
-      qf[s] = g < G ? ldg16(qrow + 32 * s + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
-  }
-
-  // ---- scores: C[head][token] for 4 n-tiles of 16 tokens
-  f32x4 sc[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; s++) c = mfma16x16x32<DT>(qf[s], kf[j][s], c);
-    sc[j] = c;
-  }
-  // lane l holds rows 4*(l/16)+i, column l%16: head g = 4*(l/16)+i
-  float mloc[4], lloc[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      int t = wt0 + 16 * j + (lane % 16);
-      float v = t < len ? sc[j][i] * a.scale_log2 : -INFINITY;
-      sc[j][i] = v;
-      m = fmaxf(m, v);
-    }
-    // max over the 16 lanes sharing l/16
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-    float l = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float p = m == -INFINITY ? 0.f : exp2f(sc[j][i] - m);
-      sc[j][i] = p;
-      l += p;
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
-    mloc[i] = m;
-    lloc[i] = l;
-    int g = 4 * (lane / 16) + i;
-    if (g < G) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) s_p[wave][g][16 * j + (lane % 16)] = sc[j][i];
-      if ((lane % 16) == 0) {
-        s_m[wave][g] = m;
-        s_l[wave][g] = l;
-      }
+    for (int s = 0; s < 4; s++) {
+      qf[s] = ldg16(qrow + 32 * s + (lane / 16) * 8);
+      if (g >= G) qf[s] = make_uint4(0, 0, 0, 0);
     }
   }
   __syncthreads();
 
-  // ---- O = P V over the wave's tokens; lane: dims (lane%16)*8.., tokens lane/16 + 4i
+  const int nblk = c1 > c0 ? (c1 - c0 + DEC_BLK - 1) / DEC_BLK : 0;
+  const int mine = nblk > wave ? (nblk - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's blocks
+  // element offset of token t (clamped into [c0, c1): finite data, masked)
+  auto tok_off = [&](int t) __attribute__((always_inline)) -> size_t {
+    t = min(max(t, c0), c1 - 1);
+    const int pg = s_pg[t / a.page - pg0];
+    return ((size_t)pg * a.page + t % a.page) * tok_stride + (size_t)hk * D;
+  };
+  struct Blk {
+    uint4 k[2][4];  // [16-token tile j][k step s]: token 16 j + lane % 16, d = 32 s + 8 (lane / 16)
+    uint4 v[8];     // token lane / 16 + 4 i, d = 8 (lane % 16)
+  };
+  auto issue = [&](Blk& bk, int j) __attribute__((always_inline)) {
+    const int tb = c0 + (wave + DEC_WAVES * j) * DEC_BLK;
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+      const size_t off = tok_off(tb + 16 * n + lane % 16) + (lane / 16) * 8;
+#pragma unroll
+      for (int s = 0; s < 4; s++) bk.k[n][s] = ldg16(a.kc + off + 32 * s);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) bk.v[i] = ldg16(a.vc + tok_off(tb + lane / 16 + 4 * i) + (lane % 16) * 8);
+  };
+
+  // online softmax state of rows 4 (lane / 16) + i, and O for this lane's dims
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
   float o[G][8];
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
     for (int e = 0; e < 8; e++) o[g][e] = 0.f;
+
+  auto consume = [&](const Blk& bk, int j) __attribute__((always_inline)) {
+    const int tb = c0 + (wave + DEC_WAVES * j) * DEC_BLK;
+    f32x4 sc[2];
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    int tl = lane / 16 + 4 * i;
-    uint32_t vw[4] = {vf[i].x, vf[i].y, vf[i].z, vf[i].w};
-    float v[8];
+    for (int n = 0; n < 2; n++) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      v[2 * e] = lo16<DT>(vw[e]);
-      v[2 * e + 1] = hi16<DT>(vw[e]);
+      for (int s = 0; s < 4; s++) c = mfma16x16x32<DT>(qf[s], bk.k[n][s], c);
+      sc[n] = c;
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int n = 0; n < 2; n++) {
+        const float v = tb + 16 * n + lane % 16 < c1 ? sc[n][i] * a.scale_log2 : -INFINITY;
+        sc[n][i] = v;
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int o2 = 8; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, kWave));
+      const float mnew = fmaxf(m_run[i], mx);
+      const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_run[i] - mnew);
+      float ls = 0.f;
+      const int g = 4 * (lane / 16) + i;
+#pragma unroll
+      for (int n = 0; n < 2; n++) {
+        const float p = mnew == -INFINITY ? 0.f : exp2f(sc[n][i] - mnew);
+        ls += p;
+        if (g < G) s_p[wave][g][16 * n + lane % 16] = p;
+      }
+#pragma unroll
+      for (int o2 = 8; o2 > 0; o2 >>= 1) ls += __shfl_xor(ls, o2, kWave);
+      l_run[i] = l_run[i] * alpha + ls;
+      m_run[i] = mnew;
+      if (g < G && (lane % 16) == 0) s_alpha[wave][g] = alpha;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes done (lgkmcnt 0)
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int g = 0; g < G; g++) {
-      float p = s_p[wave][g][tl];
+      const float al = s_alpha[wave][g];
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[g][e] = fmaf(p, v[e], o[g][e]);
+      for (int e = 0; e < 8; e++) o[g][e] *= al;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int tl = lane / 16 + 4 * i;
+      const uint32_t vw[4] = {bk.v[i].x, bk.v[i].y, bk.v[i].z, bk.v[i].w};
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = lo16<DT>(vw[e]);
+        v[2 * e + 1] = hi16<DT>(vw[e]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const float p = s_p[wave][g][tl];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[g][e] = fmaf(p, v[e], o[g][e]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // s_p / s_alpha are rewritten by the next block
+  };
+
+  if (mine > 0) {
+    Blk ring[RING];
+#pragma unroll
+    for (int r = 0; r < RING; r++) issue(ring[r], r);
+    for (int j0 = 0; j0 < mine; j0 += RING) {
+#pragma unroll
+      for (int r = 0; r < RING; r++) {
+        const int j = j0 + r;
+        if (j < mine) {
+          consume(ring[r], j);
+          issue(ring[r], j + RING);  // loads past the split are clamped, results unused
+        }
+      }
     }
   }
+
+  // ---- O over the 4 token lane groups, then the 8 waves through LDS
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
@@ -189,20 +224,29 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; e++) s_o[wave][g][lane * 8 + e] = o[g][e];
   }
+  if ((lane % 16) == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int g = 4 * (lane / 16) + i;
+      if (g < G) {
+        s_m[wave][g] = m_run[i];
+        s_l[wave][g] = l_run[i];
+      }
+    }
+  }
   __syncthreads();
 
-  // ---- merge the 4 waves: thread -> (g, d)
   const int REC = D + 2;
   float* rec_base = a.partial + (((size_t)b * a.Hkv + hk) * a.splits) * G * REC;
   for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
-    int g = idx / D, d = idx % D;
+    const int g = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; w++) M = fmaxf(M, s_m[w][g]);
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < DEC_WAVES; w++) {
-      float f = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+      const float f = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
       L += s_l[w][g] * f;
       O += s_o[w][g][d] * f;
     }
@@ -219,11 +263,11 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   }
   if (a.splits == 1) return;
 
-  // ---- split merge by the last workgroup of this (b, hk)
+  // ---- split merge by the last workgroup of this (b, hk): every record in
+  // flight at once (one thread per (g, d, split lane j of P))
   if (!arrive_last(&a.tickets[b * a.Hkv + hk], a.splits)) return;
   for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
-    int g = idx / D, d = idx % D;
-    // one pass over the splits, 16 records in flight per round trip
+    const int g = idx / D, d = idx % D;
     float M = -INFINITY, L = 0.f, O = 0.f;
     for (int s0 = 0; s0 < a.splits; s0 += 16) {
       float mv[16], lv[16], ov[16];
@@ -243,12 +287,12 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
       float mb = M;
 #pragma unroll
       for (int u = 0; u < 16; u++) mb = fmaxf(mb, mv[u]);
-      float f0 = M == -INFINITY ? 0.f : exp2f(M - mb);
+      const float f0 = M == -INFINITY ? 0.f : exp2f(M - mb);
       L *= f0;
       O *= f0;
 #pragma unroll
       for (int u = 0; u < 16; u++) {
-        float f = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mb);
+        const float f = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mb);
         L += lv[u] * f;
         O += ov[u] * f;
       }
@@ -258,8 +302,24 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   }
 }
 
-
-static int dec_splits(int max_len) { return (max_len + DEC_CHUNK - 1) / DEC_CHUNK; }
+// Splits per (sequence, kv head): about DEC_TARGET_WG workgroups in total,
+// each split a whole number of 32-token blocks.
+struct DecPlan {
+  int splits, chunk;
+};
+// A split also spans at most DEC_MAXPG - 2 pages (the staged page ids).
+static DecPlan dec_plan(int batch, int hkv, int max_len, int page) {
+  DecPlan p;
+  const int pairs = batch * hkv > 0 ? batch * hkv : 1;
+  int sp = (DEC_TARGET_WG + pairs - 1) / pairs;
+  const int maxsp = (max_len + DEC_BLK - 1) / DEC_BLK;
+  sp = sp < 1 ? 1 : sp > maxsp ? maxsp : sp;
+  p.chunk = ((max_len + sp - 1) / sp + DEC_BLK - 1) / DEC_BLK * DEC_BLK;
+  const long cap = ((long)(DEC_MAXPG - 2) * (page > 0 ? page : 1)) / DEC_BLK * DEC_BLK;
+  if (p.chunk > cap) p.chunk = (int)cap;
+  p.splits = (max_len + p.chunk - 1) / p.chunk;
+  return p;
+}
 
 // ---------------------------------------------------------------- prefill
 constexpr int PF_WAVES = 4;
@@ -456,8 +516,7 @@ using namespace yr;
 extern "C" {
 
 size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv_len, int page_size) {
-  (void)page_size;
-  int sp = dec_splits(max_kv_len);
+  int sp = dec_plan(batch, hkv, max_kv_len, page_size).splits;
   if (sp <= 1 || hkv <= 0) return 0;
   int G = hq / hkv;
   return kTicketBytes + (size_t)batch * hkv * sp * G * (d + 2) * sizeof(float);
@@ -493,7 +552,12 @@ int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_ca
   a.Hq = hq;
   a.Hkv = hkv;
   a.page = page_size;
-  a.splits = dec_splits(max_kv_len);
+  const DecPlan dp = dec_plan(batch, hkv, max_kv_len, page_size);
+  a.splits = dp.splits;
+  a.chunk = dp.chunk;
+  if (dp.chunk / page_size + 2 > DEC_MAXPG)
+    return fail(YR_E_INVALID, "%s: %d pages per split exceed %d (page_size too small)", nm, dp.chunk / page_size + 2,
+                DEC_MAXPG);
   a.tickets = (uint32_t*)workspace;
   a.partial = need ? (float*)((char*)workspace + kTicketBytes) : nullptr;
   a.scale_log2 = kLog2e / sqrtf((float)d);

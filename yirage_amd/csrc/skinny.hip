@@ -309,7 +309,7 @@ template <int DT, int NMAT, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   constexpr int TW = 64, KS = 64, MB = 128;
   constexpr int LDW = TW + 8, LDX = KS + 8;   // padded LDS rows (fewer bank conflicts)
-  constexpr int CHQ = 4;                      // chunks in flight
+  constexpr int CHQ = 3;                      // chunks in flight (measured best of 2..6)
   constexpr bool NORM = EPI == EPI_RMSNORM;
   __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][KS * LDW];
   __shared__ __attribute__((aligned(16))) uint16_t xl[2][MB * LDX];
