@@ -5,8 +5,9 @@
 //   workgroup = 8 waves covers a chunk of tokens of one (sequence, kv head)
 //   for all G = Hq/Hkv query heads of the group.  Q.K^T runs on MFMA 16x16x32
 //   with the K rows as the B operand straight from HBM (16-byte loads, no
-//   LDS); P.V runs on VALU with lanes along head_dim.  Every wave streams its
-//   own 32-token blocks with an online softmax; the 8 waves merge in LDS, and
+//   LDS); P.V runs on MFMA too, V going through LDS and coming back as B
+//   fragments by transposing reads.  Every wave streams its own 32-token
+//   blocks with an online softmax; the 8 waves merge in LDS, and
 //   splits merge through the workspace with the last-arriving workgroup
 //   (atomic ticket) writing the output.
 //
@@ -23,9 +24,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Streaming split-KV decode: grid = (splits, kv heads, batch) with about one
 // workgroup per CU in total; a workgroup (8 waves) owns `chunk` tokens of one
 // (sequence, kv head).  Its page ids are staged in LDS first, so no K/V load
-// waits on a page-table load.  Wave w streams 32-token blocks w, w + 8, ...
-// with RING blocks in flight (K as MFMA B fragments, V along head_dim), keeps
-// an online softmax per head row, and the 8 waves then the splits merge
+// waits on a page-table load.  The waves stream 32-token blocks (K straight
+// from HBM as MFMA B fragments, V through LDS), keep an online softmax per
+// head row, and the 8 waves then the splits merge
 // (splits through fp32 records, the last workgroup to arrive writing out).
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * kWave;
@@ -47,33 +48,33 @@ struct DecodeArgs {
   float scale_log2;        // log2(e) / sqrt(D)
 };
 
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
-  if constexpr (DT == DT_F16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c,
-                                                  0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b),
-                                                   c, 0, 0, 0);
-  }
-}
+#ifdef YR_DEC_PROF
+__device__ uint64_t g_dec_prof[4096 * 8];
+#define DPROF(i) \
+  if (threadIdx.x == 0) g_dec_prof[(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define DPROF(i)
+#endif
 
 // D = 128, G <= 16
 template <int DT, int G>
 __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = 128;
-  constexpr int RING = G <= 8 ? 2 : 1;  // blocks in flight per wave
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int len = a.kv_len[b];
   const int c0 = split * a.chunk, c1 = min(len, c0 + a.chunk);
   const size_t tok_stride = (size_t)a.Hkv * D;  // elements between tokens in a page
+  DPROF(0)
 
+  constexpr int LDV = D + 8;       // padded V rows: transposing reads without bank conflicts
+  constexpr int LDP = DEC_BLK + 8;
+  static_assert(G * D * 4 <= DEC_BLK * LDV * 2, "wave's O must fit its V slot");
   __shared__ int s_pg[DEC_MAXPG];
-  __shared__ float s_p[DEC_WAVES][G][DEC_BLK];
-  __shared__ float s_alpha[DEC_WAVES][G];
+  // per wave: the V block (then, after the loop, the wave's O as fp32 [G][D])
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[DEC_WAVES][DEC_BLK * LDV];
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[DEC_WAVES][16 * LDP];  // P as 16-bit [row][token]
   __shared__ float s_m[DEC_WAVES][G], s_l[DEC_WAVES][G];
-  __shared__ float s_o[DEC_WAVES][G][D];
 
   // ---- page ids of this split
   const int pg0 = c0 / a.page;
@@ -92,9 +93,9 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     }
   }
   __syncthreads();
+  DPROF(1)
 
   const int nblk = c1 > c0 ? (c1 - c0 + DEC_BLK - 1) / DEC_BLK : 0;
-  const int mine = nblk > wave ? (nblk - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's blocks
   // element offset of token t (clamped into [c0, c1): finite data, masked)
   auto tok_off = [&](int t) __attribute__((always_inline)) -> size_t {
     t = min(max(t, c0), c1 - 1);
@@ -105,8 +106,8 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     uint4 k[2][4];  // [16-token tile j][k step s]: token 16 j + lane % 16, d = 32 s + 8 (lane / 16)
     uint4 v[8];     // token lane / 16 + 4 i, d = 8 (lane % 16)
   };
-  auto issue = [&](Blk& bk, int j) __attribute__((always_inline)) {
-    const int tb = c0 + (wave + DEC_WAVES * j) * DEC_BLK;
+  auto issue = [&](Blk& bk, int blk) __attribute__((always_inline)) {
+    const int tb = c0 + blk * DEC_BLK;
 #pragma unroll
     for (int n = 0; n < 2; n++) {
       const size_t off = tok_off(tb + 16 * n + lane % 16) + (lane / 16) * 8;
@@ -117,26 +118,35 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 8; i++) bk.v[i] = ldg16(a.vc + tok_off(tb + lane / 16 + 4 * i) + (lane % 16) * 8);
   };
 
-  // online softmax state of rows 4 (lane / 16) + i, and O for this lane's dims
+  // online softmax state of rows 4 (lane / 16) + i; O in the MFMA C layout:
+  // o[n][i] = row 4 (lane / 16) + i, dim 16 n + lane % 16
   float m_run[4], l_run[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
-  float o[G][8];
+  f32x4 o[D / 16];
 #pragma unroll
-  for (int g = 0; g < G; g++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[g][e] = 0.f;
+  for (int n = 0; n < D / 16; n++) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint16_t* vs = s_v[wave];
+  uint16_t* ps = s_p[wave];
 
-  auto consume = [&](const Blk& bk, int j) __attribute__((always_inline)) {
-    const int tb = c0 + (wave + DEC_WAVES * j) * DEC_BLK;
+  // S = Q K^T and P V both on MFMA 16x16x32.  P goes through LDS as 16-bit
+  // values (the A operand wants 8 consecutive tokens per lane), V through LDS
+  // unchanged and comes back as B fragments by transposing reads.  Rows past G
+  // hold finite values from zero Q rows and are never written out.
+  auto consume = [&](const Blk& bk, int blk) __attribute__((always_inline)) {
+    const int tb = c0 + blk * DEC_BLK;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      *reinterpret_cast<uint4*>(vs + (lane / 16 + 4 * i) * LDV + (lane % 16) * 8) = bk.v[i];
     f32x4 sc[2];
 #pragma unroll
     for (int n = 0; n < 2; n++) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; s++) c = mfma16x16x32<DT>(qf[s], bk.k[n][s], c);
+      for (int s = 0; s < 4; s++) c = mfma16<DT>(qf[s], bk.k[n][s], c);
       sc[n] = c;
     }
+    float alpha[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       float mx = -INFINITY;
@@ -149,88 +159,65 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int o2 = 8; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, kWave));
       const float mnew = fmaxf(m_run[i], mx);
-      const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_run[i] - mnew);
+      alpha[i] = mnew == -INFINITY ? 1.f : exp2f(m_run[i] - mnew);
       float ls = 0.f;
-      const int g = 4 * (lane / 16) + i;
+      const int r = 4 * (lane / 16) + i;
 #pragma unroll
       for (int n = 0; n < 2; n++) {
-        const float p = mnew == -INFINITY ? 0.f : exp2f(sc[n][i] - mnew);
-        ls += p;
-        if (g < G) s_p[wave][g][16 * n + lane % 16] = p;
+        const float p = round_to<DT>(mnew == -INFINITY ? 0.f : exp2f(sc[n][i] - mnew));
+        ls += p;  // the sum uses the same rounded P as P V
+        ps[r * LDP + 16 * n + lane % 16] = (uint16_t)st_elem<DT>(p);
       }
 #pragma unroll
       for (int o2 = 8; o2 > 0; o2 >>= 1) ls += __shfl_xor(ls, o2, kWave);
-      l_run[i] = l_run[i] * alpha + ls;
+      l_run[i] = l_run[i] * alpha[i] + ls;
       m_run[i] = mnew;
-      if (g < G && (lane % 16) == 0) s_alpha[wave][g] = alpha;
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes done (lgkmcnt 0)
-    __builtin_amdgcn_wave_barrier();
+    // LDS operations of one wave complete in order; the asm keeps the
+    // compiler from moving the reads above the writes.
+    asm volatile("" ::: "memory");
+    const uint4 pa = *reinterpret_cast<const uint4*>(ps + (lane % 16) * LDP + (lane / 16) * 8);
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      const float al = s_alpha[wave][g];
+    for (int n = 0; n < D / 16; n++) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) o[g][e] *= al;
+      for (int i = 0; i < 4; i++) o[n][i] *= alpha[i];
+      o[n] = mfma16<DT>(pa, b_frag(vs + 16 * n, LDV, 0, lane), o[n]);
     }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int tl = lane / 16 + 4 * i;
-      const uint32_t vw[4] = {bk.v[i].x, bk.v[i].y, bk.v[i].z, bk.v[i].w};
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        v[2 * e] = lo16<DT>(vw[e]);
-        v[2 * e + 1] = hi16<DT>(vw[e]);
-      }
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        const float p = s_p[wave][g][tl];
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[g][e] = fmaf(p, v[e], o[g][e]);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();  // s_p / s_alpha are rewritten by the next block
+    asm volatile("" ::: "memory");  // the next block's writes stay after these reads
   };
 
-  if (mine > 0) {
-    Blk ring[RING];
-#pragma unroll
-    for (int r = 0; r < RING; r++) issue(ring[r], r);
-    for (int j0 = 0; j0 < mine; j0 += RING) {
-#pragma unroll
-      for (int r = 0; r < RING; r++) {
-        const int j = j0 + r;
-        if (j < mine) {
-          consume(ring[r], j);
-          issue(ring[r], j + RING);  // loads past the split are clamped, results unused
-        }
-      }
+  // Wave w takes blocks w, w + 8, ... (a fixed order, so results do not
+  // depend on timing).  One block in flight per wave: with every workgroup
+  // resident that is ~64 MiB queued at once, and deeper queues only lengthen
+  // the tail.
+  int cur = wave;
+  if (cur < nblk) {
+    Blk bk;
+    issue(bk, cur);
+    bool first = true;
+    for (;;) {
+      const int nxt = cur + DEC_WAVES;
+      consume(bk, cur);
+      if (first) DPROF(2)
+      first = false;
+      if (nxt >= nblk) break;
+      issue(bk, nxt);
+      cur = nxt;
     }
   }
 
-  // ---- O over the 4 token lane groups, then the 8 waves through LDS
+  DPROF(3)
+  // ---- the 8 waves merge through LDS (O over the wave's own V slot)
+  float* os = reinterpret_cast<float*>(vs);
 #pragma unroll
-  for (int g = 0; g < G; g++)
+  for (int i = 0; i < 4; i++) {
+    const int r = 4 * (lane / 16) + i;
+    if (r < G) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      float x = o[g][e];
-      x += __shfl_xor(x, 16, kWave);
-      x += __shfl_xor(x, 32, kWave);
-      o[g][e] = x;
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) s_o[wave][g][lane * 8 + e] = o[g][e];
-  }
-  if ((lane % 16) == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int g = 4 * (lane / 16) + i;
-      if (g < G) {
-        s_m[wave][g] = m_run[i];
-        s_l[wave][g] = l_run[i];
+      for (int n = 0; n < D / 16; n++) os[r * D + 16 * n + lane % 16] = o[n][i];
+      if ((lane % 16) == 0) {
+        s_m[wave][r] = m_run[i];
+        s_l[wave][r] = l_run[i];
       }
     }
   }
@@ -248,7 +235,7 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     for (int w = 0; w < DEC_WAVES; w++) {
       const float f = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
       L += s_l[w][g] * f;
-      O += s_o[w][g][d] * f;
+      O += reinterpret_cast<const float*>(s_v[w])[g * D + d] * f;
     }
     if (a.splits == 1) {
       a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
@@ -261,11 +248,13 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
       }
     }
   }
+  DPROF(4)
   if (a.splits == 1) return;
 
   // ---- split merge by the last workgroup of this (b, hk): every record in
   // flight at once (one thread per (g, d, split lane j of P))
   if (!arrive_last(&a.tickets[b * a.Hkv + hk], a.splits)) return;
+  DPROF(5)
   for (int idx = tid; idx < G * D; idx += DEC_THREADS) {
     const int g = idx / D, d = idx % D;
     float M = -INFINITY, L = 0.f, O = 0.f;
@@ -300,6 +289,7 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     }
     a.out[((size_t)b * a.Hq + (size_t)hk * G + g) * D + d] = (uint16_t)st_elem<DT>(L > 0.f ? O / L : 0.f);
   }
+  DPROF(6)
 }
 
 // Splits per (sequence, kv head): about DEC_TARGET_WG workgroups in total,
@@ -403,7 +393,7 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
 #pragma unroll
       for (int s = 0; s < 4; s++) {
         uint4 kb = *reinterpret_cast<const uint4*>(&sk[(16 * j + lane % 16) * KP + 32 * s + (lane / 16) * 8]);
-        c = mfma16x16x32<DT>(qf[s], kb, c);
+        c = mfma16<DT>(qf[s], kb, c);
       }
       s4[j] = c;
     }
@@ -451,7 +441,7 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
 #pragma unroll
       for (int n = 0; n < 8; n++) {
         uint4 vb = *reinterpret_cast<const uint4*>(&svt[(16 * n + lane % 16) * VP + 32 * ks + (lane / 16) * 8]);
-        acc[n] = mfma16x16x32<DT>(pa, vb, acc[n]);
+        acc[n] = mfma16<DT>(pa, vb, acc[n]);
       }
     }
   }
@@ -614,5 +604,11 @@ int yr_hip_argmax(const void* x, int64_t* out, int rows, int n, int n_valid, int
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
 }
+
+#ifdef YR_DEC_PROF
+int yr_dec_prof_read(void* host) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(yr::g_dec_prof), sizeof(yr::g_dec_prof)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 }  // extern "C"

@@ -48,35 +48,6 @@ struct Args {
 __device__ __forceinline__ int unit_lo(int v, int U, int G) { return (int)(((long long)v * U) / G); }
 __device__ __forceinline__ int owner_of(int u, int U, int G) { return (int)(((long long)(u + 1) * G - 1) / U); }
 
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-// B fragment of a 32 x 16 block of a row-major [rows][ld] bf16/f16 tile in
-// LDS whose first row is `row0`.
-__device__ __forceinline__ uint4 b_frag(const uint16_t* tile, int ld, int row0, int lane) {
-  const int g = lane >> 4, j = lane & 15, e = j >> 2, q = j & 3;
-  const uint16_t* p0 = tile + (row0 + 8 * g + e) * ld + 4 * q;
-  const uint16_t* p1 = p0 + 4 * ld;
-  auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
-    return reinterpret_cast<const lds_v4i16*>(
-        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
-            reinterpret_cast<uintptr_t>(p)));
-  };
-  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p0)));
-  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p1)));
-  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-  return make_uint4(l2.x, l2.y, h2.x, h2.y);
-}
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
-  if constexpr (DT == DT_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
-                                                   0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
-                                                  0, 0);
-}
 
 // 16-byte loads through a buffer descriptor: an offset at or past `bytes`
 // returns zero without a memory access, so bounds checks need no branch (a
@@ -309,7 +280,7 @@ template <int DT, int NMAT, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   constexpr int TW = 64, KS = 64, MB = 128;
   constexpr int LDW = TW + 8, LDX = KS + 8;   // padded LDS rows (fewer bank conflicts)
-  constexpr int CHQ = 3;                      // chunks in flight (measured best of 2..6)
+  constexpr int CHQ = 2;                      // chunks in flight (2 measured best of 2, 3, 4, 6)
   constexpr bool NORM = EPI == EPI_RMSNORM;
   __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][KS * LDW];
   __shared__ __attribute__((aligned(16))) uint16_t xl[2][MB * LDX];
@@ -369,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   for (int c0 = 0; c0 < nchunks; c0 += CHQ) {
 #pragma unroll
     for (int j = 0; j < CHQ; j++) {
-      const int ci = c0 + j, lb = j & 1;
+      const int ci = c0 + j, lb = ci & 1;  // LDS stages alternate per chunk
       Chunk& c = ring[j];
       // stage chunk ci (x scaled by gamma for RMSNorm, row sums first)
 #pragma unroll

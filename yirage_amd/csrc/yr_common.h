@@ -207,6 +207,39 @@ __device__ __forceinline__ void sum_records(const float* base, int S, int rec, f
   }
 }
 
+// ---------------------------------------------------------------- MFMA operands
+// ds_read_b64_tr_b16: within a 16-lane group, lane i element e of the result
+// is element i % 4 of the 64-bit row that lane 4e + i / 4 addressed.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// B fragment of a 32 x 16 block of a row-major [rows][ld] bf16/f16 tile in
+// LDS whose first row is `row0`.
+__device__ __forceinline__ uint4 b_frag(const uint16_t* tile, int ld, int row0, int lane) {
+  const int g = lane >> 4, j = lane & 15, e = j >> 2, q = j & 3;
+  const uint16_t* p0 = tile + (row0 + 8 * g + e) * ld + 4 * q;
+  const uint16_t* p1 = p0 + 4 * ld;
+  auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
+    return reinterpret_cast<const lds_v4i16*>(
+        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+            reinterpret_cast<uintptr_t>(p)));
+  };
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p0)));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(cast(p1)));
+  const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+  return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
+                                                  0, 0);
+}
+
 __host__ __device__ constexpr int round_up4(int x) { return (x + 3) & ~3; }
 
 __device__ __forceinline__ float silu(float a) { return a / (1.0f + __expf(-a)); }
