@@ -161,14 +161,20 @@ def test_gqa_decode_paged(B, Hq, Hkv, L, page, dtype):
     _close(out, ref, "gqa_decode")
 
 
-@pytest.mark.parametrize("S,causal,dtype", [(2048, True, torch.bfloat16), (300, True, torch.float16),
-                                            (200, False, torch.bfloat16)])
-def test_gqa_prefill(S, causal, dtype):
+@pytest.mark.parametrize("S,causal,dtype,B,Hq,Hkv", [
+    (2048, True, torch.bfloat16, 1, 32, 8),
+    (300, True, torch.float16, 1, 32, 8),    # odd block count: the middle block runs alone
+    (200, False, torch.bfloat16, 1, 32, 8),
+    (300, True, torch.float16, 1, 8, 8),     # MHA (one head per wave)
+    (130, True, torch.bfloat16, 2, 6, 2),    # odd group size, batch 2
+    (77, False, torch.float16, 2, 4, 1),
+])
+def test_gqa_prefill(S, causal, dtype, B, Hq, Hkv):
     import yirage_amd.fused as F
 
-    print(f"case gqa_prefill S={S} causal={causal} {dtype}", flush=True)
+    print(f"case gqa_prefill S={S} causal={causal} {dtype} B={B} Hq={Hq} Hkv={Hkv}", flush=True)
     g = torch.Generator().manual_seed(0)
-    B, Hq, Hkv, D = 1, 32, 8, 128
+    D = 128
     q = _randn((B, S, Hq, D), 1.0, dtype, g)
     k = _randn((B, S, Hkv, D), 1.0, dtype, g)
     v = _randn((B, S, Hkv, D), 1.0, dtype, g)

@@ -312,9 +312,23 @@ static DecPlan dec_plan(int batch, int hkv, int max_len, int page) {
 }
 
 // ---------------------------------------------------------------- prefill
+// Flash attention computed transposed: S^T = K Q^T and O^T += V^T P^T on
+// MFMA 16x16x32, so a lane of the S^T accumulator holds one query row (its
+// column) and 16 tokens of each 64-token tile:
+//   * the softmax row max / sum is an in-register reduction plus two shuffles;
+//   * P^T is the B operand of P V straight from registers: MFMA only needs the
+//     k order of A and B to agree, so lane group h's k slots 8h + 4j + i carry
+//     tokens 16 j + 4h + i of each 32-token step (j, i < 2, 4);
+//   * V^T (the A operand) comes from the row-major V tile in LDS by
+//     transposing reads, addressed for that same token order.
+// A workgroup (4 waves x 16 query rows) serves HPW heads of one kv group, so
+// each K / V fragment read from LDS feeds HPW MFMAs.  K / V tiles are double
+// buffered in LDS (one barrier per tile).  For causal attention a workgroup
+// takes the query blocks i and N - 1 - i, so every workgroup does the same
+// amount of work.
 constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = PF_WAVES * kWave;
-constexpr int PF_QROWS = 16 * PF_WAVES;  // 64 query rows per workgroup
+constexpr int PF_QROWS = 16 * PF_WAVES;  // 64 query rows per block
 constexpr int PF_KT = 64;                // kv tokens per tile
 
 struct PrefillArgs {
@@ -322,138 +336,180 @@ struct PrefillArgs {
   const uint16_t* k;  // [B][S][Hkv][D]
   const uint16_t* v;
   uint16_t* o;
-  int B, S, Hq, Hkv, causal;
+  int B, S, Hq, Hkv, causal, nblk;
+  int paired;  // blocks (i, nblk - 1 - i) per workgroup (causal)
   float scale_log2;
 };
 
-template <int DT>
+// 4 consecutive 16-bit elements from LDS, transposed across each 16-lane group
+__device__ __forceinline__ uint2 lds_tr4(const uint16_t* p) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(
+      reinterpret_cast<const lds_v4i16*>(reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+          reinterpret_cast<uintptr_t>(p)))));
+  return __builtin_bit_cast(uint2, r);
+}
+
+template <int DT, int HPW>
 __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) {
   constexpr int D = 128;
-  // LDS: K tile [64 tok][128 d] (row pad 8 elems), V^T tile [128 d][64 tok] (pad 8)
-  constexpr int KP = D + 8, VP = PF_KT + 8;
-  __shared__ __align__(16) uint16_t sk[PF_KT * KP];
-  __shared__ __align__(16) uint16_t svt[D * VP];
-  __shared__ __align__(16) uint16_t sp[PF_WAVES][16 * (PF_KT + 8)];
+  constexpr int LDK = D + 8;  // padded rows (16 B): conflict-free b128 and transposing reads
+  __shared__ __attribute__((aligned(16))) uint16_t sk[2][PF_KT * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sv[2][PF_KT * LDK];
 
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int G = a.Hq / a.Hkv, hk = h / G;
+  const int pair = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
+  const int G = a.Hq / a.Hkv;
+  const int h0 = hg * HPW, hk = h0 / G;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int q0 = qt * PF_QROWS + wave * 16;  // first query row of this wave
+  const int col = lane % 16, grp = lane / 16;
   const size_t qstride = (size_t)a.Hq * D, kstride = (size_t)a.Hkv * D;
+  const uint16_t* kbase = a.k + (size_t)b * a.S * kstride + (size_t)hk * D;
+  const uint16_t* vbase = a.v + (size_t)b * a.S * kstride + (size_t)hk * D;
+  // staging: thread -> token tid / 16 (+16 per step), d chunk 8 (tid % 16)
+  const int st_tok = tid / 16, st_d = 8 * (tid % 16);
 
-  // Q fragments (A operand): row q0 + lane%16, d = 32 s + 8 (lane/16)
-  uint4 qf[4];
-  {
-    int r = q0 + lane % 16;
-    const uint16_t* qrow = a.q + ((size_t)b * a.S + r) * qstride + (size_t)h * D;
+  for (int pass = 0; pass < (a.paired ? 2 : 1); pass++) {
+    const int blk = pass == 0 ? pair : a.nblk - 1 - pair;
+    if (pass == 1 && blk <= pair) break;  // the middle block of an odd count runs once
+    const int q0 = blk * PF_QROWS + wave * 16;  // this wave's first query row
+    const int qr = q0 + col;                    // this lane's query row
+    // Q^T as the B operand: column = query row, k = d 32 s + 8 grp .. +7
+    uint4 qf[HPW][4];
 #pragma unroll
-    for (int s = 0; s < 4; s++)
-      qf[s] = r < a.S ? ldg16(qrow + 32 * s + (lane / 16) * 8) : make_uint4(0, 0, 0, 0);
-  }
-  f32x4 acc[8];  // O[16 rows][128 d] as 8 n-tiles of 16 d
+    for (int hh = 0; hh < HPW; hh++) {
+      const uint16_t* qrow = a.q + ((size_t)b * a.S + min(qr, a.S - 1)) * qstride + (size_t)(h0 + hh) * D;
 #pragma unroll
-  for (int n = 0; n < 8; n++) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_i[4], l_i[4];  // rows 4*(lane/16)+i of the wave's 16
+      for (int s = 0; s < 4; s++) qf[hh][s] = ldg16(qrow + 32 * s + 8 * grp);
+    }
+    f32x4 acc[HPW][D / 16];  // O^T: rows d 16 dt + 4 grp + i, column = query row
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    m_i[i] = -INFINITY;
-    l_i[i] = 0.f;
-  }
+    for (int hh = 0; hh < HPW; hh++)
+#pragma unroll
+      for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_i[HPW], l_i[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+      m_i[hh] = -INFINITY;
+      l_i[hh] = 0.f;
+    }
 
-  const int wg_last_row = (qt + 1) * PF_QROWS - 1;
-  const int kv_end = a.causal ? min(a.S, wg_last_row + 1) : a.S;
-  for (int t0 = 0; t0 < kv_end; t0 += PF_KT) {
+    const int kv_end = a.causal ? min(a.S, (blk + 1) * PF_QROWS) : a.S;
+    const int ntile = (kv_end + PF_KT - 1) / PF_KT;
+    uint4 kr[4], vr[4];
+    auto fetch = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int tok = min(t * PF_KT + st_tok + 16 * r, a.S - 1);  // clamped rows are masked
+        kr[r] = ldg16(kbase + (size_t)tok * kstride + st_d);
+        vr[r] = ldg16(vbase + (size_t)tok * kstride + st_d);
+      }
+    };
+    auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        *reinterpret_cast<uint4*>(&sk[buf][(st_tok + 16 * r) * LDK + st_d]) = kr[r];
+        *reinterpret_cast<uint4*>(&sv[buf][(st_tok + 16 * r) * LDK + st_d]) = vr[r];
+      }
+    };
+    __syncthreads();  // the previous pass's last tile has been read by every wave
+    fetch(0);
+    stage(0);
     __syncthreads();
-    // stage K tile (row-major) and V tile (transposed) : 64 tok x 128 d each
-    for (int c = tid; c < PF_KT * (D / 8); c += PF_THREADS) {
-      int tr = c / (D / 8), dc = (c % (D / 8)) * 8;
-      int t = t0 + tr;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (t < a.S) {
-        size_t off = ((size_t)b * a.S + t) * kstride + (size_t)hk * D + dc;
-        kv = ldg16(a.k + off);
-        vv = ldg16(a.v + off);
-      }
-      *reinterpret_cast<uint4*>(&sk[tr * KP + dc]) = kv;
-      uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+    for (int t = 0; t < ntile; t++) {
+      const int buf = t & 1, t0 = t * PF_KT;
+      if (t + 1 < ntile) fetch(t + 1);
+      if (!a.causal || t0 <= q0 + 15) {
+        const uint16_t* kt = sk[buf];
+        const uint16_t* vt = sv[buf];
+        // S^T = K Q^T: 4 blocks of 16 tokens; lane holds tokens t0 + 16 n + 4 grp + i
+        f32x4 sc[HPW][4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        svt[(dc + 2 * e) * VP + tr] = (uint16_t)(vw[e] & 0xffff);
-        svt[(dc + 2 * e + 1) * VP + tr] = (uint16_t)(vw[e] >> 16);
+        for (int n = 0; n < 4; n++) {
+          uint4 kf[4];
+#pragma unroll
+          for (int s = 0; s < 4; s++)
+            kf[s] = *reinterpret_cast<const uint4*>(&kt[(16 * n + col) * LDK + 32 * s + 8 * grp]);
+#pragma unroll
+          for (int hh = 0; hh < HPW; hh++) {
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; s++) c = mfma16<DT>(kf[s], qf[hh][s], c);
+            sc[hh][n] = c;
+          }
+        }
+        // online softmax of this lane's query row
+        uint4 pb[HPW][2];  // P^T B operands for the two 32-token steps
+#pragma unroll
+        for (int hh = 0; hh < HPW; hh++) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const int tok = t0 + 16 * n + 4 * grp + i;
+              const bool ok = tok < a.S && (!a.causal || tok <= qr);
+              const float v = ok ? sc[hh][n][i] * a.scale_log2 : -INFINITY;
+              sc[hh][n][i] = v;
+              mx = fmaxf(mx, v);
+            }
+          mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+          const float mnew = fmaxf(m_i[hh], mx);
+          const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[hh] - mnew);
+          float ls = 0.f;
+          float pv[4][4];
+#pragma unroll
+          for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const float p = round_to<DT>(mnew == -INFINITY ? 0.f : exp2f(sc[hh][n][i] - mnew));
+              pv[n][i] = p;
+              ls += p;
+            }
+          ls += __shfl_xor(ls, 16, kWave);
+          ls += __shfl_xor(ls, 32, kWave);
+          l_i[hh] = l_i[hh] * alpha + ls;
+          m_i[hh] = mnew;
+#pragma unroll
+          for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] *= alpha;
+          // k slot 8 grp + 4 j + i of step m <-> token 32 m + 16 j + 4 grp + i
+#pragma unroll
+          for (int m = 0; m < 2; m++)
+            pb[hh][m] = make_uint4(pack2<DT>(pv[2 * m][0], pv[2 * m][1]), pack2<DT>(pv[2 * m][2], pv[2 * m][3]),
+                                   pack2<DT>(pv[2 * m + 1][0], pv[2 * m + 1][1]),
+                                   pack2<DT>(pv[2 * m + 1][2], pv[2 * m + 1][3]));
+        }
+        // O^T += V^T P^T.  V^T fragment (rows d 16 dt + col, k slots as above):
+        // lane 4e + q of group grp reads tokens 32 m + 16 j + 4 grp + e,
+        // d 16 dt + 4 q .. +3; the transposing read hands lane col its d.
+        const int e = col / 4, qd = 4 * (col % 4);
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+          for (int dt = 0; dt < D / 16; dt++) {
+            const uint2 lo = lds_tr4(&vt[(32 * m + 4 * grp + e) * LDK + 16 * dt + qd]);
+            const uint2 hi = lds_tr4(&vt[(32 * m + 16 + 4 * grp + e) * LDK + 16 * dt + qd]);
+            const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+            for (int hh = 0; hh < HPW; hh++) acc[hh][dt] = mfma16<DT>(vf, pb[hh][m], acc[hh][dt]);
+          }
+      }
+      if (t + 1 < ntile) stage(buf ^ 1);
+      __syncthreads();
+    }
+    // O[query row][d 16 dt + 4 grp + i]
+    if (qr < a.S) {
+#pragma unroll
+      for (int hh = 0; hh < HPW; hh++) {
+        const float inv = l_i[hh] > 0.f ? 1.f / l_i[hh] : 0.f;
+        uint16_t* orow = a.o + ((size_t)b * a.S + qr) * qstride + (size_t)(h0 + hh) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+          const f32x4 v = acc[hh][dt];
+          *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * grp) =
+              make_uint2(pack2<DT>(v[0] * inv, v[1] * inv), pack2<DT>(v[2] * inv, v[3] * inv));
+        }
       }
     }
-    __syncthreads();
-    if (a.causal && t0 > q0 + 15) continue;  // whole tile masked for this wave
-
-    // S = Q K^T : 4 n-tiles of 16 tokens
-    f32x4 s4[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; s++) {
-        uint4 kb = *reinterpret_cast<const uint4*>(&sk[(16 * j + lane % 16) * KP + 32 * s + (lane / 16) * 8]);
-        c = mfma16<DT>(qf[s], kb, c);
-      }
-      s4[j] = c;
-    }
-    // online softmax per row (row = 4*(lane/16)+i, col = token 16 j + lane%16)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int r = q0 + 4 * (lane / 16) + i;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        int t = t0 + 16 * j + lane % 16;
-        bool ok = t < a.S && (!a.causal || t <= r);
-        float v = ok ? s4[j][i] * a.scale_log2 : -INFINITY;
-        s4[j][i] = v;
-        mx = fmaxf(mx, v);
-      }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-      float mnew = fmaxf(m_i[i], mx);
-      float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[i] - mnew);
-      float ls = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float p = mnew == -INFINITY ? 0.f : exp2f(s4[j][i] - mnew);
-        s4[j][i] = p;
-        ls += p;
-      }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) ls += __shfl_xor(ls, o, kWave);
-      l_i[i] = l_i[i] * alpha + ls;
-      m_i[i] = mnew;
-#pragma unroll
-      for (int n = 0; n < 8; n++) acc[n][i] *= alpha;
-      // P (rounded to the input dtype) to LDS as [row][token]
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        sp[wave][(4 * (lane / 16) + i) * (PF_KT + 8) + 16 * j + lane % 16] = (uint16_t)st_elem<DT>(s4[j][i]);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes of this wave done
-    __builtin_amdgcn_wave_barrier();
-    // O += P V : A = P[16 rows][32 tok] (lane: row lane%16, tok 8(lane/16)..), B = V[32 tok][16 d]
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      uint4 pa = *reinterpret_cast<const uint4*>(&sp[wave][(lane % 16) * (PF_KT + 8) + 32 * ks + (lane / 16) * 8]);
-#pragma unroll
-      for (int n = 0; n < 8; n++) {
-        uint4 vb = *reinterpret_cast<const uint4*>(&svt[(16 * n + lane % 16) * VP + 32 * ks + (lane / 16) * 8]);
-        acc[n] = mfma16<DT>(pa, vb, acc[n]);
-      }
-    }
-  }
-  // write O rows 4*(lane/16)+i, d = 16 n + lane%16
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    int r = q0 + 4 * (lane / 16) + i;
-    if (r >= a.S) continue;
-    float inv = l_i[i] > 0.f ? 1.f / l_i[i] : 0.f;
-    uint16_t* orow = a.o + ((size_t)b * a.S + r) * qstride + (size_t)h * D;
-#pragma unroll
-    for (int n = 0; n < 8; n++) orow[16 * n + lane % 16] = (uint16_t)st_elem<DT>(acc[n][i] * inv);
   }
 }
 
@@ -581,11 +637,21 @@ int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, i
   a.Hq = hq;
   a.Hkv = hkv;
   a.causal = causal ? 1 : 0;
+  a.nblk = (seq + PF_QROWS - 1) / PF_QROWS;
   a.scale_log2 = kLog2e / sqrtf((float)d);
-  dim3 grid((seq + PF_QROWS - 1) / PF_QROWS, hq, batch);
+  const int hpw = (hq / hkv) % 2 == 0 ? 2 : 1;
+  // causal: block pairs (i, nblk - 1 - i) per workgroup; full: one block each
+  a.paired = a.causal;
+  dim3 grid(a.paired ? (a.nblk + 1) / 2 : a.nblk, hq / hpw, batch);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL(gqa_prefill_kernel<DT_F16>, grid, dim3(PF_THREADS), 0, st, a);
-  else hipLaunchKernelGGL(gqa_prefill_kernel<DT_BF16>, grid, dim3(PF_THREADS), 0, st, a);
+  const bool bf = dtype == YR_DTYPE_BF16;
+  if (hpw == 2) {
+    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, 2>), grid, dim3(PF_THREADS), 0, st, a);
+    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, 2>), grid, dim3(PF_THREADS), 0, st, a);
+  } else {
+    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, 1>), grid, dim3(PF_THREADS), 0, st, a);
+    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, 1>), grid, dim3(PF_THREADS), 0, st, a);
+  }
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
 }
