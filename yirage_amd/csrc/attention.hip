@@ -330,6 +330,7 @@ constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = PF_WAVES * kWave;
 constexpr int PF_QROWS = 16 * PF_WAVES;  // 64 query rows per block
 constexpr int PF_KT = 64;                // kv tokens per tile
+constexpr float kLazy = 8.f;             // running-max slack (log2 units)
 
 struct PrefillArgs {
   const uint16_t* q;  // [B][S][Hq][D]
@@ -396,11 +397,20 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
     const int ntile = (kv_end + PF_KT - 1) / PF_KT;
     uint4 kr[4], vr[4];
     auto fetch = [&](int t) __attribute__((always_inline)) {
+      if ((t + 1) * PF_KT <= a.S) {
+        const size_t off = (size_t)(t * PF_KT + st_tok) * kstride + st_d;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int tok = min(t * PF_KT + st_tok + 16 * r, a.S - 1);  // clamped rows are masked
-        kr[r] = ldg16(kbase + (size_t)tok * kstride + st_d);
-        vr[r] = ldg16(vbase + (size_t)tok * kstride + st_d);
+        for (int r = 0; r < 4; r++) {
+          kr[r] = ldg16(kbase + off + (size_t)(16 * r) * kstride);
+          vr[r] = ldg16(vbase + off + (size_t)(16 * r) * kstride);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int tok = min(t * PF_KT + st_tok + 16 * r, a.S - 1);  // clamped rows are masked
+          kr[r] = ldg16(kbase + (size_t)tok * kstride + st_d);
+          vr[r] = ldg16(vbase + (size_t)tok * kstride + st_d);
+        }
       }
     };
     auto stage = [&](int buf) __attribute__((always_inline)) {
@@ -436,41 +446,55 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
             sc[hh][n] = c;
           }
         }
-        // online softmax of this lane's query row
+        // online softmax of this lane's query row.  The running max only moves
+        // when it grows by more than kLazy (log2 units): P stays <= 2^kLazy,
+        // exact after the final 1 / l, and the O rescale is skipped by the
+        // whole wave on most tiles.
+        const bool edge = (a.causal && t0 + PF_KT - 1 > q0) || t0 + PF_KT > a.S;
         uint4 pb[HPW][2];  // P^T B operands for the two 32-token steps
 #pragma unroll
         for (int hh = 0; hh < HPW; hh++) {
+#pragma unroll
+          for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sc[hh][n][i] *= a.scale_log2;
+          if (edge) {
+#pragma unroll
+            for (int n = 0; n < 4; n++)
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                const int tok = t0 + 16 * n + 4 * grp + i;
+                if (tok >= a.S || (a.causal && tok > qr)) sc[hh][n][i] = -INFINITY;
+              }
+          }
           float mx = -INFINITY;
 #pragma unroll
           for (int n = 0; n < 4; n++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const int tok = t0 + 16 * n + 4 * grp + i;
-              const bool ok = tok < a.S && (!a.causal || tok <= qr);
-              const float v = ok ? sc[hh][n][i] * a.scale_log2 : -INFINITY;
-              sc[hh][n][i] = v;
-              mx = fmaxf(mx, v);
-            }
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[hh][n][i]);
           mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
           mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-          const float mnew = fmaxf(m_i[hh], mx);
-          const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[hh] - mnew);
+          const bool grow = mx > m_i[hh] + kLazy;
+          if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float mnew = grow ? mx : m_i[hh];
+            const float alpha = m_i[hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i[hh] - mnew);
+            m_i[hh] = mnew;
+            l_i[hh] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] *= alpha;
+          }
+          const float mref = m_i[hh] == -INFINITY ? 0.f : m_i[hh];  // all -inf so far: P = 0
           float ls = 0.f;
           float pv[4][4];
 #pragma unroll
           for (int n = 0; n < 4; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-              const float p = round_to<DT>(mnew == -INFINITY ? 0.f : exp2f(sc[hh][n][i] - mnew));
+              const float p = __builtin_amdgcn_exp2f(sc[hh][n][i] - mref);
               pv[n][i] = p;
               ls += p;
             }
-          ls += __shfl_xor(ls, 16, kWave);
-          ls += __shfl_xor(ls, 32, kWave);
-          l_i[hh] = l_i[hh] * alpha + ls;
-          m_i[hh] = mnew;
-#pragma unroll
-          for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] *= alpha;
+          l_i[hh] += ls;  // per lane; the four lane groups add up at the end
           // k slot 8 grp + 4 j + i of step m <-> token 32 m + 16 j + 4 grp + i
 #pragma unroll
           for (int m = 0; m < 2; m++)
@@ -497,6 +521,11 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
       __syncthreads();
     }
     // O[query row][d 16 dt + 4 grp + i]
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) {
+      l_i[hh] += __shfl_xor(l_i[hh], 16, kWave);
+      l_i[hh] += __shfl_xor(l_i[hh], 32, kWave);
+    }
     if (qr < a.S) {
 #pragma unroll
       for (int hh = 0; hh < HPW; hh++) {
@@ -639,7 +668,11 @@ int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, i
   a.causal = causal ? 1 : 0;
   a.nblk = (seq + PF_QROWS - 1) / PF_QROWS;
   a.scale_log2 = kLog2e / sqrtf((float)d);
+#ifdef YR_PF_HPW
+  const int hpw = (hq / hkv) % YR_PF_HPW == 0 ? YR_PF_HPW : 1;
+#else
   const int hpw = (hq / hkv) % 2 == 0 ? 2 : 1;
+#endif
   // causal: block pairs (i, nblk - 1 - i) per workgroup; full: one block each
   a.paired = a.causal;
   dim3 grid(a.paired ? (a.nblk + 1) / 2 : a.nblk, hq / hpw, batch);
