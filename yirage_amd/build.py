@@ -35,6 +35,13 @@ FLAGS = [
     "-I", os.path.join(ROOT, "include"),
 ]
 
+# Per-source extra flags.  Attention keeps MFMA accumulators in VGPRs: its
+# online-softmax rescale touches them between MFMAs, and AGPR-resident
+# accumulators cost a copy in and out on every tile.
+EXTRA = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def _deps_mtime() -> float:
     hdrs = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(ROOT, "include", "*.h"))
@@ -47,7 +54,7 @@ def _compile(src: str, force: bool, hdr_t: float) -> str:
         t = os.path.getmtime(obj)
         if t >= os.path.getmtime(src) and t >= hdr_t:
             return obj
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -326,9 +326,7 @@ static DecPlan dec_plan(int batch, int hkv, int max_len, int page) {
 // buffered in LDS (one barrier per tile).  For causal attention a workgroup
 // takes the query blocks i and N - 1 - i, so every workgroup does the same
 // amount of work.
-constexpr int PF_WAVES = 4;
-constexpr int PF_THREADS = PF_WAVES * kWave;
-constexpr int PF_QROWS = 16 * PF_WAVES;  // 64 query rows per block
+constexpr int PF_QROWS = 64;             // query rows per block (4 row waves x 16)
 constexpr int PF_KT = 64;                // kv tokens per tile
 constexpr float kLazy = 8.f;             // running-max slack (log2 units)
 
@@ -350,28 +348,52 @@ __device__ __forceinline__ uint2 lds_tr4(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-template <int DT, int HPW>
-__global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) {
+// 16-byte chunk permutation of a 256-byte LDS row: bits 1..3 = row % 8,
+// bit 0 = (row / 8) % 2.  16 consecutive rows get 16 distinct values (K
+// fragment reads, one chunk column over 16 rows), and 8 rows starting at a
+// multiple of 8 keep bit 0 fixed (transposing V reads, chunk pairs 2c, 2c + 1).
+__device__ __forceinline__ int pf_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+
+// 16 bytes per lane from global memory straight into LDS: lane l's data
+// lands at lds_base + 16 l (lds_base wave-uniform)
+__device__ __forceinline__ void lds_load16(const uint16_t* g, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(
+      (const __attribute__((address_space(1))) void*)(g),
+      reinterpret_cast<__attribute__((address_space(3))) void*>(
+          reinterpret_cast<__attribute__((address_space(3))) char*>(reinterpret_cast<uintptr_t>(lds_base))),
+      16, 0, 0);
+}
+
+// HPW heads per wave, HG head groups (of 4 row waves) per workgroup
+template <int DT, int HPW, int HG>
+__global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   constexpr int D = 128;
-  constexpr int LDK = D + 8;  // padded rows (16 B): conflict-free b128 and transposing reads
-  __shared__ __attribute__((aligned(16))) uint16_t sk[2][PF_KT * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[2][PF_KT * LDK];
+  // K / V tiles: unpadded 256-byte rows whose 16-byte chunks are permuted by
+  // pf_swz(row); they arrive by direct global -> LDS loads (no registers)
+  // separate objects per stage: the compiler then knows that reads of one
+  // stage do not wait for the direct loads still filling the other
+  __shared__ __attribute__((aligned(16))) uint16_t sk0[PF_KT * D], sk1[PF_KT * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sv0[PF_KT * D], sv1[PF_KT * D];
 
   const int pair = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
   const int G = a.Hq / a.Hkv;
-  const int h0 = hg * HPW, hk = h0 / G;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int rw = wave % 4;                              // row wave
+  const int h0 = (hg * HG + wave / 4) * HPW, hk = h0 / G;  // this wave's first head
   const int col = lane % 16, grp = lane / 16;
   const size_t qstride = (size_t)a.Hq * D, kstride = (size_t)a.Hkv * D;
   const uint16_t* kbase = a.k + (size_t)b * a.S * kstride + (size_t)hk * D;
   const uint16_t* vbase = a.v + (size_t)b * a.S * kstride + (size_t)hk * D;
-  // staging: thread -> token tid / 16 (+16 per step), d chunk 8 (tid % 16)
-  const int st_tok = tid / 16, st_d = 8 * (tid % 16);
+  // staging: wave w fills rows RPW w .. RPW w + RPW - 1, four rows per load;
+  // lane l writes physical chunk l % 16 of row 4 u + l / 16, i.e. source
+  // chunk (l % 16) ^ pf_swz(row)
+  constexpr int RPW = 16 / HG;
+  const int st_row0 = RPW * wave + lane / 16;
 
   for (int pass = 0; pass < (a.paired ? 2 : 1); pass++) {
     const int blk = pass == 0 ? pair : a.nblk - 1 - pair;
     if (pass == 1 && blk <= pair) break;  // the middle block of an odd count runs once
-    const int q0 = blk * PF_QROWS + wave * 16;  // this wave's first query row
+    const int q0 = blk * PF_QROWS + rw * 16;  // this wave's first query row
     const int qr = q0 + col;                    // this lane's query row
     // Q^T as the B operand: column = query row, k = d 32 s + 8 grp .. +7
     uint4 qf[HPW][4];
@@ -395,49 +417,36 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
 
     const int kv_end = a.causal ? min(a.S, (blk + 1) * PF_QROWS) : a.S;
     const int ntile = (kv_end + PF_KT - 1) / PF_KT;
-    uint4 kr[4], vr[4];
-    auto fetch = [&](int t) __attribute__((always_inline)) {
-      if ((t + 1) * PF_KT <= a.S) {
-        const size_t off = (size_t)(t * PF_KT + st_tok) * kstride + st_d;
+    auto fetch = [&](int t, uint16_t* sk, uint16_t* sv) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          kr[r] = ldg16(kbase + off + (size_t)(16 * r) * kstride);
-          vr[r] = ldg16(vbase + off + (size_t)(16 * r) * kstride);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int tok = min(t * PF_KT + st_tok + 16 * r, a.S - 1);  // clamped rows are masked
-          kr[r] = ldg16(kbase + (size_t)tok * kstride + st_d);
-          vr[r] = ldg16(vbase + (size_t)tok * kstride + st_d);
-        }
-      }
-    };
-    auto stage = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        *reinterpret_cast<uint4*>(&sk[buf][(st_tok + 16 * r) * LDK + st_d]) = kr[r];
-        *reinterpret_cast<uint4*>(&sv[buf][(st_tok + 16 * r) * LDK + st_d]) = vr[r];
+      for (int u = 0; u < RPW / 4; u++) {
+        const int row = st_row0 + 4 * u;
+        const int tok = min(t * PF_KT + row, a.S - 1);  // clamped rows are masked
+        const size_t off = (size_t)tok * kstride + 8 * ((lane % 16) ^ pf_swz(row));
+        lds_load16(kbase + off, sk + (RPW * wave + 4 * u) * D);
+        lds_load16(vbase + off, sv + (RPW * wave + 4 * u) * D);
       }
     };
     __syncthreads();  // the previous pass's last tile has been read by every wave
-    fetch(0);
-    stage(0);
+    fetch(0, sk0, sv0);
+    wait_vm();
     __syncthreads();
-    for (int t = 0; t < ntile; t++) {
-      const int buf = t & 1, t0 = t * PF_KT;
-      if (t + 1 < ntile) fetch(t + 1);
+    // one tile from (kt, vt) while tile t + 1 streams into (nk, nv)
+    auto tile = [&](int t, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv)
+                    __attribute__((always_inline)) {
+      const int t0 = t * PF_KT;
+      if (t + 1 < ntile) fetch(t + 1, nk, nv);
       if (!a.causal || t0 <= q0 + 15) {
-        const uint16_t* kt = sk[buf];
-        const uint16_t* vt = sv[buf];
         // S^T = K Q^T: 4 blocks of 16 tokens; lane holds tokens t0 + 16 n + 4 grp + i
         f32x4 sc[HPW][4];
 #pragma unroll
         for (int n = 0; n < 4; n++) {
           uint4 kf[4];
 #pragma unroll
-          for (int s = 0; s < 4; s++)
-            kf[s] = *reinterpret_cast<const uint4*>(&kt[(16 * n + col) * LDK + 32 * s + 8 * grp]);
+          for (int s = 0; s < 4; s++) {
+            const int row = 16 * n + col;
+            kf[s] = *reinterpret_cast<const uint4*>(&kt[row * D + 8 * ((4 * s + grp) ^ pf_swz(row))]);
+          }
 #pragma unroll
           for (int hh = 0; hh < HPW; hh++) {
             f32x4 c = {0.f, 0.f, 0.f, 0.f};
@@ -505,20 +514,25 @@ __global__ __launch_bounds__(PF_THREADS) void gqa_prefill_kernel(PrefillArgs a) 
         // O^T += V^T P^T.  V^T fragment (rows d 16 dt + col, k slots as above):
         // lane 4e + q of group grp reads tokens 32 m + 16 j + 4 grp + e,
         // d 16 dt + 4 q .. +3; the transposing read hands lane col its d.
-        const int e = col / 4, qd = 4 * (col % 4);
+        const int e = col / 4, qc = (col % 4) / 2, qh = 4 * (col % 2);
 #pragma unroll
         for (int m = 0; m < 2; m++)
 #pragma unroll
           for (int dt = 0; dt < D / 16; dt++) {
-            const uint2 lo = lds_tr4(&vt[(32 * m + 4 * grp + e) * LDK + 16 * dt + qd]);
-            const uint2 hi = lds_tr4(&vt[(32 * m + 16 + 4 * grp + e) * LDK + 16 * dt + qd]);
+            const int r0 = 32 * m + 4 * grp + e, r1 = r0 + 16;
+            const uint2 lo = lds_tr4(&vt[r0 * D + 8 * ((2 * dt + qc) ^ pf_swz(r0)) + qh]);
+            const uint2 hi = lds_tr4(&vt[r1 * D + 8 * ((2 * dt + qc) ^ pf_swz(r1)) + qh]);
             const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
             for (int hh = 0; hh < HPW; hh++) acc[hh][dt] = mfma16<DT>(vf, pb[hh][m], acc[hh][dt]);
           }
       }
-      if (t + 1 < ntile) stage(buf ^ 1);
+      wait_vm();  // tile t + 1 has landed in LDS
       __syncthreads();
+    };
+    for (int t = 0; t < ntile; t += 2) {
+      tile(t, sk0, sv0, sk1, sv1);
+      if (t + 1 < ntile) tile(t + 1, sk1, sv1, sk0, sv0);
     }
     // O[query row][d 16 dt + 4 grp + i]
 #pragma unroll
@@ -668,23 +682,25 @@ int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, i
   a.causal = causal ? 1 : 0;
   a.nblk = (seq + PF_QROWS - 1) / PF_QROWS;
   a.scale_log2 = kLog2e / sqrtf((float)d);
-#ifdef YR_PF_HPW
-  const int hpw = (hq / hkv) % YR_PF_HPW == 0 ? YR_PF_HPW : 1;
-#else
-  const int hpw = (hq / hkv) % 2 == 0 ? 2 : 1;
+  // heads per workgroup: 2 when the group size allows (two groups of 4 row
+  // waves sharing each K / V tile), one head per wave
+  const int G = hq / hkv;
+#ifndef YR_PF_CFG
+#define YR_PF_CFG 2
 #endif
-  // causal: block pairs (i, nblk - 1 - i) per workgroup; full: one block each
+  const int hpw = (YR_PF_CFG == 0 || YR_PF_CFG == 3) && G % 2 == 0 ? 2 : 1;
+  const int hgw = (YR_PF_CFG >= 2) && (G / hpw) % 2 == 0 ? 2 : 1;
   a.paired = a.causal;
-  dim3 grid(a.paired ? (a.nblk + 1) / 2 : a.nblk, hq / hpw, batch);
+  dim3 grid(a.paired ? (a.nblk + 1) / 2 : a.nblk, hq / (hpw * hgw), batch);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == YR_DTYPE_BF16;
-  if (hpw == 2) {
-    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, 2>), grid, dim3(PF_THREADS), 0, st, a);
-    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, 2>), grid, dim3(PF_THREADS), 0, st, a);
-  } else {
-    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, 1>), grid, dim3(PF_THREADS), 0, st, a);
-    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, 1>), grid, dim3(PF_THREADS), 0, st, a);
+#define YR_PF(H, W)                                                                                        \
+  if (hpw == H && hgw == W) {                                                                              \
+    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, H, W>), grid, dim3(256 * W), 0, st, a);         \
+    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, H, W>), grid, dim3(256 * W), 0, st, a);             \
   }
+  YR_PF(1, 1) YR_PF(1, 2) YR_PF(2, 1) YR_PF(2, 2)
+#undef YR_PF
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
 }
