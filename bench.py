@@ -20,6 +20,10 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+# HBM bytes per pk_worker_kernel launch of the batch-1 headline step, from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a 1 GiB copy kernel: x2.0 /
+# x1.0); profiles/pk_worker_kernel_llama3_8b_decode_b1.md has the runs.
+PK_B1_TRAFFIC_BYTES = 15_665_570_201
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 
 
@@ -174,6 +178,8 @@ def main():
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only copy a 1 GiB device buffer 3 times (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the hip backend's persistent kernel is single-GPU; "
@@ -184,6 +190,13 @@ def main():
     from yirage_amd.llama import LLAMA3_8B, LlamaDecodeModel
 
     torch.cuda.set_device(0)
+    if args.copy_calib:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
     model = LlamaDecodeModel(LLAMA3_8B, batch=1, kv_len=4096, seed=0)
     model.set_input_tokens([128000])
     for _ in range(args.warmup):
@@ -237,7 +250,7 @@ def main():
                    "vocab": 128256, "page_size": 64, "parallelism": "single GPU",
                    "tasks_per_step": info["tasks"], "workers": info["workers"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": PK_B1_TRAFFIC_BYTES,
                      "algorithmic_bytes": step_bytes},
         "tokens_per_s": round(1e3 / ms, 2),
         "cpu_baseline": cpu,

@@ -327,7 +327,11 @@ static DecPlan dec_plan(int batch, int hkv, int max_len, int page) {
 // takes the query blocks i and N - 1 - i, so every workgroup does the same
 // amount of work.
 constexpr int PF_QROWS = 64;             // query rows per block (4 row waves x 16)
-constexpr int PF_KT = 64;                // kv tokens per tile
+#ifndef YR_PF_KT
+#define YR_PF_KT 64
+#endif
+constexpr int PF_KT = YR_PF_KT;          // kv tokens per tile
+constexpr int PF_NB = PF_KT / 16;        // 16-token MFMA blocks per tile
 constexpr float kLazy = 8.f;             // running-max slack (log2 units)
 
 struct PrefillArgs {
@@ -387,7 +391,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   // staging: wave w fills rows RPW w .. RPW w + RPW - 1, four rows per load;
   // lane l writes physical chunk l % 16 of row 4 u + l / 16, i.e. source
   // chunk (l % 16) ^ pf_swz(row)
-  constexpr int RPW = 16 / HG;
+  constexpr int RPW = PF_KT / (4 * HG);
   const int st_row0 = RPW * wave + lane / 16;
 
   for (int pass = 0; pass < (a.paired ? 2 : 1); pass++) {
@@ -438,9 +442,9 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
       if (t + 1 < ntile) fetch(t + 1, nk, nv);
       if (!a.causal || t0 <= q0 + 15) {
         // S^T = K Q^T: 4 blocks of 16 tokens; lane holds tokens t0 + 16 n + 4 grp + i
-        f32x4 sc[HPW][4];
+        f32x4 sc[HPW][PF_NB];
 #pragma unroll
-        for (int n = 0; n < 4; n++) {
+        for (int n = 0; n < PF_NB; n++) {
           uint4 kf[4];
 #pragma unroll
           for (int s = 0; s < 4; s++) {
@@ -460,16 +464,16 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
         // exact after the final 1 / l, and the O rescale is skipped by the
         // whole wave on most tiles.
         const bool edge = (a.causal && t0 + PF_KT - 1 > q0) || t0 + PF_KT > a.S;
-        uint4 pb[HPW][2];  // P^T B operands for the two 32-token steps
+        uint4 pb[HPW][PF_NB / 2];  // P^T B operands of the 32-token steps
 #pragma unroll
         for (int hh = 0; hh < HPW; hh++) {
 #pragma unroll
-          for (int n = 0; n < 4; n++)
+          for (int n = 0; n < PF_NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) sc[hh][n][i] *= a.scale_log2;
           if (edge) {
 #pragma unroll
-            for (int n = 0; n < 4; n++)
+            for (int n = 0; n < PF_NB; n++)
 #pragma unroll
               for (int i = 0; i < 4; i++) {
                 const int tok = t0 + 16 * n + 4 * grp + i;
@@ -478,7 +482,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
           }
           float mx = -INFINITY;
 #pragma unroll
-          for (int n = 0; n < 4; n++)
+          for (int n = 0; n < PF_NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[hh][n][i]);
           mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
@@ -494,9 +498,9 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
           }
           const float mref = m_i[hh] == -INFINITY ? 0.f : m_i[hh];  // all -inf so far: P = 0
           float ls = 0.f;
-          float pv[4][4];
+          float pv[PF_NB][4];
 #pragma unroll
-          for (int n = 0; n < 4; n++)
+          for (int n = 0; n < PF_NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const float p = __builtin_amdgcn_exp2f(sc[hh][n][i] - mref);
@@ -506,7 +510,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
           l_i[hh] += ls;  // per lane; the four lane groups add up at the end
           // k slot 8 grp + 4 j + i of step m <-> token 32 m + 16 j + 4 grp + i
 #pragma unroll
-          for (int m = 0; m < 2; m++)
+          for (int m = 0; m < PF_NB / 2; m++)
             pb[hh][m] = make_uint4(pack2<DT>(pv[2 * m][0], pv[2 * m][1]), pack2<DT>(pv[2 * m][2], pv[2 * m][3]),
                                    pack2<DT>(pv[2 * m + 1][0], pv[2 * m + 1][1]),
                                    pack2<DT>(pv[2 * m + 1][2], pv[2 * m + 1][3]));
@@ -516,7 +520,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
         // d 16 dt + 4 q .. +3; the transposing read hands lane col its d.
         const int e = col / 4, qc = (col % 4) / 2, qh = 4 * (col % 2);
 #pragma unroll
-        for (int m = 0; m < 2; m++)
+        for (int m = 0; m < PF_NB / 2; m++)
 #pragma unroll
           for (int dt = 0; dt < D / 16; dt++) {
             const int r0 = 32 * m + 4 * grp + e, r1 = r0 + 16;
