@@ -302,6 +302,14 @@ __device__ __forceinline__ uint4 ld_sc1(__amdgpu_buffer_rsrc_t r, uint32_t byte_
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSC1));
 }
 
+__device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
+                                                 0, 0, 0);
+}
+
+// Column e of staged activation row b (b < 8): 16-byte chunk e / 8 XOR b.
+__device__ __forceinline__ int xs_swz(int b, int e) { return (((e >> 3) ^ b) << 3) | (e & 7); }
+
 // Sync wave: rows [0, TM) of elements [k0, k0 + KB) of op.x into xs[b][KB];
 // rows b >= T are zero.  16 loads per lane in flight.
 template <int TM>
@@ -330,14 +338,15 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
       co += 1024;
       if (co == k * 1024) { co = 0; rb += row_bytes; }
     }
-    int xb = mb0 * KB + mc0 * 512;
-    int xc = mc0;
+    // element (row b, column e) lives at b * KB + xs_swz(b, e): 16-byte
+    // chunks XOR-permuted by row so that the MFMA B reads of 8 rows hit 8
+    // different bank groups (identity for row 0, the batch-1 layout)
+    int xr = mb0, xc = mc0;
 #pragma unroll
     for (int u = 0; u < NB; u++) {
-      uint16_t* dst = g + u < total ? sm.xs + xb : junk;
-      *reinterpret_cast<uint4*>(dst + lane * 8) = v[u];
-      xb += 512;
-      if (++xc == k) { xc = 0; xb += KB - k * 512; }
+      uint16_t* dst = g + u < total ? sm.xs + xr * KB + xs_swz(xr, xc * 512 + lane * 8) : junk + lane * 8;
+      *reinterpret_cast<uint4*>(dst) = v[u];
+      if (++xc == k) { xc = 0; xr++; }
     }
   }
 }
@@ -397,7 +406,7 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
   for (int b = 0; b < T; b++) {
     float ss = 0.f;
     for (int c = lane * 8; c < K; c += kWave * 8) {
-      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
+      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + xs_swz(b, c)]);
       uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -418,7 +427,7 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
       } else {
         g = ldg16(op.norm + c);
       }
-      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + c]);
+      uint4 v = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + xs_swz(b, c)]);
       uint32_t xv[4] = {v.x, v.y, v.z, v.w}, gv[4] = {g.x, g.y, g.z, g.w}, o[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -426,7 +435,7 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
         float hi = hi16<DT_BF16>(xv[e]) * (r * hi16<DT_BF16>(gv[e]));
         o[e] = pack2<DT_BF16>(lo, hi);
       }
-      *reinterpret_cast<uint4*>(&sm.xs[b * KB + c]) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
@@ -521,7 +530,14 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int NC = K >> 9;                           // 512-element chunks per row
   const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM);
   const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
-  const int U = RT * NCB;                          // units per block
+  // A unit is one 16-byte weight load per lane.  TM == 1: 512 elements of
+  // one row (dot products on VALU); TM == 8: a 16-row x 32-column MFMA A
+  // fragment (rows = a 16-row tile of the weight, columns = 8 tokens x 2).
+  constexpr bool MF = TM > 1;
+  constexpr int USH = MF ? 5 : 9;                  // log2 columns per unit
+  const int NT = MF ? (RT + 15) / 16 : RT;         // rows (TM == 1) or 16-row tiles
+  const int UPR = KB >> USH;                       // units per row / tile and block
+  const int U = NT * UPR;                          // units per block
   // wave index as a scalar: role branches are wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(tix() / kWave), lane = tix() % kWave;
   const bool is_sync = wave == CW;
@@ -530,24 +546,32 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   // this compute wave's unit range (the same in every block)
   const int u0 = (wave * U) / CW, u1 = ((wave + 1) * U) / CW;
   const int n = is_sync ? 0 : u1 - u0, total = n * nkb;
-  const int row0 = u0 / NCB, c00 = u0 - row0 * NCB;
-  // load cursor: unit l_i of the wave's stream, at row l_row, chunk l_c;
-  // lrow points at lane's element of chunk 0 of that row in the current block
+  const int row0 = u0 / UPR, c00 = u0 - row0 * UPR;
+  // load cursor: unit l_i of the wave's stream, at row / tile l_row, unit
+  // l_c of it; lrow points at lane's element of unit 0 of that row / tile in
+  // the current block (TM == 8: lane's weight row 16 tile + lane % 16,
+  // clamped to the last row, columns 8 (lane / 16) ..)
   const uint16_t* const w1b = t.w1 + lane * 8;
   auto row_ptr = [&](int row, int kb) __attribute__((always_inline)) -> const uint16_t* {
-    return (row < seg ? t.w0 + (size_t)row * K : t.w1 + (size_t)(row - seg) * K) + (size_t)kb * KB + lane * 8;
+    if constexpr (MF) {
+      const int r = min(row * 16 + lane % 16, RT - 1);
+      return (r < seg ? t.w0 + (size_t)r * K : t.w1 + (size_t)(r - seg) * K) + (size_t)kb * KB + (lane / 16) * 8;
+    } else {
+      return (row < seg ? t.w0 + (size_t)row * K : t.w1 + (size_t)(row - seg) * K) + (size_t)kb * KB + lane * 8;
+    }
   };
   int l_i = 0, l_ib = 0, l_kb = 0, l_row = row0, l_c = c00;
   const uint16_t* lrow = row_ptr(row0, 0);
   uint4 ring[RING];
   auto issue = [&](uint4& dst) __attribute__((always_inline)) {
     if (l_i < total) {
-      dst = ldg16(lrow + (l_c << 9));
+      dst = ldg16(lrow + (l_c << USH));
       l_i++;
-      if (++l_c == NCB) {
+      if (++l_c == UPR) {
         l_c = 0;
         l_row++;
-        lrow = l_row == seg ? w1b + (size_t)l_kb * KB : lrow + K;
+        if constexpr (MF) lrow = row_ptr(l_row, l_kb);
+        else lrow = l_row == seg ? w1b + (size_t)l_kb * KB : lrow + K;
       }
       if (TM > 1 && ++l_ib == n) {
         l_ib = 0;
@@ -580,7 +604,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     } else if (a.profile && lane == 0) {
       a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     }
-    for (int i = lane; i < (RT + CW) * TM; i += kWave) slots[i] = 0.f;
+    for (int i = lane; i < (MF ? (NT + CW) * 16 : RT + CW) * TM; i += kWave) slots[i] = 0.f;
     if (lane == 0) {
       sm.last_T = T;
       sm.last_op = nkb == 1 ? t.op : -1;
@@ -605,6 +629,48 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   } else {
     // ---------------- compute waves: stream the unit range
+    if constexpr (MF) {
+      // C of tile tl: rows 16 tl + 4 (lane / 16) + i, token lane % 16 (< TM
+      // valid); partial sums go to slot tile (tl + wave), so the tiles of
+      // one wave never share slots with another wave's
+      const int bt = lane % 16;
+      const bool bok = bt < TM;
+      const uint16_t* xrow = sm.xs + bt * KB;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      int tl = row0, c = c00, ib = 0;
+      for (int g0 = 0; g0 < total; g0 += RING) {
+#pragma unroll
+        for (int s = 0; s < RING; s++) {
+          if (g0 + s < total) {
+            if (ib == n) {  // next staged block
+              ib = 0;
+              tl = row0;
+              c = c00;
+              __syncthreads();
+              __syncthreads();
+            }
+            const uint4 w = ring[s];
+            issue(ring[s]);
+            const uint4 xv = bok ? *reinterpret_cast<const uint4*>(xrow + xs_swz(bt, (c << 5) + (lane / 16) * 8))
+                                 : make_uint4(0, 0, 0, 0);
+            acc = mfma_bf16(w, xv, acc);
+            ++ib;
+            if (++c == UPR || ib == n) {
+              if (bok) {
+                float* sl = slots + ((tl + wave) * 16 + 4 * (lane / 16)) * TM + bt;
+#pragma unroll
+                for (int i = 0; i < 4; i++) sl[i * TM] += acc[i];
+              }
+              acc = f32x4{0.f, 0.f, 0.f, 0.f};
+              if (c == UPR) {
+                c = 0;
+                tl++;
+              }
+            }
+          }
+        }
+      }
+    } else {
     float acc[TM];
 #pragma unroll
     for (int b = 0; b < TM; b++) acc[b] = 0.f;
@@ -644,6 +710,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         }
       }
     }
+    }
   }
   __syncthreads();  // [O]: every partial sum is in its slot
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
@@ -652,9 +719,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   // ---------------- sync wave: epilogue, stores, publish
   // value of weight row j for token b: its slots, in wave order
   auto rowval = [&](int j, int b) __attribute__((always_inline)) -> float {
-    const int wlo = ((j * NCB + 1) * CW - 1) / U, whi = ((j * NCB + NCB) * CW - 1) / U;
+    const int tj = MF ? j / 16 : j;
+    const int wlo = ((tj * UPR + 1) * CW - 1) / U, whi = ((tj * UPR + UPR) * CW - 1) / U;
     float v = 0.f;
-    for (int w = wlo; w <= whi; w++) v += slots[(j + w) * TM + b];
+    for (int w = wlo; w <= whi; w++) v += slots[(MF ? (tj + w) * 16 + j % 16 : j + w) * TM + b];
     return v;
   };
   float* vals = &sm.attn_p[0][0][0];  // argmax: bf16-rounded logits [T][R]
@@ -756,10 +824,6 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
 // (RoPE, append to the paged cache, causal mask), as the reference does in
 // multitoken_paged_attention_4_16.cuh:227-560.  Query rows = token j * G + g
 // (<= 16) in one MFMA 16x16x32 row block.
-__device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
-                                                 0, 0, 0);
-}
 
 // RoPE (rotate-half, rotary_embedding.cuh:22-81) of one head vector held as
 // four 8-element chunks per lane: chunk q covers d = 32 q + 8 (lane / 16).
@@ -769,15 +833,13 @@ __device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
 struct RopeVec {
   uint4 x[4], c[4], s[4];
 };
-// cos/sin rows of position pos (no dependency on the task's inputs)
-__device__ __forceinline__ void rope_load_tab(RopeVec& v, int D, OpRef op, int pos, bool ok, int lane) {
+// cos/sin of one position from a [cos 128 | sin 128] row staged in LDS
+__device__ __forceinline__ void rope_tab_lds(RopeVec& v, const uint16_t* row, int lane) {
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int d = 32 * q + (lane / 16) * 8;
-    if (op.cos_t) {
-      v.c[q] = ok ? ldg16(op.cos_t + (size_t)pos * D + d) : make_uint4(0, 0, 0, 0);
-      v.s[q] = ok ? ldg16(op.sin_t + (size_t)pos * D + d) : make_uint4(0, 0, 0, 0);
-    }
+    v.c[q] = *reinterpret_cast<const uint4*>(row + d);
+    v.s[q] = *reinterpret_cast<const uint4*>(row + 128 + d);
   }
 }
 __device__ __forceinline__ void rope_apply(const RopeVec& v, uint4 (&out)[4], OpRef op) {
@@ -813,10 +875,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   // previous launch's prepare_batch task)
   const AttnGeom gm = attn_geom(m, op, r, s);
   const int t0 = gm.t0, nt = gm.nt, pb = gm.pb, np = gm.np, base = gm.base, c0 = gm.c0, c1 = gm.c1;
-  if (a.profile && wave == 0) {
-    wait_vm();
-    if (lane == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
-  }
   const bool last = s == S - 1;
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
   const float scale = 1.4426950408889634f / sqrtf((float)D);
@@ -834,10 +892,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     const int pg0 = p0 / kPage;
     const int idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
     const int idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
-    if (a.profile && wave == 0) {
-      wait_vm();
-      if (lane == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
-    }
     const size_t page_elems = (size_t)kPage * tok_stride;
     const uint16_t* kA = op.k_cache + (size_t)idA * page_elems + (size_t)h * D;
     const uint16_t* kB = op.k_cache + (size_t)idB * page_elems + (size_t)h * D;
@@ -866,10 +920,6 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   const bool qok = qrow < nt * G;
   int pg_tok = 0;
   if (newtok && qrow < nt) pg_tok = m.kv_indices[pb + (base + qrow) / kPage];
-  if (a.profile && wave == 0) {
-    wait_vm();
-    if (lane == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
-  }
 
   // a link-tensor qkv is validated word by word below: no event wait
   if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
@@ -900,6 +950,17 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     // The sync wave of the last split holds no cached block, so the raw
     // words of the new tokens' k / v land in its kf / vf registers.
     Link8 qr[4];
+    // RoPE tables depend only on positions: rows base .. base + nt - 1 go to
+    // this wave's attn_p area ([pos][cos 128 | sin 128]) before the q / k
+    // words are awaited (nt <= 4 here: nt * G <= 16)
+    uint16_t* const tabs = reinterpret_cast<uint16_t*>(&sm.attn_p[wave][0][0]);
+    if (op.cos_t) {
+      for (int c = lane; c < nt * 32; c += kWave) {
+        const int pp = c / 32, tb = (c / 16) & 1, d = (c % 16) * 8;
+        *reinterpret_cast<uint4*>(tabs + pp * 256 + tb * 128 + d) =
+            ldg16((tb ? op.sin_t : op.cos_t) + (size_t)(base + pp) * D + d);
+      }
+    }
     long long spins = 0;
     for (;;) {  // all loads in flight at once; re-read if any word is stale
 #pragma unroll
@@ -933,14 +994,14 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       if (!__any(stale) || !link_retry(a, spins)) break;
     }
     RopeVec qin;
-    rope_load_tab(qin, D, op, base + qj, qok, lane);
+    rope_tab_lds(qin, tabs + (qok ? qj : 0) * 256, lane);
 #pragma unroll
     for (int q = 0; q < 4; q++) qin.x[q] = act8_data(lk, qr[q]);
     if (newtok) {
       const int i = lane % 16;
       const bool kok = i < nt;
       RopeVec kin;
-      rope_load_tab(kin, D, op, base + i, kok, lane);
+      rope_tab_lds(kin, tabs + (kok ? i : 0) * 256, lane);
 #pragma unroll
       for (int q = 0; q < 4; q++) kin.x[q] = act8_data(lk, Link8{kf[1][q], kf[2][q]});
 #pragma unroll
@@ -965,6 +1026,9 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
     rope_apply(qin, qf, op);
   }
+  // profile: 5 = q (and new k / v) loaded and valid, 4 = waves merged,
+  // 7 = arrival ticket taken, 6 = split merge written (last split only)
+  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
 
   // per-wave online softmax state for rows 4*(lane/16)+i
   float m_i[4], l_i[4];
@@ -1051,6 +1115,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
 
   // new tokens: causal block on the sync wave of the last split
   if (newtok) process(base, nt, true);
+  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 1] = now_10ns();  // wave 0 processed
 
   // sum o over the 4 lane groups (positions lane/16 + 4 i), then merge the
   // 8 waves: per row, (m, l) in LDS, o through LDS (xs reused as float)
@@ -1080,6 +1145,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   }
   __syncthreads();
+  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   const int rows = nt * G;
   float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * kAttnRecFloats;
   float* rec = rec_base + (size_t)s * kAttnRecFloats;
@@ -1102,6 +1168,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   }
   const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
+  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
   if (merge) {
     // Online-softmax merge of the S split records in one memory round trip:
     // every (m, l) pair and every o chunk is loaded before anything waits.
