@@ -39,6 +39,7 @@ struct Shared {
   int flag;                       // last wait succeeded (0 after a watchdog exit)
   int last_op;                    // op whose activations are staged in xs (-1: none)
   int last_T;
+  int norm_rows;                  // batch > 1: rows staged raw, normalized by waves 0..T-1
   KernelArgs args;                // this launch's arguments, for the task functions
 };
 
@@ -440,6 +441,49 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
   }
 }
 
+// One wave, batch > 1: row b of the staged activations (all of K <= 4096
+// in one block) times rsqrt(mean(x^2) + eps) * gamma (gamma staged in
+// attn_p), rounded to bf16, in place -- the arithmetic of norm_x, with every
+// LDS read of the row in flight at once.
+__device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, int lane) {
+  const int K = op.K;
+  const uint16_t* gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
+  uint4 xv[8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int c = (lane + kWave * j) * 8;
+    xv[j] = c < K ? *reinterpret_cast<const uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t w4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
+      ss += lo * lo + hi * hi;
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)K + op.eps);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int c = (lane + kWave * j) * 8;
+    if (c < K) {
+      const uint4 g = *reinterpret_cast<const uint4*>(gam + c);
+      const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w}, gw[4] = {g.x, g.y, g.z, g.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float lo = lo16<DT_BF16>(xw[e]) * (r * lo16<DT_BF16>(gw[e]));
+        const float hi = hi16<DT_BF16>(xw[e]) * (r * hi16<DT_BF16>(gw[e]));
+        o[e] = pack2<DT_BF16>(lo, hi);
+      }
+      *reinterpret_cast<uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
 // Sync wave: one-lane event poll (the watchdog exits through sm.flag).
 __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (tix() == SYNC_T0) {
@@ -599,12 +643,24 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         T = active_tokens(a, op);
         if (TM == 1 && (op.flags & OPF_X_LL)) stage_x_link(a, op, KB, 0, sm, lane);
         else stage_x<TM>(op, T, KB, 0, sm, lane);
-        if (NORM) norm_x(op, T, KB, sm, nr, pre, lane);
+        if (NORM && MF && pre) {
+          // batch > 1: gamma to LDS; every wave then normalizes one row
+          uint16_t* gam = reinterpret_cast<uint16_t*>(&sm.attn_p[0][0][0]);
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const int c = (lane + kWave * j) * 8;
+            if (c < K) *reinterpret_cast<uint4*>(gam + c) = nr.g[j];
+          }
+          if (lane == 0) sm.norm_rows = T;
+        } else if (NORM) {
+          norm_x(op, T, KB, sm, nr, pre, lane);
+        }
       }
     } else if (a.profile && lane == 0) {
       a.profile[(size_t)task_id * 8 + 1] = now_10ns();
     }
     for (int i = lane; i < (MF ? (NT + CW) * 16 : RT + CW) * TM; i += kWave) slots[i] = 0.f;
+    if (lane == 0 && (same_op || !(NORM && MF && K <= 4096))) sm.norm_rows = 0;
     if (lane == 0) {
       sm.last_T = T;
       sm.last_op = nkb == 1 ? t.op : -1;
@@ -614,6 +670,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
+  if constexpr (NORM && MF) {
+    const int nr = __builtin_amdgcn_readfirstlane(sm.norm_rows);
+    if (nr > 0) {  // workgroup-uniform
+      if (wave < nr) norm_row(op, wave, KB, sm, lane);
+      __syncthreads();  // rows normalized
+    }
+  }
 
   if (is_sync) {
     for (int kb = 1; kb < nkb; kb++) {
@@ -726,33 +789,48 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     return v;
   };
   float* vals = &sm.attn_p[0][0][0];  // argmax: bf16-rounded logits [T][R]
-  for (int b = 0; b < T; b++) {
-    for (int p = lane; p < R / 2; p += kWave) {
-      float v0, v1;
-      if constexpr (SILU) {
-        // silu_mul.cuh:31-40 on the bf16 gate/up results
-        float g0 = round_to<DT_BF16>(rowval(2 * p, b)), g1 = round_to<DT_BF16>(rowval(2 * p + 1, b));
-        float x0 = round_to<DT_BF16>(rowval(R + 2 * p, b)), x1 = round_to<DT_BF16>(rowval(R + 2 * p + 1, b));
-        v0 = round_to<DT_BF16>(g0 / (1.0f + expf(-g0))) * x0;
-        v1 = round_to<DT_BF16>(g1 / (1.0f + expf(-g1))) * x1;
-      } else {
-        v0 = rowval(2 * p, b);
-        v1 = rowval(2 * p + 1, b);
-        if (op.flags & OPF_RESIDUAL) {
+  // (token, column pair) items, four per lane per round: the residual loads
+  // of a round are all in flight before any is used
+  const int NP = R / 2, tot = T * NP;
+  const bool resid = !SILU && (op.flags & OPF_RESIDUAL);
+  for (int i0 = 0; i0 < tot; i0 += 4 * kWave) {
+    uint32_t rw[4] = {0u, 0u, 0u, 0u};
+    if (resid) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int idx = i0 + k * kWave + lane;
+        if (idx < tot) {
+          const int b = idx / NP, p = idx - b * NP;
           const size_t re = (size_t)b * op.res_ld + t.row0 + 2 * p;
-          const uint32_t rw = op.flags & OPF_RES_LL ? link_load(a, op.residual, re, link_tag(a, op.res_src))
-                                                    : ld_agent_u32(op.residual + re);
-          v0 += lo16<DT_BF16>(rw);
-          v1 += hi16<DT_BF16>(rw);
+          rw[k] = op.flags & OPF_RES_LL ? link_load(a, op.residual, re, link_tag(a, op.res_src))
+                                        : ld_agent_u32(op.residual + re);
         }
       }
-      const uint32_t packed = pack2<DT_BF16>(v0, v1);
-      const size_t oe = (size_t)b * op.out_ld + t.row0 + 2 * p;
-      if (op.flags & OPF_OUT_LL) link_store(op.out, oe, packed, link_tag(a, t.op));
-      else st_agent_u32(op.out + oe, packed);
-      if (EPI == EPI_ARGMAX) {
-        vals[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
-        vals[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int idx = i0 + k * kWave + lane;
+      if (idx < tot) {
+        const int b = idx / NP, p = idx - b * NP;
+        float v0, v1;
+        if constexpr (SILU) {
+          // silu_mul.cuh:31-40 on the bf16 gate/up results
+          float g0 = round_to<DT_BF16>(rowval(2 * p, b)), g1 = round_to<DT_BF16>(rowval(2 * p + 1, b));
+          float x0 = round_to<DT_BF16>(rowval(R + 2 * p, b)), x1 = round_to<DT_BF16>(rowval(R + 2 * p + 1, b));
+          v0 = round_to<DT_BF16>(g0 / (1.0f + expf(-g0))) * x0;
+          v1 = round_to<DT_BF16>(g1 / (1.0f + expf(-g1))) * x1;
+        } else {
+          v0 = rowval(2 * p, b) + (resid ? lo16<DT_BF16>(rw[k]) : 0.f);
+          v1 = rowval(2 * p + 1, b) + (resid ? hi16<DT_BF16>(rw[k]) : 0.f);
+        }
+        const uint32_t packed = pack2<DT_BF16>(v0, v1);
+        const size_t oe = (size_t)b * op.out_ld + t.row0 + 2 * p;
+        if (op.flags & OPF_OUT_LL) link_store(op.out, oe, packed, link_tag(a, t.op));
+        else st_agent_u32(op.out + oe, packed);
+        if (EPI == EPI_ARGMAX) {
+          vals[b * R + 2 * p] = lo16<DT_BF16>(packed);  // argmax runs on the bf16 logits
+          vals[b * R + 2 * p + 1] = hi16<DT_BF16>(packed);
+        }
       }
     }
   }
@@ -1381,6 +1459,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     sm.flag = 1;
     sm.last_op = -1;
     sm.last_T = 0;
+    sm.norm_rows = 0;
   }
   __syncthreads();
   for (int q = q0; q < q1; q++) {
