@@ -310,8 +310,10 @@ void Graph::build(const char* text) {
       d.num_kv_heads = (int)o["num_kv_heads"].i64();
       d.head_dim = (int)o["head_dim"].i64(128);
       d.splits = (int)o["splits"].i64(1);
-      // a split holds at most 7 compute waves x 64 cached positions
-      int min_splits = (cfg.max_seq_len + 447) / 448;
+      // a split holds at most 7 compute waves x kAttnBlocksPerWave x 64
+      // cached positions
+      const int per_split = 7 * kAttnBlocksPerWave * 64;
+      int min_splits = (cfg.max_seq_len + per_split - 1) / per_split;
       if (d.splits < min_splits) d.splits = min_splits;
       d.page_size = cfg.page_size;
       if (d.head_dim != 128) throw std::runtime_error("attention: head_dim must be 128");

@@ -15,6 +15,8 @@ namespace pk {
 // Scratch floats per attention split record: 16 query rows x (head_dim + 2).
 constexpr int kAttnRecRows = 16;
 constexpr int kAttnRecFloats = kAttnRecRows * (128 + 2);
+// cached 64-position blocks one attention compute wave streams per task
+constexpr int kAttnBlocksPerWave = 3;
 
 struct Tensor {
   std::string name;

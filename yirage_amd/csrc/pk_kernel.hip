@@ -957,40 +957,56 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
   const float scale = 1.4426950408889634f / sqrtf((float)D);
 
-  // cached positions: blocks of 64 per wave (wave w: blocks w, w + 8, ...)
+  // cached positions: blocks of 64; compute wave w takes blocks w, w + CW, ...
+  // (at most kAttnBlocksPerWave each)
   const int nblk = (c1 - c0 + 63) / 64;
-  // prefetch the first block of this wave before waiting
   uint4 kf[4][4], vf[16];
-  auto load_block = [&](int blk) __attribute__((always_inline)) {
-    // a 64-position block spans at most two pages (the builder fixes the page
-    // at kPage positions).  Both page ids are read first, so no K/V load waits
-    // on them; positions past c1 are clamped to c1 - 1 (finite data whose
-    // scores are masked), so the 32 loads issue without branches.
+  // a 64-position block spans at most two pages (the builder fixes the page
+  // at kPage positions).  Both page ids are read first, so no K/V load waits
+  // on them; positions past c1 are clamped to c1 - 1 (finite data whose
+  // scores are masked), so the 32 loads issue without branches.
+  struct BlkAddr {
+    const uint16_t *kA, *kB, *vA, *vB;
+    int plast, pw0;
+  };
+  auto blk_addr = [&](int blk) __attribute__((always_inline)) -> BlkAddr {
     const int p0 = c0 + blk * 64;
     const int pg0 = p0 / kPage;
     const int idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
     const int idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
     const size_t page_elems = (size_t)kPage * tok_stride;
-    const uint16_t* kA = op.k_cache + (size_t)idA * page_elems + (size_t)h * D;
-    const uint16_t* kB = op.k_cache + (size_t)idB * page_elems + (size_t)h * D;
-    const uint16_t* vA = op.v_cache + (size_t)idA * page_elems + (size_t)h * D;
-    const uint16_t* vB = op.v_cache + (size_t)idB * page_elems + (size_t)h * D;
-    const int plast = c1 - 1 - pg0 * kPage;  // last valid in-window offset
-    const int pw0 = p0 - pg0 * kPage;        // window offset of p0
+    BlkAddr ba;
+    ba.kA = op.k_cache + (size_t)idA * page_elems + (size_t)h * D;
+    ba.kB = op.k_cache + (size_t)idB * page_elems + (size_t)h * D;
+    ba.vA = op.v_cache + (size_t)idA * page_elems + (size_t)h * D;
+    ba.vB = op.v_cache + (size_t)idB * page_elems + (size_t)h * D;
+    ba.plast = c1 - 1 - pg0 * kPage;  // last valid in-window offset
+    ba.pw0 = p0 - pg0 * kPage;        // window offset of p0
+    return ba;
+  };
+  auto load_k = [&](const BlkAddr& ba) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      int o = min(pw0 + 16 * j + lane % 16, plast);
-      const uint16_t* src = (o >= kPage ? kB : kA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane / 16) * 8;
+      int o = min(ba.pw0 + 16 * j + lane % 16, ba.plast);
+      const uint16_t* src =
+          (o >= kPage ? ba.kB : ba.kA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane / 16) * 8;
 #pragma unroll
       for (int q = 0; q < 4; q++) kf[j][q] = ldg16(src + 32 * q);
     }
+  };
+  auto load_v = [&](const BlkAddr& ba) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      int o = min(pw0 + lane / 16 + 4 * i, plast);
-      vf[i] = ldg16((o >= kPage ? vB : vA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane % 16) * 8);
+      int o = min(ba.pw0 + lane / 16 + 4 * i, ba.plast);
+      vf[i] = ldg16((o >= kPage ? ba.vB : ba.vA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane % 16) * 8);
     }
   };
-  if (nt > 0 && wave < nblk && wave < CW) load_block(wave);
+  // prefetch the first block of this wave before waiting
+  if (nt > 0 && wave < nblk && wave < CW) {
+    const BlkAddr ba = blk_addr(wave);
+    load_k(ba);
+    load_v(ba);
+  }
   // the page of new token lane % 16 (sync wave of the last split) does not
   // depend on the QKV results either
   const bool newtok = last && wave == CW;
@@ -1005,7 +1021,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     signal_event(a, t);
     return;
   }
-  if (nt * G > 16 || nblk > CW) {  // beyond one MFMA row block / one block per wave
+  if (nt * G > 16 || nblk > CW * kAttnBlocksPerWave) {  // beyond one MFMA row block / the block budget
     if (tix() == 0) {
       __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1118,8 +1134,9 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
 #pragma unroll
     for (int e = 0; e < 8; e++) o_acc[rr][e] = 0.f;
 
-  // process one 64-position block held in kf/vf; mask(p_local, row) -> visible
-  auto process = [&](int p0, int npos, bool causal_new) __attribute__((always_inline)) {
+  // one 64-position block: qk_softmax (uses kf) then pv (uses vf);
+  // mask(p_local, row) -> visible
+  auto qk_softmax = [&](int p0, int npos, bool causal_new) __attribute__((always_inline)) {
     f32x4 sc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -1160,6 +1177,8 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+  };
+  auto pv = [&]() __attribute__((always_inline)) {
     // O[row][d] = O * alpha + sum_p P[row][p] V[p][d]; lane: d-chunk lane%16, positions lane/16 + 4i
 #pragma unroll
     for (int rr = 0; rr < RMAX; rr++) {
@@ -1187,12 +1206,37 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     __builtin_amdgcn_wave_barrier();
   };
 
-  // one 64-position block per compute wave (the builder sizes splits so that
-  // a split never holds more than CW * 64 cached positions)
-  if (wave < nblk && wave < CW) process(c0 + wave * 64, (c1 - c0) - wave * 64 < 64 ? (c1 - c0) - wave * 64 : 64, false);
+  // the compute waves' blocks: the next block's K loads go out once this
+  // block's K is consumed, its V loads once this block's V is
+  if (wave < CW) {
+    // every block but the wave's last also loads its successor (loads stay
+    // unconditional, so no register array is live twice)
+    int blk = wave;
+    for (; blk + CW < nblk; blk += CW) {
+      const BlkAddr bn = blk_addr(blk + CW);
+      qk_softmax(c0 + blk * 64, 64, false);
+      // scheduling fences: the next block's loads must not move above the
+      // uses of the registers they overwrite
+      __builtin_amdgcn_sched_barrier(0);
+      load_k(bn);
+      __builtin_amdgcn_sched_barrier(0);
+      pv();
+      __builtin_amdgcn_sched_barrier(0);
+      load_v(bn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (blk < nblk) {
+      const int npos = (c1 - c0) - blk * 64;
+      qk_softmax(c0 + blk * 64, npos < 64 ? npos : 64, false);
+      pv();
+    }
+  }
 
   // new tokens: causal block on the sync wave of the last split
-  if (newtok) process(base, nt, true);
+  if (newtok) {
+    qk_softmax(base, nt, true);
+    pv();
+  }
   if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 1] = now_10ns();  // wave 0 processed
 
   // sum o over the 4 lane groups (positions lane/16 + 4 i), then merge the
@@ -1448,7 +1492,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
   auto load_descs = [&](int first) __attribute__((always_inline)) {
     const int n = q1 - first < 256 ? q1 - first : 256;
     const int words = (int)(sizeof(TaskDesc) / 4);
-    for (int i = threadIdx.x; i < n * words; i += PK_THREADS) {
+    for (int i = tix(); i < n * words; i += PK_THREADS) {
       int k = i / words, e = i % words;
       reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = reinterpret_cast<const uint32_t*>(&a.tasks[a.queue[first + k]])[e];
     }
