@@ -793,11 +793,14 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   // of a round are all in flight before any is used
   const int NP = R / 2, tot = T * NP;
   const bool resid = !SILU && (op.flags & OPF_RESIDUAL);
-  for (int i0 = 0; i0 < tot; i0 += 4 * kWave) {
-    uint32_t rw[4] = {0u, 0u, 0u, 0u};
+  constexpr int KR = TM == 1 ? 1 : 4;  // items per lane and round
+  for (int i0 = 0; i0 < tot; i0 += KR * kWave) {
+    uint32_t rw[KR];
+#pragma unroll
+    for (int k = 0; k < KR; k++) rw[k] = 0u;
     if (resid) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
+      for (int k = 0; k < KR; k++) {
         const int idx = i0 + k * kWave + lane;
         if (idx < tot) {
           const int b = idx / NP, p = idx - b * NP;
@@ -808,7 +811,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KR; k++) {
       const int idx = i0 + k * kWave + lane;
       if (idx < tot) {
         const int b = idx / NP, p = idx - b * NP;
