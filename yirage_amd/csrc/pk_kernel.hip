@@ -68,6 +68,17 @@ __device__ __forceinline__ int tix() {
   return t;
 }
 
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
+// workgroup release fence, which waits for every outstanding global store of
+// the wave (a memory round trip after link / cache / record stores); here the
+// wave only waits for its own LDS operations.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------ protocol
 __device__ __forceinline__ bool aborted(const KernelArgs& a) {
   return __hip_atomic_load(a.meta.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -290,7 +301,7 @@ enum { EPI_LIN = 0, EPI_NORM = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 constexpr int CW = PK_WAVES - 1;           // compute waves
 constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
 #ifndef YR_PK_RING
-#define YR_PK_RING 8
+#define YR_PK_RING 16
 #endif
 constexpr int RING = YR_PK_RING;           // weight loads in flight per compute lane (RING * 7 KiB per CU)
 constexpr int kCpolSC1 = 16;               // buffer cache policy: agent-coherent (sc1)
@@ -1254,7 +1265,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       o_acc[rr][e] = x;
     }
   float* o_lds = reinterpret_cast<float*>(sm.xs);  // [wave][16 rows][128]
-  __syncthreads();
+  lds_sync();
   if (lane < 16) {
 #pragma unroll
     for (int rr = 0; rr < RMAX; rr++)
@@ -1269,7 +1280,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       sm.attn_ml[wave][4 * (lane / 16) + i][1] = l_i[i];
     }
   }
-  __syncthreads();
+  lds_sync();
   if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   const int rows = nt * G;
   float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * kAttnRecFloats;
@@ -1319,7 +1330,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     for (int q = 0; q < 8; q++)
       ob[q] = q < ns ? ld_agent4(rec_base + (size_t)(j + q * P) * kAttnRecFloats + rr * (D + 2) + d4)
                      : make_float4(0.f, 0.f, 0.f, 0.f);
-    __syncthreads();
+    lds_sync();
     float M = -INFINITY, L = 0.f;
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (act) {
@@ -1345,7 +1356,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       float* pp = part + (size_t)(u * P + j) * 6;
       pp[0] = M; pp[1] = L; pp[2] = O.x; pp[3] = O.y; pp[4] = O.z; pp[5] = O.w;
     }
-    __syncthreads();
+    lds_sync();
     if (act && j == 0) {
       const float* pp = part + (size_t)u * P * 6;
       float Mt = -INFINITY;
@@ -1559,7 +1570,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     // comes after its own [X] barrier, which the sync wave reaches only after
     // publishing this task, so the compute waves run ahead and put the next
     // task's weights in flight meanwhile
-    if (!gemv) __syncthreads();
+    if (!gemv) lds_sync();
     if (a.profile && threadIdx.x == 0) a.profile[(size_t)tid * 8 + 2] = now_10ns();
     if (!sm.flag) break;  // a dependency never arrived: leave the queue
   }
