@@ -311,7 +311,11 @@ class PersistentKernel:
                 continue
             if k == "attention":
                 per = self.max_num_batched_requests * l["num_kv_heads"]
-                splits = max(1, min(256, W // per))
+                # about half the workers: fewer, larger splits merge faster
+                # (measured at batch 1: 16 splits per kv head 3.82 ms, 32:
+                # 3.88 ms, 8: 3.90 ms); the builder raises it to what the
+                # per-task block budget needs
+                splits = max(1, min(256, W // (2 * per)))
                 ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
                                 v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
                                 sin=l["sin"].name if l["sin"] is not None else None, out=l["output"].name,
