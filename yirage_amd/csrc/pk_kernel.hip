@@ -29,6 +29,21 @@ constexpr int PK_THREADS = PK_WAVES * kWave;
 constexpr int XS_ELEMS = 32768;   // staged activation elements (64 KiB)
 constexpr int OUT_ELEMS = 16384;  // GEMV partial-sum slots (32 KiB as float)
 
+// An attention task's request geometry and the page ids of its first
+// blocks, read from the batch metadata when the worker loads its task
+// descriptors: the metadata is written by the host or by the previous
+// launch's prepare_batch task and does not change before this launch's last
+// attention task, so the task itself starts its K/V and q loads without a
+// dependent metadata round trip.
+struct AttnPre {
+  int t0, nt, pb, np, base, c0, c1, ok;
+  int id[14];     // pages (A, B) of block w, for compute waves w < 7
+  int pg_tok[4];  // pages of new tokens 0..3
+  int pad[6];
+};
+constexpr int kPreMax = 64;
+constexpr uint8_t kPreNone = 255;
+
 struct Shared {
   uint16_t xs[XS_ELEMS];          // activations (bf16), [token][KB]
   uint16_t outs[OUT_ELEMS];       // GEMV partial-sum slots (float)
@@ -36,6 +51,9 @@ struct Shared {
   float attn_p[PK_WAVES][16][64]; // attention probabilities per wave
   float attn_ml[PK_WAVES][16][2];
   TaskDesc tq[256];               // this worker's first 256 task descriptors
+  AttnPre pre[kPreMax];           // attention geometry / page ids, read when descriptors load
+  uint8_t pre_of[256];            // descriptor slot -> pre entry (kPreNone: none)
+  int pre_n;
   int flag;                       // last wait succeeded (0 after a watchdog exit)
   int last_op;                    // op whose activations are staged in xs (-1: none)
   int last_T;
@@ -122,8 +140,8 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
 // Outputs that are link tensors need not be complete: their readers check
 // tags, so only the other stores of the task are waited for.
 __device__ void signal_event(const KernelArgs& a, const TaskDesc& t, bool link_out = false) {
-  if (!link_out) wait_vm();
-  __syncthreads();
+  if (!link_out) wait_vm();  // every wave's stores complete before the one signal
+  lds_sync();
   if (tix() == POLL_T && t.trigger_event >= 0)
     __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -956,7 +974,8 @@ __device__ __forceinline__ void rope_apply(const RopeVec& v, uint4 (&out)[4], Op
 }
 
 template <int RMAX>
-__device__ __forceinline__ void task_attention_body(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+__device__ __forceinline__ void task_attention_body(const KernelArgs& a, const TaskDesc& t, int task_id, int slot,
+                                                    Shared& sm) {
   OpRef op = op_of(a, t.op);
   constexpr int D = 128;
   const int r = t.i0, h = t.i1, s = t.i2, S = op.splits;
@@ -964,8 +983,23 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   const int wave = __builtin_amdgcn_readfirstlane(tix() / kWave), lane = tix() % kWave;
   const BatchMeta& m = a.meta;
   // request geometry (the page table is written by the host or by the
-  // previous launch's prepare_batch task)
-  const AttnGeom gm = attn_geom(m, op, r, s);
+  // previous launch's prepare_batch task), read at descriptor load when the
+  // worker's table had room
+  const int pe = __builtin_amdgcn_readfirstlane((int)sm.pre_of[__builtin_amdgcn_readfirstlane(slot)]);
+  const bool have_pre = pe != kPreNone;
+  AttnGeom gm;
+  if (have_pre) {
+    const AttnPre& P = sm.pre[pe];
+    gm.t0 = __builtin_amdgcn_readfirstlane(P.t0);
+    gm.nt = __builtin_amdgcn_readfirstlane(P.nt);
+    gm.pb = __builtin_amdgcn_readfirstlane(P.pb);
+    gm.np = __builtin_amdgcn_readfirstlane(P.np);
+    gm.base = __builtin_amdgcn_readfirstlane(P.base);
+    gm.c0 = __builtin_amdgcn_readfirstlane(P.c0);
+    gm.c1 = __builtin_amdgcn_readfirstlane(P.c1);
+  } else {
+    gm = attn_geom(m, op, r, s);
+  }
   const int t0 = gm.t0, nt = gm.nt, pb = gm.pb, np = gm.np, base = gm.base, c0 = gm.c0, c1 = gm.c1;
   const bool last = s == S - 1;
   const size_t tok_stride = (size_t)op.num_kv_heads * D;
@@ -983,11 +1017,17 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     const uint16_t *kA, *kB, *vA, *vB;
     int plast, pw0;
   };
-  auto blk_addr = [&](int blk) __attribute__((always_inline)) -> BlkAddr {
+  auto blk_addr = [&](int blk, bool pre_ids) __attribute__((always_inline)) -> BlkAddr {
     const int p0 = c0 + blk * 64;
     const int pg0 = p0 / kPage;
-    const int idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
-    const int idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
+    int idA, idB;
+    if (pre_ids) {
+      idA = __builtin_amdgcn_readfirstlane(sm.pre[pe].id[2 * blk]);
+      idB = __builtin_amdgcn_readfirstlane(sm.pre[pe].id[2 * blk + 1]);
+    } else {
+      idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
+      idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
+    }
     const size_t page_elems = (size_t)kPage * tok_stride;
     BlkAddr ba;
     ba.kA = op.k_cache + (size_t)idA * page_elems + (size_t)h * D;
@@ -1015,124 +1055,135 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       vf[i] = ldg16((o >= kPage ? ba.vB : ba.vA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane % 16) * 8);
     }
   };
-  // prefetch the first block of this wave before waiting
-  if (nt > 0 && wave < nblk && wave < CW) {
-    const BlkAddr ba = blk_addr(wave);
-    load_k(ba);
-    load_v(ba);
-  }
-  // the page of new token lane % 16 (sync wave of the last split) does not
-  // depend on the QKV results either
-  const bool newtok = last && wave == CW;
-  const int qrow = lane % 16, qj = qrow / G, qg = qrow % G;
-  const bool qok = qrow < nt * G;
-  int pg_tok = 0;
-  if (newtok && qrow < nt) pg_tok = m.kv_indices[pb + (base + qrow) / kPage];
-
-  // a link-tensor qkv is validated word by word below: no event wait
-  if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
-  if (nt <= 0) {
-    signal_event(a, t);
-    return;
-  }
-  if (nt * G > 16 || nblk > CW * kAttnBlocksPerWave) {  // beyond one MFMA row block / the block budget
-    if (tix() == 0) {
+  const bool fits = nt > 0 && nt * G <= 16 && nblk <= CW * kAttnBlocksPerWave;
+  if (!fits) {  // nothing to do / beyond one MFMA row block or the block budget
+    if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
+    if (nt > 0 && tix() == 0)
       __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     signal_event(a, t);
     return;
   }
-
-  // Q fragments: row = j * G + g, k = d.  In the last split the sync wave
-  // (which holds no cached block) also takes the new tokens: their k/v loads
-  // go out together with its q loads, and it processes them while the
-  // compute waves process the cached blocks.
-  uint4 qf[4];
-  {
-    // element offsets into qkv (plain or link tensor): row t0 + j, head column
-    const bool lk = (op.flags & OPF_X_LL) != 0;
-    const uint32_t xtag = lk ? link_tag(a, op.x_src) : 0u;
-    const size_t e_grp = (size_t)t0 * op.qkv_ld + (size_t)h * (G + 2) * D;
-    const size_t e_q = e_grp + (size_t)qj * op.qkv_ld + (size_t)qg * D;
-    const Link8 z8 = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    // The sync wave of the last split holds no cached block, so the raw
-    // words of the new tokens' k / v land in its kf / vf registers.
-    Link8 qr[4];
-    // RoPE tables depend only on positions: rows base .. base + nt - 1 go to
-    // this wave's attn_p area ([pos][cos 128 | sin 128]) before the q / k
-    // words are awaited (nt <= 4 here: nt * G <= 16)
-    uint16_t* const tabs = reinterpret_cast<uint16_t*>(&sm.attn_p[wave][0][0]);
-    if (op.cos_t) {
-      for (int c = lane; c < nt * 32; c += kWave) {
-        const int pp = c / 32, tb = (c / 16) & 1, d = (c % 16) * 8;
-        *reinterpret_cast<uint4*>(tabs + pp * 256 + tb * 128 + d) =
-            ldg16((tb ? op.sin_t : op.cos_t) + (size_t)(base + pp) * D + d);
+  // The sync wave (no cached block) reads q -- and in the last split the new
+  // tokens' k / v -- applies RoPE, appends the new k / v to the cache and
+  // stages the fragments in xs (free until the final wave merge), while the
+  // compute waves' cached-block loads are already in flight.
+  const bool newtok = last && wave == CW;
+  uint4* const qst = reinterpret_cast<uint4*>(sm.xs);  // [4][64 lanes] q fragments (RoPE applied)
+  uint4* const kst = qst + 4 * kWave;                  // [4][64] new k, MFMA B layout (RoPE applied)
+  uint4* const vst = kst + 4 * kWave;                  // [4][64] new v rows lane / 16 + 4 i2
+  const bool lk = (op.flags & OPF_X_LL) != 0;
+  if (wave == CW) {
+    // a link-tensor qkv is validated word by word: no event poll
+    if (lk || poll_event_sync(a, t, task_id, sm)) {
+      const int qrow = lane % 16, qj = qrow / G, qg = qrow % G;
+      const bool qok = qrow < nt * G;
+      const uint32_t xtag = lk ? link_tag(a, op.x_src) : 0u;
+      // element offsets into qkv (plain or link tensor): row t0 + j, head column
+      const size_t e_grp = (size_t)t0 * op.qkv_ld + (size_t)h * (G + 2) * D;
+      const size_t e_q = e_grp + (size_t)qj * op.qkv_ld + (size_t)qg * D;
+      const Link8 z8 = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+      // new token i = lane % 16 (k, MFMA B layout) / lane / 16 + 4 i2 (v);
+      // nt * G <= 16 keeps every new v row below i2 = 4
+      const int ik = lane % 16;
+      const size_t e_k = e_grp + (size_t)ik * op.qkv_ld + (size_t)G * D;
+      Link8 qr[4], kr[4], vr[4];
+      auto issue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) qr[q] = qok ? act8_issue(lk, op.x, e_q + 32 * q + (lane / 16) * 8) : z8;
+        if (newtok) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) kr[q] = ik < nt ? act8_issue(lk, op.x, e_k + 32 * q + (lane / 16) * 8) : z8;
+#pragma unroll
+          for (int i2 = 0; i2 < 4; i2++) {
+            const int iv = lane / 16 + 4 * i2;
+            vr[i2] = iv < nt ? act8_issue(lk, op.x,
+                                          e_grp + (size_t)iv * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
+                             : z8;
+          }
+        }
+      };
+      auto stale = [&]() __attribute__((always_inline)) -> bool {
+        bool st = false;
+#pragma unroll
+        for (int q = 0; q < 4; q++) st |= qok && !act8_ok(lk, qr[q], xtag);
+        if (newtok) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) st |= ik < nt && !act8_ok(lk, kr[q], xtag);
+#pragma unroll
+          for (int i2 = 0; i2 < 4; i2++) st |= lane / 16 + 4 * i2 < nt && !act8_ok(lk, vr[i2], xtag);
+        }
+        return __any(st);
+      };
+      issue();
+      int pg_tok = 0;  // page of new token lane % 16
+      if (newtok && qrow < nt)
+        pg_tok = have_pre && qrow < 4 ? sm.pre[pe].pg_tok[qrow] : m.kv_indices[pb + (base + qrow) / kPage];
+      // RoPE tables of positions base .. base + nt - 1 ([pos][cos 128 | sin
+      // 128]) in this wave's attn_p area
+      uint16_t* const tabs = reinterpret_cast<uint16_t*>(&sm.attn_p[wave][0][0]);
+      if (op.cos_t) {
+        for (int c = lane; c < nt * 32; c += kWave) {
+          const int pp = c / 32, tb = (c / 16) & 1, d = (c % 16) * 8;
+          *reinterpret_cast<uint4*>(tabs + pp * 256 + tb * 128 + d) =
+              ldg16((tb ? op.sin_t : op.cos_t) + (size_t)(base + pp) * D + d);
+        }
       }
-    }
-    long long spins = 0;
-    for (;;) {  // all loads in flight at once; re-read if any word is stale
+      long long spins = 0;
+      while (stale() && link_retry(a, spins)) issue();  // re-read while any word is stale
+      RopeVec qin;
+      rope_tab_lds(qin, tabs + (qok ? qj : 0) * 256, lane);
 #pragma unroll
-      for (int q = 0; q < 4; q++) qr[q] = qok ? act8_issue(lk, op.x, e_q + 32 * q + (lane / 16) * 8) : z8;
-      bool stale = false;
+      for (int q = 0; q < 4; q++) qin.x[q] = act8_data(lk, qr[q]);
+      uint4 qo[4];
+      rope_apply(qin, qo, op);
 #pragma unroll
-      for (int q = 0; q < 4; q++) stale |= qok && !act8_ok(lk, qr[q], xtag);
+      for (int q = 0; q < 4; q++) qst[q * kWave + lane] = qo[q];
       if (newtok) {
-        // new token i = lane % 16 (k, MFMA B layout) / lane / 16 + 4 i2 (v);
-        // nt * G <= 16 keeps every new v row below i2 = 4
-        const int i = lane % 16;
-        const size_t e_k = e_grp + (size_t)i * op.qkv_ld + (size_t)G * D;
+        const bool kok = ik < nt;
+        RopeVec kin;
+        rope_tab_lds(kin, tabs + (kok ? ik : 0) * 256, lane);
+#pragma unroll
+        for (int q = 0; q < 4; q++) kin.x[q] = act8_data(lk, kr[q]);
+        uint4 ko[4];
+        rope_apply(kin, ko, op);
+        auto tok_off = [&](int pg, int pos) __attribute__((always_inline)) -> size_t {
+          return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
+        };
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const Link8 r = i < nt ? act8_issue(lk, op.x, e_k + 32 * q + (lane / 16) * 8) : z8;
-          kf[1][q] = r.w0;
-          kf[2][q] = r.w1;
-          stale |= i < nt && !act8_ok(lk, r, xtag);
+          kst[q * kWave + lane] = ko[q];
+          if (kok) *reinterpret_cast<uint4*>(op.k_cache + tok_off(pg_tok, base + ik) + 32 * q + (lane / 16) * 8) = ko[q];
         }
 #pragma unroll
         for (int i2 = 0; i2 < 4; i2++) {
           const int iv = lane / 16 + 4 * i2;
-          const Link8 r =
-              iv < nt ? act8_issue(lk, op.x, e_grp + (size_t)iv * op.qkv_ld + (size_t)(G + 1) * D + (lane % 16) * 8)
-                      : z8;
-          vf[4 + i2] = r.w0;
-          vf[8 + i2] = r.w1;
-          stale |= iv < nt && !act8_ok(lk, r, xtag);
+          const int pgv = __shfl(pg_tok, iv & 15, kWave);
+          const uint4 vv = act8_data(lk, vr[i2]);
+          vst[i2 * kWave + lane] = vv;
+          if (iv < nt) *reinterpret_cast<uint4*>(op.v_cache + tok_off(pgv, base + iv) + (lane % 16) * 8) = vv;
         }
       }
-      if (!__any(stale) || !link_retry(a, spins)) break;
     }
-    RopeVec qin;
-    rope_tab_lds(qin, tabs + (qok ? qj : 0) * 256, lane);
+  }
+  // prefetch the first cached block of this wave
+  if (wave < nblk && wave < CW) {
+    const BlkAddr ba = blk_addr(wave, have_pre);
+    load_k(ba);
+    load_v(ba);
+  }
+  lds_sync();  // q (and new k / v) staged
+  if (!__builtin_amdgcn_readfirstlane(sm.flag)) return;
+  uint4 qf[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) qin.x[q] = act8_data(lk, qr[q]);
-    if (newtok) {
-      const int i = lane % 16;
-      const bool kok = i < nt;
-      RopeVec kin;
-      rope_tab_lds(kin, tabs + (kok ? i : 0) * 256, lane);
+  for (int q = 0; q < 4; q++) qf[q] = qst[q * kWave + lane];
+  if (newtok) {
 #pragma unroll
-      for (int q = 0; q < 4; q++) kin.x[q] = act8_data(lk, Link8{kf[1][q], kf[2][q]});
-#pragma unroll
-      for (int i2 = 0; i2 < 4; i2++) vf[i2] = act8_data(lk, Link8{vf[4 + i2], vf[8 + i2]});
-#pragma unroll
-      for (int i2 = 4; i2 < 16; i2++) vf[i2] = make_uint4(0, 0, 0, 0);
-      rope_apply(kin, kf[0], op);
-      auto tok_off = [&](int pg, int pos) __attribute__((always_inline)) -> size_t {
-        return ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D;
-      };
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        kf[1][q] = kf[2][q] = kf[3][q] = make_uint4(0, 0, 0, 0);
-        if (kok) *reinterpret_cast<uint4*>(op.k_cache + tok_off(pg_tok, base + i) + 32 * q + (lane / 16) * 8) = kf[0][q];
-      }
-#pragma unroll
-      for (int i2 = 0; i2 < 4; i2++) {
-        const int iv = lane / 16 + 4 * i2;
-        const int pgv = __shfl(pg_tok, iv & 15, kWave);
-        if (iv < nt) *reinterpret_cast<uint4*>(op.v_cache + tok_off(pgv, base + iv) + (lane % 16) * 8) = vf[i2];
-      }
+    for (int q = 0; q < 4; q++) {
+      kf[0][q] = kst[q * kWave + lane];
+      kf[1][q] = kf[2][q] = kf[3][q] = make_uint4(0, 0, 0, 0);
     }
-    rope_apply(qin, qf, op);
+#pragma unroll
+    for (int i2 = 0; i2 < 16; i2++) vf[i2] = i2 < 4 ? vst[i2 * kWave + lane] : make_uint4(0, 0, 0, 0);
   }
   // profile: 5 = q (and new k / v) loaded and valid, 4 = waves merged,
   // 7 = arrival ticket taken, 6 = split merge written (last split only)
@@ -1227,7 +1278,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     // unconditional, so no register array is live twice)
     int blk = wave;
     for (; blk + CW < nblk; blk += CW) {
-      const BlkAddr bn = blk_addr(blk + CW);
+      const BlkAddr bn = blk_addr(blk + CW, false);
       qk_softmax(c0 + blk * 64, 64, false);
       // scheduling fences: the next block's loads must not move above the
       // uses of the registers they overwrite
@@ -1460,6 +1511,45 @@ __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc
   signal_event(a, t);
 }
 
+// Attention tasks among descriptor slots [0, n) of the first descriptor
+// chunk: their request geometry and the page ids of their first blocks from
+// the batch metadata (one thread per slot; at most kPreMax tasks, the rest
+// read the metadata themselves).
+__device__ __forceinline__ void fill_pre(const KernelArgs& a, int n, Shared& sm) {
+  const int k = tix();
+  if (k == 0) sm.pre_n = 0;
+  __syncthreads();
+  if (k < n) {
+    int idx = kPreNone;
+    const TaskDesc& t = sm.tq[k];
+    OpRef op = op_of(a, t.op);
+    if (op.type == TASK_ATTENTION) {
+      const int e = atomicAdd(&sm.pre_n, 1);
+      if (e < kPreMax) {
+        idx = e;
+        const BatchMeta& m = a.meta;
+        const AttnGeom g = attn_geom(m, op, t.i0, t.i2);
+        AttnPre& P = sm.pre[e];
+        P.t0 = g.t0; P.nt = g.nt; P.pb = g.pb; P.np = g.np; P.base = g.base; P.c0 = g.c0; P.c1 = g.c1;
+        for (int w = 0; w < 7; w++) {
+          const int p0 = g.c0 + w * 64;
+          int idA = 0, idB = 0;
+          if (g.nt > 0 && p0 < g.c1) {
+            const int pg0 = p0 / kPage;
+            idA = m.kv_indices[g.pb + pg0];
+            idB = pg0 + 1 < g.np ? m.kv_indices[g.pb + pg0 + 1] : idA;
+          }
+          P.id[2 * w] = idA;
+          P.id[2 * w + 1] = idB;
+        }
+        for (int i = 0; i < 4; i++) P.pg_tok[i] = i < g.nt ? m.kv_indices[g.pb + (g.base + i) / kPage] : 0;
+      }
+    }
+    sm.pre_of[k] = (uint8_t)idx;
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------ kernel
 // ------------------------------------------------------------ task entry points
 // Each task type is its own function: the worker loop calls it with the
@@ -1481,13 +1571,13 @@ __device__ __forceinline__ void run_gemv(int slot, int tid) {
 template <int RMAX>
 __device__ __forceinline__ void run_attention(int slot, int tid) {
   const TaskDesc t = task_at(slot);
-  task_attention_body<RMAX>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+  task_attention_body<RMAX>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), slot, g_sm);
 }
 // the multi-token variant (rare on the decode path, heavy register use) stays
 // out of line so that it cannot push the hot paths into spilling
 __device__ __attribute__((noinline)) void run_attention_large(int slot, int tid) {
   const TaskDesc t = task_at(slot);
-  task_attention_body<16>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+  task_attention_body<16>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), slot, g_sm);
 }
 __device__ __forceinline__ void run_embed(int slot, int tid) {
   const TaskDesc t = task_at(slot);
@@ -1512,6 +1602,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     }
   };
   load_descs(q0);
+  __syncthreads();
+  fill_pre(a, q1 - q0 < 256 ? q1 - q0 : 256, sm);
   if (threadIdx.x == 0) {
     sm.args = a;
     sm.flag = 1;
@@ -1524,6 +1616,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     if (q > q0 && (q - q0) % 256 == 0) {
       __syncthreads();
       load_descs(q);
+      // (later descriptor chunks: attention tasks read their metadata)
+      for (int i = tix(); i < 256; i += PK_THREADS) sm.pre_of[i] = kPreNone;
       __syncthreads();
     }
     const int tid = __builtin_amdgcn_readfirstlane(a.queue[q]);
