@@ -343,7 +343,7 @@ __device__ __forceinline__ int xs_swz(int b, int e) { return (((e >> 3) ^ b) << 
 // Sync wave: rows [0, TM) of elements [k0, k0 + KB) of op.x into xs[b][KB];
 // rows b >= T are zero.  16 loads per lane in flight.
 template <int TM>
-__device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared& sm, int lane) {
+__device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared& sm, int lane, int xoff = 0) {
   // groups of 64 chunks (one 16-byte load per lane): group m is row m / k,
   // chunks (m % k) * 64 + lane.  Row and group offsets are wave-uniform, so
   // a load is one buffer load at (lane * 16 + scalar offset), and groups past
@@ -374,7 +374,7 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
     int xr = mb0, xc = mc0;
 #pragma unroll
     for (int u = 0; u < NB; u++) {
-      uint16_t* dst = g + u < total ? sm.xs + xr * KB + xs_swz(xr, xc * 512 + lane * 8) : junk + lane * 8;
+      uint16_t* dst = g + u < total ? sm.xs + xoff + xr * KB + xs_swz(xr, xc * 512 + lane * 8) : junk + lane * 8;
       *reinterpret_cast<uint4*>(dst) = v[u];
       if (++xc == k) { xc = 0; xr++; }
     }
@@ -584,13 +584,17 @@ __device__ __forceinline__ void flush_acc(float (&acc)[TM], float* slot, int lan
 }
 
 // Number of staged K blocks: the fewest equal blocks of whole 512-element
-// chunks whose activations fit the staging buffer.
+// chunks whose activations fit the staging buffer -- or, when one block does
+// not hold all of K, half of it: blocks then alternate between the two
+// halves, and block kb + 1 is staged while block kb is consumed.
 __device__ __forceinline__ int gemv_blocks(int NC, int TM) {
-  const int maxc = (XS_ELEMS / TM) >> 9;
+  int maxc = (XS_ELEMS / TM) >> 9;
+  if (NC > maxc) maxc >>= 1;
   int nkb = (NC + maxc - 1) / maxc;
   while (NC % nkb) nkb++;
   return nkb;
 }
+constexpr int XS_HALF = XS_ELEMS / 2;  // second staging buffer (multi-block K)
 
 template <int TM, int EPI>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
@@ -708,17 +712,15 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   }
 
   if (is_sync) {
+    // multi-block K (batch > 1 only): block kb goes to half kb & 1 while the
+    // compute waves consume block kb - 1 from the other half; barrier [Bkb]
+    // = block kb staged and block kb - 1 consumed
     for (int kb = 1; kb < nkb; kb++) {
-      __syncthreads();  // compute waves are done with block kb - 1
-      if (TM == 1 && (op.flags & OPF_X_LL)) stage_x_link(a, op, KB, kb * KB, sm, lane);
-      else stage_x<TM>(op, T, KB, kb * KB, sm, lane);
-      __syncthreads();  // block kb staged
+      stage_x<TM>(op, T, KB, kb * KB, sm, lane, (kb & 1) * XS_HALF);
+      lds_sync();  // [Bkb]
     }
   } else if (n == 0) {
-    for (int kb = 1; kb < nkb; kb++) {
-      __syncthreads();
-      __syncthreads();
-    }
+    for (int kb = 1; kb < nkb; kb++) lds_sync();
   } else {
     // ---------------- compute waves: stream the unit range
     if constexpr (MF) {
@@ -729,17 +731,18 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       const bool bok = bt < TM;
       const uint16_t* xrow = sm.xs + bt * KB;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      int tl = row0, c = c00, ib = 0;
+      int tl = row0, c = c00, ib = 0, kb = 0;
       for (int g0 = 0; g0 < total; g0 += RING) {
 #pragma unroll
         for (int s = 0; s < RING; s++) {
           if (g0 + s < total) {
-            if (ib == n) {  // next staged block
+            if (ib == n) {  // next staged block, in the other half
               ib = 0;
               tl = row0;
               c = c00;
-              __syncthreads();
-              __syncthreads();
+              kb++;
+              xrow = sm.xs + (kb & 1) * XS_HALF + bt * KB;
+              lds_sync();  // [Bkb]
             }
             const uint4 w = ring[s];
             issue(ring[s]);
@@ -771,12 +774,11 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
 #pragma unroll
       for (int s = 0; s < RING; s++) {
         if (g0 + s < total) {
-          if (TM > 1 && ib == n) {  // next staged block
+          if (TM > 1 && ib == n) {  // (batch 1 stages all of K at once)
             ib = 0;
             row = row0;
             c = c00;
-            __syncthreads();
-            __syncthreads();
+            lds_sync();
           }
           const uint4 w = ring[s];
           issue(ring[s]);
