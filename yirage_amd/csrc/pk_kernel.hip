@@ -808,7 +808,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   }
   __syncthreads();  // [O]: every partial sum is in its slot
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
-  if (!is_sync) return;
+  if (!is_sync) {
+    // [E]: the sync wave's output stores go into the CU's memory queue ahead
+    // of this wave's next-task weight loads (behind ~100 KiB of loads they
+    // became visible to the consumers microseconds later)
+    lds_sync();
+    return;
+  }
 
   // ---------------- sync wave: epilogue, stores, publish
   // value of weight row j for token b: its slots, in wave order
@@ -868,6 +874,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
   }
+  lds_sync();  // [E]
   if constexpr (EPI == EPI_ARGMAX) {
     // local (value, index) maximum per token over this task's valid rows;
     // lowest index wins ties (torch.argmax semantics)
