@@ -467,10 +467,8 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
         uint4 pb[HPW][PF_NB / 2];  // P^T B operands of the 32-token steps
 #pragma unroll
         for (int hh = 0; hh < HPW; hh++) {
-#pragma unroll
-          for (int n = 0; n < PF_NB; n++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) sc[hh][n][i] *= a.scale_log2;
+          // scores stay unscaled: the max commutes with the positive scale,
+          // which is folded into the exponent's fma below
           if (edge) {
 #pragma unroll
             for (int n = 0; n < PF_NB; n++)
@@ -487,6 +485,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[hh][n][i]);
           mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
           mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+          mx *= a.scale_log2;
           const bool grow = mx > m_i[hh] + kLazy;
           if (__builtin_amdgcn_ballot_w64(grow)) {
             const float mnew = grow ? mx : m_i[hh];
@@ -503,7 +502,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
           for (int n = 0; n < PF_NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-              const float p = __builtin_amdgcn_exp2f(sc[hh][n][i] - mref);
+              const float p = __builtin_amdgcn_exp2f(fmaf(sc[hh][n][i], a.scale_log2, -mref));
               pv[n][i] = p;
               ls += p;
             }
