@@ -470,10 +470,10 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
   }
 }
 
-// One wave, batch > 1: row b of the staged activations (all of K <= 4096
-// in one block) times rsqrt(mean(x^2) + eps) * gamma (gamma staged in
-// attn_p), rounded to bf16, in place -- the arithmetic of norm_x, with every
-// LDS read of the row in flight at once.
+// One wave: row b of the staged activations (all of K <= 4096 in one
+// block) times rsqrt(mean(x^2) + eps) * gamma (gamma staged in attn_p),
+// rounded to bf16, in place -- the arithmetic of norm_x, with every LDS read
+// of the row in flight at once.
 __device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, int lane) {
   const int K = op.K;
   const uint16_t* gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
@@ -674,8 +674,12 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       // faster than polling the producers' counter first)
       if ((op.flags & OPF_X_LL) || poll_event_sync(a, t, task_id, sm)) {
         T = active_tokens(a, op);
-        if (TM == 1 && (op.flags & OPF_X_LL)) stage_x_link(a, op, KB, 0, sm, lane);
-        else stage_x<TM>(op, T, KB, 0, sm, lane);
+        if (TM == 1 && (op.flags & OPF_X_LL)) {
+          stage_x_link(a, op, KB, 0, sm, lane);
+          if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
+        } else {
+          stage_x<TM>(op, T, KB, 0, sm, lane);
+        }
         if (NORM && MF && pre) {
           // batch > 1: gamma to LDS; every wave then normalizes one row
           uint16_t* gam = reinterpret_cast<uint16_t*>(&sm.attn_p[0][0][0]);
@@ -685,6 +689,15 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
             if (c < K) *reinterpret_cast<uint4*>(gam + c) = nr.g[j];
           }
           if (lane == 0) sm.norm_rows = T;
+        } else if (NORM && TM == 1 && pre) {
+          // one row: the same parallel form, gamma through attn_p
+          uint16_t* gam = reinterpret_cast<uint16_t*>(&sm.attn_p[0][0][0]);
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const int c = (lane + kWave * j) * 8;
+            if (c < K) *reinterpret_cast<uint4*>(gam + c) = nr.g[j];
+          }
+          if (T > 0) norm_row(op, 0, KB, sm, lane);
         } else if (NORM) {
           norm_x(op, T, KB, sm, nr, pre, lane);
         }
@@ -699,7 +712,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       sm.last_op = nkb == 1 ? t.op : -1;
     }
   }
-  __syncthreads();  // [X]: block 0 staged, slots cleared
+  lds_sync();  // [X]: block 0 staged, slots cleared
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
@@ -707,7 +720,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     const int nr = __builtin_amdgcn_readfirstlane(sm.norm_rows);
     if (nr > 0) {  // workgroup-uniform
       if (wave < nr) norm_row(op, wave, KB, sm, lane);
-      __syncthreads();  // rows normalized
+      lds_sync();  // rows normalized
     }
   }
 
@@ -806,7 +819,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
     }
   }
-  __syncthreads();  // [O]: every partial sum is in its slot
+  lds_sync();  // [O]: every partial sum is in its slot
   if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
   if (!is_sync) {
     // [E]: the sync wave's output stores go into the CU's memory queue ahead
