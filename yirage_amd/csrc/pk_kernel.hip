@@ -1137,6 +1137,9 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         return __any(st);
       };
       issue();
+      // [Q] (plain input): the q loads go into the CU's memory queue ahead of
+      // the compute waves' cached-block loads (~200 KiB at batch 8)
+      if (!lk) lds_sync();
       int pg_tok = 0;  // page of new token lane % 16
       if (newtok && qrow < nt)
         pg_tok = have_pre && qrow < 4 ? sm.pre[pe].pg_tok[qrow] : m.kv_indices[pb + (base + qrow) / kPage];
@@ -1186,8 +1189,12 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         }
       }
     }
+    else if (!lk) {
+      lds_sync();  // [Q] (the poll failed; nothing to issue)
+    }
   }
   // prefetch the first cached block of this wave
+  if (!lk && wave < CW) lds_sync();  // [Q]
   if (wave < nblk && wave < CW) {
     const BlkAddr ba = blk_addr(wave, have_pre);
     load_k(ba);
