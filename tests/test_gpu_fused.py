@@ -168,6 +168,8 @@ def test_gqa_decode_paged(B, Hq, Hkv, L, page, dtype):
     (300, True, torch.float16, 1, 8, 8),     # MHA (one head per wave)
     (130, True, torch.bfloat16, 2, 6, 2),    # odd group size, batch 2
     (77, False, torch.float16, 2, 4, 1),
+    (64, False, torch.bfloat16, 1, 4, 1),    # one full tile, no masked positions
+    (1, True, torch.float16, 1, 4, 2),       # single token: output is V
 ])
 def test_gqa_prefill(S, causal, dtype, B, Hq, Hkv):
     import yirage_amd.fused as F
@@ -180,7 +182,8 @@ def test_gqa_prefill(S, causal, dtype, B, Hq, Hkv):
     v = _randn((B, S, Hkv, D), 1.0, dtype, g)
     out = F.gqa_prefill(q.cuda(), k.cuda(), v.cuda(), causal=causal)
     torch.cuda.synchronize()
-    rows = sorted(set([0, 1, 15, 16, 63, 64, S // 2, S - 2, S - 1] + list(range(0, S, max(1, S // 24)))))
+    rows = sorted(set(r for r in [0, 1, 15, 16, 63, 64, S // 2, S - 2, S - 1] + list(range(0, S, max(1, S // 24)))
+                      if 0 <= r < S))
     ref = O.gqa_prefill(_f(q), _f(k), _f(v), causal=causal, rows=rows)
     _close(out[:, rows], ref[:, rows], "gqa_prefill")
 

@@ -327,10 +327,7 @@ static DecPlan dec_plan(int batch, int hkv, int max_len, int page) {
 // takes the query blocks i and N - 1 - i, so every workgroup does the same
 // amount of work.
 constexpr int PF_QROWS = 64;             // query rows per block (4 row waves x 16)
-#ifndef YR_PF_KT
-#define YR_PF_KT 64
-#endif
-constexpr int PF_KT = YR_PF_KT;          // kv tokens per tile
+constexpr int PF_KT = 64;                // kv tokens per tile
 constexpr int PF_NB = PF_KT / 16;        // 16-token MFMA blocks per tile
 constexpr float kLazy = 8.f;             // running-max slack (log2 units)
 
@@ -341,6 +338,7 @@ struct PrefillArgs {
   uint16_t* o;
   int B, S, Hq, Hkv, causal, nblk;
   int paired;  // blocks (i, nblk - 1 - i) per workgroup (causal)
+  int npair, ngrp, nwg;  // workgroups per (batch, head group); head groups; total
   float scale_log2;
 };
 
@@ -350,6 +348,17 @@ __device__ __forceinline__ uint2 lds_tr4(const uint16_t* p) {
       reinterpret_cast<const lds_v4i16*>(reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
           reinterpret_cast<uintptr_t>(p)))));
   return __builtin_bit_cast(uint2, r);
+}
+
+// max over lanes l and l ^ 16 (l ^ 32): a permlane swap of the value with
+// itself hands each 16-lane row its partner row, in registers (no LDS trip)
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // 16-byte chunk permutation of a 256-byte LDS row: bits 1..3 = row % 8,
@@ -378,12 +387,22 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   // stage do not wait for the direct loads still filling the other
   __shared__ __attribute__((aligned(16))) uint16_t sk0[PF_KT * D], sk1[PF_KT * D];
   __shared__ __attribute__((aligned(16))) uint16_t sv0[PF_KT * D], sv1[PF_KT * D];
+  // Q^T fragments in fragment order (lane l's 16 bytes at 16 l: no bank
+  // conflicts), re-read by every S^T block instead of held in registers
+  __shared__ uint4 sq[4 * HG][HPW][4][kWave];
 
-  const int pair = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
+  // workgroup i runs on XCD i % 8; work items are numbered so that one
+  // XCD's share is contiguous, i.e. whole kv heads whose K / V stay in that
+  // XCD's L2
+  const int id = blockIdx.x;
+  const int w = a.nwg % 8 == 0 ? (id % 8) * (a.nwg / 8) + id / 8 : id;
+  const int pair = w % a.npair, hg = (w / a.npair) % a.ngrp, b = w / (a.npair * a.ngrp);
   const int G = a.Hq / a.Hkv;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int rw = wave % 4;                              // row wave
-  const int h0 = (hg * HG + wave / 4) * HPW, hk = h0 / G;  // this wave's first head
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave index, uniform
+  const int rw = wv % 4;                                       // row wave
+  const int h0 = (hg * HG + wv / 4) * HPW;                     // this wave's first head
+  const int hk = hg * HG * HPW / G;  // the workgroup's heads share one kv head (G % (HG HPW) == 0)
   const int col = lane % 16, grp = lane / 16;
   const size_t qstride = (size_t)a.Hq * D, kstride = (size_t)a.Hkv * D;
   const uint16_t* kbase = a.k + (size_t)b * a.S * kstride + (size_t)hk * D;
@@ -392,7 +411,28 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   // lane l writes physical chunk l % 16 of row 4 u + l / 16, i.e. source
   // chunk (l % 16) ^ pf_swz(row)
   constexpr int RPW = PF_KT / (4 * HG);
-  const int st_row0 = RPW * wave + lane / 16;
+  const int st_row0 = RPW * wv + lane / 16;
+  // per-lane byte offsets of the staged chunks within a tile (rows of a tile
+  // below S), and the element offsets of the K fragment reads (block n adds
+  // 16 n D: pf_swz of row 16 n + col does not depend on n)
+  uint32_t foff[RPW / 4];
+#pragma unroll
+  for (int u = 0; u < RPW / 4; u++) {
+    const int row = st_row0 + 4 * u;
+    foff[u] = 2u * (uint32_t)(row * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
+  }
+  uint32_t koff[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) koff[s] = col * D + 8 * ((4 * s + grp) ^ pf_swz(col));
+  // V^T fragment reads: lane 4e + q of group grp reads tokens 32 m + 16 j +
+  // 4 grp + e, d 16 dt + 4 q .. +3 (q = 2 qc + qh / 4); pf_swz of those rows
+  // depends on neither m nor j, so (m, j) add 16 (2 m + j) D
+  uint32_t voff[D / 16];
+  {
+    const int e = col / 4, qc = (col % 4) / 2, qh = 4 * (col % 2), r0 = 4 * grp + e;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) voff[dt] = r0 * D + 8 * ((2 * dt + qc) ^ pf_swz(r0)) + qh;
+  }
 
   for (int pass = 0; pass < (a.paired ? 2 : 1); pass++) {
     const int blk = pass == 0 ? pair : a.nblk - 1 - pair;
@@ -400,12 +440,11 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
     const int q0 = blk * PF_QROWS + rw * 16;  // this wave's first query row
     const int qr = q0 + col;                    // this lane's query row
     // Q^T as the B operand: column = query row, k = d 32 s + 8 grp .. +7
-    uint4 qf[HPW][4];
 #pragma unroll
     for (int hh = 0; hh < HPW; hh++) {
       const uint16_t* qrow = a.q + ((size_t)b * a.S + min(qr, a.S - 1)) * qstride + (size_t)(h0 + hh) * D;
 #pragma unroll
-      for (int s = 0; s < 4; s++) qf[hh][s] = ldg16(qrow + 32 * s + 8 * grp);
+      for (int s = 0; s < 4; s++) sq[wv][hh][s][lane] = ldg16(qrow + 32 * s + 8 * grp);
     }
     f32x4 acc[HPW][D / 16];  // O^T: rows d 16 dt + 4 grp + i, column = query row
 #pragma unroll
@@ -421,122 +460,174 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
 
     const int kv_end = a.causal ? min(a.S, (blk + 1) * PF_QROWS) : a.S;
     const int ntile = (kv_end + PF_KT - 1) / PF_KT;
-    auto fetch = [&](int t, uint16_t* sk, uint16_t* sv) __attribute__((always_inline)) {
+    // tiles that need no mask: below every query row of the block and
+    // entirely inside the sequence
+    const int nfull = a.causal ? min(ntile, blk * PF_QROWS / PF_KT) : a.S / PF_KT;
+    // causal: the last tile holding a key at or below this wave's rows
+    const int tw_end = a.causal ? min(ntile, (q0 + 15) / PF_KT + 1) : ntile;
+    auto fetch = [&](int t, const uint16_t* base, uint16_t* dst) __attribute__((always_inline)) {
+      const char* tb = reinterpret_cast<const char*>(base + (size_t)t * PF_KT * kstride);  // uniform
+      const bool whole = (t + 1) * PF_KT <= a.S;
 #pragma unroll
       for (int u = 0; u < RPW / 4; u++) {
-        const int row = st_row0 + 4 * u;
-        const int tok = min(t * PF_KT + row, a.S - 1);  // clamped rows are masked
-        const size_t off = (size_t)tok * kstride + 8 * ((lane % 16) ^ pf_swz(row));
-        lds_load16(kbase + off, sk + (RPW * wave + 4 * u) * D);
-        lds_load16(vbase + off, sv + (RPW * wave + 4 * u) * D);
+        uint32_t off = foff[u];
+        if (!whole) {  // last tile: rows past S re-read token S - 1 (masked)
+          const int row = st_row0 + 4 * u;
+          const int r = min(t * PF_KT + row, a.S - 1) - t * PF_KT;
+          off = 2u * (uint32_t)(r * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
+        }
+        lds_load16(reinterpret_cast<const uint16_t*>(tb + off), dst + (RPW * wv + 4 * u) * D);
       }
     };
-    __syncthreads();  // the previous pass's last tile has been read by every wave
-    fetch(0, sk0, sv0);
-    wait_vm();
-    __syncthreads();
-    // one tile from (kt, vt) while tile t + 1 streams into (nk, nv)
-    auto tile = [&](int t, const uint16_t* kt, const uint16_t* vt, uint16_t* nk, uint16_t* nv)
-                    __attribute__((always_inline)) {
-      const int t0 = t * PF_KT;
-      if (t + 1 < ntile) fetch(t + 1, nk, nv);
-      if (!a.causal || t0 <= q0 + 15) {
-        // S^T = K Q^T: 4 blocks of 16 tokens; lane holds tokens t0 + 16 n + 4 grp + i
-        f32x4 sc[HPW][PF_NB];
+    // S^T = K Q^T: 4 blocks of 16 tokens; lane holds tokens t0 + 16 n + 4 grp + i
+    using Scores = f32x4[HPW][PF_NB];
+    using PFrag = uint4[HPW][PF_NB / 2];
+    auto qk = [&](const uint16_t* kt, Scores& sc) __attribute__((always_inline)) {
 #pragma unroll
-        for (int n = 0; n < PF_NB; n++) {
-          uint4 kf[4];
+      for (int n = 0; n < PF_NB; n++) {
+        uint4 kf[4];
 #pragma unroll
-          for (int s = 0; s < 4; s++) {
-            const int row = 16 * n + col;
-            kf[s] = *reinterpret_cast<const uint4*>(&kt[row * D + 8 * ((4 * s + grp) ^ pf_swz(row))]);
-          }
-#pragma unroll
-          for (int hh = 0; hh < HPW; hh++) {
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 4; s++) c = mfma16<DT>(kf[s], qf[hh][s], c);
-            sc[hh][n] = c;
-          }
-        }
-        // online softmax of this lane's query row.  The running max only moves
-        // when it grows by more than kLazy (log2 units): P stays <= 2^kLazy,
-        // exact after the final 1 / l, and the O rescale is skipped by the
-        // whole wave on most tiles.
-        const bool edge = (a.causal && t0 + PF_KT - 1 > q0) || t0 + PF_KT > a.S;
-        uint4 pb[HPW][PF_NB / 2];  // P^T B operands of the 32-token steps
+        for (int s = 0; s < 4; s++) kf[s] = *reinterpret_cast<const uint4*>(&kt[koff[s] + 16 * n * D]);
 #pragma unroll
         for (int hh = 0; hh < HPW; hh++) {
-          // scores stay unscaled: the max commutes with the positive scale,
-          // which is folded into the exponent's fma below
-          if (edge) {
+          f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int n = 0; n < PF_NB; n++)
+          for (int s = 0; s < 4; s++) c = mfma16<DT>(kf[s], sq[wv][hh][s][lane], c);
+          sc[hh][n] = c;
+        }
+      }
+    };
+    // online softmax of this lane's query row over tile t, in two parts so
+    // that S(t + 1) can be issued between them.  smax: mask (EDGE: the tile
+    // crosses the causal diagonal or the end of the sequence), row max, O
+    // rescale.  The running max only moves when it grows by more than kLazy
+    // (log2 units): P stays <= 2^kLazy, exact after the final 1 / l, and the
+    // rescale is skipped by the whole wave on most tiles.  Scores stay
+    // unscaled: the max commutes with the positive scale, which is folded
+    // into the exponent's fma.
+    auto smax = [&](int t, Scores& sc, auto edge_c) __attribute__((always_inline)) {
+      constexpr bool EDGE = decltype(edge_c)::value;
+      const int t0 = t * PF_KT;
 #pragma unroll
-              for (int i = 0; i < 4; i++) {
-                const int tok = t0 + 16 * n + 4 * grp + i;
-                if (tok >= a.S || (a.causal && tok > qr)) sc[hh][n][i] = -INFINITY;
-              }
-          }
-          float mx = -INFINITY;
-#pragma unroll
-          for (int n = 0; n < PF_NB; n++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[hh][n][i]);
-          mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-          mx *= a.scale_log2;
-          const bool grow = mx > m_i[hh] + kLazy;
-          if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float mnew = grow ? mx : m_i[hh];
-            const float alpha = m_i[hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i[hh] - mnew);
-            m_i[hh] = mnew;
-            l_i[hh] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] *= alpha;
-          }
-          const float mref = m_i[hh] == -INFINITY ? 0.f : m_i[hh];  // all -inf so far: P = 0
-          float ls = 0.f;
-          float pv[PF_NB][4];
+      for (int hh = 0; hh < HPW; hh++) {
+        if (EDGE) {
 #pragma unroll
           for (int n = 0; n < PF_NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-              const float p = __builtin_amdgcn_exp2f(fmaf(sc[hh][n][i], a.scale_log2, -mref));
-              pv[n][i] = p;
-              ls += p;
+              const int tok = t0 + 16 * n + 4 * grp + i;
+              if (tok >= a.S || (a.causal && tok > qr)) sc[hh][n][i] = -INFINITY;
             }
-          l_i[hh] += ls;  // per lane; the four lane groups add up at the end
-          // k slot 8 grp + 4 j + i of step m <-> token 32 m + 16 j + 4 grp + i
-#pragma unroll
-          for (int m = 0; m < PF_NB / 2; m++)
-            pb[hh][m] = make_uint4(pack2<DT>(pv[2 * m][0], pv[2 * m][1]), pack2<DT>(pv[2 * m][2], pv[2 * m][3]),
-                                   pack2<DT>(pv[2 * m + 1][0], pv[2 * m + 1][1]),
-                                   pack2<DT>(pv[2 * m + 1][2], pv[2 * m + 1][3]));
         }
-        // O^T += V^T P^T.  V^T fragment (rows d 16 dt + col, k slots as above):
-        // lane 4e + q of group grp reads tokens 32 m + 16 j + 4 grp + e,
-        // d 16 dt + 4 q .. +3; the transposing read hands lane col its d.
-        const int e = col / 4, qc = (col % 4) / 2, qh = 4 * (col % 2);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < PF_NB; n++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[hh][n][i]);
+        mx = max_xor16(mx);
+        mx = max_xor32(mx);
+        mx *= a.scale_log2;
+        const bool grow = mx > m_i[hh] + kLazy;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          const float mnew = grow ? mx : m_i[hh];
+          const float alpha = m_i[hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i[hh] - mnew);
+          m_i[hh] = mnew;
+          l_i[hh] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < D / 16; dt++) acc[hh][dt] *= alpha;
+        }
+      }
+    };
+    // sexp: P = exp2(s scale - m) as the B operands of P V, row sums in l
+    auto sexp = [&](const Scores& sc, PFrag& pb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int hh = 0; hh < HPW; hh++) {
+        const float mref = m_i[hh] == -INFINITY ? 0.f : m_i[hh];  // all -inf so far: P = 0
+        float ls = 0.f;
+        float pv[PF_NB][4];
+#pragma unroll
+        for (int n = 0; n < PF_NB; n++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sc[hh][n][i], a.scale_log2, -mref));
+            pv[n][i] = p;
+            ls += p;
+          }
+        l_i[hh] += ls;  // per lane; the four lane groups add up at the end
+        // k slot 8 grp + 4 j + i of step m <-> token 32 m + 16 j + 4 grp + i
 #pragma unroll
         for (int m = 0; m < PF_NB / 2; m++)
-#pragma unroll
-          for (int dt = 0; dt < D / 16; dt++) {
-            const int r0 = 32 * m + 4 * grp + e, r1 = r0 + 16;
-            const uint2 lo = lds_tr4(&vt[r0 * D + 8 * ((2 * dt + qc) ^ pf_swz(r0)) + qh]);
-            const uint2 hi = lds_tr4(&vt[r1 * D + 8 * ((2 * dt + qc) ^ pf_swz(r1)) + qh]);
-            const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-            for (int hh = 0; hh < HPW; hh++) acc[hh][dt] = mfma16<DT>(vf, pb[hh][m], acc[hh][dt]);
-          }
+          pb[hh][m] = make_uint4(pack2<DT>(pv[2 * m][0], pv[2 * m][1]), pack2<DT>(pv[2 * m][2], pv[2 * m][3]),
+                                 pack2<DT>(pv[2 * m + 1][0], pv[2 * m + 1][1]),
+                                 pack2<DT>(pv[2 * m + 1][2], pv[2 * m + 1][3]));
       }
-      wait_vm();  // tile t + 1 has landed in LDS
+    };
+    // O^T += V^T P^T.  V^T fragment (rows d 16 dt + col, k slots as above):
+    // lane 4e + q of group grp reads tokens 32 m + 16 j + 4 grp + e, d 16 dt
+    // + 4 q .. +3; the transposing read hands lane col its d.
+    auto pv = [&](const uint16_t* vt, const PFrag& pb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int m = 0; m < PF_NB / 2; m++)
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+          const uint2 lo = lds_tr4(&vt[voff[dt] + 32 * m * D]);
+          const uint2 hi = lds_tr4(&vt[voff[dt] + (32 * m + 16) * D]);
+          const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+          for (int hh = 0; hh < HPW; hh++) acc[hh][dt] = mfma16<DT>(vf, pb[hh][m], acc[hh][dt]);
+        }
+    };
+    // Software pipeline: step t computes S(t + 1) on MFMA while the softmax
+    // of S(t) runs on VALU, then P(t) V(t).  K runs one tile ahead of V, so
+    // step t reads K(t + 1) and V(t) while K(t + 2) and V(t + 1) stream into
+    // the buffers whose previous contents step t - 1 finished reading.
+    Scores sA, sB;
+    PFrag pb;
+    __syncthreads();  // the previous pass's last tiles have been read by every wave
+    fetch(0, kbase, sk0);
+    fetch(0, vbase, sv0);
+    if (ntile > 1) fetch(1, kbase, sk1);
+    wait_vm();
+    __syncthreads();
+    qk(sk0, sA);
+    __syncthreads();  // every wave is done with K(0) before K(2) replaces it
+    // a step with a following tile (t + 1 < ntile) and no mask
+    auto step = [&](int t, const uint16_t* kq, const uint16_t* vp, uint16_t* nk, uint16_t* nv, Scores& scur,
+                    Scores& snext) __attribute__((always_inline)) {
+      if (t + 2 < ntile) fetch(t + 2, kbase, nk);
+      fetch(t + 1, vbase, nv);
+      smax(t, scur, std::false_type{});
+      qk(kq, snext);
+      sexp(scur, pb);
+      pv(vp, pb);
+      wait_vm();  // K(t + 2) and V(t + 1) have landed in LDS
       __syncthreads();
     };
-    for (int t = 0; t < ntile; t += 2) {
-      tile(t, sk0, sv0, sk1, sv1);
-      if (t + 1 < ntile) tile(t + 1, sk1, sv1, sk0, sv0);
+    // the last tile: masked, nothing to fetch or prefetch
+    auto last = [&](int t, const uint16_t* vp, Scores& scur) __attribute__((always_inline)) {
+      if (t < tw_end) {
+        smax(t, scur, std::true_type{});
+        sexp(scur, pb);
+        pv(vp, pb);
+      }
+    };
+    // tiles below nfull need no mask; the last tile always takes the masked
+    // path (for causal blocks it is the diagonal one)
+    const int nstep = min(nfull, ntile - 1);
+    int t = 0;
+    for (; t + 1 < nstep; t += 2) {
+      step(t, sk1, sv0, sk0, sv1, sA, sB);
+      step(t + 1, sk0, sv1, sk1, sv0, sB, sA);
     }
+    if (t < nstep) {
+      step(t, sk1, sv0, sk0, sv1, sA, sB);
+      t++;
+    }
+    // t == ntile - 1 here: ntile - nfull <= 1 (non-causal: floor and ceiling
+    // of S / PF_KT; causal: the block's rows start at blk PF_QROWS, so tiles
+    // below blk PF_QROWS / PF_KT are full and one more reaches its last row)
+    if (t % 2 == 0) last(t, sv0, sA);
+    else last(t, sv1, sB);
     // O[query row][d 16 dt + 4 grp + i]
 #pragma unroll
     for (int hh = 0; hh < HPW; hh++) {
@@ -694,7 +785,10 @@ int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, i
   const int hpw = (YR_PF_CFG == 0 || YR_PF_CFG == 3) && G % 2 == 0 ? 2 : 1;
   const int hgw = (YR_PF_CFG >= 2) && (G / hpw) % 2 == 0 ? 2 : 1;
   a.paired = a.causal;
-  dim3 grid(a.paired ? (a.nblk + 1) / 2 : a.nblk, hq / (hpw * hgw), batch);
+  a.npair = a.paired ? (a.nblk + 1) / 2 : a.nblk;
+  a.ngrp = hq / (hpw * hgw);
+  a.nwg = a.npair * a.ngrp * batch;
+  dim3 grid(a.nwg);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == YR_DTYPE_BF16;
 #define YR_PF(H, W)                                                                                        \
