@@ -366,6 +366,12 @@ __device__ __forceinline__ float max_xor32(float x) {
 // fragment reads, one chunk column over 16 rows), and 8 rows starting at a
 // multiple of 8 keep bit 0 fixed (transposing V reads, chunk pairs 2c, 2c + 1).
 __device__ __forceinline__ int pf_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+// K tiles: chunk permutation row % 16.  A 16-byte LDS read is served 8 lanes
+// per 128 bytes: the K fragment read (lanes = 16 consecutive rows, one chunk
+// column) then gives any 8 consecutive lanes 8 distinct chunks modulo 8,
+// which pf_swz (even chunks for rows 0..7) does not (measured: all bank
+// conflicts of the kernel were K reads)
+__device__ __forceinline__ int pk_swz(int row) { return row & 15; }
 
 // 16 bytes per lane from global memory straight into LDS: lane l's data
 // lands at lds_base + 16 l (lds_base wave-uniform)
@@ -415,15 +421,16 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   // per-lane byte offsets of the staged chunks within a tile (rows of a tile
   // below S), and the element offsets of the K fragment reads (block n adds
   // 16 n D: pf_swz of row 16 n + col does not depend on n)
-  uint32_t foff[RPW / 4];
+  // (V tiles' offsets are formed per fetch: one register array fewer)
+  uint32_t foffk[RPW / 4];
 #pragma unroll
   for (int u = 0; u < RPW / 4; u++) {
     const int row = st_row0 + 4 * u;
-    foff[u] = 2u * (uint32_t)(row * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
+    foffk[u] = 2u * (uint32_t)(row * (int)kstride + 8 * ((lane % 16) ^ pk_swz(row)));
   }
   uint32_t koff[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) koff[s] = col * D + 8 * ((4 * s + grp) ^ pf_swz(col));
+  for (int s = 0; s < 4; s++) koff[s] = col * D + 8 * ((4 * s + grp) ^ pk_swz(col));
   // V^T fragment reads: lane 4e + q of group grp reads tokens 32 m + 16 j +
   // 4 grp + e, d 16 dt + 4 q .. +3 (q = 2 qc + qh / 4); pf_swz of those rows
   // depends on neither m nor j, so (m, j) add 16 (2 m + j) D
@@ -465,16 +472,20 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
     const int nfull = a.causal ? min(ntile, blk * PF_QROWS / PF_KT) : a.S / PF_KT;
     // causal: the last tile holding a key at or below this wave's rows
     const int tw_end = a.causal ? min(ntile, (q0 + 15) / PF_KT + 1) : ntile;
-    auto fetch = [&](int t, const uint16_t* base, uint16_t* dst) __attribute__((always_inline)) {
+    // IS_K: the K tile's chunk permutation (pk_swz), else V's (pf_swz)
+    auto fetch = [&](int t, const uint16_t* base, uint16_t* dst, auto is_k_c) __attribute__((always_inline)) {
+      constexpr bool IS_K = decltype(is_k_c)::value;
       const char* tb = reinterpret_cast<const char*>(base + (size_t)t * PF_KT * kstride);  // uniform
       const bool whole = (t + 1) * PF_KT <= a.S;
 #pragma unroll
       for (int u = 0; u < RPW / 4; u++) {
-        uint32_t off = foff[u];
+        const int row = st_row0 + 4 * u;
+        uint32_t off;
+        if constexpr (IS_K) off = foffk[u];
+        else off = 2u * (uint32_t)(row * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
         if (!whole) {  // last tile: rows past S re-read token S - 1 (masked)
-          const int row = st_row0 + 4 * u;
           const int r = min(t * PF_KT + row, a.S - 1) - t * PF_KT;
-          off = 2u * (uint32_t)(r * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
+          off = 2u * (uint32_t)(r * (int)kstride + 8 * ((lane % 16) ^ (IS_K ? pk_swz(row) : pf_swz(row))));
         }
         lds_load16(reinterpret_cast<const uint16_t*>(tb + off), dst + (RPW * wv + 4 * u) * D);
       }
@@ -584,9 +595,9 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
     Scores sA, sB;
     PFrag pb;
     __syncthreads();  // the previous pass's last tiles have been read by every wave
-    fetch(0, kbase, sk0);
-    fetch(0, vbase, sv0);
-    if (ntile > 1) fetch(1, kbase, sk1);
+    fetch(0, kbase, sk0, std::true_type{});
+    fetch(0, vbase, sv0, std::false_type{});
+    if (ntile > 1) fetch(1, kbase, sk1, std::true_type{});
     wait_vm();
     __syncthreads();
     qk(sk0, sA);
@@ -594,8 +605,8 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
     // a step with a following tile (t + 1 < ntile) and no mask
     auto step = [&](int t, const uint16_t* kq, const uint16_t* vp, uint16_t* nk, uint16_t* nv, Scores& scur,
                     Scores& snext) __attribute__((always_inline)) {
-      if (t + 2 < ntile) fetch(t + 2, kbase, nk);
-      fetch(t + 1, vbase, nv);
+      if (t + 2 < ntile) fetch(t + 2, kbase, nk, std::true_type{});
+      fetch(t + 1, vbase, nv, std::false_type{});
       smax(t, scur, std::false_type{});
       qk(kq, snext);
       sexp(scur, pb);
