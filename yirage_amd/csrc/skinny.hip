@@ -276,10 +276,32 @@ __global__ __launch_bounds__(kThreads, 1) void sk16_kernel(Args a) {
 // (2 x 2 MFMA blocks per matrix), A fragments by ds_read_b128, B fragments
 // by transposing reads.  Splits of one tile add up through fp32 records and
 // an arrival ticket (in split order).
+// 64-column W rows (128 bytes) with their 16-byte chunks permuted by
+// w_swz(row): the rows a transposing 32-lane read touches (8g + e and
+// 8g + e + 4 for e < 4, g < 2) get distinct chunk pairs
+__device__ __forceinline__ int w_swz(int r) { return (((r >> 1) & 1) | (((r >> 3) & 1) << 1)) << 1; }
+// b_frag of a w_swz-permuted 64-column tile: 16 columns from chunk cb
+__device__ __forceinline__ uint4 b_frag_swz(const uint16_t* tile, int cb, int row0, int lane) {
+  const int g = lane >> 4, j = lane & 15, e = j >> 2, q = j & 3;
+  const int r0 = row0 + 8 * g + e, r1 = r0 + 4, c = cb + (q >> 1);
+  const uint16_t* p0 = tile + r0 * 64 + ((c ^ w_swz(r0)) << 3) + (q & 1) * 4;
+  const uint16_t* p1 = tile + r1 * 64 + ((c ^ w_swz(r1)) << 3) + (q & 1) * 4;
+  auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
+    return const_cast<lds_v4i16*>(reinterpret_cast<const lds_v4i16*>(
+        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(reinterpret_cast<uintptr_t>(p))));
+  };
+  const uint2 l2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p0)));
+  const uint2 h2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p1)));
+  return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
 template <int DT, int NMAT, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   constexpr int TW = 64, KS = 64, MB = 128;
-  constexpr int LDW = TW + 8, LDX = KS + 8;   // padded LDS rows (fewer bank conflicts)
+  // W rows unpadded with chunks permuted by w_swz; x rows padded (A
+  // fragments by 16-byte reads of 16 rows at one k)
+  constexpr int LDW = TW, LDX = KS + 8;
+  static_assert(TW == 64, "w_swz / b_frag_swz assume 64-column W rows");
   constexpr int CHQ = 2;                      // chunks in flight (2 measured best of 2, 3, 4, 6)
   constexpr bool NORM = EPI == EPI_RMSNORM;
   __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][KS * LDW];
@@ -344,7 +366,8 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
       Chunk& c = ring[j];
       // stage chunk ci (x scaled by gamma for RMSNorm, row sums first)
 #pragma unroll
-      for (int m = 0; m < NMAT; m++) *reinterpret_cast<uint4*>(&wl[lb][m][wr_ * LDW + wc]) = c.w[m];
+      for (int m = 0; m < NMAT; m++)
+        *reinterpret_cast<uint4*>(&wl[lb][m][wr_ * LDW + (((wc >> 3) ^ w_swz(wr_)) << 3)]) = c.w[m];
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         uint4 xv = c.x[h];
@@ -366,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
         for (int m = 0; m < NMAT; m++)
 #pragma unroll
           for (int j2 = 0; j2 < 2; j2++) {
-            const uint4 bf = b_frag(&wl[lb][m][32 * ng + 16 * j2], LDW, 32 * ks, lane);
+            const uint4 bf = b_frag_swz(wl[lb][m], 4 * ng + 2 * j2, 32 * ks, lane);
 #pragma unroll
             for (int i = 0; i < 2; i++) acc[m][i][j2] = mfma16<DT>(af[i], bf, acc[m][i][j2]);
           }
