@@ -388,7 +388,8 @@ template <int DT, int HPW, int HG>
 __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   constexpr int D = 128;
   // K / V tiles: unpadded 256-byte rows whose 16-byte chunks are permuted by
-  // pf_swz(row); they arrive by direct global -> LDS loads (no registers)
+  // row (pk_swz for K, pf_swz for V); they arrive by direct global -> LDS
+  // loads (no registers)
   // separate objects per stage: the compiler then knows that reads of one
   // stage do not wait for the direct loads still filling the other
   __shared__ __attribute__((aligned(16))) uint16_t sk0[PF_KT * D], sk1[PF_KT * D];
@@ -415,12 +416,12 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   const uint16_t* vbase = a.v + (size_t)b * a.S * kstride + (size_t)hk * D;
   // staging: wave w fills rows RPW w .. RPW w + RPW - 1, four rows per load;
   // lane l writes physical chunk l % 16 of row 4 u + l / 16, i.e. source
-  // chunk (l % 16) ^ pf_swz(row)
+  // chunk (l % 16) ^ pk_swz(row) (K) or ^ pf_swz(row) (V)
   constexpr int RPW = PF_KT / (4 * HG);
   const int st_row0 = RPW * wv + lane / 16;
   // per-lane byte offsets of the staged chunks within a tile (rows of a tile
   // below S), and the element offsets of the K fragment reads (block n adds
-  // 16 n D: pf_swz of row 16 n + col does not depend on n)
+  // 16 n D: pk_swz of row 16 n + col does not depend on n)
   // (V tiles' offsets are formed per fetch: one register array fewer)
   uint32_t foffk[RPW / 4];
 #pragma unroll
