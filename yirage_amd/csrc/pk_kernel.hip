@@ -1491,10 +1491,11 @@ __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc
         for (int j = 0; j < npg; j++) { s.page_queue[tail % MP] = s.kv_indices[kp + j]; tail++; }
       }
     }
-    // the page-table snapshot lives in LDS (xs reused as int32)
-    int* snap = reinterpret_cast<int*>(sm.xs);
-    int all = s.kv_indptr[MR];
-    for (int i = 0; i < all && i < XS_ELEMS / 2; i++) snap[i] = s.kv_indices[i];
+    // the page table is rebuilt in place: requests keep their old pages from
+    // a snapshot (device memory of max_pages ids owned by the handle)
+    int* snap = s.page_snap;
+    const int all = s.kv_indptr[MR];
+    for (int i = 0; i < all && i < MP; i++) snap[i] = s.kv_indices[i];
     int nreq = 0, ntok = 0, npg = 0;
     for (int i = 0; i < MR; i++) {
       int rid = s.request_ids[i];
@@ -1729,7 +1730,7 @@ struct Handle {
   uint32_t* d_tickets = nullptr;
   float* d_scratch = nullptr;
   int* d_status = nullptr;
-  int* d_owned_meta = nullptr;  // request_ids, next_request_id, page_queue, head, tail
+  int* d_owned_meta = nullptr;  // request_ids, next_request_id, page_queue, head, tail, page snapshot
   BatchMeta meta;
   uint32_t epoch = 0;
   long long spin_limit = 1ll << 26;
@@ -1798,7 +1799,7 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   YRA(h->d_scratch, sizeof(float) * (g->scratch_floats + 4));
   YRA(h->d_status, sizeof(int) * 4);
   const int MR = g->cfg.max_requests, MP = g->cfg.max_pages;
-  YRA(h->d_owned_meta, sizeof(int) * (MR + 1 + MP + 2));
+  YRA(h->d_owned_meta, sizeof(int) * (MR + 1 + MP + 2 + MP));
 #undef YRA
   if (rc == YR_OK) rc = hip_ok(hipMemcpy(h->d_ops, g->ops.data(), sizeof(OpDesc) * h->n_ops, hipMemcpyHostToDevice), "copy ops");
   if (rc == YR_OK) rc = hip_ok(hipMemcpy(h->d_tasks, g->tasks.data(), sizeof(TaskDesc) * h->n_tasks, hipMemcpyHostToDevice), "copy tasks");
@@ -1827,6 +1828,7 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   m.page_queue = h->d_owned_meta + MR + 1;
   m.page_queue_head = h->d_owned_meta + MR + 1 + MP;
   m.page_queue_tail = h->d_owned_meta + MR + 2 + MP;
+  m.page_snap = h->d_owned_meta + MR + 3 + MP;
   m.status = h->d_status;
   m.max_requests = MR;
   m.max_tokens = g->cfg.max_tokens;

@@ -57,6 +57,14 @@ def _check_cuda(*ts):
                 raise _lib.YirageHipError("hip backend: tensors must be contiguous (row-major)")
 
 
+def _same_dtype(x, *others):
+    """Every 16-bit operand must share x's dtype (the kernels read them all
+    as x's element type)."""
+    for t in others:
+        if t is not None and t.dtype != x.dtype:
+            raise _lib.YirageHipError(f"hip backend: operand dtype {t.dtype} differs from x's {x.dtype}")
+
+
 def _w_layout_and_n(w: torch.Tensor, k: int, layout: int | None):
     if layout is None:
         layout = _lib.W_KN
@@ -72,6 +80,7 @@ def _w_layout_and_n(w: torch.Tensor, k: int, layout: int | None):
 def rmsnorm_linear(x, gamma, w, eps: float = 1e-6, w_layout: int | None = None, out=None):
     """out = (x * rsqrt(mean(x^2) + eps) * gamma) @ W  (fp32 accumulate)."""
     _check_cuda(x, gamma, w)
+    _same_dtype(x, gamma, w)
     B, K = x.shape
     layout, N = _w_layout_and_n(w, K, w_layout)
     dt = dtype_code(x.dtype)
@@ -87,6 +96,7 @@ def rmsnorm_linear(x, gamma, w, eps: float = 1e-6, w_layout: int | None = None, 
 def gated_mlp(x, w1, w3, w_layout: int | None = None, out=None):
     """out = silu(x @ W1) * (x @ W3)."""
     _check_cuda(x, w1, w3)
+    _same_dtype(x, w1, w3)
     B, K = x.shape
     layout, N = _w_layout_and_n(w1, K, w_layout)
     if w3.shape != w1.shape:
@@ -104,6 +114,7 @@ def gated_mlp(x, w1, w3, w_layout: int | None = None, out=None):
 def linear(x, w, residual=None, w_layout: int | None = _lib.W_NK, out=None):
     """out = x @ W^T (NK layout, torch Linear.weight) or x @ W (KN) (+ residual)."""
     _check_cuda(x, w, residual)
+    _same_dtype(x, w, residual)
     B, K = x.shape
     layout, N = _w_layout_and_n(w, K, w_layout)
     dt = dtype_code(x.dtype)
@@ -119,6 +130,7 @@ def linear(x, w, residual=None, w_layout: int | None = _lib.W_NK, out=None):
 def gqa_decode_paged(q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, max_kv_len: int | None = None, out=None):
     """Paged GQA decode: q[B,Hq,D], caches [P,page,Hkv,D], int32 page table."""
     _check_cuda(q, k_cache, v_cache, kv_indptr, kv_indices, kv_len)
+    _same_dtype(q, k_cache, v_cache)
     B, Hq, D = q.shape
     P, page, Hkv, D2 = k_cache.shape
     if D2 != D or v_cache.shape != k_cache.shape:
@@ -142,6 +154,7 @@ def gqa_decode_paged(q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, max_kv_
 def gqa_prefill(q, k, v, causal: bool = True, out=None):
     """Prefill attention q[B,S,Hq,D], k/v[B,S,Hkv,D]."""
     _check_cuda(q, k, v)
+    _same_dtype(q, k, v)
     B, S, Hq, D = q.shape
     Hkv = k.shape[2]
     dt = dtype_code(q.dtype)

@@ -98,6 +98,15 @@ class PersistentKernel:
         assert meta_tensors["paged_kv_indptr_buffer"].shape == (max_num_batched_requests + 1,)
         assert meta_tensors["paged_kv_indices_buffer"].shape == (max_num_pages,)
         assert meta_tensors["paged_kv_last_page_len_buffer"].shape == (max_num_batched_requests,)
+        # element types of the meta tensors (persistent_kernel.py:268-279 of the reference)
+        want = {"step": torch.int32, "tokens": torch.int64, "input_tokens": torch.int64,
+                "output_tokens": torch.int64, "num_new_tokens": torch.int32, "prompt_lengths": torch.int32,
+                "qo_indptr_buffer": torch.int32, "paged_kv_indptr_buffer": torch.int32,
+                "paged_kv_indices_buffer": torch.int32, "paged_kv_last_page_len_buffer": torch.int32}
+        for key, dt in want.items():
+            t = meta_tensors.get(key)
+            if t is not None and t.dtype != dt:
+                raise YirageHipError(f"meta tensor {key} must be {dt}, got {t.dtype}")
         self._tensors: dict[str, DTensor] = {}
         self._layers: list[dict] = []
         self._owned: list[torch.Tensor] = []
@@ -207,8 +216,11 @@ class PersistentKernel:
         self._add("argmax_reduce", input=None, output=output)
 
     def prepare_batch_layer(self):
-        """Append the on-device batch/page manager (prepare_next_batch of
-        persistent_kernel.cuh:169-322) as the last task of the graph."""
+        """The on-device batch/page manager (prepare_next_batch of
+        persistent_kernel.cuh:169-322).  It must be the last layer recorded:
+        every attention task reads the batch metadata once at launch start,
+        and prepare_batch rewrites it for the next launch (compile() refuses
+        any other placement)."""
         self._add("prepare_batch")
 
     # ------------------------------------------------------------ fusion + JSON
@@ -236,6 +248,10 @@ class PersistentKernel:
 
     def _fuse(self):
         L = self._layers
+        for i, l in enumerate(L):
+            if l["kind"] == "prepare_batch" and i != len(L) - 1:
+                raise YirageHipError("hip backend: prepare_batch_layer must be the last layer of the graph "
+                                     "(attention reads the batch metadata at launch start)")
         consumers = {}
         for i, l in enumerate(L):
             for k in ("input", "norm", "residual"):
