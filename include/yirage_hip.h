@@ -119,6 +119,21 @@ int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_ca
                             int page_size, int max_kv_len, int dtype, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* yr_hip_gqa_decode_paged without a workspace argument and without any
+ * allocation: its tickets and split records live in a fixed device array of
+ * yr_hip_gqa_decode_noalloc_max_bytes() bytes per GPU (held until the
+ * process ends).  Shapes needing more scratch are rejected with
+ * YR_E_WORKSPACE.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (different streams, threads) race; serialize them.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Results are bit-identical to yr_hip_gqa_decode_paged. */
+size_t yr_hip_gqa_decode_noalloc_max_bytes(void);
+int yr_hip_gqa_decode_paged_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* kv_indptr, const int32_t* kv_indices,
+                                    const int32_t* kv_len, void* out, int batch, int hq, int hkv, int d,
+                                    int page_size, int max_kv_len, int dtype, void* stream);
+
 /* Causal (or full) GQA prefill attention, q[batch][seq][hq][d],
  * k/v[batch][seq][hkv][d], out like q; fp32 softmax statistics, MFMA
  * contractions.  Replaces the prefill path of the MPK attention task

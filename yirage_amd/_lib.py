@@ -62,6 +62,8 @@ SIGNATURES = {
     "yr_hip_linear": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "yr_hip_gqa_decode_workspace": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "yr_hip_gqa_decode_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "yr_hip_gqa_decode_noalloc_max_bytes": (_SZ, []),
+    "yr_hip_gqa_decode_paged_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "yr_hip_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "yr_hip_argmax": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "yr_hip_run_fused": (_I, [_I, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),

@@ -14,6 +14,8 @@
 // Prefill (MFMA-bound): flash attention, one workgroup per (64 query rows,
 //   q head, batch); K tiles and transposed V tiles are staged in LDS, S = Q K^T
 //   and O += P V both on MFMA 16x16x32, fp32 running max/sum per row.
+#include <mutex>
+
 #include "yr_common.h"
 
 namespace yr {
@@ -717,11 +719,14 @@ size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv
   return kTicketBytes + (size_t)batch * hkv * sp * G * (d + 2) * sizeof(float);
 }
 
-int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
-                            const int32_t* kv_indices, const int32_t* kv_len, void* out, int batch, int hq,
-                            int hkv, int d, int page_size, int max_kv_len, int dtype, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  const char* nm = "yr_hip_gqa_decode_paged";
+}  // extern "C"
+
+// The decode launch shared by the workspace and the no-allocation entry
+// points: checks the shape, plans the splits and launches.
+static int gqa_decode_launch(const char* nm, const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len, void* out,
+                             int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype,
+                             void* workspace, size_t workspace_bytes, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !kv_indptr || !kv_indices || !kv_len || !out)
     return fail(YR_E_INVALID, "%s: null pointer", nm);
   if (batch <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: hq must be a multiple of hkv", nm);
@@ -757,7 +762,6 @@ int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_ca
   a.partial = need ? (float*)((char*)workspace + kTicketBytes) : nullptr;
   a.scale_log2 = kLog2e / sqrtf((float)d);
   dim3 grid(a.splits, hkv, batch);
-  hipStream_t st = (hipStream_t)stream;
 #define YR_DEC(G_)                                                                                        \
   if (G == G_) {                                                                                          \
     if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL((gqa_decode_kernel<DT_F16, G_>), grid, dim3(DEC_THREADS), 0, st, a); \
@@ -767,6 +771,84 @@ int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_ca
 #undef YR_DEC
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
+}
+
+// ---------------------------------------------------------------- no-allocation decode
+// Device-resident scratch of yr_hip_gqa_decode_paged_noalloc: arrival
+// tickets in [0, kTicketBytes), split records after them.  One copy per GPU,
+// held until the process ends; every call on a GPU shares it, so calls that
+// overlap on one GPU race.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address): it
+// uses the address hipGetSymbolAddress returns for the current device.
+// Its size covers every shape the decode accepts: the plan gives each of the
+// B * Hkv (sequence, kv head) pairs ceil(DEC_TARGET_WG / pairs) splits or
+// one (then no records), so records exist for fewer than 2 * DEC_TARGET_WG
+// splits of at most 16 rows of D + 2 floats (D = 128).
+constexpr size_t kNoAllocScratchBytes = kTicketBytes + (size_t)2 * DEC_TARGET_WG * 16 * (128 + 2) * sizeof(float);
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+__global__ void fill_u32_kernel(uint32_t* p, int n, uint32_t v) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
+}
+
+// Device address of this device's scratch (looked up once per device, with
+// that device current).
+static int noalloc_scratch(const char* nm, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return check_hip(e, nm);
+  if (dev < 0 || dev >= kMaxDevices) return fail(YR_E_INVALID, "%s: device %d out of range", nm, dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(YR_E_HIP, "%s: hipGetSymbolAddress(scratch) failed (%d)", nm, (int)e);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return YR_OK;
+}
+
+extern "C" {
+
+size_t yr_hip_gqa_decode_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_cache, const int32_t* kv_indptr,
+                            const int32_t* kv_indices, const int32_t* kv_len, void* out, int batch, int hq,
+                            int hkv, int d, int page_size, int max_kv_len, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  return gqa_decode_launch("yr_hip_gqa_decode_paged", q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch,
+                           hq, hkv, d, page_size, max_kv_len, dtype, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int yr_hip_gqa_decode_paged_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len,
+                                    void* out, int batch, int hq, int hkv, int d, int page_size, int max_kv_len,
+                                    int dtype, void* stream) {
+  const char* nm = "yr_hip_gqa_decode_paged_noalloc";
+  if (batch <= 0 || hkv <= 0 || hq % hkv || page_size <= 0 || max_kv_len <= 0)
+    return fail(YR_E_INVALID, "%s: bad shape", nm);
+  const size_t need = yr_hip_gqa_decode_workspace(batch, hq, hkv, d, max_kv_len, page_size);
+  if (need > kNoAllocScratchBytes)
+    return fail(YR_E_WORKSPACE, "%s: needs %zu bytes of scratch, above the fixed %zu", nm, need,
+                kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = noalloc_scratch(nm, &ws);
+  if (rc != YR_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (need) {
+    // the tickets this call uses start at zero whatever an earlier call left
+    // (a fill kernel, not a memset node, so the call can be graph-captured)
+    const int nt = batch * hkv;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((nt + 255) / 256), dim3(256), 0, st, (uint32_t*)ws, nt, 0u);
+    YR_CHECK_LAUNCH(nm);
+  }
+  return gqa_decode_launch(nm, q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch, hq, hkv, d,
+                           page_size, max_kv_len, dtype, need ? ws : nullptr, need ? kNoAllocScratchBytes : 0, st);
 }
 
 int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, int batch, int seq, int hq,
