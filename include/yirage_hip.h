@@ -146,27 +146,93 @@ int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, i
  * argmax_reduce (tasks/ampere/argmax.cuh:71-155). */
 int yr_hip_argmax(const void* x, int64_t* out, int rows, int n, int n_valid, int dtype, void* stream);
 
+/* ------------------------------------------------------- kernel-graph operators */
+/* The operators of the reference's kernel graph (python/yirage/kernel.py:
+ * 248-321; shape rules src/kernel/{matmul,element_unary,element_binary,
+ * reduction,rms_norm}.cc) for the parts of a graph that no fused pattern
+ * covers.  16-bit storage (f16 / bf16), fp32 math, one rounding per op, dense
+ * row-major tensors unless a stride list says otherwise. */
+
+/* Kernel-graph attention O[g] = softmax(scale * Q[g] K[g]) V[g] with
+ * Q [G][M][d], K [G][d][L] (the graph's matmul operand: rows are head dims),
+ * V [G][L][d] and O [G][M][d], each given by three element strides in
+ * strides12 = {q0,q1,q2, k0,k1,k2, v0,v1,v2, o0,o1,o2}; d <= 128, d % 8 == 0.
+ * The pattern matmul(div(exp(matmul(Q,K)), reduction(exp(.),2)), V) of
+ * benchmark/group_query_attention.py:37-46 and
+ * demo/reference_mugraphs/group_query_attention.py:10-34 (the reference's
+ * graph has no scale: scale = 1). */
+size_t yr_hip_graph_attention_workspace(int G, int M, int L, int d, const int64_t* strides12);
+int yr_hip_graph_attention(const void* q, const void* k, const void* v, void* out, int G, int M, int L, int d,
+                           const int64_t* strides12, float scale, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
+/* dst[i][r][c] = c < cols ? src[i s0 + r s1 + c s2] : 0 for c < dst_cols, at
+ * dst + i d0 + r d1 + c d2; strides6 = {s0,s1,s2,d0,d1,d2}.  Makes strided
+ * (e.g. column-major, kernel.py:196-210) graph inputs dense. */
+int yr_hip_graph_pack(const void* src, void* dst, int g, int rows, int cols, int dst_cols, const int64_t* strides6,
+                      int dtype, void* stream);
+/* y = f(x) elementwise; kind 0 exp, 1 silu, 2 gelu (erf form), 3 relu,
+ * 4 clamp(lo, hi), 5 sqrt, 6 square
+ * (include/yirage/transpiler/runtime/kernel/element_unary.h:22-40). */
+int yr_hip_graph_unary(const void* x, void* y, int64_t n, int kind, float lo, float hi, int dtype, void* stream);
+/* out = a (op) b with size-1 broadcasting over ndim <= 6 dims (output dims
+ * = elementwise max); kind 0 add, 1 mul, 2 div, 3 pow
+ * (src/kernel/element_binary.cc:74-95). */
+int yr_hip_graph_binary(const void* a, const void* b, void* out, int ndim, const int64_t* dims_a,
+                        const int64_t* dims_b, int kind, int dtype, void* stream);
+/* y[o][i] = sum_r x[o][r][i]: reduction(x, dim) to size 1
+ * (src/kernel/reduction.cc:61-77, python reduction(A, dim) = size 1). */
+int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype, void* stream);
+/* y[row] = x[row] * rsqrt(mean(x[row]^2) + eps) over the n trailing
+ * elements (rms_norm(X, normalized_shape), src/kernel/rms_norm.cc:71-114). */
+int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream);
+/* c[b] = a[b] (m x k) @ b[b] (k x n), all row-major; n, k multiples of 8;
+ * MFMA, fp32 accumulate (src/kernel/matmul.cc:44-96). */
+int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m, int n, int k, int dtype,
+                        void* stream);
+
 /* ------------------------------------------------------- generic launcher */
-/* One fused operator by kind, with the shape of the reference's
+/* One operator by kind, with the shape of the reference's
  * execute_mugraph(inputs, outputs, buffer, stream, profiler) launcher
  * (python/yirage/kernel.py:22-72,411-421): inputs and outputs are arrays of
- * device pointers, `params` holds the integer shape/attribute list of the op.
- * op_kind / param layouts:
+ * device pointers, `params` holds the integer shape/attribute list of the op
+ * (floats travel as their IEEE-754 bits).  op_kind / layouts:
  *   YR_OP_RMSNORM_LINEAR: in {x, gamma|NULL, w}, out {o};
- *        params {batch, k, n, dtype, w_layout, eps_as_float_bits}
+ *        params {batch, k, n, dtype, w_layout, eps_bits}
  *   YR_OP_GATED_MLP:      in {x, w1, w3}, out {o};
  *        params {batch, k, n, dtype, w_layout}
  *   YR_OP_GQA_PREFILL:    in {q, k, v}, out {o};
  *        params {batch, seq, hq, hkv, d, causal, dtype}
  *   YR_OP_LINEAR:         in {x, w, residual|NULL}, out {o};
- *        params {batch, k, n, dtype, w_layout} */
+ *        params {batch, k, n, dtype, w_layout}
+ *   YR_OP_GQA_DECODE:     in {q, k_cache, v_cache, kv_indptr, kv_indices, kv_len}, out {o};
+ *        params {batch, hq, hkv, d, page_size, max_kv_len, dtype}
+ *   YR_OP_ATTENTION:      in {q, k, v}, out {o};
+ *        params {G, M, L, d, dtype, scale_bits, strides12...}   (18 params)
+ *   YR_OP_MATMUL:         in {a, b}, out {c}; params {batch, m, n, k, dtype}
+ *   YR_OP_UNARY:          in {x}, out {y}; params {n, kind, dtype, lo_bits, hi_bits}
+ *   YR_OP_BINARY:         in {a, b}, out {c}; params {ndim, kind, dtype, dims_a[ndim], dims_b[ndim]}
+ *   YR_OP_REDUCTION:      in {x}, out {y}; params {outer, red, inner, dtype}
+ *   YR_OP_RMSNORM:        in {x}, out {y}; params {rows, n, dtype, eps_bits}
+ *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...} */
 #define YR_OP_RMSNORM_LINEAR 1
 #define YR_OP_GATED_MLP 2
 #define YR_OP_GQA_PREFILL 3
 #define YR_OP_LINEAR 4
+#define YR_OP_GQA_DECODE 5
+#define YR_OP_ATTENTION 6
+#define YR_OP_MATMUL 7
+#define YR_OP_UNARY 8
+#define YR_OP_BINARY 9
+#define YR_OP_REDUCTION 10
+#define YR_OP_RMSNORM 11
+#define YR_OP_PACK 12
 int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);
+/* Workspace bytes yr_hip_run_fused needs for an op (0 if none); the
+ * workspace layout is shared by every kind (tickets first), so one
+ * zero-filled buffer of the maximum over a graph's steps serves them all. */
+size_t yr_hip_fused_workspace(int op_kind, int n_params, const int64_t* params);
 
 /* ------------------------------------------------------- persistent kernel */
 /* Task graph of the persistent megakernel, built on the host (no GPU needed).

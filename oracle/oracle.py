@@ -144,7 +144,7 @@ def linear(x: np.ndarray, W: np.ndarray, wdt, layout: int, residual: np.ndarray 
 
 def rmsnorm_linear(x, gamma, W, wdt, layout=W_KN, eps=1e-6):
     x = _c(x, np.float32)
-    g = _c(gamma, np.float32)
+    g = None if gamma is None else _c(gamma, np.float32)
     W = _c(W, np.uint16)
     B, K = x.shape
     N = W.shape[1] if layout == W_KN else W.shape[0]

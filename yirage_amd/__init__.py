@@ -2,6 +2,7 @@
 
 Mirrors the reference's public API for the hot path:
   new_kernel_graph() / KNGraph ops / graph.superoptimize(backend='hip') / graph(inputs=...)
+  new_threadblock_graph() / TBGraph (bodies of `customized` ops)
   PersistentKernel(...).*_layer(...) / compile() / __call__()
   get_available_backends() & co.
 Compute runs only through libyirage_hip.so (hand-written gfx950 kernels).
@@ -14,5 +15,29 @@ from .backend_api import (
     get_registered_backends,
     is_backend_available,
 )
+from .dtypes import (
+    bfloat16,
+    convert_dtype_to_torch_type,
+    dtype,
+    float16,
+    float32,
+    float64,
+    int8,
+    int32,
+    int64,
+    uint8,
+)
+from .graph_dataset import graph_dataset
+from .kernel import DTensor, KNGraph, check_stride, new_kernel_graph
+from .threadblock import STensor, TBGraph, new_threadblock_graph
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"
+
+
+def __getattr__(name):
+    # the persistent kernel pulls in more of torch; load it on first use
+    if name in ("PersistentKernel", "get_configurations_from_gpu"):
+        from . import persistent_kernel
+
+        return getattr(persistent_kernel, name)
+    raise AttributeError(name)

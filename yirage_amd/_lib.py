@@ -15,7 +15,8 @@ LIB_PATH = os.environ.get("YIRAGE_HIP_LIB") or os.path.join(_HERE, "libyirage_hi
 YR_OK = 0
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64 = 940, 941, 950, 955, 965
 W_NK, W_KN = 0, 1
-OP_RMSNORM_LINEAR, OP_GATED_MLP, OP_GQA_PREFILL, OP_LINEAR = 1, 2, 3, 4
+(OP_RMSNORM_LINEAR, OP_GATED_MLP, OP_GQA_PREFILL, OP_LINEAR, OP_GQA_DECODE, OP_ATTENTION, OP_MATMUL, OP_UNARY,
+ OP_BINARY, OP_REDUCTION, OP_RMSNORM, OP_PACK) = range(1, 13)
 
 
 class YirageHipError(RuntimeError):
@@ -67,6 +68,15 @@ SIGNATURES = {
     "yr_hip_gqa_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "yr_hip_argmax": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "yr_hip_run_fused": (_I, [_I, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "yr_hip_fused_workspace": (_SZ, [_I, _I, _P]),
+    "yr_hip_graph_attention_workspace": (_SZ, [_I, _I, _I, _I, _P]),
+    "yr_hip_graph_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _F, _I, _P, _SZ, _P]),
+    "yr_hip_graph_pack": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "yr_hip_graph_unary": (_I, [_P, _P, ctypes.c_int64, _I, _F, _F, _I, _P]),
+    "yr_hip_graph_binary": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _P]),
+    "yr_hip_graph_reduction": (_I, [_P, _P, ctypes.c_int64, _I, ctypes.c_int64, _I, _P]),
+    "yr_hip_graph_rmsnorm": (_I, [_P, _P, _I, _I, _F, _I, _P]),
+    "yr_hip_graph_matmul": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "yr_pk_graph_build": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "yr_pk_graph_free": (None, [_P]),
     "yr_pk_graph_info": (_I, [_P, ctypes.POINTER(ctypes.c_int64), _I]),

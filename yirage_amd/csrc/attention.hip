@@ -17,6 +17,7 @@
 #include <mutex>
 
 #include "yr_common.h"
+#include "attn_launch.h"
 
 namespace yr {
 
@@ -334,11 +335,13 @@ constexpr int PF_NB = PF_KT / 16;        // 16-token MFMA blocks per tile
 constexpr float kLazy = 8.f;             // running-max slack (log2 units)
 
 struct PrefillArgs {
-  const uint16_t* q;  // [B][S][Hq][D]
-  const uint16_t* k;  // [B][S][Hkv][D]
+  const uint16_t* q;  // [B] x [Sq] rows x [Hq][D]: row r of batch b at b q_bs + r q_ld
+  const uint16_t* k;  // [B] x [Sk] rows x [Hkv][D]: b kv_bs + r kv_ld
   const uint16_t* v;
-  uint16_t* o;
-  int B, S, Hq, Hkv, causal, nblk;
+  uint16_t* o;        // like q: b o_bs + r o_ld
+  long long q_bs, kv_bs, o_bs;  // batch strides (elements)
+  int q_ld, kv_ld, o_ld;        // row strides (elements)
+  int B, Sq, Sk, Hq, Hkv, causal, nblk;  // causal needs Sq == Sk
   int paired;  // blocks (i, nblk - 1 - i) per workgroup (causal)
   int npair, ngrp, nwg;  // workgroups per (batch, head group); head groups; total
   float scale_log2;
@@ -413,9 +416,9 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
   const int h0 = (hg * HG + wv / 4) * HPW;                     // this wave's first head
   const int hk = hg * HG * HPW / G;  // the workgroup's heads share one kv head (G % (HG HPW) == 0)
   const int col = lane % 16, grp = lane / 16;
-  const size_t qstride = (size_t)a.Hq * D, kstride = (size_t)a.Hkv * D;
-  const uint16_t* kbase = a.k + (size_t)b * a.S * kstride + (size_t)hk * D;
-  const uint16_t* vbase = a.v + (size_t)b * a.S * kstride + (size_t)hk * D;
+  const size_t kstride = (size_t)a.kv_ld;
+  const uint16_t* kbase = a.k + (size_t)b * a.kv_bs + (size_t)hk * D;
+  const uint16_t* vbase = a.v + (size_t)b * a.kv_bs + (size_t)hk * D;
   // staging: wave w fills rows RPW w .. RPW w + RPW - 1, four rows per load;
   // lane l writes physical chunk l % 16 of row 4 u + l / 16, i.e. source
   // chunk (l % 16) ^ pk_swz(row) (K) or ^ pf_swz(row) (V)
@@ -452,7 +455,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
     // Q^T as the B operand: column = query row, k = d 32 s + 8 grp .. +7
 #pragma unroll
     for (int hh = 0; hh < HPW; hh++) {
-      const uint16_t* qrow = a.q + ((size_t)b * a.S + min(qr, a.S - 1)) * qstride + (size_t)(h0 + hh) * D;
+      const uint16_t* qrow = a.q + (size_t)b * a.q_bs + (size_t)min(qr, a.Sq - 1) * a.q_ld + (size_t)(h0 + hh) * D;
 #pragma unroll
       for (int s = 0; s < 4; s++) sq[wv][hh][s][lane] = ldg16(qrow + 32 * s + 8 * grp);
     }
@@ -468,26 +471,26 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
       l_i[hh] = 0.f;
     }
 
-    const int kv_end = a.causal ? min(a.S, (blk + 1) * PF_QROWS) : a.S;
+    const int kv_end = a.causal ? min(a.Sk, (blk + 1) * PF_QROWS) : a.Sk;
     const int ntile = (kv_end + PF_KT - 1) / PF_KT;
     // tiles that need no mask: below every query row of the block and
     // entirely inside the sequence
-    const int nfull = a.causal ? min(ntile, blk * PF_QROWS / PF_KT) : a.S / PF_KT;
+    const int nfull = a.causal ? min(ntile, blk * PF_QROWS / PF_KT) : a.Sk / PF_KT;
     // causal: the last tile holding a key at or below this wave's rows
     const int tw_end = a.causal ? min(ntile, (q0 + 15) / PF_KT + 1) : ntile;
     // IS_K: the K tile's chunk permutation (pk_swz), else V's (pf_swz)
     auto fetch = [&](int t, const uint16_t* base, uint16_t* dst, auto is_k_c) __attribute__((always_inline)) {
       constexpr bool IS_K = decltype(is_k_c)::value;
       const char* tb = reinterpret_cast<const char*>(base + (size_t)t * PF_KT * kstride);  // uniform
-      const bool whole = (t + 1) * PF_KT <= a.S;
+      const bool whole = (t + 1) * PF_KT <= a.Sk;
 #pragma unroll
       for (int u = 0; u < RPW / 4; u++) {
         const int row = st_row0 + 4 * u;
         uint32_t off;
         if constexpr (IS_K) off = foffk[u];
         else off = 2u * (uint32_t)(row * (int)kstride + 8 * ((lane % 16) ^ pf_swz(row)));
-        if (!whole) {  // last tile: rows past S re-read token S - 1 (masked)
-          const int r = min(t * PF_KT + row, a.S - 1) - t * PF_KT;
+        if (!whole) {  // last tile: rows past Sk re-read token Sk - 1 (masked)
+          const int r = min(t * PF_KT + row, a.Sk - 1) - t * PF_KT;
           off = 2u * (uint32_t)(r * (int)kstride + 8 * ((lane % 16) ^ (IS_K ? pk_swz(row) : pf_swz(row))));
         }
         lds_load16(reinterpret_cast<const uint16_t*>(tb + off), dst + (RPW * wv + 4 * u) * D);
@@ -530,7 +533,7 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const int tok = t0 + 16 * n + 4 * grp + i;
-              if (tok >= a.S || (a.causal && tok > qr)) sc[hh][n][i] = -INFINITY;
+              if (tok >= a.Sk || (a.causal && tok > qr)) sc[hh][n][i] = -INFINITY;
             }
         }
         float mx = -INFINITY;
@@ -648,11 +651,11 @@ __global__ __launch_bounds__(256 * HG) void gqa_prefill_kernel(PrefillArgs a) {
       l_i[hh] += __shfl_xor(l_i[hh], 16, kWave);
       l_i[hh] += __shfl_xor(l_i[hh], 32, kWave);
     }
-    if (qr < a.S) {
+    if (qr < a.Sq) {
 #pragma unroll
       for (int hh = 0; hh < HPW; hh++) {
         const float inv = l_i[hh] > 0.f ? 1.f / l_i[hh] : 0.f;
-        uint16_t* orow = a.o + ((size_t)b * a.S + qr) * qstride + (size_t)(h0 + hh) * D;
+        uint16_t* orow = a.o + (size_t)b * a.o_bs + (size_t)qr * a.o_ld + (size_t)(h0 + hh) * D;
 #pragma unroll
         for (int dt = 0; dt < D / 16; dt++) {
           const f32x4 v = acc[hh][dt];
@@ -723,10 +726,10 @@ size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv
 
 // The decode launch shared by the workspace and the no-allocation entry
 // points: checks the shape, plans the splits and launches.
-static int gqa_decode_launch(const char* nm, const void* q, const void* k_cache, const void* v_cache,
+int yr::gqa_decode_launch(const char* nm, const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len, void* out,
                              int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype,
-                             void* workspace, size_t workspace_bytes, hipStream_t st) {
+                             void* workspace, size_t workspace_bytes, hipStream_t st, float scale) {
   if (!q || !k_cache || !v_cache || !kv_indptr || !kv_indices || !kv_len || !out)
     return fail(YR_E_INVALID, "%s: null pointer", nm);
   if (batch <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: hq must be a multiple of hkv", nm);
@@ -760,7 +763,8 @@ static int gqa_decode_launch(const char* nm, const void* q, const void* k_cache,
                 DEC_MAXPG);
   a.tickets = (uint32_t*)workspace;
   a.partial = need ? (float*)((char*)workspace + kTicketBytes) : nullptr;
-  a.scale_log2 = kLog2e / sqrtf((float)d);
+  if (!(scale > 0.f)) return fail(YR_E_INVALID, "%s: scale must be positive", nm);
+  a.scale_log2 = kLog2e * scale;
   dim3 grid(a.splits, hkv, batch);
 #define YR_DEC(G_)                                                                                        \
   if (G == G_) {                                                                                          \
@@ -769,6 +773,67 @@ static int gqa_decode_launch(const char* nm, const void* q, const void* k_cache,
   }
   YR_DEC(1) YR_DEC(2) YR_DEC(4) YR_DEC(8) YR_DEC(16)
 #undef YR_DEC
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+// The prefill launch behind yr_hip_gqa_prefill and the kernel-graph
+// attention: q rows Sq, kv rows Sk (causal needs Sq == Sk), explicit batch /
+// row strides in elements, softmax scale `scale` (scores are multiplied by
+// it before the exponential).
+int yr::prefill_launch(const char* nm, const void* q, const void* k, const void* v, void* out, int batch, int sq, int sk,
+                   int hq, int hkv, int d, int causal, int dtype, long long q_bs, int q_ld, long long kv_bs, int kv_ld,
+                   long long o_bs, int o_ld, float scale, hipStream_t st) {
+  if (!q || !k || !v || !out) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (batch <= 0 || sq <= 0 || sk <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: bad shape", nm);
+  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  if (causal && sq != sk) return fail(YR_E_INVALID, "%s: causal attention needs as many query as kv rows", nm);
+  if (q_ld % 8 || kv_ld % 8 || o_ld % 8 || q_bs % 8 || kv_bs % 8 || o_bs % 8 || q_ld < hq * d || kv_ld < hkv * d ||
+      o_ld < hq * d)
+    return fail(YR_E_INVALID, "%s: strides must be multiples of 8 elements and cover a row", nm);
+  if ((long long)kv_ld * 64 * 2 >= (1ll << 31)) return fail(YR_E_INVALID, "%s: kv row stride too large", nm);
+  if (!(scale > 0.f)) return fail(YR_E_INVALID, "%s: scale must be positive", nm);
+  PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.o = (uint16_t*)out;
+  a.q_bs = q_bs;
+  a.kv_bs = kv_bs;
+  a.o_bs = o_bs;
+  a.q_ld = q_ld;
+  a.kv_ld = kv_ld;
+  a.o_ld = o_ld;
+  a.B = batch;
+  a.Sq = sq;
+  a.Sk = sk;
+  a.Hq = hq;
+  a.Hkv = hkv;
+  a.causal = causal ? 1 : 0;
+  a.nblk = (sq + PF_QROWS - 1) / PF_QROWS;
+  a.scale_log2 = kLog2e * scale;
+  // heads per workgroup: 2 when the group size allows (two groups of 4 row
+  // waves sharing each K / V tile), one head per wave
+  const int G = hq / hkv;
+#ifndef YR_PF_CFG
+#define YR_PF_CFG 2
+#endif
+  const int hpw = (YR_PF_CFG == 0 || YR_PF_CFG == 3) && G % 2 == 0 ? 2 : 1;
+  const int hgw = (YR_PF_CFG >= 2) && (G / hpw) % 2 == 0 ? 2 : 1;
+  a.paired = a.causal;
+  a.npair = a.paired ? (a.nblk + 1) / 2 : a.nblk;
+  a.ngrp = hq / (hpw * hgw);
+  a.nwg = a.npair * a.ngrp * batch;
+  dim3 grid(a.nwg);
+  const bool bf = dtype == YR_DTYPE_BF16;
+#define YR_PF(H, W)                                                                                        \
+  if (hpw == H && hgw == W) {                                                                              \
+    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, H, W>), grid, dim3(256 * W), 0, st, a);         \
+    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, H, W>), grid, dim3(256 * W), 0, st, a);             \
+  }
+  YR_PF(1, 1) YR_PF(1, 2) YR_PF(2, 1) YR_PF(2, 2)
+#undef YR_PF
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
 }
@@ -822,7 +887,8 @@ int yr_hip_gqa_decode_paged(const void* q, const void* k_cache, const void* v_ca
                             int hkv, int d, int page_size, int max_kv_len, int dtype, void* workspace,
                             size_t workspace_bytes, void* stream) {
   return gqa_decode_launch("yr_hip_gqa_decode_paged", q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch,
-                           hq, hkv, d, page_size, max_kv_len, dtype, workspace, workspace_bytes, (hipStream_t)stream);
+                           hq, hkv, d, page_size, max_kv_len, dtype, workspace, workspace_bytes, (hipStream_t)stream,
+                           1.f / sqrtf((float)d));
 }
 
 int yr_hip_gqa_decode_paged_noalloc(const void* q, const void* k_cache, const void* v_cache,
@@ -848,52 +914,17 @@ int yr_hip_gqa_decode_paged_noalloc(const void* q, const void* k_cache, const vo
     YR_CHECK_LAUNCH(nm);
   }
   return gqa_decode_launch(nm, q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch, hq, hkv, d,
-                           page_size, max_kv_len, dtype, need ? ws : nullptr, need ? kNoAllocScratchBytes : 0, st);
+                           page_size, max_kv_len, dtype, need ? ws : nullptr, need ? kNoAllocScratchBytes : 0, st,
+                           1.f / sqrtf((float)d));
 }
 
 int yr_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out, int batch, int seq, int hq,
                        int hkv, int d, int causal, int dtype, void* stream) {
-  const char* nm = "yr_hip_gqa_prefill";
-  if (!q || !k || !v || !out) return fail(YR_E_INVALID, "%s: null pointer", nm);
-  if (batch <= 0 || seq <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: bad shape", nm);
-  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
-  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
-  PrefillArgs a;
-  a.q = (const uint16_t*)q;
-  a.k = (const uint16_t*)k;
-  a.v = (const uint16_t*)v;
-  a.o = (uint16_t*)out;
-  a.B = batch;
-  a.S = seq;
-  a.Hq = hq;
-  a.Hkv = hkv;
-  a.causal = causal ? 1 : 0;
-  a.nblk = (seq + PF_QROWS - 1) / PF_QROWS;
-  a.scale_log2 = kLog2e / sqrtf((float)d);
-  // heads per workgroup: 2 when the group size allows (two groups of 4 row
-  // waves sharing each K / V tile), one head per wave
-  const int G = hq / hkv;
-#ifndef YR_PF_CFG
-#define YR_PF_CFG 2
-#endif
-  const int hpw = (YR_PF_CFG == 0 || YR_PF_CFG == 3) && G % 2 == 0 ? 2 : 1;
-  const int hgw = (YR_PF_CFG >= 2) && (G / hpw) % 2 == 0 ? 2 : 1;
-  a.paired = a.causal;
-  a.npair = a.paired ? (a.nblk + 1) / 2 : a.nblk;
-  a.ngrp = hq / (hpw * hgw);
-  a.nwg = a.npair * a.ngrp * batch;
-  dim3 grid(a.nwg);
-  hipStream_t st = (hipStream_t)stream;
-  const bool bf = dtype == YR_DTYPE_BF16;
-#define YR_PF(H, W)                                                                                        \
-  if (hpw == H && hgw == W) {                                                                              \
-    if (bf) hipLaunchKernelGGL((gqa_prefill_kernel<DT_BF16, H, W>), grid, dim3(256 * W), 0, st, a);         \
-    else hipLaunchKernelGGL((gqa_prefill_kernel<DT_F16, H, W>), grid, dim3(256 * W), 0, st, a);             \
-  }
-  YR_PF(1, 1) YR_PF(1, 2) YR_PF(2, 1) YR_PF(2, 2)
-#undef YR_PF
-  YR_CHECK_LAUNCH(nm);
-  return YR_OK;
+  if (seq <= 0 || hkv <= 0) return fail(YR_E_INVALID, "yr_hip_gqa_prefill: bad shape");
+  const long long qld = (long long)hq * d, kld = (long long)hkv * d;
+  return prefill_launch("yr_hip_gqa_prefill", q, k, v, out, batch, seq, seq, hq, hkv, d, causal, dtype, seq * qld,
+                        (int)qld, seq * kld, (int)kld, seq * qld, (int)qld, 1.f / sqrtf((float)d),
+                        (hipStream_t)stream);
 }
 
 int yr_hip_argmax(const void* x, int64_t* out, int rows, int n, int n_valid, int dtype, void* stream) {

@@ -1,39 +1,118 @@
 // Generic fused-operator launcher with the argument shape of the reference's
 // execute_mugraph(inputs, outputs, buffer, stream, profiler)
-// (python/yirage/kernel.py:22-72,411-421).
+// (python/yirage/kernel.py:22-72,411-421): the kernel-graph front end turns
+// a graph into a list of (op kind, inputs, outputs, integer params) steps and
+// runs each one through yr_hip_run_fused on a shared workspace.
 #include <string.h>
 
 #include "yr_common.h"
 
 using namespace yr;
 
-extern "C" int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, void* const* out,
-                                int n_params, const int64_t* p, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+namespace {
+
+float f32_of(int64_t bits) {
+  float f;
+  const int32_t b = (int32_t)bits;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+struct Arity {
+  int n_in, n_out, n_params;  // n_params < 0: at least -n_params
+};
+
+bool arity_of(int kind, Arity* a) {
+  switch (kind) {
+    case YR_OP_RMSNORM_LINEAR: *a = {3, 1, 6}; return true;
+    case YR_OP_GATED_MLP: *a = {3, 1, 5}; return true;
+    case YR_OP_GQA_PREFILL: *a = {3, 1, 7}; return true;
+    case YR_OP_LINEAR: *a = {3, 1, 5}; return true;
+    case YR_OP_GQA_DECODE: *a = {6, 1, 7}; return true;
+    case YR_OP_ATTENTION: *a = {3, 1, 18}; return true;
+    case YR_OP_MATMUL: *a = {2, 1, 5}; return true;
+    case YR_OP_UNARY: *a = {1, 1, 5}; return true;
+    case YR_OP_BINARY: *a = {2, 1, -3}; return true;
+    case YR_OP_REDUCTION: *a = {1, 1, 4}; return true;
+    case YR_OP_RMSNORM: *a = {1, 1, 4}; return true;
+    case YR_OP_PACK: *a = {1, 1, 11}; return true;
+    default: return false;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t yr_hip_fused_workspace(int op_kind, int n_params, const int64_t* p) {
+  Arity ar;
+  if (!arity_of(op_kind, &ar) || (n_params && !p)) return 0;
+  if (ar.n_params >= 0 ? n_params != ar.n_params : n_params < -ar.n_params) return 0;
+  switch (op_kind) {
+    case YR_OP_RMSNORM_LINEAR:
+      return yr_hip_rmsnorm_linear_workspace((int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4]);
+    case YR_OP_GATED_MLP:
+      return yr_hip_gated_mlp_workspace((int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4]);
+    case YR_OP_LINEAR:
+      return yr_hip_linear_workspace((int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4]);
+    case YR_OP_GQA_DECODE:
+      return yr_hip_gqa_decode_workspace((int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[5], (int)p[4]);
+    case YR_OP_ATTENTION:
+      return yr_hip_graph_attention_workspace((int)p[0], (int)p[1], (int)p[2], (int)p[3], p + 6);
+    default:
+      return 0;
+  }
+}
+
+int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, void* const* out, int n_params,
+                     const int64_t* p, void* workspace, size_t workspace_bytes, void* stream) {
   const char* nm = "yr_hip_run_fused";
   if ((n_in && !in) || (n_out && !out) || (n_params && !p)) return fail(YR_E_INVALID, "%s: null array", nm);
+  Arity ar;
+  if (!arity_of(op_kind, &ar)) return fail(YR_E_INVALID, "%s: unknown op kind %d", nm, op_kind);
+  if (n_in != ar.n_in || n_out != ar.n_out ||
+      (ar.n_params >= 0 ? n_params != ar.n_params : n_params < -ar.n_params))
+    return fail(YR_E_INVALID, "%s: op kind %d takes %d inputs, %d outputs and %s%d params (got %d, %d, %d)", nm,
+                op_kind, ar.n_in, ar.n_out, ar.n_params < 0 ? ">= " : "", ar.n_params < 0 ? -ar.n_params : ar.n_params,
+                n_in, n_out, n_params);
   switch (op_kind) {
-    case YR_OP_RMSNORM_LINEAR: {
-      if (n_in != 3 || n_out != 1 || n_params != 6) return fail(YR_E_INVALID, "%s: rmsnorm_linear arity", nm);
-      float eps;
-      int32_t bits = (int32_t)p[5];
-      memcpy(&eps, &bits, 4);
+    case YR_OP_RMSNORM_LINEAR:
       return yr_hip_rmsnorm_linear(in[0], in[1], in[2], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3],
-                                   (int)p[4], eps, workspace, workspace_bytes, stream);
-    }
+                                   (int)p[4], f32_of(p[5]), workspace, workspace_bytes, stream);
     case YR_OP_GATED_MLP:
-      if (n_in != 3 || n_out != 1 || n_params != 5) return fail(YR_E_INVALID, "%s: gated_mlp arity", nm);
       return yr_hip_gated_mlp(in[0], in[1], in[2], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4],
                               workspace, workspace_bytes, stream);
     case YR_OP_GQA_PREFILL:
-      if (n_in != 3 || n_out != 1 || n_params != 7) return fail(YR_E_INVALID, "%s: gqa_prefill arity", nm);
       return yr_hip_gqa_prefill(in[0], in[1], in[2], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3],
                                 (int)p[4], (int)p[5], (int)p[6], stream);
     case YR_OP_LINEAR:
-      if (n_in != 3 || n_out != 1 || n_params != 5) return fail(YR_E_INVALID, "%s: linear arity", nm);
       return yr_hip_linear(in[0], in[1], in[2], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4],
                            workspace, workspace_bytes, stream);
+    case YR_OP_GQA_DECODE:
+      return yr_hip_gqa_decode_paged(in[0], in[1], in[2], (const int32_t*)in[3], (const int32_t*)in[4],
+                                     (const int32_t*)in[5], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3],
+                                     (int)p[4], (int)p[5], (int)p[6], workspace, workspace_bytes, stream);
+    case YR_OP_ATTENTION:
+      return yr_hip_graph_attention(in[0], in[1], in[2], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], p + 6,
+                                    f32_of(p[5]), (int)p[4], workspace, workspace_bytes, stream);
+    case YR_OP_MATMUL:
+      return yr_hip_graph_matmul(in[0], in[1], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], (int)p[4], stream);
+    case YR_OP_UNARY:
+      return yr_hip_graph_unary(in[0], out[0], p[0], (int)p[1], f32_of(p[3]), f32_of(p[4]), (int)p[2], stream);
+    case YR_OP_BINARY: {
+      const int nd = (int)p[0];
+      if (nd < 1 || n_params != 3 + 2 * nd) return fail(YR_E_INVALID, "%s: binary takes 3 + 2 ndim params", nm);
+      return yr_hip_graph_binary(in[0], in[1], out[0], nd, p + 3, p + 3 + nd, (int)p[1], (int)p[2], stream);
+    }
+    case YR_OP_REDUCTION:
+      return yr_hip_graph_reduction(in[0], out[0], p[0], (int)p[1], p[2], (int)p[3], stream);
+    case YR_OP_RMSNORM:
+      return yr_hip_graph_rmsnorm(in[0], out[0], (int)p[0], (int)p[1], f32_of(p[3]), (int)p[2], stream);
+    case YR_OP_PACK:
+      return yr_hip_graph_pack(in[0], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], p + 5, (int)p[4], stream);
     default:
       return fail(YR_E_INVALID, "%s: unknown op kind %d", nm, op_kind);
   }
 }
+
+}  // extern "C"

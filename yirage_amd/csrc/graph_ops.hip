@@ -1,0 +1,463 @@
+// Kernel-graph operators of the hip backend: the ops a KNGraph is built from
+// (python/yirage/kernel.py:248-321; shape rules of src/kernel/matmul.cc,
+// element_unary.cc, element_binary.cc, reduction.cc, rms_norm.cc), for the
+// parts of a graph that no fused pattern covers, plus the kernel-graph form of
+// attention (Q[G][M][d] x K^T[G][d][L] -> softmax -> x V[G][L][d]).
+//
+// Elementwise math is fp32 with one rounding to the 16-bit storage type per
+// op, as the reference's transpiled element ops do
+// (include/yirage/transpiler/runtime/kernel/element_unary.h:22-40,
+// element_binary.h).  Every tensor handed to these kernels is dense
+// row-major except where a stride list says otherwise.
+#include <math.h>
+#include <string.h>
+
+#include <type_traits>
+
+#include "attn_launch.h"
+#include "yr_common.h"
+
+namespace yr {
+namespace graph {
+
+// ------------------------------------------------------------------ pack
+// dst[g][r][c] = c < C ? src[g s0 + r s1 + c s2] : 0 for c < Cd (destination
+// strides d0 d1 d2).  One workgroup moves a 64 x 64 (r, c) tile through LDS:
+// it reads along whichever of r / c is unit-stride in the source and writes
+// along whichever is unit-stride in the destination, so transposing copies
+// stay coalesced on both sides.
+struct PackArgs {
+  const uint16_t* src;
+  uint16_t* dst;
+  long long s0, s1, s2, d0, d1, d2;
+  int R, C, Cd;  // rows, source columns, destination columns (>= C: zero padded)
+  int src_c_unit, dst_c_unit;
+};
+
+__global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
+  __shared__ uint16_t tile[64][66];
+  const int g = blockIdx.z, r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int t = threadIdx.x;
+  const uint16_t* src = a.src + (size_t)g * a.s0;
+#pragma unroll 4
+  for (int i = 0; i < 16; i++) {
+    const int u = t % 64, v = t / 64 + 4 * i;  // u runs along the unit-stride dim
+    const int r = a.src_c_unit ? r0 + v : r0 + u;
+    const int c = a.src_c_unit ? c0 + u : c0 + v;
+    uint16_t x = 0;
+    if (r < a.R && c < a.C) x = src[(size_t)r * a.s1 + (size_t)c * a.s2];
+    tile[r - r0][c - c0] = x;
+  }
+  __syncthreads();
+  uint16_t* dst = a.dst + (size_t)g * a.d0;
+#pragma unroll 4
+  for (int i = 0; i < 16; i++) {
+    const int u = t % 64, v = t / 64 + 4 * i;
+    const int r = a.dst_c_unit ? r0 + v : r0 + u;
+    const int c = a.dst_c_unit ? c0 + u : c0 + v;
+    if (r < a.R && c < a.Cd) dst[(size_t)r * a.d1 + (size_t)c * a.d2] = tile[r - r0][c - c0];
+  }
+}
+
+static int pack(const char* nm, const void* src, void* dst, int G, int R, int C, int Cd, long long s0, long long s1,
+                long long s2, long long d0, long long d1, long long d2, hipStream_t st) {
+  PackArgs a;
+  a.src = (const uint16_t*)src;
+  a.dst = (uint16_t*)dst;
+  a.s0 = s0; a.s1 = s1; a.s2 = s2; a.d0 = d0; a.d1 = d1; a.d2 = d2;
+  a.R = R; a.C = C; a.Cd = Cd;
+  a.src_c_unit = s2 == 1 || s1 != 1;
+  a.dst_c_unit = d2 == 1 || d1 != 1;
+  if (G <= 0 || R <= 0 || Cd <= 0 || G > 65535) return fail(YR_E_INVALID, "%s: pack shape", nm);
+  dim3 grid((Cd + 63) / 64, (R + 63) / 64, G);
+  if (grid.y > 65535) return fail(YR_E_INVALID, "%s: pack rows", nm);
+  hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, st, a);
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+// ------------------------------------------------------------------ elementwise
+enum UnaryKind { U_EXP = 0, U_SILU = 1, U_GELU = 2, U_RELU = 3, U_CLAMP = 4, U_SQRT = 5, U_SQUARE = 6 };
+enum BinaryKind { B_ADD = 0, B_MUL = 1, B_DIV = 2, B_POW = 3 };
+
+template <int DT>
+__global__ __launch_bounds__(256) void unary_kernel(const uint16_t* x, uint16_t* y, long long n, int kind, float lo,
+                                                    float hi) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const float a = ld_elem<DT>(x[i]);
+    float r;
+    switch (kind) {
+      case U_EXP: r = expf(a); break;
+      case U_SILU: r = a / (1.f + expf(-a)); break;
+      case U_GELU: r = 0.5f * a * (1.f + erff(a * 0.70710678118654752f)); break;
+      case U_RELU: r = fmaxf(a, 0.f); break;
+      case U_CLAMP: r = fminf(fmaxf(a, lo), hi); break;
+      case U_SQRT: r = sqrtf(a); break;
+      default: r = a * a; break;
+    }
+    y[i] = (uint16_t)st_elem<DT>(r);
+  }
+}
+
+constexpr int kMaxDims = 6;
+struct BinaryArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  uint16_t* out;
+  long long n;
+  int nd, kind;
+  long long dims[kMaxDims];  // output dims
+  long long sa[kMaxDims], sb[kMaxDims];  // element strides of a / b per output dim (0: broadcast)
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void binary_kernel(BinaryArgs p) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n;
+       i += (long long)gridDim.x * blockDim.x) {
+    long long rem = i, oa = 0, ob = 0;
+    for (int d = p.nd - 1; d >= 0; d--) {
+      const long long c = rem % p.dims[d];
+      rem /= p.dims[d];
+      oa += c * p.sa[d];
+      ob += c * p.sb[d];
+    }
+    const float x = ld_elem<DT>(p.a[oa]), y = ld_elem<DT>(p.b[ob]);
+    float r;
+    switch (p.kind) {
+      case B_ADD: r = x + y; break;
+      case B_MUL: r = x * y; break;
+      case B_DIV: r = x / y; break;
+      default: r = powf(x, y); break;
+    }
+    p.out[i] = (uint16_t)st_elem<DT>(r);
+  }
+}
+
+// ------------------------------------------------------------------ reductions
+// out[o][i] = sum_r x[o][r][i] (fp32), one thread per (o, i)
+template <int DT>
+__global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* x, uint16_t* y, long long outer, int red,
+                                                     long long inner) {
+  const long long n = outer * inner;
+  for (long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (long long)gridDim.x * blockDim.x) {
+    const long long o = j / inner, i = j % inner;
+    const uint16_t* p = x + o * red * inner + i;
+    float s = 0.f;
+    for (int r = 0; r < red; r++) s += ld_elem<DT>(p[(long long)r * inner]);
+    y[j] = (uint16_t)st_elem<DT>(s);
+  }
+}
+
+// y[row] = x[row] * rsqrt(mean(x[row]^2) + eps): one workgroup per row
+template <int DT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, uint16_t* y, int n, float eps) {
+  const uint16_t* xr = x + (size_t)blockIdx.x * n;
+  uint16_t* yr_ = y + (size_t)blockIdx.x * n;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = ld_elem<DT>(xr[i]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  __shared__ float part[4];
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float inv = rsqrtf(tot / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) yr_[i] = (uint16_t)st_elem<DT>(ld_elem<DT>(xr[i]) * inv);
+}
+
+// ------------------------------------------------------------------ batched matmul
+// C[b] = A[b] (M x K, row-major) x B[b] (K x N, row-major), fp32 accumulate on
+// MFMA 16x16x32.  Workgroup = 64 x 64 tile of C, 4 waves of 32 x 32 (2 x 2
+// MFMA blocks); K in steps of 32 through LDS.  A fragments are 16-byte LDS
+// reads of padded rows; B fragments come from the row-major K x N tile by
+// transposing reads.  K and N must be multiples of 8 (16-byte rows).
+constexpr int MM_T = 64, MM_KS = 32;
+template <int DT>
+__global__ __launch_bounds__(256) void matmul_kernel(const uint16_t* A, const uint16_t* B, uint16_t* C, int M, int N,
+                                                     int K, long long sA, long long sB, long long sC) {
+  constexpr int LDA = MM_KS + 8, LDB = MM_T + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t as[MM_T * LDA];
+  __shared__ __attribute__((aligned(16))) uint16_t bs[MM_KS * LDB];
+  const int b = blockIdx.z, m0 = blockIdx.y * MM_T, n0 = blockIdx.x * MM_T;
+  const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+  const int wm = (w / 2) * 32, wn = (w % 2) * 32;
+  A += (size_t)b * sA;
+  B += (size_t)b * sB;
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // staging: A tile 64 x 32 = 256 chunks of 8 (row t / 4, chunk t % 4);
+  // B tile 32 x 64 = 256 chunks (row t / 8, chunk t % 8)
+  const int ar = t / 4, ac = (t % 4) * 8, br = t / 8, bc = (t % 8) * 8;
+  for (int k0 = 0; k0 < K; k0 += MM_KS) {
+    uint4 av = make_uint4(0, 0, 0, 0), bv = make_uint4(0, 0, 0, 0);
+    if (m0 + ar < M && k0 + ac < K) av = ldg16(A + (size_t)(m0 + ar) * K + k0 + ac);
+    if (k0 + br < K && n0 + bc < N) bv = ldg16(B + (size_t)(k0 + br) * N + n0 + bc);
+    __syncthreads();
+    *reinterpret_cast<uint4*>(&as[ar * LDA + ac]) = av;
+    *reinterpret_cast<uint4*>(&bs[br * LDB + bc]) = bv;
+    __syncthreads();
+    uint4 af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+      af[i] = *reinterpret_cast<const uint4*>(&as[(wm + 16 * i + lane % 16) * LDA + (lane / 16) * 8]);
+#pragma unroll
+    for (int j = 0; j < 2; j++) bf[j] = b_frag(bs + wn + 16 * j, LDB, 0, lane);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = mfma16<DT>(af[i], bf[j], acc[i][j]);
+  }
+  C += (size_t)b * sC;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int r = m0 + wm + 16 * i + 4 * (lane / 16) + e, c = n0 + wn + 16 * j + lane % 16;
+        if (r < M && c < N) C[(size_t)r * N + c] = (uint16_t)st_elem<DT>(acc[i][j][e]);
+      }
+}
+
+// identity page table of the kernel-graph decode: G sequences of L tokens,
+// one page each
+__global__ void page_iota_kernel(int32_t* indptr, int32_t* indices, int32_t* lens, int G, int L) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i <= G; i += gridDim.x * blockDim.x) {
+    indptr[i] = i;
+    if (i < G) {
+      indices[i] = i;
+      lens[i] = L;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ graph attention
+// O[g] = softmax(scale * Q[g] K[g]) V[g] with Q [G][M][d], K [G][d][L]
+// (the kernel-graph operand: its rows are head dims), V [G][L][d], each given
+// by three element strides.  Up to 16 query rows per group (a power of two)
+// run on the split-KV decode kernel over an identity page table (one page of
+// L tokens per group), more on the flash-attention prefill kernel.  Operands
+// not already laid out as [G][rows][128] contiguous are packed into the
+// workspace first (zero-padded to d = 128 for d < 128, which leaves the
+// scores and the first d output columns unchanged).
+struct AttnPlan {
+  bool decode, pack_q, pack_k, pack_v, pack_o;
+  size_t off_q, off_k, off_v, off_o, off_pt, dec_ws, total;
+};
+
+static bool dense_rows(const long long* s, int G, int rows, int d) {
+  // [G][rows][d] contiguous with d == 128 (the group stride is unused when G == 1)
+  return d == 128 && s[2] == 1 && s[1] == 128 && (G == 1 || s[0] == (long long)rows * 128);
+}
+
+static AttnPlan attn_plan(int G, int M, int L, int d, const long long* sq, const long long* sk, const long long* sv,
+                          const long long* so) {
+  AttnPlan p;
+  p.decode = M <= 16 && (M & (M - 1)) == 0;
+  p.pack_q = !dense_rows(sq, G, M, d);
+  // K as the kernel wants it is [G][L][128]: K^T's strides swapped
+  const long long skt[3] = {sk[0], sk[2], sk[1]};
+  p.pack_k = !dense_rows(skt, G, L, d);
+  p.pack_v = !dense_rows(sv, G, L, d);
+  p.pack_o = !dense_rows(so, G, M, d);
+  // the shared workspace layout: arrival tickets in [0, kTicketBytes) (zero
+  // at rest, whichever operator ran last), then the decode's split records,
+  // then the packed operands
+  size_t off = kTicketBytes;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) & ~(size_t)255;
+    return o;
+  };
+  p.dec_ws = p.decode ? yr_hip_gqa_decode_workspace(G, M, 1, 128, L, L) : 0;
+  if (p.dec_ws) take(p.dec_ws - kTicketBytes);
+  p.off_q = p.pack_q ? take((size_t)G * M * 128 * 2) : 0;
+  p.off_k = p.pack_k ? take((size_t)G * L * 128 * 2) : 0;
+  p.off_v = p.pack_v ? take((size_t)G * L * 128 * 2) : 0;
+  p.off_o = p.pack_o ? take((size_t)G * M * 128 * 2) : 0;
+  p.off_pt = p.decode ? take((size_t)(3 * G + 1) * 4) : 0;
+  p.total = off;
+  return p;
+}
+
+}  // namespace graph
+}  // namespace yr
+
+using namespace yr;
+using namespace yr::graph;
+
+namespace {
+
+template <class F>
+int by_dtype(int dtype, F f) {
+  if (dtype == YR_DTYPE_F16) return f(std::integral_constant<int, DT_F16>{});
+  if (dtype == YR_DTYPE_BF16) return f(std::integral_constant<int, DT_BF16>{});
+  return fail(YR_E_INVALID, "graph op: dtype %d unsupported (f16 / bf16)", dtype);
+}
+
+int grid_for(long long n) {
+  long long g = (n + 255) / 256;
+  return (int)(g < 1 ? 1 : g > 8192 ? 8192 : g);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t yr_hip_graph_attention_workspace(int G, int M, int L, int d, const int64_t* strides12) {
+  if (G <= 0 || M <= 0 || L <= 0 || d <= 0 || d > 128 || !strides12) return 0;
+  const long long* s = reinterpret_cast<const long long*>(strides12);
+  return attn_plan(G, M, L, d, s, s + 3, s + 6, s + 9).total;
+}
+
+int yr_hip_graph_attention(const void* q, const void* k, const void* v, void* out, int G, int M, int L, int d,
+                           const int64_t* strides12, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  const char* nm = "yr_hip_graph_attention";
+  if (!q || !k || !v || !out || !strides12) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (G <= 0 || M <= 0 || L <= 0 || d <= 0 || d > 128 || d % 8)
+    return fail(YR_E_INVALID, "%s: shape G=%d M=%d L=%d d=%d (d <= 128, multiple of 8)", nm, G, M, L, d);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  const long long* s = reinterpret_cast<const long long*>(strides12);
+  const long long *sq = s, *sk = s + 3, *sv = s + 6, *so = s + 9;
+  const AttnPlan p = attn_plan(G, M, L, d, sq, sk, sv, so);
+  if (p.total > workspace_bytes || (p.total && !workspace))
+    return fail(YR_E_WORKSPACE, "%s: workspace %zu < %zu", nm, workspace_bytes, p.total);
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const void* qd = q;
+  const void* kd = k;
+  const void* vd = v;
+  void* od = out;
+  int rc = YR_OK;
+  const long long RM = (long long)M * 128, RL = (long long)L * 128;
+  if (p.pack_q) {
+    qd = ws + p.off_q;
+    rc = pack(nm, q, ws + p.off_q, G, M, d, 128, sq[0], sq[1], sq[2], RM, 128, 1, st);
+  }
+  if (rc == YR_OK && p.pack_k) {  // rows of the packed K are tokens: source strides (g, token, dim)
+    kd = ws + p.off_k;
+    rc = pack(nm, k, ws + p.off_k, G, L, d, 128, sk[0], sk[2], sk[1], RL, 128, 1, st);
+  }
+  if (rc == YR_OK && p.pack_v) {
+    vd = ws + p.off_v;
+    rc = pack(nm, v, ws + p.off_v, G, L, d, 128, sv[0], sv[1], sv[2], RL, 128, 1, st);
+  }
+  if (rc != YR_OK) return rc;
+  if (p.pack_o) od = ws + p.off_o;
+  if (p.decode) {
+    int32_t* pt = reinterpret_cast<int32_t*>(ws + p.off_pt);
+    hipLaunchKernelGGL(page_iota_kernel, dim3((G + 256) / 256), dim3(256), 0, st, pt, pt + G + 1, pt + 2 * G + 1, G, L);
+    YR_CHECK_LAUNCH(nm);
+    rc = gqa_decode_launch(nm, qd, kd, vd, pt, pt + G + 1, pt + 2 * G + 1, od, G, M, 1, 128, L, L, dtype,
+                           p.dec_ws ? ws : nullptr, p.dec_ws, st, scale);
+  } else {
+    rc = prefill_launch(nm, qd, kd, vd, od, G, M, L, 1, 1, 128, 0, dtype, RM, 128, RL, 128, RM, 128, scale, st);
+  }
+  if (rc == YR_OK && p.pack_o) rc = pack(nm, ws + p.off_o, out, G, M, d, d, RM, 128, 1, so[0], so[1], so[2], st);
+  return rc;
+}
+
+int yr_hip_graph_pack(const void* src, void* dst, int g, int rows, int cols, int dst_cols, const int64_t* strides6,
+                      int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_pack";
+  if (!src || !dst || !strides6) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  const long long* s = reinterpret_cast<const long long*>(strides6);
+  return pack(nm, src, dst, g, rows, cols, dst_cols, s[0], s[1], s[2], s[3], s[4], s[5], (hipStream_t)stream);
+}
+
+int yr_hip_graph_unary(const void* x, void* y, int64_t n, int kind, float lo, float hi, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_unary";
+  if (!x || !y || n <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+  if (kind < U_EXP || kind > U_SQUARE) return fail(YR_E_INVALID, "%s: unknown kind %d", nm, kind);
+  hipStream_t st = (hipStream_t)stream;
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((unary_kernel<decltype(dt)::value>), dim3(grid_for(n)), dim3(256), 0, st, (const uint16_t*)x,
+                       (uint16_t*)y, (long long)n, kind, lo, hi);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+int yr_hip_graph_binary(const void* a, const void* b, void* out, int ndim, const int64_t* dims_a,
+                        const int64_t* dims_b, int kind, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_binary";
+  if (!a || !b || !out || !dims_a || !dims_b) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (ndim <= 0 || ndim > kMaxDims) return fail(YR_E_INVALID, "%s: %d dims (1..%d)", nm, ndim, kMaxDims);
+  if (kind < B_ADD || kind > B_POW) return fail(YR_E_INVALID, "%s: unknown kind %d", nm, kind);
+  BinaryArgs p;
+  p.a = (const uint16_t*)a;
+  p.b = (const uint16_t*)b;
+  p.out = (uint16_t*)out;
+  p.nd = ndim;
+  p.kind = kind;
+  long long sa = 1, sb = 1, n = 1;
+  for (int d = ndim - 1; d >= 0; d--) {
+    const long long da = dims_a[d], db = dims_b[d];
+    if (da <= 0 || db <= 0 || (da != db && da != 1 && db != 1))
+      return fail(YR_E_INVALID, "%s: dims %lld and %lld of axis %d do not broadcast", nm, da, db, d);
+    p.dims[d] = da > db ? da : db;
+    p.sa[d] = da == 1 && p.dims[d] > 1 ? 0 : sa;
+    p.sb[d] = db == 1 && p.dims[d] > 1 ? 0 : sb;
+    sa *= da;
+    sb *= db;
+    n *= p.dims[d];
+  }
+  p.n = n;
+  hipStream_t st = (hipStream_t)stream;
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((binary_kernel<decltype(dt)::value>), dim3(grid_for(n)), dim3(256), 0, st, p);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_reduction";
+  if (!x || !y || outer <= 0 || red <= 0 || inner <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+  hipStream_t st = (hipStream_t)stream;
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((reduce_kernel<decltype(dt)::value>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
+                       (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_rmsnorm";
+  if (!x || !y || rows <= 0 || n <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+  hipStream_t st = (hipStream_t)stream;
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((rmsnorm_kernel<decltype(dt)::value>), dim3(rows), dim3(256), 0, st, (const uint16_t*)x,
+                       (uint16_t*)y, n, eps);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m, int n, int k, int dtype,
+                        void* stream) {
+  const char* nm = "yr_hip_graph_matmul";
+  if (!a || !b || !c) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return fail(YR_E_INVALID, "%s: bad shape", nm);
+  if (n % 8 || k % 8) return fail(YR_E_INVALID, "%s: N and K must be multiples of 8 (got %d, %d)", nm, n, k);
+  if (batch > 65535 || (m + MM_T - 1) / MM_T > 65535) return fail(YR_E_INVALID, "%s: grid too large", nm);
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((n + MM_T - 1) / MM_T, (m + MM_T - 1) / MM_T, batch);
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((matmul_kernel<decltype(dt)::value>), grid, dim3(256), 0, st, (const uint16_t*)a,
+                       (const uint16_t*)b, (uint16_t*)c, m, n, k, (long long)m * k, (long long)k * n,
+                       (long long)m * n);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+}  // extern "C"

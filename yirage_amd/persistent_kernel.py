@@ -138,6 +138,7 @@ class PersistentKernel:
         assert name is not None
         if io_category not in ("cuda_tensor", "nvshmem_tensor"):
             raise RuntimeError(f"Invalid io_category: {io_category}")
+        dtype = int(dtype)  # a yirage_amd dtype (yr.bfloat16) or its integer code
         t = torch.zeros(dims, dtype=_DT2TORCH[dtype], device=self.meta_tensors["qo_indptr_buffer"].device)
         self._owned.append(t)
         return self._register(DTensor(name, tuple(dims), dtype, t))
