@@ -89,8 +89,9 @@ def test_gated_mlp(B, K, N, layout):
     _close(out, ref, "gated_mlp")
 
 
-def test_gated_mlp_batch128_column_sample():
-    """Config 2b (batch 128): checked on a 512-column sample of the oracle."""
+def test_gated_mlp_batch128_all_columns():
+    """Config 2b (batch 128, the MFMA path): every one of the 14336 columns
+    against the oracle."""
     import yirage_amd.fused as F
 
     g = torch.Generator().manual_seed(0)
@@ -100,9 +101,9 @@ def test_gated_mlp_batch128_column_sample():
     w3 = _randn((K, N), 0.02, torch.bfloat16, g)
     out = F.gated_mlp(x.cuda(), w1.cuda(), w3.cuda())
     torch.cuda.synchronize()
-    cols = np.r_[0:256, N - 256:N]
-    ref = O.gated_mlp(_f(x), _bits(w1)[:, cols], _bits(w3)[:, cols], "bf16", 1)
-    _close(out[:, cols], ref, "gated_mlp_b128")
+    O.set_num_threads(16)
+    ref = O.gated_mlp(_f(x), _bits(w1), _bits(w3), "bf16", 1)
+    _close(out, ref, "gated_mlp_b128")
 
 
 @pytest.mark.parametrize("dtype,layout,B", [(torch.float16, 0, 4), (torch.bfloat16, 0, 4), (torch.bfloat16, 1, 4),
@@ -182,10 +183,10 @@ def test_gqa_prefill(S, causal, dtype, B, Hq, Hkv):
     v = _randn((B, S, Hkv, D), 1.0, dtype, g)
     out = F.gqa_prefill(q.cuda(), k.cuda(), v.cuda(), causal=causal)
     torch.cuda.synchronize()
-    rows = sorted(set(r for r in [0, 1, 15, 16, 63, 64, S // 2, S - 2, S - 1] + list(range(0, S, max(1, S // 24)))
-                      if 0 <= r < S))
-    ref = O.gqa_prefill(_f(q), _f(k), _f(v), causal=causal, rows=rows)
-    _close(out[:, rows], ref[:, rows], "gqa_prefill")
+    # every query row of every head against the oracle
+    O.set_num_threads(16)
+    ref = O.gqa_prefill(_f(q), _f(k), _f(v), causal=causal)
+    _close(out, ref, "gqa_prefill")
 
 
 def test_argmax_planted_and_ties():
