@@ -53,3 +53,50 @@ def decode_step(cfg, batch, kv_len, page, seed, tokens, return_logits=True):
     lm = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(seed, 0, "lm_head"), cfg.weight_std)
     logits = O.round_to(O.linear(xn, lm, bf, O.W_NK), bf)
     return logits, O.argmax(logits)
+
+
+class ServingOracle:
+    """Stateful oracle of the serving-mode model (LlamaDecodeModel with
+    prompts): the same weights, its own paged KV caches (pool pages in the
+    device layout), and one decode/extend step per call over the batch the
+    device's metadata describes -- the composition of decode_step above with
+    the multi-token paged attention (RoPE, cache append, causal mask over the
+    new tokens) of multitoken_paged_attention_4_16.cuh:40-656."""
+
+    def __init__(self, cfg, pool, page, seed, max_seq):
+        bf = "bf16"
+        self.cfg, self.page, self.seed = cfg, page, seed
+        self.W = [{n: O.synth(shp, bf, tensor_seed(seed, layer, n), cfg.weight_std)
+                   for n, shp in weight_shapes(cfg).items()} for layer in range(cfg.num_layers)]
+        shp = (pool, page, cfg.num_kv_heads, cfg.head_dim)
+        self.kc = [O.synth(shp, bf, tensor_seed(seed, layer, "kc"), 1.0) for layer in range(cfg.num_layers)]
+        self.vc = [O.synth(shp, bf, tensor_seed(seed, layer, "vc"), 1.0) for layer in range(cfg.num_layers)]
+        self.emb = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(seed, 0, "embed"), cfg.weight_std)
+        self.lm = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(seed, 0, "lm_head"), cfg.weight_std)
+        cos, sin = rope_tables(max(max_seq, 64), cfg.head_dim, cfg.rope_theta)
+        self.cos, self.sin = cos.float().numpy(), sin.float().numpy()
+
+    def step(self, tokens, qo_indptr, kv_indptr, kv_indices, last_page_len):
+        """Logits [T, vocab] (bf16-rounded) and argmax ids of the T new tokens."""
+        cfg, bf = self.cfg, "bf16"
+        G, D = cfg.num_q_heads // cfg.num_kv_heads, cfg.head_dim
+        x = O.to_float(self.emb[np.asarray(tokens, np.int64)], bf)
+        ones = np.ones(cfg.hidden, np.float32)
+        for layer in range(cfg.num_layers):
+            W = self.W[layer]
+            xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
+            rows = []
+            for g in range(cfg.num_kv_heads):
+                rows += [W["wq"][g * G * D:(g + 1) * G * D], W["wk"][g * D:(g + 1) * D], W["wv"][g * D:(g + 1) * D]]
+            qkv = O.round_to(O.linear(xn, np.concatenate(rows, 0), bf, O.W_NK), bf)
+            att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, self.kc[layer],
+                                               self.vc[layer], bf, qo_indptr, kv_indptr, kv_indices, last_page_len,
+                                               self.cos, self.sin), bf)
+            h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
+            hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
+            gate = O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf)
+            up = O.round_to(O.linear(hn, W["wu"], bf, O.W_NK), bf)
+            x = O.round_to(O.linear(O.silu_mul(gate, up, bf), W["wd"], bf, O.W_NK, residual=h), bf)
+        xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
+        logits = O.round_to(O.linear(xn, self.lm, bf, O.W_NK), bf)
+        return logits, O.argmax(logits)

@@ -15,13 +15,19 @@ from yirage_amd.llama import LlamaConfig, LlamaDecodeModel
 pytestmark = pytest.mark.gpu
 
 
-def _check(model, tokens, ref_logits, ref_ids, what, rel_l2=None):
+def _check(model, tokens, ref_logits, ref_ids, what, rel_l2=None, elementwise=False):
     got = model.t["argmax_in"].tensor.float().cpu().numpy()[: model.batch]
     ids = model.meta["output_tokens"].cpu().numpy().reshape(-1)[: model.batch]
     err = np.abs(got - ref_logits)
     scale = np.abs(ref_logits).max()
     print(f"[{what}] logits max abs err {err.max():.4f} (max |logit| {scale:.3f}), ids {ids.tolist()} "
           f"ref {ref_ids.tolist()}", flush=True)
+    if elementwise:
+        # the north-star tolerance, element by element (only where the
+        # model's own rounding noise stays below it: one layer)
+        bad = err > 1e-2 + 1e-2 * np.abs(ref_logits)
+        print(f"  element-wise rtol/atol 1e-2: {bad.sum()} of {bad.size} outside", flush=True)
+        assert not bad.any(), f"{what}: logits outside rtol/atol 1e-2"
     if rel_l2 is None:
         assert err.max() <= 2e-2 * max(1.0, scale), f"{what}: logits differ"
     else:
@@ -57,6 +63,27 @@ def test_small_llama_decode_step(batch, kv_len):
     model.step()
     torch.cuda.synchronize()
     assert torch.equal(first, model.t["argmax_in"].tensor)
+
+
+@pytest.mark.parametrize("batch", [1])
+def test_llama3_8b_dims_one_layer_elementwise(batch):
+    """One layer at full Llama-3-8B dims: logits element-wise within rtol /
+    atol 1e-2 of the oracle.  (From two layers on, +-1 ulp of rounding noise
+    in the activations alone moves some logits by more than that -- measured
+    oracle against perturbed oracle in tests/test_oracle.py -- so deeper
+    stacks are bounded by magnitude and relative L2 instead; at batch 8
+    even one layer leaves 25 of 1,026,048 logits just outside.)"""
+    cfg = LlamaConfig(num_layers=1)
+    print(f"case llama3-8b dims, 1 layer, B={batch} kv=4096", flush=True)
+    model = LlamaDecodeModel(cfg, batch=batch, kv_len=4096, seed=0)
+    tokens = (np.arange(batch) * 15013 + 128000) % cfg.vocab
+    model.set_input_tokens(tokens)
+    model.step()
+    torch.cuda.synchronize()
+    rc, st = model.pk.status()
+    assert rc == 0, st
+    ref_logits, ref_ids = decode_step(cfg, batch, 4096, 64, 0, tokens)
+    _check(model, tokens, ref_logits, ref_ids, f"llama3-8b 1 layer B={batch}", elementwise=True)
 
 
 @pytest.mark.parametrize("batch", [1, 8])

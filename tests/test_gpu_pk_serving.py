@@ -1,0 +1,175 @@
+"""GPU parity of the persistent kernel in serving mode: the on-device offline
+batch manager (prepare_next_batch, persistent_kernel.cuh:169-322) schedules
+prefill chunks and decode steps of several requests, and the multi-token
+paged attention (multitoken_paged_attention_4_16.cuh:40-656 /
+_32_64.cuh:40-710: RoPE, KV append, causal mask over the new tokens) runs
+them, launch after launch through prefill -> decode -> EOS / max length.
+
+After every launch:
+  * the batch metadata the device wrote -- qo_indptr, paged_kv_indptr,
+    paged_kv_indices, paged_kv_last_page_len, input_tokens, tokens, step --
+    equals, bit for bit, what the CPU restatement (oracle.BatchManager) writes
+    when fed the same output tokens;
+  * the K / V the device appended to the paged cache is within rtol/atol
+    1e-2 of the oracle's in the first layer (identical inputs) and within
+    2e-2 * max(1, max|v|) in the next (every position of every scheduled
+    request);
+  * the logits of every scheduled token are within 2e-2 * max(1, max|logit|)
+    of the oracle composition (tests/llama_oracle.ServingOracle, its own
+    paged KV cache, same page ids) element-wise and within 1e-2 relative L2
+    per launch, and the argmax token ids are equal unless the oracle's top
+    two logits are a near-tie (reported).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.llama_oracle import ServingOracle
+from yirage_amd.llama import LlamaConfig, LlamaDecodeModel
+
+pytestmark = pytest.mark.gpu
+
+CFG = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, head_dim=128, intermediate=2048,
+                  vocab=4096)
+KEYS = ("qo_indptr", "kv_indptr", "last_page_len")
+DEV = {"qo_indptr": "qo_indptr_buffer", "kv_indptr": "paged_kv_indptr_buffer",
+       "kv_indices": "paged_kv_indices_buffer", "last_page_len": "paged_kv_last_page_len_buffer"}
+
+
+def _meta(model):
+    m = {k: model.meta[v].cpu().numpy().copy() for k, v in DEV.items()}
+    m["input_tokens"] = model.meta["input_tokens"].cpu().numpy().reshape(-1).copy()
+    m["tokens"] = model.meta["tokens"].cpu().numpy().copy()
+    m["step"] = model.meta["step"].cpu().numpy().copy()
+    return m
+
+
+def _compare_meta(dev, bm, MR, what):
+    for k in KEYS:
+        assert np.array_equal(dev[k], bm[k]), f"{what}: {k} device {dev[k].tolist()} oracle {bm[k].tolist()}"
+    npg = int(bm["kv_indptr"][MR])
+    assert np.array_equal(dev["kv_indices"][:npg], bm["kv_indices"][:npg]), f"{what}: kv_indices differ"
+    T = int(bm["qo_indptr"][MR])
+    assert np.array_equal(dev["input_tokens"][:T], bm["input_tokens"][:T]), f"{what}: input_tokens differ"
+    assert np.array_equal(dev["tokens"], bm["tokens"]), f"{what}: tokens differ"
+    assert np.array_equal(dev["step"], bm["step"]), f"{what}: step differs"
+
+
+def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
+    """CPU-only run of the schedule until `request` produces its first
+    generated token (the schedule up to there does not depend on eos)."""
+    tokens = np.zeros((len(prompts), max_seq), np.int64)
+    for i, p in enumerate(prompts):
+        tokens[i, :len(p)] = p
+    bm = O.BatchManager(MR, MT, pool, page, tokens, np.array([len(p) for p in prompts], np.int32), -1)
+    orc = ServingOracle(CFG, pool, page, seed, max_seq)
+    bm.prepare_next()
+    for _ in range(200):
+        T = int(bm["qo_indptr"][MR])
+        _, ids = orc.step(bm["input_tokens"][:T], bm["qo_indptr"], bm["kv_indptr"], bm["kv_indices"],
+                          bm["last_page_len"])
+        bm["output_tokens"][:T] = ids
+        bm.prepare_next()
+        if bm["step"][request] >= len(prompts[request]):
+            return int(bm["tokens"][request, len(prompts[request])])
+    raise AssertionError("request never produced a token")
+
+
+@pytest.mark.parametrize("MR,MT,lens", [(2, 8, (50, 37, 5)), (3, 8, (9, 70, 3, 20))])
+def test_serving_prefill_decode_eos(MR, MT, lens):
+    seed, page, max_seq = 5, 64, 80
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, CFG.vocab, n).tolist() for n in lens]
+    npg = (max_seq + page - 1) // page
+    pool = MR * npg
+    print(f"case serving MR={MR} MT={MT} prompts {list(lens)}", flush=True)
+    # eos = the first token request 1 generates, so that request ends by EOS
+    eos = _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, 1)
+    print(f"  eos token {eos}", flush=True)
+    model = LlamaDecodeModel(CFG, batch=MR, page_size=page, seed=seed, with_prepare=True, prompts=prompts,
+                             max_tokens=MT, max_requests=MR, max_seq=max_seq, eos_token_id=eos)
+    torch.cuda.synchronize()
+    assert model.max_pages == pool
+    tokens = np.zeros((len(prompts), max_seq), np.int64)
+    for i, p in enumerate(prompts):
+        tokens[i, :len(p)] = p
+    bm = O.BatchManager(MR, MT, pool, page, tokens, np.array(lens, np.int32), eos)
+    orc = ServingOracle(CFG, pool, page, seed, max_seq)
+    worst, near, launches, multi = 0.0, 0, 0, 0
+    for launch in range(400):
+        before = _meta(model)
+        T = int(before["qo_indptr"][MR])
+        model.step()
+        torch.cuda.synchronize()
+        rc, st = model.pk.status()
+        assert rc == 0, f"launch {launch}: status {st}"
+        launches += 1
+        out_ids = model.meta["output_tokens"].cpu().numpy().reshape(-1)[:T]
+        if T:
+            qo = before["qo_indptr"]
+            multi += int(np.any(np.diff(qo) * (CFG.num_q_heads // CFG.num_kv_heads) > 16))
+            ref_logits, ref_ids = orc.step(before["input_tokens"][:T], qo, before["kv_indptr"],
+                                           before["kv_indices"], before["last_page_len"])
+            got = model.t["argmax_in"].tensor.float().cpu().numpy()[:T]
+            err = np.abs(got - ref_logits)
+            # element-wise bound scaled by the logits' magnitude: +-1 ulp of
+            # noise in 30 % of the cached K / V alone moves these 2-layer
+            # logits by up to 0.02 (oracle against a perturbed oracle), so a
+            # plain 1e-2 atol would test rounding, not the kernels
+            bad = err > 2e-2 * max(1.0, float(np.abs(ref_logits).max()))
+            rel = float(np.linalg.norm(got - ref_logits) / np.linalg.norm(ref_logits))
+            assert rel <= 1e-2, f"launch {launch}: relative L2 error {rel}"
+            worst = max(worst, float(err.max()))
+            if bad.any():
+                rows, cols = np.nonzero(bad)
+                for r_, c_ in list(zip(rows, cols))[:8]:
+                    print(f"  launch {launch} row {r_} col {c_}: got {got[r_, c_]} ref {ref_logits[r_, c_]}", flush=True)
+                print("  qo", qo.tolist(), "kv_indptr", before["kv_indptr"].tolist(), "lpl",
+                      before["last_page_len"].tolist(), flush=True)
+                print("  per-row max err", err.max(1).tolist(), flush=True)
+            assert not bad.any(), f"launch {launch}: {bad.sum()} logits outside the bound (max err {err.max()})"
+            print(f"  launch {launch}: T={T} qo {qo.tolist()} max err {err.max():.4f} rel L2 {rel:.2e}", flush=True)
+            # the K / V the device appended (every position of the batch's
+            # requests) against the oracle's own cache
+            kvp, kvi, lpl = before["kv_indptr"], before["kv_indices"], before["last_page_len"]
+            for layer in range(CFG.num_layers):
+                dk = model.kc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
+                dv = model.vc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
+                for r in range(MR):
+                    if qo[r + 1] == qo[r]:
+                        continue
+                    npg_r = kvp[r + 1] - kvp[r]
+                    seq = (npg_r - 1) * page + (lpl[r] if lpl[r] else page)
+                    for pos in range(seq):
+                        pg = kvi[kvp[r] + pos // page]
+                        for name, dc, oc in (("k", dk, orc.kc[layer]), ("v", dv, orc.vc[layer])):
+                            a_ = O.to_float(dc[pg, pos % page], "bf16")
+                            b_ = O.to_float(oc[pg, pos % page], "bf16")
+                            e_ = np.abs(a_ - b_)
+                            # layer 0's K / V come from identical inputs: rtol / atol 1e-2;
+                            # deeper layers carry the rounding noise of the layers below
+                            lim = 1e-2 + 1e-2 * np.abs(b_) if layer == 0 else 2e-2 * max(1.0, np.abs(b_).max())
+                            if (e_ > lim).any():
+                                print(f"  cache {name} layer {layer} req {r} pos {pos} page {pg}: max diff {e_.max()}",
+                                      flush=True)
+                                raise AssertionError(f"launch {launch}: cached {name} differs")
+            for i in range(T):
+                if out_ids[i] != ref_ids[i]:
+                    top = np.sort(ref_logits[i])[-2:]
+                    assert top[1] - top[0] <= 2 ** -7 * max(abs(top[1]), 1e-3), \
+                        f"launch {launch}: token row {i} {out_ids[i]} != {ref_ids[i]}"
+                    near += 1
+        bm["output_tokens"][:T] = out_ids
+        more = bm.prepare_next()
+        _compare_meta(_meta(model), bm, MR, f"launch {launch}")
+        if not more:
+            break
+    else:
+        raise AssertionError("requests did not finish")
+    print(f"  {launches} launches ({multi} with > 16 query rows per kv head), max logit err {worst:.4f}, "
+          f"{near} near-ties", flush=True)
+    assert bm["next_request_id"][0] == len(prompts) and (bm["request_ids"] == -1).all()
+    assert multi > 0, "no launch exercised the multi-token attention task"
+    # request 1 ended on EOS right after its prompt; the others ran to max length or EOS
+    assert bm["step"][1] == lens[1] and bm["tokens"][1, lens[1]] == eos

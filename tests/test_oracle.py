@@ -364,3 +364,38 @@ def test_page_manager_eos_frees_pages_and_admits_next():
     # every live page index is distinct
     live = bm["kv_indices"][: bm["kv_indptr"][2]]
     assert len(set(live.tolist())) == len(live)
+
+
+def test_logit_noise_floor_of_a_two_layer_model():
+    """Pins the end-to-end logit tolerance of the persistent-kernel tests.
+    The oracle against itself with +-1 ulp of noise in 30 % of the cached
+    K / V (the size of the rounding differences any two bf16
+    implementations have) already moves 2-layer logits by more than an
+    element-wise rtol/atol of 1e-2, but stays within 2e-2 * max(1, max|logit|)
+    and 1e-2 relative L2: the bounds the decode / serving tests use."""
+    import copy
+
+    from tests.llama_oracle import ServingOracle
+    from yirage_amd.llama import LlamaConfig
+
+    cfg = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, head_dim=128, intermediate=2048,
+                      vocab=4096)
+    O.set_num_threads(8)
+    orc = ServingOracle(cfg, 2, 64, 5, 80)
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, cfg.vocab, 16)
+    kvi = np.array([0, 1], np.int32)
+    # launch 1: positions 0..7; launch 2: positions 8..15 over the cache
+    orc.step(toks[:8], np.array([0, 8], np.int32), np.array([0, 1], np.int32), kvi, np.array([8], np.int32))
+    noisy = copy.deepcopy(orc)
+    r = np.random.default_rng(1)
+    for layer in range(cfg.num_layers):
+        for c in (noisy.kc[layer], noisy.vc[layer]):
+            c[:, :8] += (r.integers(-1, 2, c[:, :8].shape) * (r.random(c[:, :8].shape) < 0.3)).astype(np.uint16)
+    args = (toks[8:], np.array([0, 8], np.int32), np.array([0, 1], np.int32), kvi, np.array([16], np.int32))
+    a, _ = orc.step(*args)
+    b, _ = noisy.step(*args)
+    err = np.abs(a - b)
+    assert err.max() > 1e-2                                  # below the noise floor: not a usable bound
+    assert err.max() <= 2e-2 * max(1.0, np.abs(a).max())    # the bound the GPU tests use
+    assert np.linalg.norm(a - b) / np.linalg.norm(a) <= 1e-2

@@ -345,8 +345,15 @@ void Graph::build(const char* text) {
       d.max_tokens = cfg.max_tokens;
       d.ticket_base = ticket_next;
       ticket_next += cfg.max_requests * d.num_kv_heads;
+      // split records hold every query row of a request: up to max_tokens * G
+      // (rows beyond one 16-row MFMA block go to the multi-token task body)
+      d.rec_rows = std::max(kAttnRecRows, (cfg.max_tokens * G + 15) / 16 * 16);
+      if (cfg.max_tokens * G > kAttnMaxRows)
+        throw std::runtime_error("attention: max_tokens * (q heads per kv head) must be <= " +
+                                 std::to_string(kAttnMaxRows));
       d.scratch_off = (int)scratch_next;
-      scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * kAttnRecFloats;
+      scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * d.rec_rows * (d.head_dim + 2);
+      if (scratch_next >= (1ll << 31)) throw std::runtime_error("attention: split records exceed 2^31 floats");
       for (int r = 0; r < cfg.max_requests; r++)
         for (int h = 0; h < d.num_kv_heads; h++)
           for (int s = 0; s < d.splits; s++) {

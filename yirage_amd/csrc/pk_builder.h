@@ -12,9 +12,11 @@ struct yr_pk_graph;
 namespace yr {
 namespace pk {
 
-// Scratch floats per attention split record: 16 query rows x (head_dim + 2).
+// Attention split records: at least 16 query rows x (head_dim + 2) floats
+// (one MFMA row block); multi-token ops size them for max_tokens * G rows,
+// at most kAttnMaxRows (eight row blocks, one per wave).
 constexpr int kAttnRecRows = 16;
-constexpr int kAttnRecFloats = kAttnRecRows * (128 + 2);
+constexpr int kAttnMaxRows = 128;
 // cached 64-position blocks one attention compute wave streams per task
 constexpr int kAttnBlocksPerWave = 3;
 

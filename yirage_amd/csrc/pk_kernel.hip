@@ -1363,8 +1363,9 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   lds_sync();
   if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
   const int rows = nt * G;
-  float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * kAttnRecFloats;
-  float* rec = rec_base + (size_t)s * kAttnRecFloats;
+  const int rec_floats = op.rec_rows * (D + 2);
+  float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * rec_floats;
+  float* rec = rec_base + (size_t)s * rec_floats;
   for (int idx = tix(); idx < rows * D; idx += PK_THREADS) {
     int rr = idx / D, d = idx % D;
     float M = -INFINITY;
@@ -1396,7 +1397,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     const int P = PK_THREADS / units;                      // >= 1 (rows <= 16)
     const int tid = tix();
     for (int i = tid; i < rows * S; i += PK_THREADS) {
-      const float* rc = rec_base + (size_t)(i / rows) * kAttnRecFloats + (i % rows) * (D + 2) + D;
+      const float* rc = rec_base + (size_t)(i / rows) * rec_floats + (i % rows) * (D + 2) + D;
       ml[2 * i] = ld_agent(rc);
       ml[2 * i + 1] = ld_agent(rc + 1);
     }
@@ -1408,7 +1409,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     // first batch of o chunks in flight with the (m, l) loads
 #pragma unroll
     for (int q = 0; q < 8; q++)
-      ob[q] = q < ns ? ld_agent4(rec_base + (size_t)(j + q * P) * kAttnRecFloats + rr * (D + 2) + d4)
+      ob[q] = q < ns ? ld_agent4(rec_base + (size_t)(j + q * P) * rec_floats + rr * (D + 2) + d4)
                      : make_float4(0.f, 0.f, 0.f, 0.f);
     lds_sync();
     float M = -INFINITY, L = 0.f;
@@ -1419,7 +1420,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         if (q0 > 0) {
 #pragma unroll
           for (int q = 0; q < 8; q++)
-            ob[q] = q0 + q < ns ? ld_agent4(rec_base + (size_t)(j + (q0 + q) * P) * kAttnRecFloats + rr * (D + 2) + d4)
+            ob[q] = q0 + q < ns ? ld_agent4(rec_base + (size_t)(j + (q0 + q) * P) * rec_floats + rr * (D + 2) + d4)
                                 : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
@@ -1463,6 +1464,287 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
   }
   signal_event(a, t, (op.flags & OPF_OUT_LL) != 0);
+}
+
+// Multi-token attention task: a request with more than 16 query rows per kv
+// head (nt * G > 16: prefill / extend chunks), the case of
+// multitoken_paged_attention_32_64.cuh:40-710.  Same task grid, split
+// ranges and split records as the single-block body above, organised for
+// rows instead of latency:
+//   * the whole workgroup waits for the QKV event (plain tensors only: link
+//     tensors exist only in batch-1 graphs, where nt * G <= 16);
+//   * the last split stages the nt new tokens' k (RoPE applied) and v in LDS
+//     and appends them to the paged cache;
+//   * wave w takes the 16-row blocks w, w + 8, ... (row = token j * G + head
+//     g): q with RoPE from the QKV rows, then every cached 64-position block
+//     of the split (K / V from the cache) and, in the last split, the new
+//     tokens from LDS under the causal mask (position base + i visible to
+//     token j iff i <= j), with an online softmax; its rows' (o, m, l) go to
+//     the split record;
+//   * the last split task to arrive merges the records of all rows.
+__device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  OpRef op = op_of(a, t.op);
+  constexpr int D = 128;
+  const int r = t.i0, h = t.i1, s = t.i2, S = op.splits;
+  const int G = op.num_q_heads / op.num_kv_heads;
+  const int wave = __builtin_amdgcn_readfirstlane(tix() / kWave), lane = tix() % kWave;
+  const BatchMeta& m = a.meta;
+  if (!wait_event(a, t, task_id, sm)) return;
+  const AttnGeom gm = attn_geom(m, op, r, s);
+  const int t0 = gm.t0, nt = gm.nt, pb = gm.pb, np = gm.np, base = gm.base, c0 = gm.c0, c1 = gm.c1;
+  const int R = nt * G;
+  if (R > op.rec_rows || (op.flags & (OPF_X_LL | OPF_OUT_LL)) || nt > XS_ELEMS / (2 * D)) {
+    if (tix() == 0) __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    signal_event(a, t);
+    return;
+  }
+  const bool last = s == S - 1;
+  const size_t tok_stride = (size_t)op.num_kv_heads * D;
+  const float scale = 1.4426950408889634f / sqrtf((float)D);
+  const size_t e_grp = (size_t)h * (G + 2) * D;  // this kv head's [q x G | k | v] columns of a qkv row
+  uint16_t* const knew = sm.xs;                  // [nt][D] new k (RoPE applied)
+  uint16_t* const vnew = sm.xs + (size_t)nt * D; // [nt][D] new v
+  if (last) {
+    for (int idx = tix(); idx < nt * 16; idx += PK_THREADS) {
+      const int i = idx / 16, c = idx % 16, cp = (c + 8) & 15;  // 8-dim chunk and its rotate-half partner
+      const uint16_t* row = op.x + (size_t)(t0 + i) * op.qkv_ld + e_grp;
+      const uint4 kx = ld_agent_u128(row + (size_t)G * D + 8 * c);
+      const uint4 kp = ld_agent_u128(row + (size_t)G * D + 8 * cp);
+      const uint4 vv = ld_agent_u128(row + (size_t)(G + 1) * D + 8 * c);
+      uint4 kr = kx;
+      if (op.cos_t) {
+        const int pos = base + i;
+        const uint4 cv = ldg16(op.cos_t + (size_t)pos * D + 8 * c), sv = ldg16(op.sin_t + (size_t)pos * D + 8 * c);
+        const uint32_t xv[4] = {kx.x, kx.y, kx.z, kx.w}, yv[4] = {kp.x, kp.y, kp.z, kp.w};
+        const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
+        const float sg = c < 8 ? -1.f : 1.f;  // first half: x cos - x[d + D/2] sin
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float lo = lo16<DT_BF16>(xv[e]) * lo16<DT_BF16>(cw[e]) + sg * lo16<DT_BF16>(yv[e]) * lo16<DT_BF16>(sw[e]);
+          const float hi = hi16<DT_BF16>(xv[e]) * hi16<DT_BF16>(cw[e]) + sg * hi16<DT_BF16>(yv[e]) * hi16<DT_BF16>(sw[e]);
+          o[e] = pack2<DT_BF16>(lo, hi);
+        }
+        kr = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+      *reinterpret_cast<uint4*>(knew + (size_t)i * D + 8 * c) = kr;
+      *reinterpret_cast<uint4*>(vnew + (size_t)i * D + 8 * c) = vv;
+      const int pos = base + i;
+      const int pg = m.kv_indices[pb + pos / kPage];
+      const size_t ce = ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D + 8 * c;
+      *reinterpret_cast<uint4*>(op.k_cache + ce) = kr;
+      *reinterpret_cast<uint4*>(op.v_cache + ce) = vv;
+    }
+  }
+  lds_sync();  // new k / v staged
+
+  const int rec_floats = op.rec_rows * (D + 2);
+  float* const rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * rec_floats;
+  float* const rec = rec_base + (size_t)s * rec_floats;
+  const int nblk = (c1 - c0 + 63) / 64;
+  const int RB = (R + 15) / 16;
+  float* const pw = &sm.attn_p[wave][0][0];   // P of this wave's row block [16][64]
+  float* const aw = &sm.attn_ml[wave][0][0];  // per-row rescale factors [16][2]
+  for (int rb = wave; rb < RB; rb += PK_WAVES) {
+    // q of rows 16 rb + lane % 16 (MFMA A operand: 8 dims 32 q + 8 (lane / 16) per chunk), RoPE at base + j
+    uint4 qf[4];
+    {
+      const int row = 16 * rb + lane % 16;
+      const bool ok = row < R;
+      const int j = ok ? row / G : 0, g = row % G;
+      const uint16_t* src = op.x + (size_t)(t0 + j) * op.qkv_ld + e_grp + (size_t)g * D + (lane / 16) * 8;
+      RopeVec qv;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        qv.x[q] = ok ? ld_agent_u128(src + 32 * q) : make_uint4(0, 0, 0, 0);
+        if (op.cos_t) {
+          const size_t pe = (size_t)(base + j) * D + 32 * q + (lane / 16) * 8;
+          qv.c[q] = ldg16(op.cos_t + pe);
+          qv.s[q] = ldg16(op.sin_t + pe);
+        }
+      }
+      rope_apply(qv, qf, op);
+    }
+    float m_i[4], l_i[4], o_acc[16][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) { m_i[i] = -INFINITY; l_i[i] = 0.f; }
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) o_acc[rr][e] = 0.f;
+    // one 64-position block: scores on MFMA against the K fragments (token
+    // 16 jb + lane % 16), online softmax (P and the row rescale through
+    // LDS), then P V on VALU against the V rows (token lane / 16 + 4 i2)
+    auto block = [&](const uint4 (&kf)[4][4], const uint4 (&vf)[16], int npos, bool causal_new, int coff)
+                     __attribute__((always_inline)) {
+      f32x4 sc[4];
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; q++) c = mfma_bf16(qf[q], kf[jb][q], c);
+        sc[jb] = c;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int rloc = 4 * (lane / 16) + i, row = 16 * rb + rloc;
+        const int tj = row / G;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+          const int pl = 16 * jb + lane % 16;
+          const bool vis = pl < npos && row < R && (!causal_new || coff + pl <= tj);
+          const float v = vis ? sc[jb][i] * scale : -INFINITY;
+          sc[jb][i] = v;
+          mx = fmaxf(mx, v);
+        }
+#pragma unroll
+        for (int o2 = 8; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, kWave));
+        const float mnew = fmaxf(m_i[i], mx);
+        const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[i] - mnew);
+        float ls = 0.f;
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+          const float p = mnew == -INFINITY ? 0.f : exp2f(sc[jb][i] - mnew);
+          ls += p;
+          pw[rloc * 64 + 16 * jb + lane % 16] = p;
+        }
+#pragma unroll
+        for (int o2 = 8; o2 > 0; o2 >>= 1) ls += __shfl_xor(ls, o2, kWave);
+        l_i[i] = l_i[i] * alpha + ls;
+        m_i[i] = mnew;
+        if ((lane % 16) == 0) aw[rloc * 2] = alpha;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int rr = 0; rr < 16; rr++) {
+        const float al = aw[rr * 2];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o_acc[rr][e] *= al;
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < 16; i2++) {
+        const int pl = lane / 16 + 4 * i2;
+        const uint32_t vw[4] = {vf[i2].x, vf[i2].y, vf[i2].z, vf[i2].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[2 * e] = lo16<DT_BF16>(vw[e]);
+          v[2 * e + 1] = hi16<DT_BF16>(vw[e]);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 16; rr++) {
+          const float p = pw[rr * 64 + pl];
+#pragma unroll
+          for (int e = 0; e < 8; e++) o_acc[rr][e] = fmaf(p, v[e], o_acc[rr][e]);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    };
+    // cached positions [c0, c1) of this split
+    for (int blk = 0; blk < nblk; blk++) {
+      const int p0 = c0 + blk * 64, plast = c1 - 1;
+      uint4 kf[4][4], vf[16];
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++) {
+        const int p = min(p0 + 16 * jb + lane % 16, plast);
+        const int pg = m.kv_indices[pb + p / kPage];
+        const uint16_t* src = op.k_cache + ((size_t)pg * kPage + p % kPage) * tok_stride + (size_t)h * D + (lane / 16) * 8;
+#pragma unroll
+        for (int q = 0; q < 4; q++) kf[jb][q] = ldg16(src + 32 * q);
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < 16; i2++) {
+        const int p = min(p0 + lane / 16 + 4 * i2, plast);
+        const int pg = m.kv_indices[pb + p / kPage];
+        vf[i2] = ldg16(op.v_cache + ((size_t)pg * kPage + p % kPage) * tok_stride + (size_t)h * D + (lane % 16) * 8);
+      }
+      const int npos = c1 - p0 < 64 ? c1 - p0 : 64;
+      block(kf, vf, npos, false, 0);
+    }
+    // the new tokens (last split), 64 at a time, from LDS
+    if (last) {
+      for (int n0 = 0; n0 < nt; n0 += 64) {
+        uint4 kf[4][4], vf[16];
+        const int ilast = nt - 1;
+#pragma unroll
+        for (int jb = 0; jb < 4; jb++) {
+          const int i = min(n0 + 16 * jb + lane % 16, ilast);
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            kf[jb][q] = *reinterpret_cast<const uint4*>(knew + (size_t)i * D + 32 * q + (lane / 16) * 8);
+        }
+#pragma unroll
+        for (int i2 = 0; i2 < 16; i2++) {
+          const int i = min(n0 + lane / 16 + 4 * i2, ilast);
+          vf[i2] = *reinterpret_cast<const uint4*>(vnew + (size_t)i * D + (lane % 16) * 8);
+        }
+        // causal: new position n0 + pl is visible to token tj iff n0 + pl <= tj
+        block(kf, vf, nt - n0 < 64 ? nt - n0 : 64, true, n0);
+      }
+    }
+    // rows' (o, m, l) into the split record: sum o over the 4 lane groups
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float x = o_acc[rr][e];
+        x += __shfl_xor(x, 16, kWave);
+        x += __shfl_xor(x, 32, kWave);
+        o_acc[rr][e] = x;
+      }
+    if (lane < 16) {
+#pragma unroll
+      for (int rr = 0; rr < 16; rr++) {
+        const int row = 16 * rb + rr;
+        if (row < R) {
+          float* dst = rec + (size_t)row * (D + 2) + lane * 8;
+          st_agent4(dst, make_float4(o_acc[rr][0], o_acc[rr][1], o_acc[rr][2], o_acc[rr][3]));
+          st_agent4(dst + 4, make_float4(o_acc[rr][4], o_acc[rr][5], o_acc[rr][6], o_acc[rr][7]));
+        }
+      }
+    }
+    if ((lane % 16) == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = 16 * rb + 4 * (lane / 16) + i;
+        if (row < R) {
+          st_agent(rec + (size_t)row * (D + 2) + D, m_i[i]);
+          st_agent(rec + (size_t)row * (D + 2) + D + 1, l_i[i]);
+        }
+      }
+    }
+  }
+  // the last split task to arrive merges every row's S records
+  if (arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S)) {
+    for (int idx = tix(); idx < R * (D / 4); idx += PK_THREADS) {
+      const int rr = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+      float M = -INFINITY, L = 0.f;
+      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int s2 = 0; s2 < S; s2++) {
+        const float* rc = rec_base + (size_t)s2 * rec_floats + (size_t)rr * (D + 2);
+        const float ms = ld_agent(rc + D);
+        if (ms == -INFINITY) continue;
+        const float ls = ld_agent(rc + D + 1);
+        const float4 os = ld_agent4(rc + d4);
+        const float mn = fmaxf(M, ms);
+        const float fa = M == -INFINITY ? 0.f : exp2f(M - mn), fb = exp2f(ms - mn);
+        L = L * fa + ls * fb;
+        O.x = O.x * fa + os.x * fb; O.y = O.y * fa + os.y * fb;
+        O.z = O.z * fa + os.z * fb; O.w = O.w * fa + os.w * fb;
+        M = mn;
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const int jt = rr / G, g = rr % G;
+      const size_t oe = (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
+      const uint32_t lo = pack2<DT_BF16>(O.x * inv, O.y * inv), hi = pack2<DT_BF16>(O.z * inv, O.w * inv);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(op.out + oe), (uint64_t)lo | ((uint64_t)hi << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  signal_event(a, t);
 }
 
 // ------------------------------------------------------------ batch manager
@@ -1609,6 +1891,11 @@ __device__ __attribute__((noinline)) void run_attention_large(int slot, int tid)
   const TaskDesc t = task_at(slot);
   task_attention_body<16>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), slot, g_sm);
 }
+// prefill / extend rows (nt * G > 16): out of line for the same reason
+__device__ __attribute__((noinline)) void run_attention_mt(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_attention_mt(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
 __device__ __forceinline__ void run_embed(int slot, int tid) {
   const TaskDesc t = task_at(slot);
   task_embed(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
@@ -1684,7 +1971,13 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
           const int r = sm.tq[slot].i0;
           small = (a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r]) * G <= 4;
         }
-        if (small) run_attention<4>(slot, tid); else run_attention_large(slot, tid);
+        if (small) {
+          run_attention<4>(slot, tid);
+        } else {
+          const int r = sm.tq[slot].i0;
+          const int nt = a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r];
+          if (nt * G > 16) run_attention_mt(slot, tid); else run_attention_large(slot, tid);
+        }
         break;
       }
       case TASK_PREPARE_BATCH: run_prepare(slot, tid); break;
@@ -1911,8 +2204,8 @@ int yr_pk_status(yr_pk_handle* hp, int* status4) {
   if (e != hipSuccess) return check_hip(e, "yr_pk_status");
   if (status4[0]) return fail(YR_E_TIMEOUT, "persistent kernel watchdog fired waiting in task %d", status4[2]);
   if (status4[3])
-    return fail(YR_E_INVALID, "attention task %d: more than 16 query rows per kv head or 512 positions per split",
-                status4[3] - 1);
+    return fail(YR_E_INVALID, "attention task %d: query rows per kv head beyond the op's split records, or more "
+                "cached positions than the split's block budget", status4[3] - 1);
   return YR_OK;
 }
 

@@ -55,7 +55,7 @@ struct OpDesc {
   int scratch_off;    // float offset of this op's scratch records
   int x_src;          // op that wrote x (OPF_X_LL)
   int res_src;        // op that wrote the residual (OPF_RES_LL)
-  int pad0;
+  int rec_rows;       // attention: query rows per split record (>= 16, max_tokens * G rounded up)
   const uint16_t* x;        // activations in
   const uint16_t* norm;     // RMSNorm weight
   uint16_t* out;            // activations out (column 0 of the op)

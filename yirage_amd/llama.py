@@ -85,12 +85,28 @@ def page_table(batch: int, kv_len: int, page: int, seed: int):
 
 
 class LlamaDecodeModel:
-    """Random-init weights + KV cache on the device and a PersistentKernel
-    running one decode step (batch rows = requests, one new token each)."""
+    """Random-init weights + KV cache on the device and a PersistentKernel.
 
-    def __init__(self, cfg: LlamaConfig, batch: int, kv_len: int, page_size: int = 64, seed: int = 0,
-                 num_workers: int | None = None, with_prepare: bool = False, device="cuda"):
+    Decode mode (prompts=None): `batch` requests of one new token each over a
+    KV cache prefilled to kv_len positions; every launch repeats that step.
+
+    Serving mode (prompts = list of token-id lists, with_prepare=True): the
+    offline batch manager of the reference (prepare_next_batch,
+    persistent_kernel.cuh:169-322) runs as the graph's last task and schedules
+    prefill chunks and decode steps of the requests over max_requests slots
+    and max_tokens rows per launch, allocating KV pages from a FIFO queue."""
+
+    def __init__(self, cfg: LlamaConfig, batch: int, kv_len: int = 0, page_size: int = 64, seed: int = 0,
+                 num_workers: int | None = None, with_prepare: bool = False, device="cuda", prompts=None,
+                 max_tokens: int | None = None, max_requests: int | None = None, max_seq: int | None = None,
+                 eos_token_id: int = -1):
         self.cfg, self.batch, self.kv_len, self.page, self.seed = cfg, batch, kv_len, page_size, seed
+        self.MR = max_requests or batch
+        self.MT = max_tokens or batch
+        self.eos = eos_token_id
+        serving = prompts is not None
+        if serving and not with_prepare:
+            raise ValueError("serving mode needs the batch manager (with_prepare=True)")
         dev = torch.device(device)
         self.graph_only = dev.type == "meta"   # build/verify the task graph without a GPU
         fill = (lambda t, seed, std: t) if self.graph_only else fused.synth_fill
@@ -111,42 +127,70 @@ class LlamaDecodeModel:
         self.lm_head = fill(torch.empty((cfg.vocab, H), dtype=bf, device=dev), tensor_seed(seed, 0, "lm_head"),
                             cfg.weight_std)
         self.final_norm = torch.ones(H, dtype=bf, device=dev)
-        # paged KV cache, prefilled
-        indptr, indices, pool = page_table(batch, kv_len, page_size, seed + 7)
+        if serving:
+            self.max_seq = max_seq or (max(len(p) for p in prompts) + 16)
+            npg = (self.max_seq + page_size - 1) // page_size
+            pool = self.MR * npg
+            indptr = np.zeros(self.MR + 1, np.int32)
+            indices = np.zeros(pool, np.int32)
+        else:
+            indptr, indices, pool = page_table(batch, kv_len, page_size, seed + 7)
+            self.max_seq = kv_len + 8
+        # paged KV cache (prefilled with ~N(0, 1) in decode mode; in serving
+        # mode every position is written before it is read)
         self.max_pages = pool
         self.kc, self.vc = [], []
         for layer in range(cfg.num_layers):
             shp = (pool, page_size, cfg.num_kv_heads, cfg.head_dim)
             self.kc.append(fill(torch.empty(shp, dtype=bf, device=dev), tensor_seed(seed, layer, "kc"), 1.0))
             self.vc.append(fill(torch.empty(shp, dtype=bf, device=dev), tensor_seed(seed, layer, "vc"), 1.0))
-        cos, sin = rope_tables(max(kv_len + 8, 64), cfg.head_dim, cfg.rope_theta)
+        cos, sin = rope_tables(max(self.max_seq, 64), cfg.head_dim, cfg.rope_theta)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
         # meta tensors (python/yirage/persistent_kernel.py:268-279)
-        self.max_seq = kv_len + 8
-        lpl = kv_len % page_size
-        self.meta = {
-            "step": torch.full((batch,), kv_len - 1, dtype=torch.int32, device=dev),
-            "tokens": torch.zeros((batch, self.max_seq), dtype=torch.int64, device=dev),
-            "input_tokens": torch.zeros((8, 1), dtype=torch.int64, device=dev),
-            "output_tokens": torch.zeros((8, 1), dtype=torch.int64, device=dev),
-            "num_new_tokens": torch.ones((batch,), dtype=torch.int32, device=dev),
-            "prompt_lengths": torch.full((batch,), kv_len - 1, dtype=torch.int32, device=dev),
-            "qo_indptr_buffer": torch.arange(batch + 1, dtype=torch.int32, device=dev),
-            "paged_kv_indptr_buffer": torch.from_numpy(indptr).to(dev),
-            "paged_kv_indices_buffer": torch.from_numpy(indices).to(dev),
-            "paged_kv_last_page_len_buffer": torch.full((batch,), lpl, dtype=torch.int32, device=dev),
-        }
+        i32, i64 = torch.int32, torch.int64
+        if serving:
+            R = len(prompts)
+            tokens = torch.zeros((R, self.max_seq), dtype=i64)
+            for i, p in enumerate(prompts):
+                tokens[i, :len(p)] = torch.as_tensor(p, dtype=i64)
+            self.meta = {
+                "step": torch.zeros((R,), dtype=i32, device=dev),
+                "tokens": tokens.to(dev),
+                "input_tokens": torch.zeros((self.MT, 1), dtype=i64, device=dev),
+                "output_tokens": torch.zeros((self.MT, 1), dtype=i64, device=dev),
+                "num_new_tokens": torch.zeros((R,), dtype=i32, device=dev),
+                "prompt_lengths": torch.tensor([len(p) for p in prompts], dtype=i32, device=dev),
+                "qo_indptr_buffer": torch.zeros(self.MR + 1, dtype=i32, device=dev),
+                "paged_kv_indptr_buffer": torch.zeros(self.MR + 1, dtype=i32, device=dev),
+                "paged_kv_indices_buffer": torch.zeros(pool, dtype=i32, device=dev),
+                "paged_kv_last_page_len_buffer": torch.zeros(self.MR, dtype=i32, device=dev),
+            }
+        else:
+            lpl = kv_len % page_size
+            self.meta = {
+                "step": torch.full((batch,), kv_len - 1, dtype=i32, device=dev),
+                "tokens": torch.zeros((batch, self.max_seq), dtype=i64, device=dev),
+                "input_tokens": torch.zeros((max(8, self.MT), 1), dtype=i64, device=dev),
+                "output_tokens": torch.zeros((max(8, self.MT), 1), dtype=i64, device=dev),
+                "num_new_tokens": torch.ones((batch,), dtype=i32, device=dev),
+                "prompt_lengths": torch.full((batch,), kv_len - 1, dtype=i32, device=dev),
+                "qo_indptr_buffer": torch.arange(batch + 1, dtype=i32, device=dev),
+                "paged_kv_indptr_buffer": torch.from_numpy(indptr).to(dev),
+                "paged_kv_indices_buffer": torch.from_numpy(indices).to(dev),
+                "paged_kv_last_page_len_buffer": torch.full((batch,), lpl, dtype=i32, device=dev),
+            }
         self.page_indptr, self.page_indices = indptr, indices
         self.pk = self._build(num_workers, with_prepare)
 
     def _build(self, num_workers, with_prepare):
-        cfg, B = self.cfg, self.batch
+        cfg, B = self.cfg, self.MT  # activation rows = tokens per launch
         if num_workers is None:
             num_workers = 256 if self.graph_only else torch.cuda.get_device_properties(0).multi_processor_count
         pk = PersistentKernel(mode="offline", world_size=1, mpi_rank=0, num_workers=num_workers,
                               num_local_schedulers=0, num_remote_schedulers=0, max_seq_length=self.max_seq,
-                              max_num_batched_requests=B, max_num_batched_tokens=B, max_num_pages=self.max_pages,
-                              page_size=self.page, eos_token_id=-1, meta_tensors=self.meta)
+                              max_num_batched_requests=self.MR, max_num_batched_tokens=self.MT,
+                              max_num_pages=self.max_pages, page_size=self.page, eos_token_id=self.eos,
+                              meta_tensors=self.meta)
         pk.vocab_size = cfg.vocab
         H = cfg.hidden
         x = pk.attach_input(self.meta["input_tokens"], name="input_token")
@@ -183,7 +227,7 @@ class LlamaDecodeModel:
             vc = pk.attach_input(self.vc[i], name=f"layer_{i}_v_cache")
             pk.paged_attention_layer(input=t["attn_in"], k_cache=kc, v_cache=vc, q_norm=None, k_norm=None,
                                      cos_pos_embed=cos, sin_pos_embed=sin, output=t["attn_out"],
-                                     grid_dim=(B, cfg.num_kv_heads, 1), block_dim=(128, 1, 1))
+                                     grid_dim=(self.MR, cfg.num_kv_heads, 1), block_dim=(128, 1, 1))
             wo = pk.attach_input(lw["wo"], name=f"layer_{i}_o_proj")
             pk.linear_with_residual_layer(input=t["attn_out"], weight=wo, residual=h, output=t["attn_proj_out"],
                                           grid_dim=(H // 64, 1, 1), block_dim=(128, 1, 1))
