@@ -40,10 +40,7 @@ static int dtype_bytes(int dt) {
   return 0;
 }
 
-struct Seg {
-  int tensor;
-  int64_t row0, rows;
-};
+using Seg = WSeg;
 
 static std::vector<Seg> read_segments(Graph& g, const json::Value& v) {
   std::vector<Seg> segs;
@@ -205,6 +202,9 @@ void Graph::build(const char* text) {
         add_task(td);
       }
       info.writes.push_back({out, 0, d.N, 1});
+      info.tok = tok;
+      info.table = tab;
+      info.out = out;
     } else if (type == "linear" || type == "rmsnorm_linear" || type == "rmsnorm_linear_silu" ||
                type == "rmsnorm_linear_argmax") {
       bool norm = type != "linear";
@@ -298,6 +298,14 @@ void Graph::build(const char* text) {
       }
       info.reads.push_back({x, 0, d.K});
       info.writes.push_back({out, col0, col0 + d.N, 1});
+      info.x = x;
+      info.out = out;
+      info.res = res;
+      info.norm = norm ? ptr_tensor(*this, o, "norm") : -1;
+      info.tok_out = amax ? ptr_tensor(*this, o, "tokens_out") : -1;
+      info.wsegs = segs;
+      info.group = group;
+      info.col0 = col0;
       if (OT.ll) {
         d.flags |= OPF_OUT_LL;
         link_writer[out] = (int)ops.size();
@@ -368,6 +376,12 @@ void Graph::build(const char* text) {
           }
       info.reads.push_back({qkv, 0, d.qkv_ld, 2});
       info.writes.push_back({out, 0, d.num_q_heads * d.head_dim, 2});
+      info.x = qkv;
+      info.out = out;
+      info.kc = kc;
+      info.vc = vc;
+      info.cos = ct;
+      info.sin = st;
       info.kv_group_width = (G + 2) * d.head_dim;
       info.kv_groups = d.num_kv_heads;
       info.group_reads_qkv = qkv;
@@ -619,38 +633,146 @@ std::string Graph::check_races(int window) const {
 // ------------------------------------------------------------------ export
 // Task graph in the reference's JSON vocabulary (runtime.cc:847-1318):
 // all_tasks / all_events / first_tasks.
+// The task graph in the reference's task_graph.json schema
+// (src/kernel/runtime.cc:847-1318): all_tasks[0] = TASK_TERMINATE,
+// all_tasks[1] = TASK_BEGIN_TASK_GRAPH, then one entry per task with the
+// reference's task type code, variant_id, inputs / outputs as {base_ptr
+// (tensor name), offset (bytes), data_type, dims, strides}, trigger_event,
+// dependent_event, request_id, expert_offset; all_events with event_type,
+// num_triggers and the [first_task_id, last_task_id) range of the tasks the
+// event launches; first_tasks.  Fused tasks of this backend use the code of
+// the reference task they extend with a variant: TASK_RMS_NORM_LINEAR (102)
+// variant 0 plain, 1 with the silu_mul epilogue over [gate | up] rows, 2 with
+// the argmax_partial / argmax_reduce epilogue.  The offline batch manager,
+// which the reference runs between iterations rather than as a task, is
+// written as task type 1000.  Each task also carries "yr" = {op, split} (its
+// op index, attention split and [gate | up] row group), which the
+// reference's loader ignores.
+namespace {
+constexpr unsigned long long kEventInvalid = 0x7ffffffffffffffeull;
+constexpr int kRefTerminate = 0, kRefBegin = 10, kRefEmbedding = 101, kRefRmsNormLinear = 102,
+              kRefLinearResidual = 108, kRefPagedAttention = 116, kRefLinear = 120, kRefPrepareBatch = 1000;
+constexpr int kRefEventLaunch = 901;
+
+struct IoOut {
+  std::ostringstream& os;
+  bool first = true;
+  void add(const Tensor& t, int64_t elem_off, std::vector<int64_t> dims, std::vector<int64_t> strides) {
+    os << (first ? "" : ",") << "{\"base_ptr\":\"" << t.name << "\",\"offset\":" << elem_off * dtype_bytes(t.dtype)
+       << ",\"data_type\":" << t.dtype << ",\"dims\":[";
+    for (size_t i = 0; i < dims.size(); i++) os << (i ? "," : "") << dims[i];
+    os << "],\"strides\":[";
+    for (size_t i = 0; i < strides.size(); i++) os << (i ? "," : "") << strides[i];
+    os << "]}";
+    first = false;
+  }
+};
+
+// pieces of virtual weight rows [r, r + n): (segment, row in its tensor, rows)
+std::vector<WSeg> seg_pieces(const std::vector<WSeg>& segs, int64_t r, int64_t n) {
+  std::vector<WSeg> out;
+  int64_t base = 0;
+  for (auto& s : segs) {
+    const int64_t lo = std::max(r, base), hi = std::min(r + n, base + s.rows);
+    if (lo < hi) out.push_back({s.tensor, s.row0 + (lo - base), hi - lo});
+    base += s.rows;
+  }
+  return out;
+}
+}  // namespace
+
 std::string Graph::export_json() const {
-  static const char* names[] = {"nop", "embedding", "linear", "rmsnorm_linear", "rmsnorm_linear_silu_mul",
-                                "paged_attention", "rmsnorm_linear_argmax", "prepare_next_batch"};
   std::ostringstream os;
+  const int64_t T = cfg.max_tokens;
   os << "{\"all_tasks\":[";
+  os << "{\"task_type\":" << kRefTerminate << ",\"variant_id\":0,\"inputs\":[],\"outputs\":[],\"trigger_event\":"
+     << kEventInvalid << ",\"dependent_event\":" << kEventInvalid << ",\"request_id\":-1,\"expert_offset\":-1},";
+  os << "{\"task_type\":" << kRefBegin << ",\"variant_id\":0,\"inputs\":[],\"outputs\":[],\"trigger_event\":"
+     << kEventInvalid << ",\"dependent_event\":" << kEventInvalid << ",\"request_id\":-1,\"expert_offset\":-1}";
   for (size_t i = 0; i < tasks.size(); i++) {
     const TaskDesc& t = tasks[i];
-    if (i) os << ",";
-    os << "{\"task_type\":\"" << names[ops[t.op].type] << "\",\"op\":" << t.op << ",\"trigger_event\":"
-       << t.trigger_event << ",\"dependent_event\":" << t.wait_event << ",\"row0\":" << t.row0 << ",\"rows\":" << t.rows
-       << ",\"request_id\":" << (ops[t.op].type == TASK_ATTENTION ? t.i0 : -1) << "}";
+    const OpDesc& d = ops[t.op];
+    const OpInfo& inf = op_info[t.op];
+    int code = 0, variant = 0;
+    std::ostringstream ins, outs;
+    IoOut I{ins}, Ot{outs};
+    switch (d.type) {
+      case TASK_EMBED: {
+        code = kRefEmbedding;
+        const Tensor& tab = tensors[inf.table];
+        I.add(tensors[inf.tok], 0, {T, 1}, {1, 1});
+        I.add(tab, t.row0, {tab.dims[0], t.rows}, {tab.dims[1], 1});
+        Ot.add(tensors[inf.out], t.row0, {T, t.rows}, {tensors[inf.out].dims[1], 1});
+        break;
+      }
+      case TASK_LINEAR:
+      case TASK_RMSNORM_LINEAR:
+      case TASK_RMSNORM_LINEAR_SILU:
+      case TASK_RMSNORM_LINEAR_ARGMAX: {
+        code = d.type == TASK_LINEAR ? (inf.res >= 0 ? kRefLinearResidual : kRefLinear) : kRefRmsNormLinear;
+        variant = d.type == TASK_RMSNORM_LINEAR_SILU ? 1 : d.type == TASK_RMSNORM_LINEAR_ARGMAX ? 2 : 0;
+        I.add(tensors[inf.x], 0, {T, d.K}, {d.K, 1});
+        std::vector<WSeg> pieces;
+        if (d.type == TASK_RMSNORM_LINEAR_SILU) {
+          const int64_t g = inf.group, gi = t.row0 / g, j = t.row0 % g;
+          for (auto& p : seg_pieces(inf.wsegs, gi * 2 * g + j, t.rows)) pieces.push_back(p);
+          for (auto& p : seg_pieces(inf.wsegs, gi * 2 * g + g + j, t.rows)) pieces.push_back(p);
+        } else {
+          pieces = seg_pieces(inf.wsegs, t.row0, t.rows);
+        }
+        for (auto& p : pieces) I.add(tensors[p.tensor], p.row0 * d.K, {p.rows, d.K}, {d.K, 1});
+        if (inf.norm >= 0) I.add(tensors[inf.norm], 0, {d.K}, {1});
+        if (inf.res >= 0) I.add(tensors[inf.res], t.row0, {T, t.rows}, {d.res_ld, 1});
+        const Tensor& ot = tensors[inf.out];
+        Ot.add(ot, inf.col0 + t.row0, {T, t.rows}, {ot.dims[1], 1});
+        if (inf.tok_out >= 0) Ot.add(tensors[inf.tok_out], 0, {T, 1}, {1, 1});
+        break;
+      }
+      case TASK_ATTENTION: {
+        code = kRefPagedAttention;
+        const int G = d.num_q_heads / d.num_kv_heads, D = d.head_dim, h = t.i1;
+        I.add(tensors[inf.x], (int64_t)h * (G + 2) * D, {T, (int64_t)(G + 2) * D}, {d.qkv_ld, 1});
+        for (int c : {inf.kc, inf.vc}) {
+          const Tensor& ct = tensors[c];
+          I.add(ct, 0, ct.dims, {ct.dims[1] * ct.dims[2] * ct.dims[3], ct.dims[2] * ct.dims[3], ct.dims[3], 1});
+        }
+        for (int c : {inf.cos, inf.sin})
+          if (c >= 0) I.add(tensors[c], 0, tensors[c].dims, {tensors[c].dims[1], 1});
+        Ot.add(tensors[inf.out], (int64_t)h * G * D, {T, (int64_t)G * D}, {tensors[inf.out].dims[1], 1});
+        break;
+      }
+      case TASK_PREPARE_BATCH:
+        code = kRefPrepareBatch;
+        break;
+      default:
+        break;
+    }
+    os << ",{\"task_type\":" << code << ",\"variant_id\":" << variant << ",\"inputs\":[" << ins.str()
+       << "],\"outputs\":[" << outs.str() << "],\"trigger_event\":"
+       << (t.trigger_event >= 0 ? (unsigned long long)t.trigger_event : kEventInvalid) << ",\"dependent_event\":"
+       << (t.wait_event >= 0 ? (unsigned long long)t.wait_event : kEventInvalid)
+       << ",\"request_id\":" << (d.type == TASK_ATTENTION ? t.i0 : -1) << ",\"expert_offset\":-1,\"yr\":{\"op\":" << t.op
+       << ",\"split\":" << (d.type == TASK_ATTENTION ? t.i2 : 0) << ",\"group\":" << inf.group << "}}";
   }
   os << "],\"all_events\":[";
   for (size_t e = 0; e < events.size(); e++) {
-    if (e) os << ",";
     int first = -1, last = -1;
-    for (int t = op_info[events[e].consumer_op].first_task;
-         t < op_info[events[e].consumer_op].first_task + op_info[events[e].consumer_op].num_tasks; t++)
+    const OpInfo& ci = op_info[events[e].consumer_op];
+    for (int t = ci.first_task; t < ci.first_task + ci.num_tasks; t++)
       if (tasks[t].wait_event == (int)e) {
         if (first < 0) first = t;
         last = t;
       }
-    os << "{\"event_type\":\"EVENT_LAUNCH_TASKS\",\"num_triggers\":" << events[e].num_triggers
-       << ",\"first_task_id\":" << first << ",\"last_task_id\":" << last + 1 << "}";
+    os << (e ? "," : "") << "{\"event_type\":" << kRefEventLaunch << ",\"num_triggers\":" << events[e].num_triggers
+       << ",\"first_task_id\":" << (first < 0 ? -1 : first + 2) << ",\"last_task_id\":" << (last < 0 ? -1 : last + 3)
+       << "}";
   }
   os << "],\"first_tasks\":[";
-  bool firstw = true;
-  for (int t = 0; t < op_info[0].num_tasks; t++) {
-    os << (firstw ? "" : ",") << t;
-    firstw = false;
-  }
-  os << "],\"num_workers\":" << num_workers << "}";
+  for (int t = 0; t < op_info[0].num_tasks; t++) os << (t ? "," : "") << t + 2;
+  os << "],\"yr_config\":{\"num_workers\":" << num_workers << ",\"max_tokens\":" << cfg.max_tokens
+     << ",\"max_requests\":" << cfg.max_requests << ",\"page_size\":" << cfg.page_size << ",\"max_pages\":"
+     << cfg.max_pages << ",\"max_seq_len\":" << cfg.max_seq_len << ",\"total_requests\":" << cfg.total_requests
+     << ",\"eos_token_id\":" << cfg.eos_token_id << "}}";
   return os.str();
 }
 

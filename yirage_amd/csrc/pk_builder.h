@@ -36,11 +36,22 @@ struct Access {
   int scope = 0;
 };
 
+// A weight segment: rows [row0, row0 + rows) of tensor `tensor`.
+struct WSeg {
+  int tensor;
+  int64_t row0, rows;
+};
+
 struct OpInfo {
   std::string name;
   int first_task = 0, num_tasks = 0;
   std::vector<Access> reads, writes;
   int kv_group_width = 0, kv_groups = 0, group_reads_qkv = -1;
+  // operand tensors (-1: none), for the task-graph export
+  int x = -1, out = -1, res = -1, norm = -1, tok = -1, table = -1, tok_out = -1, kc = -1, vc = -1, cos = -1,
+      sin = -1;
+  std::vector<WSeg> wsegs;
+  int group = 0, col0 = 0;
 };
 
 struct EventInfo {

@@ -162,6 +162,16 @@ class PersistentKernel:
                     num_groups if shuffled else 1)
         return self._register(v)
 
+    def view_tensor(self, name: str, segments: list, group: int = 0, ngroups: int = 1) -> DTensor:
+        """A weight made of row pieces [(DTensor, row0, rows), ...] in order
+        (what fuse_tensors / shuffle_tensors produce), e.g. when a task graph
+        file lists the pieces each task reads."""
+        src = segments[0][0]
+        for t, r0, n in segments:
+            assert t.num_dims == 2 and t.dim(1) == src.dim(1) and 0 <= r0 and r0 + n <= t.dim(0)
+        rows = sum(n for _, _, n in segments)
+        return self._register(DTensor(name, (rows, src.dim(1)), src.dtype, None, list(segments), group, ngroups))
+
     def fuse_tensors(self, inputs: list, fused_dim: int, num_groups: int, name: str = None) -> DTensor:
         assert fused_dim == 0
         return self._view(inputs, num_groups, name, shuffled=False)
@@ -301,7 +311,9 @@ class PersistentKernel:
                 tm8 = self.max_num_batched_tokens > 1
                 max_rows = 16 if (tm8 and K > 4096) else None
                 if nxt and nxt["kind"] == "silu_mul" and nxt["input"] is l["output"]:
-                    if k != "rmsnorm_linear" or not w.segments or len(set(s.name for s, _, _ in w.segments)) != 2:
+                    two_src = w.segments and len(set(s.name for s, _, _ in w.segments)) == 2
+                    one_shuffled = w.segments and len(w.segments) == 1 and w.group > 0  # pre-shuffled [gate | up]
+                    if k != "rmsnorm_linear" or not (two_src or one_shuffled):
                         raise YirageHipError("hip backend: silu_mul must follow an rmsnorm+linear over shuffled "
                                              "[gate, up] weights")
                     op["type"] = "rmsnorm_linear_silu"
@@ -419,6 +431,8 @@ class PersistentKernel:
         if any(o["type"] == "prepare_batch" for o in self.ops):
             check(lib().yr_pk_init_batch(h, self._stream()), "init batch")
         self._is_compiled = True
+        if self.profiler_tensor is not None:
+            self.enable_profiler(tensor=self.profiler_tensor)
 
     def _stream(self):
         return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -427,12 +441,23 @@ class PersistentKernel:
         if not self._is_compiled:
             raise YirageHipError("PersistentKernel: call compile() first")
         check(lib().yr_pk_launch(self._handle, self._stream()), "persistent kernel launch")
+        if self.profiler_tensor is not None:
+            # as the reference does after every launch (persistent_kernel.py:1322-1337)
+            name = (self.trace_name or f"yirage_{self.mpi_rank}") + ".perfetto-trace"
+            self.export_trace(name)
 
-    def enable_profiler(self, enable: bool = True):
-        """Per-task device timestamps; read them with profile()."""
+    def enable_profiler(self, enable: bool = True, tensor: torch.Tensor | None = None):
+        """Per-task device timestamps (into `tensor`, int64 / uint64 with at
+        least tasks x 8 entries, or a buffer allocated here); read them with
+        profile() or export_trace()."""
         if enable:
             n = self.graph_info()["tasks"] * 8
-            self._prof = torch.zeros(n, dtype=torch.int64, device="cuda")
+            if tensor is None:
+                tensor = torch.zeros(n, dtype=torch.int64, device="cuda")
+            if tensor.dtype not in (torch.int64, torch.uint64) or tensor.numel() < n or not tensor.is_contiguous():
+                raise YirageHipError(f"profiler tensor must be a contiguous int64 tensor of >= {n} entries")
+            tensor.zero_()
+            self._prof = tensor
             check(lib().yr_pk_set_profiler(self._handle, ctypes.c_void_p(self._prof.data_ptr()), n), "profiler")
         else:
             check(lib().yr_pk_set_profiler(self._handle, None, 0), "profiler")
@@ -441,18 +466,27 @@ class PersistentKernel:
     def profile(self):
         """[tasks, 8] int64 numpy array (10 ns ticks): start, inputs ready, end, worker,
         activations staged, compute done, outputs published (GEMV tasks), 0."""
-        return self._prof.view(-1, 8).cpu().numpy()
+        n = self.graph_info()["tasks"] * 8
+        return self._prof.view(-1)[:n].view(-1, 8).cpu().numpy()
+
+    def export_trace(self, file_name: str) -> int:
+        """The last launch's per-task profile as a Perfetto trace (one track
+        per worker, one slice per task); returns the number of slices."""
+        from .profiler import export_to_perfetto_trace
+        return export_to_perfetto_trace(self.profile(), file_name, self.task_table())
 
     def task_table(self):
         """[tasks, 10] int64: op, type, wait event, wait count, trigger event, row0, rows, i0, i1, i2."""
-        n = self.graph_info()["tasks"]
-        rec = (ctypes.c_int64 * 10)()
-        import numpy as np
-        out = np.zeros((n, 10), np.int64)
-        for t in range(n):
-            check(lib().yr_pk_graph_task(self._graph, t, rec, 10), "task")
-            out[t] = list(rec)
-        return out
+        if getattr(self, "_task_table", None) is None:
+            n = self.graph_info()["tasks"]
+            rec = (ctypes.c_int64 * 10)()
+            import numpy as np
+            out = np.zeros((n, 10), np.int64)
+            for t in range(n):
+                check(lib().yr_pk_graph_task(self._graph, t, rec, 10), "task")
+                out[t] = list(rec)
+            self._task_table = out
+        return self._task_table.copy()
 
     def status(self):
         st = (ctypes.c_int * 4)()
@@ -465,7 +499,14 @@ class PersistentKernel:
         keys = ("ops", "tasks", "events", "workers", "tickets", "scratch_floats", "max_queue")
         return dict(zip(keys, list(info)[:7]))
 
+    def load_task_graph(self, graph, tensors: dict):
+        """Record the layers of a task_graph.json (the reference's schema,
+        src/kernel/runtime.cc:847-1318) on this kernel; compile() next."""
+        from .task_graph import load_task_graph
+        return load_task_graph(graph, self, tensors)
+
     def export_task_graph(self) -> str:
+        """The compiled task graph in the reference's task_graph.json schema."""
         need = ctypes.c_size_t()
         check(lib().yr_pk_graph_export_json(self._graph, None, 0, ctypes.byref(need)), "export")
         buf = ctypes.create_string_buffer(need.value)
