@@ -127,7 +127,7 @@ def cpu_baseline(sample_layers: int = 2):
     from oracle import oracle as O
     from yirage_amd.llama import LLAMA3_8B as cfg, page_table, rope_tables, tensor_seed, weight_shapes
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = os.cpu_count() or 1
     O.set_num_threads(threads)
     bf = "bf16"
     G, D, kv_len, page = cfg.num_q_heads // cfg.num_kv_heads, cfg.head_dim, 4096, 64
@@ -165,9 +165,24 @@ def cpu_baseline(sample_layers: int = 2):
     O.argmax(logits)
     t_lm = time.perf_counter() - t0
     step_ms = (elapsed / sample_layers * cfg.num_layers + t_lm) * 1e3
+    import torch
+
     return dict(value=round(step_ms, 2), unit="ms", cores=threads, kind="port",
                 sample=f"{sample_layers} of 32 decoder layers + LM head/argmax at batch 1 (kv 4096), "
-                       f"layer time scaled x32; weight generation excluded")
+                       f"layer time scaled x32; weight generation excluded",
+                os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(), cpu_model=_cpu_model())
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -212,6 +227,9 @@ def main():
     step_bytes = model.weight_bytes() + model.kv_bytes()
     achieved = step_bytes / ms / 1e6
     info = model.pk.graph_info()
+    # release device resources explicitly (not from __del__ at interpreter
+    # shutdown, after a profiler may have torn down the runtime)
+    model.pk.finalize()
     del model
     torch.cuda.empty_cache()
 
@@ -226,10 +244,15 @@ def main():
         extra["decode_b8"] = dict(ms=round(ms8, 4), gbs=round(b8 / ms8 / 1e6, 1),
                                   frac_hbm=round(b8 / ms8 / 1e6 / HBM_PEAK_GBS, 4),
                                   tokens_per_s=round(8 / ms8 * 1e3, 1))
+        m8.pk.finalize()
         del m8
         torch.cuda.empty_cache()
     if not args.no_fused:
+        import yirage_amd.fused as F
+
         extra["fused_ops"] = bench_fused(torch)
+        torch.cuda.synchronize()
+        F._ws_cache.clear()
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
