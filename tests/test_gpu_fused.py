@@ -39,7 +39,8 @@ def _close(got: torch.Tensor, ref: np.ndarray, what: str):
 
 @pytest.mark.parametrize("B,K,N,layout", [(8, 4096, 4096, 1), (3, 1024, 776, 1), (1, 4096, 4096, 0),
                                           (8, 4096, 6144, 0), (5, 14336, 4096, 0), (20, 512, 256, 1),
-                                          (37, 1024, 200, 1), (128, 4096, 4096, 1)])
+                                          (37, 1024, 200, 1), (128, 4096, 4096, 1), (128, 4096, 4096, 0),
+                                          (45, 1000, 264, 0)])
 def test_rmsnorm_linear(B, K, N, layout):
     import yirage_amd.fused as F
 
@@ -73,7 +74,8 @@ def test_rmsnorm_linear_config1_gamma_one():
 
 
 @pytest.mark.parametrize("B,K,N,layout", [(8, 4096, 14336, 1), (2, 2048, 520, 1), (8, 4096, 2048, 0),
-                                          (1, 4096, 14336, 0), (130, 1024, 520, 1)])
+                                          (1, 4096, 14336, 0), (130, 1024, 520, 1), (140, 1024, 520, 0),
+                                          (128, 4096, 14336, 0)])
 def test_gated_mlp(B, K, N, layout):
     import yirage_amd.fused as F
 
@@ -85,6 +87,7 @@ def test_gated_mlp(B, K, N, layout):
     w3 = _randn(wshape, 0.02, torch.bfloat16, g)
     out = F.gated_mlp(x.cuda(), w1.cuda(), w3.cuda(), w_layout=layout)
     torch.cuda.synchronize()
+    O.set_num_threads(16)
     ref = O.gated_mlp(_f(x), _bits(w1), _bits(w3), "bf16", layout)
     _close(out, ref, "gated_mlp")
 
@@ -107,7 +110,8 @@ def test_gated_mlp_batch128_all_columns():
 
 
 @pytest.mark.parametrize("dtype,layout,B", [(torch.float16, 0, 4), (torch.bfloat16, 0, 4), (torch.bfloat16, 1, 4),
-                                            (torch.float16, 1, 4), (torch.bfloat16, 1, 40)])
+                                            (torch.float16, 1, 4), (torch.bfloat16, 1, 40), (torch.bfloat16, 0, 64),
+                                            (torch.float16, 0, 150), (torch.bfloat16, 0, 256)])
 def test_linear_with_residual(dtype, layout, B):
     import yirage_amd.fused as F
 

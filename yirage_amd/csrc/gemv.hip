@@ -1,13 +1,14 @@
-// Bandwidth-bound skinny GEMMs (batch <= 8) for gfx950: RMSNorm+linear, gated
-// MLP and linear(+residual), in both weight layouts.
+// Bandwidth-bound skinny GEMMs for gfx950 with the weight in N x K layout
+// (W[N][K], torch Linear.weight): RMSNorm+linear, gated MLP and
+// linear(+residual) for passes of up to 8 rows.  (K x N weights, and N x K
+// passes of more than 16 rows, run on the MFMA kernels of skinny.hip.)
 //
-// Design (one kernel per layout):
+// Design:
 //  * Weights stream once from HBM with 128-bit loads; every lane issues all of
 //    its weight loads before it touches the activations, so the whole tile is
 //    in flight while X is staged and the norm statistic is formed.
 //  * Inner products use v_dot2_f32_{f16,bf16} (two MACs per lane-op, fp32
-//    accumulate).  In the K-major-rows layout (W[K][N]) two consecutive rows
-//    are interleaved with v_perm_b32 to form the (k, k+1) pairs dot2 needs.
+//    accumulate) over contiguous K chunks of a weight row.
 //  * The K dimension is split across workgroups so the grid fills all 256
 //    CUs; each workgroup reduces its waves in LDS, writes one fp32 partial
 //    record, and the last workgroup to arrive for an output tile (atomic
@@ -25,6 +26,11 @@ size_t skinny_kn_workspace(int B, int K, int N, int nmat);
 int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
               const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
               void* ws, size_t ws_bytes, hipStream_t st, const char* name);
+// N x K weights, passes of 17..128 rows: the MFMA kernel of skinny.hip
+size_t skinny_nk128_workspace(int K, int N, int nmat);
+int skinny_nk128(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
+                 const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat,
+                 int epi, void* ws, hipStream_t st, const char* name);
 
 enum : int { EPI_LINEAR = 0, EPI_RMSNORM = 1, EPI_GATED = 2 };
 
@@ -41,189 +47,6 @@ struct GemvArgs {
   int ldx, ldo;             // row strides of x / out (elements)
   float eps;
 };
-
-// ---------------------------------------------------------------- KN layout
-// W[K][N] row-major.  Workgroup = 8 waves; a wave's lane covers 8 columns
-// (one 16-byte chunk) and ROWS consecutive rows; 16 lanes span 128 columns,
-// the 4 lane groups of a wave take 4 row blocks.  Workgroup tile: 128 columns
-// x (8 * 4 * ROWS) rows.
-constexpr int KN_WAVES = 8;
-constexpr int KN_THREADS = KN_WAVES * kWave;
-constexpr int KN_COLS = 128;
-
-template <int ROWS>
-constexpr int kn_rows_per_wg() { return KN_WAVES * 4 * ROWS; }
-
-template <int NMAT>
-__host__ __device__ constexpr int kn_rec(int nb) { return round_up4(NMAT * nb * KN_COLS + nb); }
-
-template <int DT, int NB, int NMAT, int EPI>
-__device__ __forceinline__ void tile_epilogue(const GemvArgs& a, const float* acc /*[NMAT][NB][128] in LDS*/,
-                                              const float* ss /*[NB]*/, int col_base) {
-  for (int i = threadIdx.x; i < NB * KN_COLS; i += blockDim.x) {
-    int b = i / KN_COLS, c = i % KN_COLS;
-    int n = col_base + c;
-    if (b >= a.B || n >= a.N) continue;
-    float v = acc[b * KN_COLS + c];
-    if constexpr (EPI == EPI_RMSNORM) {
-      float r = rsqrtf(ss[b] / (float)a.K + a.eps);
-      v *= r;
-    } else if constexpr (EPI == EPI_GATED) {
-      float u = acc[NB * KN_COLS + b * KN_COLS + c];
-      v = silu(v) * u;
-    }
-    if (a.residual) v += ld_elem<DT>(a.residual[(size_t)b * a.ldo + n]);
-    a.out[(size_t)b * a.ldo + n] = (uint16_t)st_elem<DT>(v);
-  }
-}
-
-// Cross-workgroup split-K reduction: write this workgroup's record; the last
-// arriving workgroup of the tile sums all records (s = 0..S-1 in order).
-template <int DT, int NB, int NMAT, int EPI>
-__device__ __forceinline__ void splitk_finish(const GemvArgs& a, float* red /*LDS, >= rec floats*/,
-                                              int tile, int split, int col_base) {
-  constexpr int REC = kn_rec<NMAT>(NB);
-  if (a.S == 1) {
-    tile_epilogue<DT, NB, NMAT, EPI>(a, red, red + NMAT * NB * KN_COLS, col_base);
-    return;
-  }
-  put_record(a.partial + ((size_t)tile * a.S + split) * REC, red, REC);
-  if (!arrive_last(&a.tickets[tile], a.S)) return;
-  sum_records(a.partial + (size_t)tile * a.S * REC, a.S, REC, red);
-  __syncthreads();
-  tile_epilogue<DT, NB, NMAT, EPI>(a, red, red + NMAT * NB * KN_COLS, col_base);
-}
-
-template <int DT, int NB, int NMAT, int EPI, int ROWS>
-__global__ __launch_bounds__(KN_THREADS) void gemv_kn_kernel(GemvArgs a) {
-  constexpr int RPW = kn_rows_per_wg<ROWS>();    // rows per workgroup
-  constexpr int NPAIR = RPW / 2;
-  __shared__ uint32_t xs[NPAIR * NB];            // packed (x[k], x[k+1]) per batch row
-  __shared__ float ssl[8];
-  __shared__ float red[kn_rec<NMAT>(NB)];
-
-  const int tid = threadIdx.x;
-  const int wave = tid / kWave, lane = tid % kWave;
-  const int grp = lane / 16, cl = lane % 16;
-  const int tile = blockIdx.x, split = blockIdx.y;
-  const int col_base = tile * KN_COLS;
-  const int col = col_base + cl * 8;
-  const int k0 = split * RPW;
-  const int row0 = k0 + wave * (4 * ROWS) + grp * ROWS;  // first row of this lane
-  const bool col_ok = col < a.N;
-
-  // 1) issue every weight load of this lane
-  uint4 w[NMAT][ROWS];
-#pragma unroll
-  for (int m = 0; m < NMAT; m++) {
-    const uint16_t* W = m == 0 ? a.w0 : a.w1;
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      int k = row0 + r;
-      if (col_ok && k < a.K) w[m][r] = ldg16(W + (size_t)k * a.N + col);
-      else w[m][r] = make_uint4(0, 0, 0, 0);
-    }
-  }
-
-  // 2) stage x (times gamma) as packed pairs; partial sum of squares per row
-  {
-    // thread -> (batch row b = wave, 8-element chunk = lane .. strided)
-    const int b = wave;
-    float ss = 0.f;
-    for (int ch = lane; ch < RPW / 8; ch += kWave) {
-      int k = k0 + ch * 8;
-      uint4 xv = make_uint4(0, 0, 0, 0), gv;
-      if (b < a.B && b < NB && k < a.K) xv = ldg16(a.x + (size_t)b * a.ldx + k);
-      uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-      uint32_t gw[4] = {0, 0, 0, 0};
-      if constexpr (EPI == EPI_RMSNORM) {
-        if (a.gamma && k < a.K) {
-          gv = ldg16(a.gamma + k);
-          gw[0] = gv.x; gw[1] = gv.y; gw[2] = gv.z; gw[3] = gv.w;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float lo = lo16<DT>(xw[j]), hi = hi16<DT>(xw[j]);
-        ss += lo * lo + hi * hi;
-        uint32_t packed = xw[j];
-        if constexpr (EPI == EPI_RMSNORM) {
-          if (a.gamma) packed = pack2<DT>(lo * lo16<DT>(gw[j]), hi * hi16<DT>(gw[j]));
-        }
-        if (b < NB) xs[(ch * 4 + j) * NB + b] = packed;
-      }
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) ssl[wave] = ss;
-  }
-  __syncthreads();
-
-  // 3) dot products: rows (2p, 2p+1) of this lane against packed x pairs
-  float acc[NMAT][NB][8];
-#pragma unroll
-  for (int m = 0; m < NMAT; m++)
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-      for (int c = 0; c < 8; c++) acc[m][b][c] = 0.f;
-
-  const int pair0 = (wave * (4 * ROWS) + grp * ROWS) / 2;
-#pragma unroll
-  for (int p = 0; p < ROWS / 2; p++) {
-    uint32_t xp[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) xp[b] = xs[(pair0 + p) * NB + b];
-#pragma unroll
-    for (int m = 0; m < NMAT; m++) {
-      uint32_t ra[4] = {w[m][2 * p].x, w[m][2 * p].y, w[m][2 * p].z, w[m][2 * p].w};
-      uint32_t rb[4] = {w[m][2 * p + 1].x, w[m][2 * p + 1].y, w[m][2 * p + 1].z, w[m][2 * p + 1].w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        uint32_t lo = __builtin_amdgcn_perm(rb[j], ra[j], 0x05040100u);
-        uint32_t hi = __builtin_amdgcn_perm(rb[j], ra[j], 0x07060302u);
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-          acc[m][b][2 * j] = dot2<DT>(lo, xp[b], acc[m][b][2 * j]);
-          acc[m][b][2 * j + 1] = dot2<DT>(hi, xp[b], acc[m][b][2 * j + 1]);
-        }
-      }
-    }
-  }
-
-  // 4) reduce the 4 lane groups of the wave, then the 8 waves through LDS
-#pragma unroll
-  for (int m = 0; m < NMAT; m++)
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        float v = acc[m][b][c];
-        v += __shfl_xor(v, 16, kWave);
-        v += __shfl_xor(v, 32, kWave);
-        acc[m][b][c] = v;
-      }
-
-  __shared__ float wbuf[KN_WAVES * NMAT * NB * KN_COLS];
-  if (grp == 0) {
-#pragma unroll
-    for (int m = 0; m < NMAT; m++)
-#pragma unroll
-      for (int b = 0; b < NB; b++)
-#pragma unroll
-        for (int c = 0; c < 8; c++)
-          wbuf[((wave * NMAT + m) * NB + b) * KN_COLS + cl * 8 + c] = acc[m][b][c];
-  }
-  __syncthreads();
-  for (int i = tid; i < NMAT * NB * KN_COLS; i += KN_THREADS) {
-    float v = 0.f;
-#pragma unroll
-    for (int wv = 0; wv < KN_WAVES; wv++) v += wbuf[wv * NMAT * NB * KN_COLS + i];
-    red[i] = v;
-  }
-  if (tid < NB) red[NMAT * NB * KN_COLS + tid] = ssl[tid];
-  __syncthreads();
-  splitk_finish<DT, NB, NMAT, EPI>(a, red, tile, split, col_base);
-}
 
 // ---------------------------------------------------------------- NK layout
 // W[N][K] row-major (torch Linear.weight).  A lane owns C 16-byte chunks of
@@ -366,8 +189,6 @@ __global__ __launch_bounds__(NK_THREADS) void gemv_nk_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------- host side
-constexpr int KN_ROWS_1 = 16;  // rows per lane, one weight matrix
-constexpr int KN_ROWS_2 = 8;   // rows per lane, two weight matrices (gated)
 constexpr int NK_C1 = 4;       // 16-byte chunks per lane per row, batch 1 (K slice 2048)
 constexpr int NK_C8 = 2;       // same for batch 2..8 (x of 8 rows stays in VGPRs)
 constexpr int NK_TROWS = 32;   // output rows per workgroup
@@ -378,31 +199,16 @@ struct Plan {
 };
 
 
-static Plan plan_gemv(int B, int K, int N, int layout, int nmat) {
+static Plan plan_gemv(int B, int K, int N, int nmat) {
   Plan p;
-  int nb = 8;
-  if (layout == YR_W_KN) {
-    int rpw = KN_WAVES * 4 * (nmat == 1 ? KN_ROWS_1 : KN_ROWS_2);
-    p.tiles = (N + KN_COLS - 1) / KN_COLS;
-    p.S = (K + rpw - 1) / rpw;
-    p.rec = round_up4(nmat * nb * KN_COLS + nb);
-  } else {
-    int ks = kWave * 8 * (B == 1 ? NK_C1 : NK_C8);
-    p.tiles = (N + NK_TROWS - 1) / NK_TROWS;
-    p.S = (K + ks - 1) / ks;
-    p.rec = round_up4(nmat * nb * NK_TROWS + nb);
-  }
+  const int nb = 8;
+  const int ks = kWave * 8 * (B == 1 ? NK_C1 : NK_C8);
+  p.tiles = (N + NK_TROWS - 1) / NK_TROWS;
+  p.S = (K + ks - 1) / ks;
+  p.rec = round_up4(nmat * nb * NK_TROWS + nb);
   p.ws = 0;
   if (p.S > 1) p.ws = kTicketBytes + (size_t)p.tiles * p.S * p.rec * sizeof(float);
-  (void)B;
   return p;
-}
-
-template <int DT, int NMAT, int EPI>
-static void launch_kn(const GemvArgs& a, hipStream_t st) {
-  dim3 grid((a.N + KN_COLS - 1) / KN_COLS, a.S);
-  constexpr int R = NMAT == 1 ? KN_ROWS_1 : KN_ROWS_2;
-  hipLaunchKernelGGL((gemv_kn_kernel<DT, 8, NMAT, EPI, R>), grid, dim3(KN_THREADS), 0, st, a);
 }
 
 template <int DT, int NMAT, int EPI>
@@ -412,6 +218,21 @@ static void launch_nk(const GemvArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((gemv_nk_kernel<DT, 1, NMAT, EPI, NK_C1, NK_TROWS>), grid, dim3(NK_THREADS), 0, st, a);
   else
     hipLaunchKernelGGL((gemv_nk_kernel<DT, 8, NMAT, EPI, NK_C8, NK_TROWS>), grid, dim3(NK_THREADS), 0, st, a);
+}
+
+// Rows of the pass starting with `left` rows to go: up to 128 on the MFMA
+// kernel while more than 16 remain, then chunks of up to 8 on the GEMV (each
+// pass streams the weights once).
+static int pass_rows(int left) { return left > 16 ? (left < 128 ? left : 128) : (left < 8 ? left : 8); }
+
+static size_t nk_workspace(int B, int K, int N, int nmat) {
+  size_t need = 0;
+  for (int b0 = 0; b0 < B; b0 += pass_rows(B - b0)) {
+    const int rows = pass_rows(B - b0);
+    const size_t w = rows > 16 ? skinny_nk128_workspace(K, N, nmat) : plan_gemv(rows, K, N, nmat).ws;
+    if (w > need) need = w;
+  }
+  return need;
 }
 
 template <int NMAT, int EPI>
@@ -425,42 +246,36 @@ static int run_gemv(GemvArgs a, int dtype, int layout, void* ws, size_t ws_bytes
   if (layout == YR_W_KN)
     return skinny_kn(a.x, a.gamma, a.w0, a.w1, a.residual, a.out, a.B, a.K, a.N, a.eps, dtype, NMAT, EPI, ws,
                      ws_bytes, st, name);
-  // every batch chunk of <= 8 rows gets its own plan; the workspace must hold
-  // the largest one
-  size_t need = 0;
-  for (int b0 = 0; b0 < a.B; b0 += 8) {
-    Plan q = plan_gemv(a.B - b0 < 8 ? a.B - b0 : 8, a.K, a.N, layout, NMAT);
-    if (q.ws > need) need = q.ws;
-  }
+  const size_t need = nk_workspace(a.B, a.K, a.N, NMAT);
   if (need > ws_bytes || (need && !ws))
     return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, need);
   {
-    Plan q = plan_gemv(a.B < 8 ? a.B : 8, a.K, a.N, layout, NMAT);
+    Plan q = plan_gemv(a.B < 8 ? a.B : 8, a.K, a.N, NMAT);
     if (q.tiles > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large (%d tiles)", name, a.N, q.tiles);
   }
   a.ldx = a.K;
   a.ldo = a.N;
   const int B = a.B;
-  // batch chunks of 8 rows (each chunk re-streams the weights)
-  for (int b0 = 0; b0 < B; b0 += 8) {
+  for (int b0 = 0; b0 < B; b0 += pass_rows(B - b0)) {
     GemvArgs c = a;
-    c.B = B - b0 < 8 ? B - b0 : 8;
-    Plan p = plan_gemv(c.B, a.K, a.N, layout, NMAT);
+    c.B = pass_rows(B - b0);
+    c.x = a.x + (size_t)b0 * a.K;
+    c.out = a.out + (size_t)b0 * a.N;
+    if (a.residual) c.residual = a.residual + (size_t)b0 * a.N;
+    if (c.B > 16) {
+      const int rc = skinny_nk128(c.x, c.gamma, c.w0, c.w1, c.residual, c.out, c.B, a.K, a.N, a.eps, dtype, NMAT,
+                                  EPI, ws, st, name);
+      if (rc != YR_OK) return rc;
+      continue;
+    }
+    Plan p = plan_gemv(c.B, a.K, a.N, NMAT);
     c.S = p.S;
     if (p.ws) {
       c.tickets = (uint32_t*)ws;
       c.partial = (float*)((char*)ws + kTicketBytes);
     }
-    c.x = a.x + (size_t)b0 * a.K;
-    c.out = a.out + (size_t)b0 * a.N;
-    if (a.residual) c.residual = a.residual + (size_t)b0 * a.N;
-    if (layout == YR_W_KN) {
-      if (dtype == YR_DTYPE_F16) launch_kn<DT_F16, NMAT, EPI>(c, st);
-      else launch_kn<DT_BF16, NMAT, EPI>(c, st);
-    } else {
-      if (dtype == YR_DTYPE_F16) launch_nk<DT_F16, NMAT, EPI>(c, st);
-      else launch_nk<DT_BF16, NMAT, EPI>(c, st);
-    }
+    if (dtype == YR_DTYPE_F16) launch_nk<DT_F16, NMAT, EPI>(c, st);
+    else launch_nk<DT_BF16, NMAT, EPI>(c, st);
     YR_CHECK_LAUNCH(name);
   }
   return YR_OK;
@@ -474,12 +289,7 @@ extern "C" {
 
 static size_t ws_for(int batch, int k, int n, int w_layout, int nmat) {
   if (w_layout == YR_W_KN) return skinny_kn_workspace(batch, k, n, nmat);
-  size_t need = 0;
-  for (int b0 = 0; b0 < batch; b0 += 8) {
-    size_t w = plan_gemv(batch - b0 < 8 ? batch - b0 : 8, k, n, w_layout, nmat).ws;
-    if (w > need) need = w;
-  }
-  return need;
+  return nk_workspace(batch, k, n, nmat);
 }
 
 size_t yr_hip_rmsnorm_linear_workspace(int batch, int k, int n, int dtype, int w_layout) {

@@ -295,16 +295,22 @@ __device__ __forceinline__ uint4 b_frag_swz(const uint16_t* tile, int cb, int ro
   return make_uint4(l2.x, l2.y, h2.x, h2.y);
 }
 
-template <int DT, int NMAT, int EPI>
+// NKL: W in N x K layout (W[N][K], torch Linear.weight).  Its rows already
+// hold 8 consecutive k of one column per 16 bytes, the B fragment's order, so
+// a W tile is staged like an x tile (64 padded rows of n) and B fragments
+// come back by plain 16-byte reads.
+template <int DT, int NMAT, int EPI, bool NKL>
 __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   constexpr int TW = 64, KS = 64, MB = 128;
-  // W rows unpadded with chunks permuted by w_swz; x rows padded (A
-  // fragments by 16-byte reads of 16 rows at one k)
-  constexpr int LDW = TW, LDX = KS + 8;
+  // K x N: W rows unpadded with chunks permuted by w_swz; x rows (and N x K
+  // W rows) padded (fragments by 16-byte reads of 16 rows at one k)
+  constexpr int LDX = KS + 8;
+  constexpr int LDW = NKL ? LDX : TW;
+  constexpr int WROWS = NKL ? TW : KS;
   static_assert(TW == 64, "w_swz / b_frag_swz assume 64-column W rows");
   constexpr int CHQ = 2;                      // chunks in flight (2 measured best of 2, 3, 4, 6)
   constexpr bool NORM = EPI == EPI_RMSNORM;
-  __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][KS * LDW];
+  __shared__ __attribute__((aligned(16))) uint16_t wl[2][NMAT][WROWS * LDW];
   __shared__ __attribute__((aligned(16))) uint16_t xl[2][MB * LDX];
   __shared__ float ssl[MB];
 
@@ -320,8 +326,9 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   const __amdgpu_buffer_rsrc_t rw1 = rsrc(NMAT == 2 ? a.w1 : a.w0, (uint32_t)((size_t)a.K * a.N * 2));
   const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)((size_t)a.B * a.K * 2));
   const __amdgpu_buffer_rsrc_t rg = rsrc(a.gamma, a.gamma ? (uint32_t)(a.K * 2) : 0u);
-  // this thread's chunk pieces: W row tid / 8, columns 8 (tid % 8); x rows
-  // tid / 8 and tid / 8 + 64, k 8 (tid % 8)
+  // this thread's chunk pieces: W row tid / 8, columns 8 (tid % 8) (N x K:
+  // column n0 + tid / 8, k 8 (tid % 8)); x rows tid / 8 and tid / 8 + 64,
+  // k 8 (tid % 8)
   const int wr_ = tid >> 3, wc = 8 * (tid & 7);
   const int xr0 = tid >> 3, xk = 8 * (tid & 7);
 
@@ -333,8 +340,14 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   auto issue = [&](Chunk& c, int ci) __attribute__((always_inline)) {
     const int k0 = kbeg + ci * KS;
     const bool ok = ci < nchunks;
-    const int kw = k0 + wr_, n = n0 + wc;
-    const uint32_t woff = ok && kw < kend && n < a.N ? (uint32_t)(((size_t)kw * a.N + n) * 2) : kOob;
+    uint32_t woff;
+    if constexpr (NKL) {
+      const int n = n0 + wr_, kw = k0 + wc;
+      woff = ok && kw < kend && n < a.N ? (uint32_t)(((size_t)n * a.K + kw) * 2) : kOob;
+    } else {
+      const int kw = k0 + wr_, n = n0 + wc;
+      woff = ok && kw < kend && n < a.N ? (uint32_t)(((size_t)kw * a.N + n) * 2) : kOob;
+    }
     c.w[0] = bload16(rw0, woff);
     if constexpr (NMAT == 2) c.w[1] = bload16(rw1, woff);
     const int kx = k0 + xk;
@@ -367,7 +380,7 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
       // stage chunk ci (x scaled by gamma for RMSNorm, row sums first)
 #pragma unroll
       for (int m = 0; m < NMAT; m++)
-        *reinterpret_cast<uint4*>(&wl[lb][m][wr_ * LDW + (((wc >> 3) ^ w_swz(wr_)) << 3)]) = c.w[m];
+        *reinterpret_cast<uint4*>(&wl[lb][m][wr_ * LDW + (NKL ? wc : ((wc >> 3) ^ w_swz(wr_)) << 3)]) = c.w[m];
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         uint4 xv = c.x[h];
@@ -389,7 +402,10 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
         for (int m = 0; m < NMAT; m++)
 #pragma unroll
           for (int j2 = 0; j2 < 2; j2++) {
-            const uint4 bf = b_frag_swz(wl[lb][m], 4 * ng + 2 * j2, 32 * ks, lane);
+            const uint4 bf =
+                NKL ? *reinterpret_cast<const uint4*>(
+                          &wl[lb][m][(32 * ng + 16 * j2 + (lane & 15)) * LDW + 32 * ks + 8 * (lane >> 4)])
+                    : b_frag_swz(wl[lb][m], 4 * ng + 2 * j2, 32 * ks, lane);
 #pragma unroll
             for (int i = 0; i < 2; i++) acc[m][i][j2] = mfma16<DT>(af[i], bf, acc[m][i][j2]);
           }
@@ -520,9 +536,9 @@ inline Plan plan128(int K, int N, int nmat) {
   return p;
 }
 
-template <int DT, int NMAT, int EPI>
+template <int DT, int NMAT, int EPI, bool NKL = false>
 static void launch128(const Args& a, hipStream_t st) {
-  hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI>), dim3(a.units), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI, NKL>), dim3(a.units), dim3(kThreads), 0, st, a);
 }
 
 size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
@@ -576,6 +592,44 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
 #undef YR_SK
     YR_CHECK_LAUNCH(name);
   }
+  return YR_OK;
+}
+
+size_t skinny_nk128_workspace(int K, int N, int nmat) { return plan128(K, N, nmat).ws; }
+
+// One pass of 17..128 rows with W in N x K layout (the caller checked shapes,
+// pointers and the workspace size).
+int skinny_nk128(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
+                 const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat,
+                 int epi, void* ws, hipStream_t st, const char* name) {
+  if ((N + 63) / 64 > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
+  if ((size_t)K * N * 2 >= kOob || (size_t)B * K * 2 >= kOob)
+    return fail(YR_E_INVALID, "%s: operands must be < 4 GiB (32-bit buffer offsets)", name);
+  const Plan p = plan128(K, N, nmat);
+  Args a = {};
+  a.x = x;
+  a.gamma = gamma;
+  a.w0 = w0;
+  a.w1 = w1;
+  a.residual = residual;
+  a.out = out;
+  a.partial = (float*)((char*)ws + kTicketBytes);
+  a.tickets = (uint32_t*)ws;
+  a.B = B;
+  a.K = K;
+  a.N = N;
+  a.eps = eps;
+  a.kch = p.kch;
+  a.units = p.units;
+  const bool bf = dtype == YR_DTYPE_BF16;
+  if (nmat == 2) {
+    if (bf) launch128<DT_BF16, 2, EPI_GATED, true>(a, st); else launch128<DT_F16, 2, EPI_GATED, true>(a, st);
+  } else if (epi == EPI_RMSNORM) {
+    if (bf) launch128<DT_BF16, 1, EPI_RMSNORM, true>(a, st); else launch128<DT_F16, 1, EPI_RMSNORM, true>(a, st);
+  } else {
+    if (bf) launch128<DT_BF16, 1, EPI_LINEAR, true>(a, st); else launch128<DT_F16, 1, EPI_LINEAR, true>(a, st);
+  }
+  YR_CHECK_LAUNCH(name);
   return YR_OK;
 }
 
