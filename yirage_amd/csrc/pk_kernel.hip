@@ -99,7 +99,7 @@ __device__ __forceinline__ void lds_sync() {
 
 // ------------------------------------------------------------ protocol
 __device__ __forceinline__ bool aborted(const KernelArgs& a) {
-  return __hip_atomic_load(a.meta.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  return __hip_atomic_load(gptr(a.meta.status), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
 // Whole-workgroup wait until events[e] >= wait_count * epoch.  Returns false
@@ -110,7 +110,7 @@ constexpr int POLL_T = (PK_WAVES - 1) * kWave;  // first lane of the sync wave (
 
 __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (t.wait_event < 0) {
-    if (a.profile && tix() == POLL_T) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    if (a.profile && tix() == POLL_T) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     return true;
   }
   if (tix() == POLL_T) {
@@ -118,18 +118,18 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
     long long spins = 0;
     int ok = 1;
     for (;;) {
-      uint32_t v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t v = __hip_atomic_load(gptr(&a.events[t.wait_event]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if ((int32_t)(v - need) >= 0) break;
       if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
       if (++spins > a.spin_limit) {
-        __hip_atomic_store(a.meta.status + 2, task_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gptr(a.meta.status + 2), task_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ok = 0;
         break;
       }
       __builtin_amdgcn_s_sleep(16);
     }
-    if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    if (a.profile) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
   }
   __syncthreads();
@@ -143,25 +143,25 @@ __device__ void signal_event(const KernelArgs& a, const TaskDesc& t, bool link_o
   if (!link_out) wait_vm();  // every wave's stores complete before the one signal
   lds_sync();
   if (tix() == POLL_T && t.trigger_event >= 0)
-    __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gptr(&a.events[t.trigger_event]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t ld_agent_u32(const void* p) {
-  return __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gptr(reinterpret_cast<const uint32_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_agent_u32(void* p, uint32_t v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gptr(reinterpret_cast<uint32_t*>(p)), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint4 ld_agent_u128(const void* p) {
   const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-  uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t lo = __hip_atomic_load(gptr(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t hi = __hip_atomic_load(gptr(q + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
 }
 __device__ __forceinline__ void st_agent_u128(void* p, uint4 v) {
   uint64_t* q = reinterpret_cast<uint64_t*>(p);
-  __hip_atomic_store(q, (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gptr(q), (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gptr(q + 1), (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 
@@ -171,7 +171,7 @@ __device__ __forceinline__ uint32_t link_tag(const KernelArgs& a, int op) {
 }
 // store the bf16 pair `pair` at (even) element `e` of a link tensor
 __device__ __forceinline__ void link_store(uint16_t* base, size_t e, uint32_t pair, uint32_t tag) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(base) + e / 2, (uint64_t)pair | ((uint64_t)tag << 32),
+  __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(base) + e / 2), (uint64_t)pair | ((uint64_t)tag << 32),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // A word that still carries another tag is re-read until it matches; the
@@ -180,12 +180,12 @@ __device__ __forceinline__ void link_store(uint16_t* base, size_t e, uint32_t pa
 __device__ __forceinline__ bool link_spin(const KernelArgs& a, const uint64_t* w, uint32_t tag, uint64_t& v) {
   long long spins = 0;
   for (;;) {
-    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v = __hip_atomic_load(gptr(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((uint32_t)(v >> 32) == tag) return true;
     if ((spins & 255) == 255 && aborted(a)) return false;
     if (++spins > a.spin_limit) {
-      __hip_atomic_store(a.meta.status + 2, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gptr(a.meta.status + 2), -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
     __builtin_amdgcn_s_sleep(2);
@@ -194,7 +194,7 @@ __device__ __forceinline__ bool link_spin(const KernelArgs& a, const uint64_t* w
 // the bf16 pair at (even) element e, waiting for this launch's producer
 __device__ __forceinline__ uint32_t link_load(const KernelArgs& a, const uint16_t* base, size_t e, uint32_t tag) {
   const uint64_t* w = reinterpret_cast<const uint64_t*>(base) + e / 2;
-  uint64_t v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t v = __hip_atomic_load(gptr(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if ((uint32_t)(v >> 32) != tag) link_spin(a, w, tag, v);
   return (uint32_t)v;
 }
@@ -219,8 +219,8 @@ __device__ __forceinline__ uint4 link8_data(const Link8& r) { return make_uint4(
 __device__ __forceinline__ bool link_retry(const KernelArgs& a, long long& spins) {
   if ((spins & 255) == 255 && aborted(a)) return false;
   if (++spins > a.spin_limit) {
-    __hip_atomic_store(a.meta.status + 2, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gptr(a.meta.status + 2), -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return false;
   }
   __builtin_amdgcn_s_sleep(2);
@@ -248,7 +248,7 @@ __device__ __forceinline__ void task_embed(const KernelArgs& a, const TaskDesc& 
   if (!wait_event(a, t, task_id, sm)) return;
   const int T = active_tokens(a, op);
   for (int b = 0; b < T; b++) {
-    uint64_t tok = (uint64_t)__hip_atomic_load(reinterpret_cast<const uint64_t*>(op.tokens_in + b), __ATOMIC_RELAXED,
+    uint64_t tok = (uint64_t)__hip_atomic_load(gptr(reinterpret_cast<const uint64_t*>(op.tokens_in + b)), __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
     if (tok >= (uint64_t)op.vocab) tok = 0;  // out-of-range ids read row 0
     const uint16_t* src = op.table + tok * (uint64_t)op.K + t.row0;
@@ -282,11 +282,11 @@ struct AttnGeom {
 __device__ __forceinline__ AttnGeom attn_geom(const BatchMeta& m, OpRef op, int r, int s) {
   AttnGeom g;
   const int S = op.splits;
-  g.t0 = m.qo_indptr[r];
-  g.nt = m.qo_indptr[r + 1] - g.t0;
-  g.pb = m.kv_indptr[r];
-  g.np = m.kv_indptr[r + 1] - g.pb;
-  const int lpl = m.last_page_len[r];
+  g.t0 = gptr(m.qo_indptr)[r];
+  g.nt = gptr(m.qo_indptr)[r + 1] - g.t0;
+  g.pb = gptr(m.kv_indptr)[r];
+  g.np = gptr(m.kv_indptr)[r + 1] - g.pb;
+  const int lpl = gptr(m.last_page_len)[r];
   const int seq = g.nt > 0 ? (g.np - 1) * kPage + (lpl == 0 ? kPage : lpl) : 0;
   g.base = seq - g.nt;
   int chunk = (g.base + S - 1) / S;
@@ -474,7 +474,7 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
 // block) times rsqrt(mean(x^2) + eps) * gamma (gamma staged in attn_p),
 // rounded to bf16, in place -- the arithmetic of norm_x, with every LDS read
 // of the row in flight at once.
-__device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, int lane) {
+__device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, int lane, float eps) {
   const int K = op.K;
   const uint16_t* gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
   uint4 xv[8];
@@ -494,7 +494,7 @@ __device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, in
     }
   }
   ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)K + op.eps);
+  const float r = rsqrtf(ss / (float)K + eps);
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int c = (lane + kWave * j) * 8;
@@ -521,20 +521,20 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
       const uint32_t need = (uint32_t)t.wait_count * a.epoch;
       long long spins = 0;
       for (;;) {
-        const uint32_t v = __hip_atomic_load(&a.events[t.wait_event], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (spins == 0 && a.profile) a.profile[(size_t)task_id * 8 + 7] = now_10ns() | ((uint64_t)((need - v) & 0xfffffu) << 44);
+        const uint32_t v = __hip_atomic_load(gptr(&a.events[t.wait_event]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (spins == 0 && a.profile) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns() | ((uint64_t)((need - v) & 0xfffffu) << 44);
         if ((int32_t)(v - need) >= 0) break;
         if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
         if (++spins > a.spin_limit) {
-          __hip_atomic_store(a.meta.status + 2, task_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(a.meta.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(gptr(a.meta.status + 2), task_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           ok = 0;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
       }
     }
-    if (a.profile) a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+    if (a.profile) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
   }
   __builtin_amdgcn_wave_barrier();
@@ -602,6 +602,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   constexpr bool NORM = EPI != EPI_LIN;
   OpRef op = op_of(a, t.op);
   const int K = op.K, R = t.rows;
+  const float eps = op.eps;
   const int RT = SILU ? 2 * R : R;                 // weight rows streamed
   const int seg = SILU ? R : t.split_row;          // rows [0, seg) from w0, the rest from w1
   const int NC = K >> 9;                           // 512-element chunks per row
@@ -676,7 +677,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         T = active_tokens(a, op);
         if (TM == 1 && (op.flags & OPF_X_LL)) {
           stage_x_link(a, op, KB, 0, sm, lane);
-          if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
+          if (a.profile && lane == 0) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
         } else {
           stage_x<TM>(op, T, KB, 0, sm, lane);
         }
@@ -697,13 +698,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
             const int c = (lane + kWave * j) * 8;
             if (c < K) *reinterpret_cast<uint4*>(gam + c) = nr.g[j];
           }
-          if (T > 0) norm_row(op, 0, KB, sm, lane);
+          if (T > 0) norm_row(op, 0, KB, sm, lane, eps);
         } else if (NORM) {
           norm_x(op, T, KB, sm, nr, pre, lane);
         }
       }
     } else if (a.profile && lane == 0) {
-      a.profile[(size_t)task_id * 8 + 1] = now_10ns();
+      gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     }
     for (int i = lane; i < (MF ? (NT + CW) * 16 : RT + CW) * TM; i += kWave) slots[i] = 0.f;
     if (lane == 0 && (same_op || !(NORM && MF && K <= 4096))) sm.norm_rows = 0;
@@ -713,13 +714,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   }
   lds_sync();  // [X]: block 0 staged, slots cleared
-  if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+  if (a.profile && tix() == SYNC_T0) gptr(a.profile)[(size_t)task_id * 8 + 4] = now_10ns();
   if (!sm.flag) return;
   const int T = sm.last_T;
   if constexpr (NORM && MF) {
     const int nr = __builtin_amdgcn_readfirstlane(sm.norm_rows);
     if (nr > 0) {  // workgroup-uniform
-      if (wave < nr) norm_row(op, wave, KB, sm, lane);
+      if (wave < nr) norm_row(op, wave, KB, sm, lane, eps);
       lds_sync();  // rows normalized
     }
   }
@@ -820,7 +821,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   }
   lds_sync();  // [O]: every partial sum is in its slot
-  if (a.profile && tix() == SYNC_T0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
+  if (a.profile && tix() == SYNC_T0) gptr(a.profile)[(size_t)task_id * 8 + 5] = now_10ns();
   if (!is_sync) {
     // [E]: the sync wave's output stores go into the CU's memory queue ahead
     // of this wave's next-task weight loads (behind ~100 KiB of loads they
@@ -915,11 +916,11 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     wait_vm();
     int last = 0;
     if (lane == 0)
-      last = __hip_atomic_fetch_add(&a.tickets[op.ticket_base], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+      last = __hip_atomic_fetch_add(gptr(&a.tickets[op.ticket_base]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              (uint32_t)(t.i1 - 1);
     last = __shfl(last, 0, kWave);
     if (last) {
-      if (lane == 0) __hip_atomic_store(&a.tickets[op.ticket_base], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) __hip_atomic_store(gptr(&a.tickets[op.ticket_base]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // reduce every task's record; task order = column order
       for (int b = 0; b < T; b++) {
         float best = -INFINITY;
@@ -937,16 +938,16 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
           if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
         }
         if (lane == 0)
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(op.tokens_out + b),
+          __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(op.tokens_out + b)),
                              (uint64_t)(int64_t)(bi == 0x7fffffff ? -1 : bi), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
   if (!(op.flags & OPF_OUT_LL)) wait_vm();  // link outputs are checked by their readers
-  if (a.profile && lane == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
+  if (a.profile && lane == 0) gptr(a.profile)[(size_t)task_id * 8 + 6] = now_10ns();
   if (lane == 0 && t.trigger_event >= 0) {
-    __hip_atomic_fetch_add(&a.events[t.trigger_event], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gptr(&a.events[t.trigger_event]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1047,8 +1048,8 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       idA = __builtin_amdgcn_readfirstlane(sm.pre[pe].id[2 * blk]);
       idB = __builtin_amdgcn_readfirstlane(sm.pre[pe].id[2 * blk + 1]);
     } else {
-      idA = __builtin_amdgcn_readfirstlane(m.kv_indices[pb + pg0]);
-      idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? m.kv_indices[pb + pg0 + 1] : idA);
+      idA = __builtin_amdgcn_readfirstlane(gptr(m.kv_indices)[pb + pg0]);
+      idB = __builtin_amdgcn_readfirstlane(pg0 + 1 < np ? gptr(m.kv_indices)[pb + pg0 + 1] : idA);
     }
     const size_t page_elems = (size_t)kPage * tok_stride;
     BlkAddr ba;
@@ -1081,7 +1082,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   if (!fits) {  // nothing to do / beyond one MFMA row block or the block budget
     if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
     if (nt > 0 && tix() == 0)
-      __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gptr(a.meta.status + 3), task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     signal_event(a, t);
     return;
   }
@@ -1142,7 +1143,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       if (!lk) lds_sync();
       int pg_tok = 0;  // page of new token lane % 16
       if (newtok && qrow < nt)
-        pg_tok = have_pre && qrow < 4 ? sm.pre[pe].pg_tok[qrow] : m.kv_indices[pb + (base + qrow) / kPage];
+        pg_tok = have_pre && qrow < 4 ? sm.pre[pe].pg_tok[qrow] : gptr(m.kv_indices)[pb + (base + qrow) / kPage];
       // RoPE tables of positions base .. base + nt - 1 ([pos][cos 128 | sin
       // 128]) in this wave's attn_p area
       uint16_t* const tabs = reinterpret_cast<uint16_t*>(&sm.attn_p[wave][0][0]);
@@ -1216,7 +1217,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   }
   // profile: 5 = q (and new k / v) loaded and valid, 4 = waves merged,
   // 7 = arrival ticket taken, 6 = split merge written (last split only)
-  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 5] = now_10ns();
+  if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 5] = now_10ns();
 
   // per-wave online softmax state for rows 4*(lane/16)+i
   float m_i[4], l_i[4];
@@ -1331,7 +1332,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     qk_softmax(base, nt, true);
     pv();
   }
-  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 1] = now_10ns();  // wave 0 processed
+  if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();  // wave 0 processed
 
   // sum o over the 4 lane groups (positions lane/16 + 4 i), then merge the
   // 8 waves: per row, (m, l) in LDS, o through LDS (xs reused as float)
@@ -1361,7 +1362,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   }
   lds_sync();
-  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 4] = now_10ns();
+  if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 4] = now_10ns();
   const int rows = nt * G;
   const int rec_floats = op.rec_rows * (D + 2);
   float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * rec_floats;
@@ -1385,7 +1386,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   }
   const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
-  if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 7] = now_10ns();
+  if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();
   if (merge) {
     // Online-softmax merge of the S split records in one memory round trip:
     // every (m, l) pair and every o chunk is loaded before anything waits.
@@ -1457,11 +1458,11 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         link_store(op.out, oe, lo, otag);
         link_store(op.out, oe + 2, hi, otag);
       } else {
-        __hip_atomic_store(reinterpret_cast<uint64_t*>(op.out + oe), (uint64_t)lo | ((uint64_t)hi << 32),
+        __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(op.out + oe)), (uint64_t)lo | ((uint64_t)hi << 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (a.profile && tix() == 0) a.profile[(size_t)task_id * 8 + 6] = now_10ns();
+    if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 6] = now_10ns();
   }
   signal_event(a, t, (op.flags & OPF_OUT_LL) != 0);
 }
@@ -1494,7 +1495,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
   const int t0 = gm.t0, nt = gm.nt, pb = gm.pb, np = gm.np, base = gm.base, c0 = gm.c0, c1 = gm.c1;
   const int R = nt * G;
   if (R > op.rec_rows || (op.flags & (OPF_X_LL | OPF_OUT_LL)) || nt > XS_ELEMS / (2 * D)) {
-    if (tix() == 0) __hip_atomic_store(a.meta.status + 3, task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tix() == 0) __hip_atomic_store(gptr(a.meta.status + 3), task_id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     signal_event(a, t);
     return;
   }
@@ -1530,7 +1531,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
       *reinterpret_cast<uint4*>(knew + (size_t)i * D + 8 * c) = kr;
       *reinterpret_cast<uint4*>(vnew + (size_t)i * D + 8 * c) = vv;
       const int pos = base + i;
-      const int pg = m.kv_indices[pb + pos / kPage];
+      const int pg = gptr(m.kv_indices)[pb + pos / kPage];
       const size_t ce = ((size_t)pg * kPage + pos % kPage) * tok_stride + (size_t)h * D + 8 * c;
       *reinterpret_cast<uint4*>(op.k_cache + ce) = kr;
       *reinterpret_cast<uint4*>(op.v_cache + ce) = vv;
@@ -1650,7 +1651,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
 #pragma unroll
       for (int jb = 0; jb < 4; jb++) {
         const int p = min(p0 + 16 * jb + lane % 16, plast);
-        const int pg = m.kv_indices[pb + p / kPage];
+        const int pg = gptr(m.kv_indices)[pb + p / kPage];
         const uint16_t* src = op.k_cache + ((size_t)pg * kPage + p % kPage) * tok_stride + (size_t)h * D + (lane / 16) * 8;
 #pragma unroll
         for (int q = 0; q < 4; q++) kf[jb][q] = ldg16(src + 32 * q);
@@ -1658,7 +1659,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
 #pragma unroll
       for (int i2 = 0; i2 < 16; i2++) {
         const int p = min(p0 + lane / 16 + 4 * i2, plast);
-        const int pg = m.kv_indices[pb + p / kPage];
+        const int pg = gptr(m.kv_indices)[pb + p / kPage];
         vf[i2] = ldg16(op.v_cache + ((size_t)pg * kPage + p % kPage) * tok_stride + (size_t)h * D + (lane % 16) * 8);
       }
       const int npos = c1 - p0 < 64 ? c1 - p0 : 64;
@@ -1740,7 +1741,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
       const int jt = rr / G, g = rr % G;
       const size_t oe = (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
       const uint32_t lo = pack2<DT_BF16>(O.x * inv, O.y * inv), hi = pack2<DT_BF16>(O.z * inv, O.w * inv);
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(op.out + oe), (uint64_t)lo | ((uint64_t)hi << 32),
+      __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(op.out + oe)), (uint64_t)lo | ((uint64_t)hi << 32),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -1757,43 +1758,43 @@ __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc
     const int MR = s.max_requests, MT = s.max_tokens, MP = s.max_pages, PS = s.page_size, MSL = s.max_seq_len;
     int head = *s.page_queue_head, tail = *s.page_queue_tail;
     for (int i = 0; i < MR; i++) {
-      int rid = s.request_ids[i];
+      int rid = gptr(s.request_ids)[i];
       if (rid == -1) continue;
-      int step = s.step[rid], qo = s.qo_indptr[i], nt = s.qo_indptr[i + 1] - qo, plen = s.prompt_lengths[rid];
+      int step = gptr(s.step)[rid], qo = gptr(s.qo_indptr)[i], nt = gptr(s.qo_indptr)[i + 1] - qo, plen = gptr(s.prompt_lengths)[rid];
       for (int j = 0; j < nt; j++)
         if (step + j + 1 >= plen && step + j + 1 < MSL)
-          s.tokens[(size_t)rid * MSL + step + j + 1] =
-              (int64_t)__hip_atomic_load(reinterpret_cast<uint64_t*>(s.output_tokens + qo + j), __ATOMIC_RELAXED,
+          gptr(s.tokens)[(size_t)rid * MSL + step + j + 1] =
+              (int64_t)__hip_atomic_load(gptr(reinterpret_cast<uint64_t*>(s.output_tokens + qo + j)), __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-      s.step[rid] = step + nt;
+      gptr(s.step)[rid] = step + nt;
       if ((step + nt + 1 >= MSL) ||
-          ((s.tokens[(size_t)rid * MSL + step + nt] == s.eos_token_id) && (step + nt >= plen))) {
-        s.request_ids[i] = -1;
-        int kp = s.kv_indptr[i], npg = s.kv_indptr[i + 1] - kp;
-        for (int j = 0; j < npg; j++) { s.page_queue[tail % MP] = s.kv_indices[kp + j]; tail++; }
+          ((gptr(s.tokens)[(size_t)rid * MSL + step + nt] == s.eos_token_id) && (step + nt >= plen))) {
+        gptr(s.request_ids)[i] = -1;
+        int kp = gptr(s.kv_indptr)[i], npg = gptr(s.kv_indptr)[i + 1] - kp;
+        for (int j = 0; j < npg; j++) { gptr(s.page_queue)[tail % MP] = gptr(s.kv_indices)[kp + j]; tail++; }
       }
     }
     // the page table is rebuilt in place: requests keep their old pages from
     // a snapshot (device memory of max_pages ids owned by the handle)
     int* snap = s.page_snap;
-    const int all = s.kv_indptr[MR];
-    for (int i = 0; i < all && i < MP; i++) snap[i] = s.kv_indices[i];
+    const int all = gptr(s.kv_indptr)[MR];
+    for (int i = 0; i < all && i < MP; i++) snap[i] = gptr(s.kv_indices)[i];
     int nreq = 0, ntok = 0, npg = 0;
     for (int i = 0; i < MR; i++) {
-      int rid = s.request_ids[i];
+      int rid = gptr(s.request_ids)[i];
       if (rid == -1) continue;
-      int kp = s.kv_indptr[i], nold = s.kv_indptr[i + 1] - kp;
-      s.request_ids[nreq] = rid;
-      s.qo_indptr[nreq] = ntok;
-      s.kv_indptr[nreq] = npg;
-      int step = s.step[rid];
-      int nnew = s.prompt_lengths[rid] - step;
+      int kp = gptr(s.kv_indptr)[i], nold = gptr(s.kv_indptr)[i + 1] - kp;
+      gptr(s.request_ids)[nreq] = rid;
+      gptr(s.qo_indptr)[nreq] = ntok;
+      gptr(s.kv_indptr)[nreq] = npg;
+      int step = gptr(s.step)[rid];
+      int nnew = gptr(s.prompt_lengths)[rid] - step;
       nnew = nnew > 0 ? (nnew < MT - ntok ? nnew : MT - ntok) : (1 < MT - ntok ? 1 : MT - ntok);
-      for (int j = 0; j < nnew; j++) s.input_tokens[ntok + j] = s.tokens[(size_t)rid * MSL + step + j];
+      for (int j = 0; j < nnew; j++) gptr(s.input_tokens)[ntok + j] = gptr(s.tokens)[(size_t)rid * MSL + step + j];
       int nnp = (step + nnew + PS - 1) / PS;
-      s.last_page_len[nreq] = (step + nnew) % PS;
-      for (int j = 0; j < nold; j++) s.kv_indices[npg + j] = snap[kp + j];
-      for (int j = nold; j < nnp; j++) { s.kv_indices[npg + j] = s.page_queue[head % MP]; head++; }
+      gptr(s.last_page_len)[nreq] = (step + nnew) % PS;
+      for (int j = 0; j < nold; j++) gptr(s.kv_indices)[npg + j] = snap[kp + j];
+      for (int j = nold; j < nnp; j++) { gptr(s.kv_indices)[npg + j] = gptr(s.page_queue)[head % MP]; head++; }
       npg += nnp;
       ntok += nnew;
       nreq++;
@@ -1801,24 +1802,24 @@ __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc
     while (nreq < MR && ntok < MT) {
       int nid = *s.next_request_id;
       if (nid >= s.total_requests) break;
-      s.request_ids[nreq] = nid;
-      s.qo_indptr[nreq] = ntok;
-      s.kv_indptr[nreq] = npg;
-      int nnew = s.prompt_lengths[nid] < MT - ntok ? s.prompt_lengths[nid] : MT - ntok;
-      for (int j = 0; j < nnew; j++) s.input_tokens[ntok + j] = s.tokens[(size_t)nid * MSL + j];
+      gptr(s.request_ids)[nreq] = nid;
+      gptr(s.qo_indptr)[nreq] = ntok;
+      gptr(s.kv_indptr)[nreq] = npg;
+      int nnew = gptr(s.prompt_lengths)[nid] < MT - ntok ? gptr(s.prompt_lengths)[nid] : MT - ntok;
+      for (int j = 0; j < nnew; j++) gptr(s.input_tokens)[ntok + j] = gptr(s.tokens)[(size_t)nid * MSL + j];
       int nnp = (nnew + PS - 1) / PS;
-      s.last_page_len[nreq] = nnew % PS;
-      for (int j = 0; j < nnp; j++) { s.kv_indices[npg + j] = s.page_queue[head % MP]; head++; }
+      gptr(s.last_page_len)[nreq] = nnew % PS;
+      for (int j = 0; j < nnp; j++) { gptr(s.kv_indices)[npg + j] = gptr(s.page_queue)[head % MP]; head++; }
       ntok += nnew;
       npg += nnp;
       nreq++;
       *s.next_request_id = nid + 1;
     }
-    for (int i = nreq; i < MR; i++) s.request_ids[i] = -1;
-    for (int i = nreq; i <= MR; i++) { s.qo_indptr[i] = ntok; s.kv_indptr[i] = npg; }
+    for (int i = nreq; i < MR; i++) gptr(s.request_ids)[i] = -1;
+    for (int i = nreq; i <= MR; i++) { gptr(s.qo_indptr)[i] = ntok; gptr(s.kv_indptr)[i] = npg; }
     *s.page_queue_head = head;
     *s.page_queue_tail = tail;
-    s.status[1] = ntok != 0;
+    gptr(s.status)[1] = ntok != 0;
   }
   signal_event(a, t);
 }
@@ -1848,13 +1849,13 @@ __device__ __forceinline__ void fill_pre(const KernelArgs& a, int n, Shared& sm)
           int idA = 0, idB = 0;
           if (g.nt > 0 && p0 < g.c1) {
             const int pg0 = p0 / kPage;
-            idA = m.kv_indices[g.pb + pg0];
-            idB = pg0 + 1 < g.np ? m.kv_indices[g.pb + pg0 + 1] : idA;
+            idA = gptr(m.kv_indices)[g.pb + pg0];
+            idB = pg0 + 1 < g.np ? gptr(m.kv_indices)[g.pb + pg0 + 1] : idA;
           }
           P.id[2 * w] = idA;
           P.id[2 * w + 1] = idB;
         }
-        for (int i = 0; i < 4; i++) P.pg_tok[i] = i < g.nt ? m.kv_indices[g.pb + (g.base + i) / kPage] : 0;
+        for (int i = 0; i < 4; i++) P.pg_tok[i] = i < g.nt ? gptr(m.kv_indices)[g.pb + (g.base + i) / kPage] : 0;
       }
     }
     sm.pre_of[k] = (uint8_t)idx;
@@ -1908,14 +1909,14 @@ __device__ __forceinline__ void run_prepare(int slot, int tid) {
 __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) {
   Shared& sm = g_sm;
   const int w = blockIdx.x;
-  const int q0 = a.queue_offsets[w], q1 = a.queue_offsets[w + 1];
+  const int q0 = gptr(a.queue_offsets)[w], q1 = gptr(a.queue_offsets)[w + 1];
   // this worker's task descriptors move to LDS, 256 at a time
   auto load_descs = [&](int first) __attribute__((always_inline)) {
     const int n = q1 - first < 256 ? q1 - first : 256;
     const int words = (int)(sizeof(TaskDesc) / 4);
     for (int i = tix(); i < n * words; i += PK_THREADS) {
       int k = i / words, e = i % words;
-      reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = reinterpret_cast<const uint32_t*>(&a.tasks[a.queue[first + k]])[e];
+      reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = gptr(reinterpret_cast<const uint32_t*>(&a.tasks[gptr(a.queue)[first + k]]))[e];
     }
   };
   load_descs(q0);
@@ -1937,12 +1938,12 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       for (int i = tix(); i < 256; i += PK_THREADS) sm.pre_of[i] = kPreNone;
       __syncthreads();
     }
-    const int tid = __builtin_amdgcn_readfirstlane(a.queue[q]);
+    const int tid = __builtin_amdgcn_readfirstlane(gptr(a.queue)[q]);
     const int slot = (q - q0) % 256;
     OpRef op = op_of(a, sm.tq[slot].op);
     if (a.profile && threadIdx.x == 0) {
-      a.profile[(size_t)tid * 8] = now_10ns();
-      a.profile[(size_t)tid * 8 + 3] = (uint64_t)w;
+      gptr(a.profile)[(size_t)tid * 8] = now_10ns();
+      gptr(a.profile)[(size_t)tid * 8 + 3] = (uint64_t)w;
     }
     const int type = op.type;
     const bool tm8 = op.max_tokens > 1;
@@ -1969,13 +1970,13 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
         bool small = op.max_tokens * G <= 4;
         if (!small) {
           const int r = sm.tq[slot].i0;
-          small = (a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r]) * G <= 4;
+          small = (gptr(a.meta.qo_indptr)[r + 1] - gptr(a.meta.qo_indptr)[r]) * G <= 4;
         }
         if (small) {
           run_attention<4>(slot, tid);
         } else {
           const int r = sm.tq[slot].i0;
-          const int nt = a.meta.qo_indptr[r + 1] - a.meta.qo_indptr[r];
+          const int nt = gptr(a.meta.qo_indptr)[r + 1] - gptr(a.meta.qo_indptr)[r];
           if (nt * G > 16) run_attention_mt(slot, tid); else run_attention_large(slot, tid);
         }
         break;
@@ -1988,7 +1989,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     // publishing this task, so the compute waves run ahead and put the next
     // task's weights in flight meanwhile
     if (!gemv) lds_sync();
-    if (a.profile && threadIdx.x == 0) a.profile[(size_t)tid * 8 + 2] = now_10ns();
+    if (a.profile && threadIdx.x == 0) gptr(a.profile)[(size_t)tid * 8 + 2] = now_10ns();
     if (!sm.flag) break;  // a dependency never arrived: leave the queue
   }
 }
@@ -1996,13 +1997,13 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
 // Batch state initialisation (persistent_kernel.cuh:107-132).
 __global__ void pk_init_batch_kernel(BatchMeta s) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    for (int i = 0; i < s.total_requests; i++) s.step[i] = 0;
+    for (int i = 0; i < s.total_requests; i++) gptr(s.step)[i] = 0;
     *s.next_request_id = 0;
-    for (int i = 0; i < s.max_requests; i++) s.request_ids[i] = -1;
-    for (int i = 0; i < s.max_requests + 1; i++) { s.qo_indptr[i] = 0; s.kv_indptr[i] = 0; }
+    for (int i = 0; i < s.max_requests; i++) gptr(s.request_ids)[i] = -1;
+    for (int i = 0; i < s.max_requests + 1; i++) { gptr(s.qo_indptr)[i] = 0; gptr(s.kv_indptr)[i] = 0; }
     *s.page_queue_head = 0;
     *s.page_queue_tail = s.max_pages;
-    for (int i = 0; i < s.max_pages; i++) s.page_queue[i] = i;
+    for (int i = 0; i < s.max_pages; i++) gptr(s.page_queue)[i] = i;
   }
 }
 

@@ -111,20 +111,40 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Global-memory pointers.  An access through a generic pointer compiles to a
+// flat instruction, which counts against lgkmcnt as well as vmcnt: every
+// later wait for an LDS or scalar result (lgkmcnt) then also waits for the
+// flat access to come back through the CU's vector memory queue, which holds
+// the whole weight prefetch (~1.7 us at 112 KiB in flight per CU, measured).
+// Every device-memory access therefore goes through these casts, which
+// make it a global_* instruction counted by vmcnt only.
+#define YR_G __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ YR_G T* gptr(T* p) {
+  return (YR_G T*)p;
+}
+template <class T>
+__device__ __forceinline__ const YR_G T* gptr(const T* p) {
+  return (const YR_G T*)p;
+}
+
+// (A plain cast of a uint4 pointer is not enough: copying the struct goes
+// back through a generic pointer.  The accesses use a native vector type.)
+typedef unsigned int yr_u32x4 __attribute__((ext_vector_type(4)));
+
 // 128-bit global load that bypasses nothing special (cached); used for weights
 __device__ __forceinline__ uint4 ldg16(const void* p) {
-  return *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(uint4, *(const YR_G yr_u32x4*)p);
+}
+
+// 128-bit global store
+__device__ __forceinline__ void stg16(void* p, uint4 v) {
+  *(YR_G yr_u32x4*)p = __builtin_bit_cast(yr_u32x4, v);
 }
 
 // streaming (non-temporal) 128-bit load for data read exactly once
 __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
-  const uint4* q = reinterpret_cast<const uint4*>(p);
-  uint4 r;
-  r.x = __builtin_nontemporal_load(&q->x);
-  r.y = __builtin_nontemporal_load(&q->y);
-  r.z = __builtin_nontemporal_load(&q->z);
-  r.w = __builtin_nontemporal_load(&q->w);
-  return r;
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const YR_G yr_u32x4*)p));
 }
 
 // ---------------------------------------------------------------- cross-CU exchange
@@ -135,25 +155,23 @@ __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
 // with agent-scope (sc1) loads.  No buffer_wbl2 / buffer_inv is issued, which
 // on gfx950 would walk the whole L2 of the XCD for every workgroup.
 __device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((YR_G uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void st_agent4(float* p, float4 v) {
   uint64_t lo = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
   uint64_t hi = (uint64_t)__float_as_uint(v.z) | ((uint64_t)__float_as_uint(v.w) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p) + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((YR_G uint64_t*)p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((YR_G uint64_t*)p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float ld_agent(const float* p) {
-  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
+  return __uint_as_float(__hip_atomic_load((const YR_G uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 __device__ __forceinline__ float4 ld_agent4(const float* p) {
-  uint64_t lo = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint64_t hi = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t lo = __hip_atomic_load((const YR_G uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t hi = __hip_atomic_load((const YR_G uint64_t*)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
                      __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
 }
@@ -174,9 +192,9 @@ __device__ __forceinline__ bool arrive_last(uint32_t* ticket, int n) {
   wait_vm();
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t old = __hip_atomic_fetch_add(gptr(ticket), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = old == (uint32_t)(n - 1);
-    if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (s_last) __hip_atomic_store(gptr(ticket), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   return s_last != 0;
