@@ -359,8 +359,10 @@ void Graph::build(const char* text) {
       if (cfg.max_tokens * G > kAttnMaxRows)
         throw std::runtime_error("attention: max_tokens * (q heads per kv head) must be <= " +
                                  std::to_string(kAttnMaxRows));
+      scratch_next = (scratch_next + 31) / 32 * 32;  // 16-byte loads of the records
       d.scratch_off = (int)scratch_next;
-      scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * d.rec_rows * (d.head_dim + 2);
+      // records of tagged 8-byte words {f32, tag}: 2 floats per value
+      scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * d.rec_rows * (d.head_dim + 2) * 2;
       if (scratch_next >= (1ll << 31)) throw std::runtime_error("attention: split records exceed 2^31 floats");
       for (int r = 0; r < cfg.max_requests; r++)
         for (int h = 0; h < d.num_kv_heads; h++)

@@ -475,42 +475,85 @@ __device__ __forceinline__ void norm_x(OpRef op, int T, int KB, Shared& sm, cons
 // rounded to bf16, in place -- the arithmetic of norm_x, with every LDS read
 // of the row in flight at once.
 __device__ __forceinline__ void norm_row(OpRef op, int b, int KB, Shared& sm, int lane, float eps) {
+  // (a latency chain on the path from the input's arrival to the weight
+  // stream: every LDS read is issued before any is waited for, addresses are
+  // clamped instead of branched around, and the sum of squares is reduced in
+  // registers)
   const int K = op.K;
   const uint16_t* gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
-  uint4 xv[8];
-  float ss = 0.f;
+  uint4 xv[8], gv[8];
+  bool in[8];
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int c = (lane + kWave * j) * 8;
-    xv[j] = c < K ? *reinterpret_cast<const uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) : make_uint4(0, 0, 0, 0);
+    in[j] = c < K;
+    const int cc = in[j] ? c : 0;
+    xv[j] = *reinterpret_cast<const uint4*>(&sm.xs[b * KB + xs_swz(b, cc)]);
+    gv[j] = *reinterpret_cast<const uint4*>(gam + cc);
   }
+  float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const uint32_t w4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+    float sj = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
-      ss += lo * lo + hi * hi;
+      sj += lo * lo + hi * hi;
     }
+    ss += in[j] ? sj : 0.f;
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_regs(ss);
   const float r = rsqrtf(ss / (float)K + eps);
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int c = (lane + kWave * j) * 8;
-    if (c < K) {
-      const uint4 g = *reinterpret_cast<const uint4*>(gam + c);
-      const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w}, gw[4] = {g.x, g.y, g.z, g.w};
-      uint32_t o[4];
+    const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w}, gw[4] = {gv[j].x, gv[j].y, gv[j].z, gv[j].w};
+    uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float lo = lo16<DT_BF16>(xw[e]) * (r * lo16<DT_BF16>(gw[e]));
-        const float hi = hi16<DT_BF16>(xw[e]) * (r * hi16<DT_BF16>(gw[e]));
-        o[e] = pack2<DT_BF16>(lo, hi);
-      }
-      *reinterpret_cast<uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
+    for (int e = 0; e < 4; e++) {
+      const float lo = lo16<DT_BF16>(xw[e]) * (r * lo16<DT_BF16>(gw[e]));
+      const float hi = hi16<DT_BF16>(xw[e]) * (r * hi16<DT_BF16>(gw[e]));
+      o[e] = pack2<DT_BF16>(lo, hi);
     }
+    if (in[j]) *reinterpret_cast<uint4*>(&sm.xs[b * KB + xs_swz(b, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
   }
+}
+
+// Row 0 (all of K <= 4096 in one block) normalized by the 8 waves together:
+// wave w takes columns [512 w, 512 w + 512), one 16-byte chunk per lane; the
+// sums of squares meet in LDS.  Same arithmetic as norm_row.
+__device__ __forceinline__ void norm_row_split(OpRef op, int KB, Shared& sm, int wave, int lane, float eps) {
+  const int K = op.K;
+  const uint16_t* gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
+  const int c = (wave * kWave + lane) * 8;
+  const bool in = c < K;
+  const int cc = in ? c : 0;
+  const uint4 xv = *reinterpret_cast<const uint4*>(&sm.xs[xs_swz(0, cc)]);
+  const uint4 g = *reinterpret_cast<const uint4*>(gam + cc);
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {g.x, g.y, g.z, g.w};
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float lo = lo16<DT_BF16>(xw[e]), hi = hi16<DT_BF16>(xw[e]);
+    s += lo * lo + hi * hi;
+  }
+  s = wave_sum_regs(in ? s : 0.f);
+  if (lane == 0) sm.red[wave] = s;
+  lds_sync();
+  float ss = 0.f;
+#pragma unroll
+  for (int w = 0; w < PK_WAVES; w++) ss += sm.red[w];
+  const float r = rsqrtf(ss / (float)K + eps);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float lo = lo16<DT_BF16>(xw[e]) * (r * lo16<DT_BF16>(gw[e]));
+    const float hi = hi16<DT_BF16>(xw[e]) * (r * hi16<DT_BF16>(gw[e]));
+    o[e] = pack2<DT_BF16>(lo, hi);
+  }
+  if (in) *reinterpret_cast<uint4*>(&sm.xs[xs_swz(0, c)]) = make_uint4(o[0], o[1], o[2], o[3]);
+  lds_sync();  // row normalized
 }
 
 // Sync wave: one-lane event poll (the watchdog exits through sm.flag).
@@ -698,7 +741,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
             const int c = (lane + kWave * j) * 8;
             if (c < K) *reinterpret_cast<uint4*>(gam + c) = nr.g[j];
           }
-          if (T > 0) norm_row(op, 0, KB, sm, lane, eps);
+          // normalized by all 8 waves after [X] (one wave alone spends ~1.5 us
+          // issuing the row's arithmetic while the others wait)
+          if (lane == 0) sm.norm_rows = T > 0 ? -1 : 0;
         } else if (NORM) {
           norm_x(op, T, KB, sm, nr, pre, lane);
         }
@@ -707,7 +752,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     }
     for (int i = lane; i < (MF ? (NT + CW) * 16 : RT + CW) * TM; i += kWave) slots[i] = 0.f;
-    if (lane == 0 && (same_op || !(NORM && MF && K <= 4096))) sm.norm_rows = 0;
+    if (lane == 0 && (same_op || !(NORM && K <= 4096))) sm.norm_rows = 0;
     if (lane == 0) {
       sm.last_T = T;
       sm.last_op = nkb == 1 ? t.op : -1;
@@ -723,6 +768,8 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       if (wave < nr) norm_row(op, wave, KB, sm, lane, eps);
       lds_sync();  // rows normalized
     }
+  } else if constexpr (NORM && TM == 1) {
+    if (__builtin_amdgcn_readfirstlane(sm.norm_rows) < 0) norm_row_split(op, KB, sm, wave, lane, eps);
   }
 
   if (is_sync) {
@@ -1363,10 +1410,20 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   }
   lds_sync();
   if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 4] = now_10ns();
+  // Split merge without an arrival ticket: every split but the last writes
+  // its (O, m, l) record as tagged words {f32, tag of this launch and op}
+  // (single-copy atomic 8-byte stores, nothing awaited); the last split --
+  // which also appended the new tokens -- keeps its own partial in LDS,
+  // re-reads the other records until every word carries this launch's tag,
+  // and merges.  (An arrival ticket costs a store acknowledgement and an
+  // atomic round trip on the chain before the merge can start.)
   const int rows = nt * G;
-  const int rec_floats = op.rec_rows * (D + 2);
-  float* rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * rec_floats;
-  float* rec = rec_base + (size_t)s * rec_floats;
+  const uint32_t rtag = link_tag(a, t.op);
+  const int rec_words = op.rec_rows * (D + 2);  // [rows][D + 2] words per split
+  uint64_t* const rec_base = reinterpret_cast<uint64_t*>(a.scratch + op.scratch_off) +
+                             (((size_t)r * op.num_kv_heads + h) * S) * rec_words;
+  float* const own = reinterpret_cast<float*>(sm.outs);  // last split: [rows][D] O, then [rows][2] (m, l)
+  float* const own_ml = own + 16 * D;
   for (int idx = tix(); idx < rows * D; idx += PK_THREADS) {
     int rr = idx / D, d = idx % D;
     float M = -INFINITY;
@@ -1379,76 +1436,136 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       L += sm.attn_ml[w][rr][1] * f;
       O += o_lds[(w * 16 + rr) * D + d] * f;
     }
-    st_agent(rec + rr * (D + 2) + d, O);
-    if (d == 0) {
-      st_agent(rec + rr * (D + 2) + D, M);
-      st_agent(rec + rr * (D + 2) + D + 1, L);
+    if (last) {
+      own[rr * D + d] = O;
+      if (d == 0) {
+        own_ml[2 * rr] = M;
+        own_ml[2 * rr + 1] = L;
+      }
+    } else {
+      uint64_t* const rec = rec_base + (size_t)s * rec_words + rr * (D + 2);
+      auto put = [&](int i, float v) __attribute__((always_inline)) {
+        __hip_atomic_store(gptr(rec + i), (uint64_t)__float_as_uint(v) | ((uint64_t)rtag << 32), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      };
+      put(d, O);
+      if (d == 0) {
+        put(D, M);
+        put(D + 1, L);
+      }
     }
   }
-  const bool merge = arrive_last(&a.tickets[op.ticket_base + r * op.num_kv_heads + h], S);
-  if (a.profile && tix() == 0) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();
-  if (merge) {
-    // Online-softmax merge of the S split records in one memory round trip:
-    // every (m, l) pair and every o chunk is loaded before anything waits.
-    // Thread -> (unit = query row x 4-float d chunk, lane j of P); lane j
-    // takes splits j, j + P, ...; the P partial states combine through LDS.
-    float* ml = reinterpret_cast<float*>(sm.xs);           // [S][rows][2] (m, l)
-    float* part = ml + 2 * kAttnRecRows * 256;             // [unit][P][6]: M, L, o0..o3
-    const int units = rows * (D / 4);
-    const int P = PK_THREADS / units;                      // >= 1 (rows <= 16)
+  if (last) {
+    lds_sync();  // own partial in outs; xs free again
     const int tid = tix();
-    for (int i = tid; i < rows * S; i += PK_THREADS) {
-      const float* rc = rec_base + (size_t)(i / rows) * rec_floats + (i % rows) * (D + 2) + D;
-      ml[2 * i] = ld_agent(rc);
-      ml[2 * i + 1] = ld_agent(rc + 1);
-    }
+    const int S1 = S - 1;                                   // records to read
+    float* const ml = reinterpret_cast<float*>(sm.xs);      // [S1][rows][2] (m, l)
+    float* const fac = ml + 2 * 256 * 16;                   // [S1 + 1][rows] weights; row totals after
+    float* const part = fac + 257 * 16;                     // [units][P][4]
+    const __amdgpu_buffer_rsrc_t rsr =
+        __builtin_amdgcn_make_buffer_rsrc(rec_base, 0, 0x7fffffff, 0x00020000);
+    auto ld16 = [&](size_t word) __attribute__((always_inline)) -> uint4 {  // two tagged words
+      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsr, (uint32_t)(word * 8), 0, kCpolSC1));
+    };
+    long long spins = 0;
+    // o: thread -> (unit = row x 4-float d chunk, lane j of P); lane j takes
+    // splits j, j + P, ... in rounds of 4.  The first round's loads go out
+    // together with the (m, l) loads: one round trip for both.
+    const int units = rows * (D / 4);
+    const int P = PK_THREADS / units;  // >= 1 (rows <= 16)
     const int u = tid / P, j = tid % P;
     const int rr = u / (D / 4), d4 = (u % (D / 4)) * 4;
     const bool act = u < units;
-    float4 ob[8];
-    const int ns = act ? (S - j + P - 1) / P : 0;           // splits of this thread
-    // first batch of o chunks in flight with the (m, l) loads
+    uint4 w[4][2];
+    auto issue = [&](int q0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 8; q++)
-      ob[q] = q < ns ? ld_agent4(rec_base + (size_t)(j + q * P) * rec_floats + rr * (D + 2) + d4)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int q = 0; q < 4; q++) {
+        const int s2 = q0 + q * P;
+        const size_t wd = (size_t)(act && s2 < S1 ? s2 : 0) * rec_words + rr * (D + 2) + d4;
+        w[q][0] = ld16(wd);
+        w[q][1] = ld16(wd + 2);
+      }
+    };
+    auto stale = [&](int q0) __attribute__((always_inline)) -> bool {
+      bool st = false;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        st |= act && q0 + q * P < S1 &&
+              (w[q][0].y != rtag || w[q][0].w != rtag || w[q][1].y != rtag || w[q][1].w != rtag);
+      return st;
+    };
+    // (m, l) of every other split: this thread's first pair, then its first
+    // round of o chunks, validated together (re-read while any word is stale)
+    auto ml_word = [&](int i) __attribute__((always_inline)) -> size_t {
+      return (size_t)(i / rows) * rec_words + (i % rows) * (D + 2) + D;
+    };
+    const bool has_ml = tid < S1 * rows;
+    uint4 mlv = ld16(has_ml ? ml_word(tid) : 0);
+    if (S1 > 0) issue(j);
+    for (;;) {
+      const bool ml_stale = has_ml && (mlv.y != rtag || mlv.w != rtag);
+      const bool o_stale = S1 > 0 && stale(j);
+      if (!(ml_stale || o_stale) || !link_retry(a, spins)) break;
+      if (ml_stale) mlv = ld16(ml_word(tid));
+      if (o_stale) issue(j);
+    }
+    if (has_ml) {
+      ml[2 * tid] = __uint_as_float(mlv.x);
+      ml[2 * tid + 1] = __uint_as_float(mlv.z);
+    }
+    for (int i = tid + PK_THREADS; i < S1 * rows; i += PK_THREADS) {  // more pairs than threads
+      uint4 v = ld16(ml_word(i));
+      while ((v.y != rtag || v.w != rtag) && link_retry(a, spins)) v = ld16(ml_word(i));
+      ml[2 * i] = __uint_as_float(v.x);
+      ml[2 * i + 1] = __uint_as_float(v.z);
+    }
     lds_sync();
-    float M = -INFINITY, L = 0.f;
+    if (a.profile && tid == 0) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();  // records valid
+    // per row: merged max, each split's weight, total l
+    if (tid < rows) {
+      float Mt = own_ml[2 * tid];
+      for (int s2 = 0; s2 < S1; s2++) Mt = fmaxf(Mt, ml[2 * (s2 * rows + tid)]);
+      float Lt = 0.f;
+      for (int s2 = 0; s2 <= S1; s2++) {
+        const float ms = s2 < S1 ? ml[2 * (s2 * rows + tid)] : own_ml[2 * tid];
+        const float ls = s2 < S1 ? ml[2 * (s2 * rows + tid) + 1] : own_ml[2 * tid + 1];
+        const float f = ms == -INFINITY ? 0.f : exp2f(ms - Mt);
+        fac[s2 * rows + tid] = f;
+        Lt += ls * f;
+      }
+      fac[257 * 16 - 16 + tid] = Lt;
+    }
+    lds_sync();
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (act) {
-      for (int s2 = j; s2 < S; s2 += P) M = fmaxf(M, ml[2 * (s2 * rows + rr)]);
-      for (int q0 = 0; q0 < ns; q0 += 8) {
-        if (q0 > 0) {
+      for (int q0 = j; q0 < S1; q0 += 4 * P) {
+        if (q0 != j) issue(q0);
+        while (stale(q0) && link_retry(a, spins)) issue(q0);
 #pragma unroll
-          for (int q = 0; q < 8; q++)
-            ob[q] = q0 + q < ns ? ld_agent4(rec_base + (size_t)(j + (q0 + q) * P) * rec_floats + rr * (D + 2) + d4)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-          if (q0 + q < ns) {
-            const int s2 = j + (q0 + q) * P;
-            const float ms = ml[2 * (s2 * rows + rr)];
-            const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-            L += ml[2 * (s2 * rows + rr) + 1] * f;
-            O.x += ob[q].x * f; O.y += ob[q].y * f; O.z += ob[q].z * f; O.w += ob[q].w * f;
+        for (int q = 0; q < 4; q++) {
+          const int s2 = q0 + q * P;
+          if (s2 < S1) {
+            const float f = fac[s2 * rows + rr];
+            O.x += __uint_as_float(w[q][0].x) * f;
+            O.y += __uint_as_float(w[q][0].z) * f;
+            O.z += __uint_as_float(w[q][1].x) * f;
+            O.w += __uint_as_float(w[q][1].z) * f;
           }
         }
       }
-      float* pp = part + (size_t)(u * P + j) * 6;
-      pp[0] = M; pp[1] = L; pp[2] = O.x; pp[3] = O.y; pp[4] = O.z; pp[5] = O.w;
+      float* pp = part + (size_t)(u * P + j) * 4;
+      pp[0] = O.x; pp[1] = O.y; pp[2] = O.z; pp[3] = O.w;
     }
     lds_sync();
     if (act && j == 0) {
-      const float* pp = part + (size_t)u * P * 6;
-      float Mt = -INFINITY;
-      for (int q = 0; q < P; q++) Mt = fmaxf(Mt, pp[q * 6]);
-      float Lt = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+      const float* pp = part + (size_t)u * P * 4;
+      const float fo = fac[S1 * rows + rr];
+      float o0 = own[rr * D + d4] * fo, o1 = own[rr * D + d4 + 1] * fo, o2 = own[rr * D + d4 + 2] * fo,
+            o3 = own[rr * D + d4 + 3] * fo;
       for (int q = 0; q < P; q++) {
-        const float f = pp[q * 6] == -INFINITY ? 0.f : exp2f(pp[q * 6] - Mt);
-        Lt += pp[q * 6 + 1] * f;
-        o0 += pp[q * 6 + 2] * f; o1 += pp[q * 6 + 3] * f; o2 += pp[q * 6 + 4] * f; o3 += pp[q * 6 + 5] * f;
+        o0 += pp[q * 4]; o1 += pp[q * 4 + 1]; o2 += pp[q * 4 + 2]; o3 += pp[q * 4 + 3];
       }
+      const float Lt = fac[257 * 16 - 16 + rr];
       const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
       const int jt = rr / G, g = rr % G;
       const size_t oe = (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
@@ -1540,7 +1657,8 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
   lds_sync();  // new k / v staged
 
   const int rec_floats = op.rec_rows * (D + 2);
-  float* const rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * rec_floats;
+  // (records sized for the tagged words of the single-block body: 2 floats each)
+  float* const rec_base = a.scratch + op.scratch_off + (((size_t)r * op.num_kv_heads + h) * S) * (2 * rec_floats);
   float* const rec = rec_base + (size_t)s * rec_floats;
   const int nblk = (c1 - c0 + 63) / 64;
   const int RB = (R + 15) / 16;

@@ -64,6 +64,9 @@ def get_configurations_from_gpu(rank: int = 0):
 
 
 class PersistentKernel:
+    # attention tasks take about 1 / ATTN_SPLIT_DIVISOR of the workers
+    ATTN_SPLIT_DIVISOR = 2
+
     def __init__(self, mode: str, world_size: int, mpi_rank: int, num_workers: int, num_local_schedulers: int,
                  num_remote_schedulers: int, max_seq_length: int, max_num_batched_requests: int,
                  max_num_batched_tokens: int, max_num_pages: int, page_size: int, eos_token_id: int,
@@ -344,7 +347,7 @@ class PersistentKernel:
                 # (measured at batch 1: 16 splits per kv head 3.82 ms, 32:
                 # 3.88 ms, 8: 3.90 ms); the builder raises it to what the
                 # per-task block budget needs
-                splits = max(1, min(256, W // (2 * per)))
+                splits = max(1, min(256, W // (self.ATTN_SPLIT_DIVISOR * per)))
                 ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
                                 v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
                                 sin=l["sin"].name if l["sin"] is not None else None, out=l["output"].name,
