@@ -1300,8 +1300,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         sc[j][i] = v;
         mx = fmaxf(mx, v);
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+      mx = row16_max(mx);
       float mnew = fmaxf(m_i[i], mx);
       float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[i] - mnew);
       float ls = 0.f;
@@ -1311,8 +1310,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         ls += p;
         sm.attn_p[wave][row][16 * j + lane % 16] = p;
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) ls += __shfl_xor(ls, o, kWave);
+      ls = row16_sum(ls);
       l_i[i] = l_i[i] * alpha + ls;
       m_i[i] = mnew;
       if ((lane % 16) == 0) sm.attn_ml[wave][row][0] = alpha;
@@ -1387,10 +1385,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   for (int rr = 0; rr < RMAX; rr++)
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      float x = o_acc[rr][e];
-      x += __shfl_xor(x, 16, kWave);
-      x += __shfl_xor(x, 32, kWave);
-      o_acc[rr][e] = x;
+      o_acc[rr][e] = add_xor32(add_xor16(o_acc[rr][e]));
     }
   float* o_lds = reinterpret_cast<float*>(sm.xs);  // [wave][16 rows][128]
   lds_sync();
@@ -1456,120 +1451,97 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
     }
   }
   if (last) {
-    lds_sync();  // own partial in outs; xs free again
+    lds_sync();  // own partial in outs
+    // thread -> (unit = row x 4-float d chunk, lane j of P, P a power of 2):
+    // lane j takes splits j, j + P, ... (the own partial is split S - 1) in
+    // rounds of 4, all of a round's words loaded at once and re-read while
+    // any is stale, folded into a running (m, l, o) in registers; the P lanes
+    // of a unit are consecutive and combine by DPP.  No LDS round trips.
     const int tid = tix();
-    const int S1 = S - 1;                                   // records to read
-    float* const ml = reinterpret_cast<float*>(sm.xs);      // [S1][rows][2] (m, l)
-    float* const fac = ml + 2 * 256 * 16;                   // [S1 + 1][rows] weights; row totals after
-    float* const part = fac + 257 * 16;                     // [units][P][4]
-    const __amdgpu_buffer_rsrc_t rsr =
-        __builtin_amdgcn_make_buffer_rsrc(rec_base, 0, 0x7fffffff, 0x00020000);
+    const int units = rows * (D / 4);
+    int P = 1;
+    while (2 * P * units <= PK_THREADS) P *= 2;
+    const int u = tid / P, j = tid % P;
+    const bool act = u < units;
+    const int rr = act ? u / (D / 4) : 0, d4 = act ? (u % (D / 4)) * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rsr = __builtin_amdgcn_make_buffer_rsrc(rec_base, 0, 0x7fffffff, 0x00020000);
     auto ld16 = [&](size_t word) __attribute__((always_inline)) -> uint4 {  // two tagged words
       return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsr, (uint32_t)(word * 8), 0, kCpolSC1));
     };
+    float m_run = -INFINITY, l_run = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
     long long spins = 0;
-    // o: thread -> (unit = row x 4-float d chunk, lane j of P); lane j takes
-    // splits j, j + P, ... in rounds of 4.  The first round's loads go out
-    // together with the (m, l) loads: one round trip for both.
-    const int units = rows * (D / 4);
-    const int P = PK_THREADS / units;  // >= 1 (rows <= 16)
-    const int u = tid / P, j = tid % P;
-    const int rr = u / (D / 4), d4 = (u % (D / 4)) * 4;
-    const bool act = u < units;
-    uint4 w[4][2];
-    auto issue = [&](int q0) __attribute__((always_inline)) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int s2 = q0 + q * P;
-        const size_t wd = (size_t)(act && s2 < S1 ? s2 : 0) * rec_words + rr * (D + 2) + d4;
-        w[q][0] = ld16(wd);
-        w[q][1] = ld16(wd + 2);
-      }
-    };
-    auto stale = [&](int q0) __attribute__((always_inline)) -> bool {
-      bool st = false;
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        st |= act && q0 + q * P < S1 &&
-              (w[q][0].y != rtag || w[q][0].w != rtag || w[q][1].y != rtag || w[q][1].w != rtag);
-      return st;
-    };
-    // (m, l) of every other split: this thread's first pair, then its first
-    // round of o chunks, validated together (re-read while any word is stale)
-    auto ml_word = [&](int i) __attribute__((always_inline)) -> size_t {
-      return (size_t)(i / rows) * rec_words + (i % rows) * (D + 2) + D;
-    };
-    const bool has_ml = tid < S1 * rows;
-    uint4 mlv = ld16(has_ml ? ml_word(tid) : 0);
-    if (S1 > 0) issue(j);
-    for (;;) {
-      const bool ml_stale = has_ml && (mlv.y != rtag || mlv.w != rtag);
-      const bool o_stale = S1 > 0 && stale(j);
-      if (!(ml_stale || o_stale) || !link_retry(a, spins)) break;
-      if (ml_stale) mlv = ld16(ml_word(tid));
-      if (o_stale) issue(j);
-    }
-    if (has_ml) {
-      ml[2 * tid] = __uint_as_float(mlv.x);
-      ml[2 * tid + 1] = __uint_as_float(mlv.z);
-    }
-    for (int i = tid + PK_THREADS; i < S1 * rows; i += PK_THREADS) {  // more pairs than threads
-      uint4 v = ld16(ml_word(i));
-      while ((v.y != rtag || v.w != rtag) && link_retry(a, spins)) v = ld16(ml_word(i));
-      ml[2 * i] = __uint_as_float(v.x);
-      ml[2 * i + 1] = __uint_as_float(v.z);
-    }
-    lds_sync();
-    if (a.profile && tid == 0) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();  // records valid
-    // per row: merged max, each split's weight, total l
-    if (tid < rows) {
-      float Mt = own_ml[2 * tid];
-      for (int s2 = 0; s2 < S1; s2++) Mt = fmaxf(Mt, ml[2 * (s2 * rows + tid)]);
-      float Lt = 0.f;
-      for (int s2 = 0; s2 <= S1; s2++) {
-        const float ms = s2 < S1 ? ml[2 * (s2 * rows + tid)] : own_ml[2 * tid];
-        const float ls = s2 < S1 ? ml[2 * (s2 * rows + tid) + 1] : own_ml[2 * tid + 1];
-        const float f = ms == -INFINITY ? 0.f : exp2f(ms - Mt);
-        fac[s2 * rows + tid] = f;
-        Lt += ls * f;
-      }
-      fac[257 * 16 - 16 + tid] = Lt;
-    }
-    lds_sync();
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (act) {
-      for (int q0 = j; q0 < S1; q0 += 4 * P) {
-        if (q0 != j) issue(q0);
-        while (stale(q0) && link_retry(a, spins)) issue(q0);
+    for (int s0 = j; s0 < S; s0 += 4 * P) {
+      uint4 wo[4][2], wm[4];
+      auto issue = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const int s2 = q0 + q * P;
-          if (s2 < S1) {
-            const float f = fac[s2 * rows + rr];
-            O.x += __uint_as_float(w[q][0].x) * f;
-            O.y += __uint_as_float(w[q][0].z) * f;
-            O.z += __uint_as_float(w[q][1].x) * f;
-            O.w += __uint_as_float(w[q][1].z) * f;
+          const int s2 = s0 + q * P;
+          const size_t base_w = (size_t)(act && s2 < S - 1 ? s2 : 0) * rec_words + rr * (D + 2);
+          wo[q][0] = ld16(base_w + d4);
+          wo[q][1] = ld16(base_w + d4 + 2);
+          wm[q] = ld16(base_w + D);
+        }
+      };
+      auto stale = [&]() __attribute__((always_inline)) -> bool {
+        bool st = false;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          st |= act && s0 + q * P < S - 1 &&
+                (wo[q][0].y != rtag || wo[q][0].w != rtag || wo[q][1].y != rtag || wo[q][1].w != rtag ||
+                 wm[q].y != rtag || wm[q].w != rtag);
+        return st;
+      };
+      issue();
+      while (stale() && link_retry(a, spins)) issue();
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int s2 = s0 + q * P;
+        if (act && s2 < S) {
+          const bool mine = s2 == S - 1;
+          const float ms = mine ? own_ml[2 * rr] : __uint_as_float(wm[q].x);
+          const float ls = mine ? own_ml[2 * rr + 1] : __uint_as_float(wm[q].z);
+          float os[4];
+          if (mine) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) os[e] = own[rr * D + d4 + e];
+          } else {
+            os[0] = __uint_as_float(wo[q][0].x);
+            os[1] = __uint_as_float(wo[q][0].z);
+            os[2] = __uint_as_float(wo[q][1].x);
+            os[3] = __uint_as_float(wo[q][1].z);
           }
+          const float mn = fmaxf(m_run, ms);
+          const float a1 = m_run == -INFINITY ? 0.f : exp2f(m_run - mn);
+          const float a2 = ms == -INFINITY ? 0.f : exp2f(ms - mn);
+          l_run = l_run * a1 + ls * a2;
+#pragma unroll
+          for (int e = 0; e < 4; e++) o[e] = o[e] * a1 + os[e] * a2;
+          m_run = mn;
         }
       }
-      float* pp = part + (size_t)(u * P + j) * 4;
-      pp[0] = O.x; pp[1] = O.y; pp[2] = O.z; pp[3] = O.w;
     }
-    lds_sync();
-    if (act && j == 0) {
-      const float* pp = part + (size_t)u * P * 4;
-      const float fo = fac[S1 * rows + rr];
-      float o0 = own[rr * D + d4] * fo, o1 = own[rr * D + d4 + 1] * fo, o2 = own[rr * D + d4 + 2] * fo,
-            o3 = own[rr * D + d4 + 3] * fo;
-      for (int q = 0; q < P; q++) {
-        o0 += pp[q * 4]; o1 += pp[q * 4 + 1]; o2 += pp[q * 4 + 2]; o3 += pp[q * 4 + 3];
+    if (a.profile && tid == 0) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();  // records read
+    // combine the P lanes of each unit
+    float Mt = m_run;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if ((2 << k) <= P) Mt = fmaxf(Mt, dpp_f(Mt, k));
+    const float f = m_run == -INFINITY ? 0.f : exp2f(m_run - Mt);
+    float lt = l_run * f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] *= f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if ((2 << k) <= P) {
+        lt += dpp_f(lt, k);
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] += dpp_f(o[e], k);
       }
-      const float Lt = fac[257 * 16 - 16 + rr];
-      const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+    if (act && j == 0) {
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
       const int jt = rr / G, g = rr % G;
       const size_t oe = (size_t)(t0 + jt) * op.out_ld + (size_t)(h * G + g) * D + d4;
-      const uint32_t lo = pack2<DT_BF16>(o0 * inv, o1 * inv), hi = pack2<DT_BF16>(o2 * inv, o3 * inv);
+      const uint32_t lo = pack2<DT_BF16>(o[0] * inv, o[1] * inv), hi = pack2<DT_BF16>(o[2] * inv, o[3] * inv);
       if (op.flags & OPF_OUT_LL) {
         const uint32_t otag = link_tag(a, t.op);
         link_store(op.out, oe, lo, otag);
@@ -1717,8 +1689,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
           sc[jb][i] = v;
           mx = fmaxf(mx, v);
         }
-#pragma unroll
-        for (int o2 = 8; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, kWave));
+        mx = row16_max(mx);
         const float mnew = fmaxf(m_i[i], mx);
         const float alpha = mnew == -INFINITY ? 1.f : exp2f(m_i[i] - mnew);
         float ls = 0.f;
@@ -1728,8 +1699,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
           ls += p;
           pw[rloc * 64 + 16 * jb + lane % 16] = p;
         }
-#pragma unroll
-        for (int o2 = 8; o2 > 0; o2 >>= 1) ls += __shfl_xor(ls, o2, kWave);
+        ls = row16_sum(ls);
         l_i[i] = l_i[i] * alpha + ls;
         m_i[i] = mnew;
         if ((lane % 16) == 0) aw[rloc * 2] = alpha;
@@ -1809,10 +1779,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
     for (int rr = 0; rr < 16; rr++)
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        float x = o_acc[rr][e];
-        x += __shfl_xor(x, 16, kWave);
-        x += __shfl_xor(x, 32, kWave);
-        o_acc[rr][e] = x;
+        o_acc[rr][e] = add_xor32(add_xor16(o_acc[rr][e]));
       }
     if (lane < 16) {
 #pragma unroll

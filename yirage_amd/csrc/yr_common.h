@@ -105,17 +105,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Max / sum over the 16 lanes of each 16-lane row (every lane of the row
+// gets the result): DPP quad permutes and row mirrors, in registers.
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+  switch (ctrl_sel) {
+    case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+  }
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) v = fmaxf(v, dpp_f(v, k));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) v += dpp_f(v, k);
+  return v;
+}
+// x + (x of lane l ^ 16) and x + (x of lane l ^ 32) by permlane swaps
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum over the 64 lanes in registers: DPP within 16-lane rows, then the
 // gfx950 permlane swaps across rows (no LDS round trips, unlike __shfl_xor).
 __device__ __forceinline__ float wave_sum_regs(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  return add_xor32(add_xor16(row16_sum(v)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
