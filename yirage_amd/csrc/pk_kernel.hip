@@ -58,6 +58,7 @@ struct Shared {
   int last_op;                    // op whose activations are staged in xs (-1: none)
   int last_T;
   int norm_rows;                  // batch > 1: rows staged raw, normalized by waves 0..T-1
+  int coop_stage;                 // batch > 1: block 0 of the input is staged by all waves after [X]
   KernelArgs args;                // this launch's arguments, for the task functions
 };
 
@@ -378,6 +379,37 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
       *reinterpret_cast<uint4*>(dst) = v[u];
       if (++xc == k) { xc = 0; xr++; }
     }
+  }
+}
+
+// Block 0 of a batch > 1 input staged by all 8 waves at once (group g of
+// stage_x goes to wave g % 8): every load is issued in one batch, so the
+// rows cost one trip through the CU's memory queue (which holds the compute
+// waves' weight prefetch) instead of one per batch of the sync wave.
+template <int TM>
+__device__ __forceinline__ void stage_x_coop(OpRef op, int T, int KB, Shared& sm, int wave, int lane) {
+  const int k = KB >> 9, total = TM * k;  // <= 64 groups (KB <= XS_ELEMS / TM)
+  const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
+  const uint32_t vo = lane * 16;
+  const int row_bytes = op.x_ld * 2;
+  uint16_t* const junk = reinterpret_cast<uint16_t*>(sm.red);
+  constexpr int NB = 8;
+  uint4 v[NB];
+#pragma unroll
+  for (int u = 0; u < NB; u++) {
+    const int g = wave + PK_WAVES * u;
+    const int mb = g / k, mc = g - mb * k;
+    const int off = g < total ? mb * row_bytes + mc * 1024 : 0x7ffffff0;
+    v[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, off, kCpolSC1));
+  }
+#pragma unroll
+  for (int u = 0; u < NB; u++) {
+    const int g = wave + PK_WAVES * u;
+    const int mb = g / k, mc = g - mb * k;
+    uint16_t* dst = g < total ? sm.xs + mb * KB + xs_swz(mb, mc * 512 + lane * 8) : junk + lane * 8;
+    *reinterpret_cast<uint4*>(dst) = v[u];
   }
 }
 
@@ -721,6 +753,8 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         if (TM == 1 && (op.flags & OPF_X_LL)) {
           stage_x_link(a, op, KB, 0, sm, lane);
           if (a.profile && lane == 0) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
+        } else if (TM > 1 && !(NORM && !pre)) {
+          if (lane == 0) sm.coop_stage = 1;  // block 0 staged by all waves after [X]
         } else {
           stage_x<TM>(op, T, KB, 0, sm, lane);
         }
@@ -758,10 +792,17 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       sm.last_op = nkb == 1 ? t.op : -1;
     }
   }
-  lds_sync();  // [X]: block 0 staged, slots cleared
-  if (a.profile && tix() == SYNC_T0) gptr(a.profile)[(size_t)task_id * 8 + 4] = now_10ns();
+  lds_sync();  // [X]: block 0 staged (or to be staged by all waves), slots cleared
   if (!sm.flag) return;
   const int T = sm.last_T;
+  if constexpr (TM > 1) {
+    if (__builtin_amdgcn_readfirstlane(sm.coop_stage)) {  // workgroup-uniform
+      stage_x_coop<TM>(op, T, KB, sm, wave, lane);
+      lds_sync();  // block 0 staged
+      if (tix() == 0) sm.coop_stage = 0;
+    }
+  }
+  if (a.profile && tix() == SYNC_T0) gptr(a.profile)[(size_t)task_id * 8 + 4] = now_10ns();
   if constexpr (NORM && MF) {
     const int nr = __builtin_amdgcn_readfirstlane(sm.norm_rows);
     if (nr > 0) {  // workgroup-uniform
@@ -2013,6 +2054,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     sm.last_op = -1;
     sm.last_T = 0;
     sm.norm_rows = 0;
+    sm.coop_stage = 0;
   }
   __syncthreads();
   for (int q = q0; q < q1; q++) {
