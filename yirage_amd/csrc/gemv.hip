@@ -22,12 +22,12 @@
 namespace yr {
 
 // K x N weights go to the MFMA kernels of skinny.hip
-size_t skinny_kn_workspace(int B, int K, int N, int nmat);
+size_t skinny_kn_workspace(int B, int K, int N, int nmat, int epi);
 int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
               const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
               void* ws, size_t ws_bytes, hipStream_t st, const char* name);
 // N x K weights, passes of 17..128 rows: the MFMA kernel of skinny.hip
-size_t skinny_nk128_workspace(int K, int N, int nmat);
+size_t skinny_nk128_workspace(int K, int N, int nmat, int epi);
 int skinny_nk128(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
                  const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat,
                  int epi, void* ws, hipStream_t st, const char* name);
@@ -225,11 +225,11 @@ static void launch_nk(const GemvArgs& a, hipStream_t st) {
 // pass streams the weights once).
 static int pass_rows(int left) { return left > 16 ? (left < 128 ? left : 128) : (left < 8 ? left : 8); }
 
-static size_t nk_workspace(int B, int K, int N, int nmat) {
+static size_t nk_workspace(int B, int K, int N, int nmat, int epi) {
   size_t need = 0;
   for (int b0 = 0; b0 < B; b0 += pass_rows(B - b0)) {
     const int rows = pass_rows(B - b0);
-    const size_t w = rows > 16 ? skinny_nk128_workspace(K, N, nmat) : plan_gemv(rows, K, N, nmat).ws;
+    const size_t w = rows > 16 ? skinny_nk128_workspace(K, N, nmat, epi) : plan_gemv(rows, K, N, nmat).ws;
     if (w > need) need = w;
   }
   return need;
@@ -246,7 +246,7 @@ static int run_gemv(GemvArgs a, int dtype, int layout, void* ws, size_t ws_bytes
   if (layout == YR_W_KN)
     return skinny_kn(a.x, a.gamma, a.w0, a.w1, a.residual, a.out, a.B, a.K, a.N, a.eps, dtype, NMAT, EPI, ws,
                      ws_bytes, st, name);
-  const size_t need = nk_workspace(a.B, a.K, a.N, NMAT);
+  const size_t need = nk_workspace(a.B, a.K, a.N, NMAT, EPI);
   if (need > ws_bytes || (need && !ws))
     return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, need);
   {
@@ -287,24 +287,24 @@ using namespace yr;
 
 extern "C" {
 
-static size_t ws_for(int batch, int k, int n, int w_layout, int nmat) {
-  if (w_layout == YR_W_KN) return skinny_kn_workspace(batch, k, n, nmat);
-  return nk_workspace(batch, k, n, nmat);
+static size_t ws_for(int batch, int k, int n, int w_layout, int nmat, int epi) {
+  if (w_layout == YR_W_KN) return skinny_kn_workspace(batch, k, n, nmat, epi);
+  return nk_workspace(batch, k, n, nmat, epi);
 }
 
 size_t yr_hip_rmsnorm_linear_workspace(int batch, int k, int n, int dtype, int w_layout) {
   (void)dtype;
-  return ws_for(batch, k, n, w_layout, 1);
+  return ws_for(batch, k, n, w_layout, 1, EPI_RMSNORM);
 }
 
 size_t yr_hip_gated_mlp_workspace(int batch, int k, int n, int dtype, int w_layout) {
   (void)dtype;
-  return ws_for(batch, k, n, w_layout, 2);
+  return ws_for(batch, k, n, w_layout, 2, EPI_GATED);
 }
 
 size_t yr_hip_linear_workspace(int batch, int k, int n, int dtype, int w_layout) {
   (void)dtype;
-  return ws_for(batch, k, n, w_layout, 1);
+  return ws_for(batch, k, n, w_layout, 1, EPI_LINEAR);
 }
 
 int yr_hip_rmsnorm_linear(const void* x, const void* gamma, const void* w, void* out, int batch, int k,

@@ -41,6 +41,7 @@ struct Args {
   float eps;
   int kch;                   // K chunks (units) per tile
   int units;                 // tiles * kch
+  int tw;                    // tile width in columns (batch-128 kernel)
 };
 
 // Unit range [lo(v), lo(v + 1)) of virtual workgroup v; the virtual workgroup
@@ -60,6 +61,7 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 constexpr uint32_t kOob = 0xfffffff0u;  // offset that is out of range for every buffer
+constexpr int kSc1 = 16;                 // buffer cache policy: sc1 (agent-scope coherence)
 
 // x * gamma, element-wise on 8 packed values, rounded to the storage type
 // (the normalised activation the reference feeds its matmul)
@@ -286,13 +288,97 @@ __device__ __forceinline__ uint4 b_frag_swz(const uint16_t* tile, int cb, int ro
   const int r0 = row0 + 8 * g + e, r1 = r0 + 4, c = cb + (q >> 1);
   const uint16_t* p0 = tile + r0 * 64 + ((c ^ w_swz(r0)) << 3) + (q & 1) * 4;
   const uint16_t* p1 = tile + r1 * 64 + ((c ^ w_swz(r1)) << 3) + (q & 1) * 4;
+  // an address-space cast (not an integer round trip) keeps the LDS object
+  // visible to the compiler's wait analysis for direct-to-LDS loads
   auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
-    return const_cast<lds_v4i16*>(reinterpret_cast<const lds_v4i16*>(
-        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(reinterpret_cast<uintptr_t>(p))));
+    return (lds_v4i16*)(const_cast<uint16_t*>(p));
   };
   const uint2 l2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p0)));
   const uint2 h2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p1)));
   return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+// 16 bytes per lane from a buffer straight into LDS (lane l's data lands at
+// lds_block + 16 l, lds_block wave-uniform); an offset past the buffer
+// writes zeros.  Issued as inline assembly: the compiler then inserts no
+// waits of its own for these loads (it cannot tell which LDS stage one
+// writes and would wait for all of them before any LDS read); the kernel
+// orders them itself (s_waitcnt vmcnt + barrier before a stage is read, and
+// a barrier after the last read of a stage before it is refilled).
+typedef int yr_i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void bload_lds16(__amdgpu_buffer_rsrc_t r, uint32_t off, void* lds_block) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(lds_block));
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+               :
+               : "v"(off), "s"(lds), "s"(r)
+               : "memory", "m0");
+}
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// K-split partial sums of a batch-128 tile: every split stores its NV
+// accumulator float4s in fragment order ([v][thread], one 1 KB store per
+// wave and v) and, for RMSNorm, its 128 row sums of squares, then arrives on
+// the tile's ticket; the last to arrive adds all records in split order (its
+// own from registers) into acc / ssl and returns true, the others false.
+// Records go through 128-bit loads / stores with the sc1 bit (the coherence
+// of agent-scope atomics, but free to pipeline).  `active`: this thread
+// holds accumulators.
+template <int NV, bool NORM>
+__device__ __forceinline__ bool merge_splits(const Args& a, int t, int splits, int sp, f32x4* acc, bool active,
+                                             float* ssl) {
+  constexpr int MB = 128;
+  constexpr int REC = NV * kThreads * 4 + MB;  // floats
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rp = rsrc(a.partial, (uint32_t)((size_t)a.units * REC * sizeof(float)));
+  const uint32_t rec0 = (uint32_t)((size_t)t * splits * REC * sizeof(float));  // split 0 of this tile
+  auto vrec = [&](int s2, int v) __attribute__((always_inline)) {
+    return rec0 + (uint32_t)(((size_t)s2 * REC + ((size_t)v * kThreads + tid) * 4) * sizeof(float));
+  };
+  if (active) {
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(yr_u32x4, acc[v]), rp, vrec(sp, v), 0, kSc1);
+  }
+  const size_t ssoff = (size_t)t * splits * REC + NV * kThreads * 4;  // floats: split 0's row sums
+  if (NORM && tid < MB) st_agent(a.partial + ssoff + (size_t)sp * REC + tid, ssl[tid]);
+  if (!arrive_last(&a.tickets[t], splits)) return false;
+  if (active) {
+    // in groups of 8 float4s: sum = record 0 + record 1 + ..., in split order
+#pragma unroll
+    for (int v0 = 0; v0 < NV; v0 += 8) {
+      constexpr int G = NV < 8 ? NV : 8;
+      static_assert(NV % G == 0, "record groups");
+      f32x4 sum[G];
+#pragma unroll
+      for (int v = 0; v < G; v++) sum[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s2 = 0; s2 < splits; s2++) {
+        f32x4 ld[G];
+#pragma unroll
+        for (int v = 0; v < G; v++)
+          ld[v] = s2 == sp ? acc[v0 + v]
+                           : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, vrec(s2, v0 + v), 0, kSc1));
+#pragma unroll
+        for (int v = 0; v < G; v++) sum[v] += ld[v];
+      }
+#pragma unroll
+      for (int v = 0; v < G; v++) acc[v0 + v] = sum[v];
+    }
+  }
+  if (NORM && tid < MB) {
+    float ssum = 0.f;
+    for (int s2 = 0; s2 < splits; s2++) ssum += ld_agent(a.partial + ssoff + (size_t)s2 * REC + tid);
+    ssl[tid] = ssum;
+  }
+  __syncthreads();
+  return true;
 }
 
 // NKL: W in N x K layout (W[N][K], torch Linear.weight).  Its rows already
@@ -300,7 +386,7 @@ __device__ __forceinline__ uint4 b_frag_swz(const uint16_t* tile, int cb, int ro
 // a W tile is staged like an x tile (64 padded rows of n) and B fragments
 // come back by plain 16-byte reads.
 template <int DT, int NMAT, int EPI, bool NKL>
-__global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
+__global__ __launch_bounds__(kThreads, 1) void sk128r_kernel(Args a) {
   constexpr int TW = 64, KS = 64, MB = 128;
   // K x N: W rows unpadded with chunks permuted by w_swz; x rows (and N x K
   // W rows) padded (fragments by 16-byte reads of 16 rows at one k)
@@ -428,42 +514,7 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
   __syncthreads();
   // C element (matrix m, block i, j2, reg q) of this lane: row 32 mg + 16 i +
   // 4 (lane / 16) + q, column 32 ng + 16 j2 + lane % 16
-  if (splits > 1) {
-    // record [split][matrix][128][64] + row sums; the last split sums them
-    constexpr int REC = NMAT * MB * TW + MB;
-    float* rec = a.partial + ((size_t)t * splits + sp) * REC;
-#pragma unroll
-    for (int m = 0; m < NMAT; m++)
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j2 = 0; j2 < 2; j2++)
-#pragma unroll
-          for (int q = 0; q < 4; q++)
-            st_agent(rec + m * MB * TW + (32 * mg + 16 * i + 4 * (lane >> 4) + q) * TW + 32 * ng + 16 * j2 + (lane & 15),
-                     acc[m][i][j2][q]);
-    if (NORM && tid < MB) st_agent(rec + NMAT * MB * TW + tid, ssl[tid]);
-    if (!arrive_last(&a.tickets[t], splits)) return;
-#pragma unroll
-    for (int m = 0; m < NMAT; m++)
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j2 = 0; j2 < 2; j2++)
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int off = m * MB * TW + (32 * mg + 16 * i + 4 * (lane >> 4) + q) * TW + 32 * ng + 16 * j2 + (lane & 15);
-            float sum = 0.f;
-            for (int s2 = 0; s2 < splits; s2++) sum += ld_agent(a.partial + ((size_t)t * splits + s2) * REC + off);
-            acc[m][i][j2][q] = sum;
-          }
-    if (NORM && tid < MB) {
-      float sum = 0.f;
-      for (int s2 = 0; s2 < splits; s2++) sum += ld_agent(a.partial + ((size_t)t * splits + s2) * REC + NMAT * MB * TW + tid);
-      ssl[tid] = sum;
-    }
-    __syncthreads();
-  }
+  if (splits > 1 && !merge_splits<NMAT * 4, NORM>(a, t, splits, sp, &acc[0][0][0], true, ssl)) return;
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -475,6 +526,244 @@ __global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
           store_out<DT, EPI>(a, b, n, acc[0][i][j2][q], NMAT == 2 ? acc[NMAT - 1][i][j2][q] : 0.f,
                              NORM ? ssl[b] : 0.f);
       }
+}
+
+// Batches of 17..128 rows: one workgroup per (tile, K split), a tile TW
+// columns of the output (128 when N allows >= 192 workgroups with two K
+// splits, else 64), a K step ("chunk") 64 rows of W per matrix and the
+// matching 128 x 64 block of x (whole 128-byte lines of x and of N x K W
+// rows: half-line chunks fetch every line twice).
+//
+// The weight stream's rate is set by how wide a row segment each workgroup
+// reads: with W in K x N layout the workgroups walk the rows of W in step,
+// each taking TW columns of every row, and 256-byte segments stream ~12 %
+// faster than 128-byte ones (measured on the gated-MLP weights, 2 x
+// 4096 x 14336; 112-byte segments, 56-column tiles on all 256 CUs, are
+// slower still).  Two K splits of 128-column tiles cost 1/16 extra bytes at
+// K = 4096 in partial records, which the pair of workgroups of one tile (on
+// one XCD) pass through that XCD's L2.
+//
+// Chunks arrive by direct buffer -> LDS loads (no registers), every 1 KB
+// one load instruction, NST - 1 chunks ahead of the MFMAs.  Each wave waits
+// for its own loads of a chunk (s_waitcnt vmcnt: one wave's loads complete
+// in order) before the barrier that publishes it; a stage is refilled only
+// after the barrier that follows its last read.  16-byte chunks of a row
+// are permuted on the global side (the LDS image of one load instruction is
+// contiguous) so that fragment reads are free of bank conflicts: 128-byte x
+// rows (and N x K W rows) by row % 8, 128-byte K x N W rows by w_swz,
+// 256-byte ones by w_swz256.
+//
+// NKL: W in N x K layout (W[N][K], torch Linear.weight).  Its rows already
+// hold 8 consecutive k of one column per 16 bytes, the B fragment's order, so
+// a W block is staged like an x block (TW rows of n) and B fragments come
+// back by plain 16-byte reads.
+__device__ __forceinline__ int x_swz(int r) { return r & 7; }
+// chunk permutation of 256-byte rows: the rows one 32-lane transposing read
+// touches (8g + e, and + 4, e < 4, g < 2) get distinct 32-byte chunk pairs
+__device__ __forceinline__ int w_swz256(int r) { return ((r & 3) | (((r >> 3) & 1) << 2)) << 1; }
+// b_frag of a w_swz256-permuted 128-column tile: 16 columns from chunk cb
+__device__ __forceinline__ uint4 b_frag_swz256(const uint16_t* tile, int cb, int lane) {
+  const int g = lane >> 4, j = lane & 15, e = j >> 2, q = j & 3;
+  const int r0 = 8 * g + e, r1 = r0 + 4, c = cb + (q >> 1);
+  const uint16_t* p0 = tile + r0 * 128 + ((c ^ w_swz256(r0)) << 3) + (q & 1) * 4;
+  const uint16_t* p1 = tile + r1 * 128 + ((c ^ w_swz256(r1)) << 3) + (q & 1) * 4;
+  auto cast = [](const uint16_t* p) __attribute__((always_inline)) {
+    return (lds_v4i16*)(const_cast<uint16_t*>(p));
+  };
+  const uint2 l2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p0)));
+  const uint2 h2 = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(cast(p1)));
+  return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+// s_waitcnt vmcnt(S * c) for a wave-uniform load count c (1 .. 8)
+template <int S>
+__device__ __forceinline__ void wait_loads(int c) {
+  switch (c) {
+    case 1: wait_vmcnt<S * 1>(); break;
+    case 2: wait_vmcnt<S * 2>(); break;
+    case 3: wait_vmcnt<S * 3>(); break;
+    case 4: wait_vmcnt<S * 4>(); break;
+    case 5: wait_vmcnt<S * 5>(); break;
+    case 6: wait_vmcnt<S * 6>(); break;
+    case 7: wait_vmcnt<S * 7>(); break;
+    default: wait_vmcnt<S * 8>(); break;
+  }
+}
+
+template <int DT, int NMAT, int EPI, bool NKL, int TW>
+__global__ __launch_bounds__(kThreads, 1) void sk128_kernel(Args a) {
+  constexpr int KS = 64, MB = 128;
+  static_assert(EPI != EPI_RMSNORM, "RMSNorm runs in sk128r_kernel (x scaled on its way into LDS)");
+  constexpr int WB = KS * TW * 2;              // bytes of one matrix's W chunk
+  constexpr int XB = MB * KS * 2;              // bytes of one x chunk
+  constexpr int SB = NMAT * WB + XB;           // bytes of a stage
+  constexpr int NST = (144 * 1024) / SB;       // stages: 3 .. 6
+  static_assert(NST >= 3, "LDS stages");
+  constexpr int NBW = WB / 1024, NB = NMAT * NBW + XB / 1024;  // 1 KB load blocks per chunk
+  constexpr int LMAX = (NB + kWaves - 1) / kWaves;
+  // compute waves: each owns 64 rows x 32 columns (4 x 2 MFMA blocks: fewer
+  // LDS fragment bytes per MFMA than 32 x 32) of every matrix, or with
+  // SPLITM (two matrices, 64-column tiles) of one: waves 0-3 W1, 4-7 W3, so
+  // that all eight waves compute; otherwise 64-column tiles leave waves 4-7
+  // to loading
+  constexpr bool SPLITM = NMAT == 2 && TW == 64;
+  constexpr int MR = 4, NBC = 2, CW = SPLITM ? kWaves : 2 * TW / 32, NMW = SPLITM ? 1 : NMAT;
+  static_assert(TW == 64 || TW == 128, "tile width");
+  __shared__ __attribute__((aligned(16))) char stg[NST][SB];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int splits = a.kch;  // K splits per tile
+  // tiles (and the splits of one tile) of one XCD (workgroup i runs on XCD
+  // i % 8) are contiguous: neighbours share DRAM pages, split pairs share L2
+  const int bid = blockIdx.x;
+  const int u = a.units % 8 == 0 ? (bid % 8) * (a.units / 8) + bid / 8 : bid;
+  const int t = u / splits, sp = u % splits;
+  const int kper = (((a.K + splits - 1) / splits) + KS - 1) / KS * KS;  // rows per split (whole chunks)
+  const int kbeg = sp * kper, kend = min(a.K, kbeg + kper);
+  const int nchunks = kend > kbeg ? (kend - kbeg + KS - 1) / KS : 0;
+  const int n0 = t * TW, nlim = min(a.N, n0 + TW);
+
+  const uint32_t wbytes = (uint32_t)((size_t)a.K * a.N * 2);
+  const __amdgpu_buffer_rsrc_t rw0 = rsrc(a.w0, wbytes);
+  const __amdgpu_buffer_rsrc_t rw1 = rsrc(NMAT == 2 ? a.w1 : a.w0, wbytes);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (uint32_t)((size_t)a.B * a.K * 2));
+
+  // load blocks j = wave + 8 i (i < cnt): j < NMAT NBW is W matrix j / NBW,
+  // block j % NBW, else x block j - NMAT NBW.  Per block: byte offset at the
+  // split's first chunk, the step per chunk, the k (relative to the chunk)
+  // that must lie below kend (1 << 30: never), the offset into a stage.
+  const int cnt = (NB - wave + kWaves - 1) / kWaves;
+  uint32_t boff[LMAX], bstep[LMAX], bdst[LMAX];
+  int bk[LMAX];
+  __amdgpu_buffer_rsrc_t rs[LMAX];
+#pragma unroll
+  for (int i = 0; i < LMAX; i++) {
+    const int j = wave + kWaves * i;
+    bdst[i] = 1024u * (uint32_t)j;
+    if (j < NMAT * NBW) {
+      const int m = j / NBW, jb = j % NBW;
+      rs[i] = m == 0 ? rw0 : rw1;
+      if constexpr (NKL) {  // 8 rows (n) of 128 bytes (64 k)
+        const int row = 8 * jb + (lane >> 3), src = (lane & 7) ^ x_swz(row), n = n0 + row;
+        const bool ok = n < nlim;
+        boff[i] = ok ? (uint32_t)(((size_t)n * a.K + kbeg + 8 * src) * 2) : kOob;
+        bstep[i] = KS * 2;
+        bk[i] = ok ? 8 * src : (1 << 30);
+      } else {              // rows (k) of TW columns: 8 rows of 128 bytes or 4 of 256
+        constexpr int CPR = TW / 8;
+        const int row = (64 / CPR) * jb + lane / CPR, p = lane % CPR;
+        const int src = p ^ (TW == 128 ? w_swz256(row) : w_swz(row)), n = n0 + 8 * src;
+        const bool ok = n < nlim;
+        boff[i] = ok ? (uint32_t)(((size_t)(kbeg + row) * a.N + n) * 2) : kOob;
+        bstep[i] = (uint32_t)(KS * a.N * 2);
+        bk[i] = ok ? row : (1 << 30);
+      }
+    } else {                // x: 8 rows of 128 bytes
+      const int row = 8 * (j - NMAT * NBW) + (lane >> 3), src = (lane & 7) ^ x_swz(row);
+      const bool ok = row < a.B && j < NB;
+      rs[i] = rx;
+      boff[i] = ok ? (uint32_t)(((size_t)row * a.K + kbeg + 8 * src) * 2) : kOob;
+      bstep[i] = KS * 2;
+      bk[i] = ok ? 8 * src : (1 << 30);
+    }
+  }
+
+  auto issue = [&](int ci, int s) __attribute__((always_inline)) {
+    const int krel = kend - kbeg - ci * KS;  // rows of the split left at chunk ci
+#pragma unroll
+    for (int i = 0; i < LMAX; i++) {
+      if (i >= cnt) break;  // wave-uniform
+      const uint32_t o = boff[i] + (uint32_t)ci * bstep[i];
+      bload_lds16(rs[i], bk[i] < krel ? o : kOob, &stg[s][bdst[i]]);
+    }
+  };
+
+  // compute wave w: rows 64 (w % 2) .., columns 32 (w / 2 % 2) .. of matrix
+  // mw (SPLITM) or of every matrix
+  const int mg = wave & 1, ng = (wave >> 1) & (TW / 32 - 1);
+  const int mw = SPLITM ? wave >> 2 : 0;
+  const bool cwave = wave < CW;
+  f32x4 acc[NMW][MR][NBC];
+#pragma unroll
+  for (int m = 0; m < NMW; m++)
+#pragma unroll
+    for (int i = 0; i < MR; i++)
+#pragma unroll
+      for (int j = 0; j < NBC; j++) acc[m][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int ci = 0; ci < NST - 1; ci++) issue(ci, ci);
+  int s = 0;  // stage of chunk ci
+  for (int ci = 0; ci < nchunks; ci++) {
+    // this wave's loads of chunk ci have landed (later chunks may be pending)
+    wait_loads<NST - 2>(cnt);
+    __syncthreads();
+    issue(ci + NST - 1, s == 0 ? NST - 1 : s - 1);  // the stage chunk ci - 1 used
+    const uint16_t* ws = reinterpret_cast<const uint16_t*>(&stg[s][0]);
+    const uint16_t* xs = reinterpret_cast<const uint16_t*>(&stg[s][NMAT * WB]);
+    if (cwave) {
+#pragma unroll
+      for (int ks = 0; ks < KS / 32; ks++) {
+        const int lc = 4 * ks + (lane >> 4);
+        uint4 af[MR];
+#pragma unroll
+        for (int i = 0; i < MR; i++) {
+          const int r = 64 * mg + 16 * i + (lane & 15);
+          af[i] = *reinterpret_cast<const uint4*>(&xs[r * KS + 8 * (lc ^ x_swz(r))]);
+        }
+#pragma unroll
+        for (int m = 0; m < NMW; m++)
+#pragma unroll
+          for (int j2 = 0; j2 < NBC; j2++) {
+            const uint16_t* wm = ws + (mw + m) * (WB / 2);
+            uint4 bf;
+            if constexpr (NKL) {
+              const int r = 32 * ng + 16 * j2 + (lane & 15);
+              bf = *reinterpret_cast<const uint4*>(&wm[r * KS + 8 * (lc ^ x_swz(r))]);
+            } else if constexpr (TW == 128) {
+              bf = b_frag_swz256(wm + 32 * ks * TW, 2 * (NBC * ng + j2), lane);
+            } else {
+              bf = b_frag_swz(wm, 2 * (NBC * ng + j2), 32 * ks, lane);
+            }
+#pragma unroll
+            for (int i = 0; i < MR; i++) acc[m][i][j2] = mfma16<DT>(af[i], bf, acc[m][i][j2]);
+          }
+      }
+    }
+    s = s + 1 == NST ? 0 : s + 1;
+  }
+  wait_vm();  // loads past the last chunk (zeros into unused stages) have landed
+  __syncthreads();
+  // C element (block i, j2, reg q) of a compute lane: row 64 mg + 16 i +
+  // 4 (lane / 16) + q, column 32 ng + 16 j2 + lane % 16
+  if (splits > 1 && !merge_splits<NMW * MR * NBC, false>(a, t, splits, sp, &acc[0][0][0], cwave, nullptr)) return;
+  // SPLITM: the W3 waves hand their sums to the W1 waves through LDS (the
+  // stages are free: every load has landed and every wave is past its reads)
+  f32x4 (*xch)[MR][NBC][kWave] = reinterpret_cast<f32x4 (*)[MR][NBC][kWave]>(&stg[0][0]);
+  if constexpr (SPLITM) {
+    static_assert(4 * MR * NBC * kWave * 16 <= NST * SB, "exchange fits the stages");
+    if (mw == 1) {
+#pragma unroll
+      for (int i = 0; i < MR; i++)
+#pragma unroll
+        for (int j2 = 0; j2 < NBC; j2++) xch[wave - 4][i][j2][lane] = acc[0][i][j2];
+    }
+    __syncthreads();
+    if (mw == 1) return;
+  }
+  if (!cwave) return;
+#pragma unroll
+  for (int i = 0; i < MR; i++)
+#pragma unroll
+    for (int j2 = 0; j2 < NBC; j2++) {
+      const f32x4 v1 = SPLITM ? xch[wave][i][j2][lane] : acc[NMW - 1][i][j2];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int b = 64 * mg + 16 * i + 4 * (lane >> 4) + q, n = n0 + 32 * ng + 16 * j2 + (lane & 15);
+        if (b < a.B && n < nlim)
+          store_out<DT, EPI>(a, b, n, acc[0][i][j2][q], NMAT == 2 ? v1[q] : 0.f, 0.f);
+      }
+    }
 }
 
 // ---------------------------------------------------------------- host side
@@ -520,31 +809,49 @@ static void launch16(const Args& a, int tw, hipStream_t st) {
   hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC>), grid, block, 0, st, a);
 }
 
-// Splits of K per 64-column tile so that tiles x splits fills the CUs.
-inline Plan plan128(int K, int N, int nmat) {
+// Batches of 17..128 rows run in sk128_kernel (direct-to-LDS) except
+// RMSNorm (x is scaled on its way into LDS, which the direct loads skip) and
+// the gated MLP with W in K x N layout, which run in sk128r_kernel
+// (register-staged); measured on MI355X at B = 128, each is the faster of
+// the two for its cases.
+inline bool dma_path(int epi, bool nkl) { return epi != EPI_RMSNORM && !(epi == EPI_GATED && !nkl); }
+
+// sk128_kernel: 128-column tiles with two K splits when that gives >= 192
+// workgroups (N >= 12288), else 64-column tiles; sk128r_kernel: 64-column
+// tiles.  K splits so that tiles x splits fills the CUs.
+inline Plan plan128(int K, int N, int nmat, int epi, bool nkl) {
   Plan p;
-  p.tw = 64;
-  p.tiles = (N + 63) / 64;
+  const bool dma = dma_path(epi, nkl);
+  p.tw = dma && (N + 127) / 128 * 2 >= 192 ? 128 : 64;
+  p.tiles = (N + p.tw - 1) / p.tw;
   int s = kGrid / p.tiles;
   const int maxs = (K + 63) / 64;
   s = s < 1 ? 1 : s > maxs ? maxs : s > 16 ? 16 : s;
   p.kch = s;
   p.kc = 0;
   p.units = p.tiles * s;
-  const int rec = nmat * 128 * 64 + 128;
+  // float4 accumulators per thread (merge_splits' NV): sk128_kernel 8 per
+  // matrix a wave holds (one of two at 64 columns), sk128r_kernel 4 per matrix
+  const int nv = dma ? (nmat == 2 && p.tw == 64 ? 1 : nmat) * 8 : nmat * 4;
+  const size_t rec = (size_t)nv * kThreads * 4 + 128;  // floats
   p.ws = s > 1 ? kTicketBytes + (size_t)p.units * rec * sizeof(float) : 0;
   return p;
 }
 
 template <int DT, int NMAT, int EPI, bool NKL = false>
 static void launch128(const Args& a, hipStream_t st) {
-  hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI, NKL>), dim3(a.units), dim3(kThreads), 0, st, a);
+  if constexpr (EPI != EPI_RMSNORM && !(EPI == EPI_GATED && !NKL)) {  // dma_path
+    if (a.tw == 128) hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI, NKL, 128>), dim3(a.units), dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL((sk128_kernel<DT, NMAT, EPI, NKL, 64>), dim3(a.units), dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((sk128r_kernel<DT, NMAT, EPI, NKL>), dim3(a.units), dim3(kThreads), 0, st, a);
+  }
 }
 
-size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
+size_t skinny_kn_workspace(int B, int K, int N, int nmat, int epi) {
   size_t need = 0;
   for (int b0 = 0; b0 < B; b0 += 128) {
-    const size_t w = B - b0 > 16 ? plan128(K, N, nmat).ws : plan16(K, N, nmat).ws;
+    const size_t w = B - b0 > 16 ? plan128(K, N, nmat, epi, false).ws : plan16(K, N, nmat).ws;
     if (w > need) need = w;
   }
   return need;
@@ -555,7 +862,7 @@ size_t skinny_kn_workspace(int B, int K, int N, int nmat) {
 int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, const uint16_t* w1,
               const uint16_t* residual, uint16_t* out, int B, int K, int N, float eps, int dtype, int nmat, int epi,
               void* ws, size_t ws_bytes, hipStream_t st, const char* name) {
-  const size_t need = skinny_kn_workspace(B, K, N, nmat);
+  const size_t need = skinny_kn_workspace(B, K, N, nmat, epi);
   if (need > ws_bytes || (need && !ws))
     return fail(YR_E_WORKSPACE, "%s: workspace %zu < required %zu", name, ws_bytes, need);
   if ((N + 63) / 64 > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
@@ -565,7 +872,7 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
   for (int b0 = 0; b0 < B; b0 += 128) {
     const int rows = B - b0 < 128 ? B - b0 : 128;
     const bool big = rows > 16;
-    const Plan p = big ? plan128(K, N, nmat) : plan16(K, N, nmat);
+    const Plan p = big ? plan128(K, N, nmat, epi, false) : plan16(K, N, nmat);
     Args a = {};
     a.x = x + (size_t)b0 * K;
     a.gamma = gamma;
@@ -581,6 +888,7 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
     a.eps = eps;
     a.kch = p.kch;
     a.units = p.units;
+    a.tw = p.tw;
 #define YR_SK(DTV, NM, EP) (big ? launch128<DTV, NM, EP>(a, st) : launch16<DTV, NM, EP>(a, p.tw, st))
     if (nmat == 2) {
       if (bf) YR_SK(DT_BF16, 2, EPI_GATED); else YR_SK(DT_F16, 2, EPI_GATED);
@@ -595,7 +903,7 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
   return YR_OK;
 }
 
-size_t skinny_nk128_workspace(int K, int N, int nmat) { return plan128(K, N, nmat).ws; }
+size_t skinny_nk128_workspace(int K, int N, int nmat, int epi) { return plan128(K, N, nmat, epi, true).ws; }
 
 // One pass of 17..128 rows with W in N x K layout (the caller checked shapes,
 // pointers and the workspace size).
@@ -605,7 +913,7 @@ int skinny_nk128(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, c
   if ((N + 63) / 64 > kMaxTickets) return fail(YR_E_INVALID, "%s: N=%d too large", name, N);
   if ((size_t)K * N * 2 >= kOob || (size_t)B * K * 2 >= kOob)
     return fail(YR_E_INVALID, "%s: operands must be < 4 GiB (32-bit buffer offsets)", name);
-  const Plan p = plan128(K, N, nmat);
+  const Plan p = plan128(K, N, nmat, epi, true);
   Args a = {};
   a.x = x;
   a.gamma = gamma;
@@ -621,6 +929,7 @@ int skinny_nk128(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, c
   a.eps = eps;
   a.kch = p.kch;
   a.units = p.units;
+  a.tw = p.tw;
   const bool bf = dtype == YR_DTYPE_BF16;
   if (nmat == 2) {
     if (bf) launch128<DT_BF16, 2, EPI_GATED, true>(a, st); else launch128<DT_F16, 2, EPI_GATED, true>(a, st);
