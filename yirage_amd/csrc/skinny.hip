@@ -208,12 +208,26 @@ __global__ __launch_bounds__(kThreads, 1) void sk16_kernel(Args a) {
       const int c0 = owner_of(tu0, U, G), c1 = owner_of(tu1 - 1, U, G);
       emit = arrive_last(&a.tickets[t], c1 - c0 + 1);
       if (emit) {
+        // contributors' records in workgroup order, up to 8 loads in flight
+        // per thread (a load consumed in the same loop iteration would cost
+        // one memory round trip per contributor)
+        // only the first contributor's range can start before the tile
+        const int side0 = unit_lo(c0, U, G) >= tu0 ? 0 : 1;
         for (int i = tid * 4; i < REC; i += kThreads * 4) {
           float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-          for (int c = c0; c <= c1; c++) {
-            const int cside = unit_lo(c, U, G) >= tu0 ? 0 : 1;
-            const float4 r = ld_agent4(a.partial + ((size_t)c * 2 + cside) * REC + i);
-            sum.x += r.x; sum.y += r.y; sum.z += r.z; sum.w += r.w;
+          for (int cb = c0; cb <= c1; cb += 8) {
+            float4 r[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+              const int c = cb + j;
+              const int cside = c == c0 ? side0 : 0;
+              r[j] = c <= c1 ? ld_agent4(a.partial + ((size_t)c * 2 + cside) * REC + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+              if (cb + j <= c1) {
+                sum.x += r[j].x; sum.y += r[j].y; sum.z += r[j].z; sum.w += r[j].w;
+              }
           }
           fin[i] = sum.x; fin[i + 1] = sum.y; fin[i + 2] = sum.z; fin[i + 3] = sum.w;
         }
