@@ -1013,11 +1013,21 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       for (int b = 0; b < T; b++) {
         float best = -INFINITY;
         int bi = 0x7fffffff;
-        for (int k = lane; k < t.i1; k += kWave) {
-          const float* rec = a.scratch + op.scratch_off + ((size_t)k * op.max_tokens + b) * 2;
-          float v = ld_agent(rec);
-          int idx = __float_as_int(ld_agent(rec + 1));
-          if (idx >= 0 && (v > best || (v == best && idx < bi))) { best = v; bi = idx; }
+        // 4 records in flight per lane (the max / lowest-index rule does not
+        // depend on the order records are compared in)
+        for (int k0 = lane; k0 < t.i1; k0 += 4 * kWave) {
+          float v[4];
+          int ix[4];
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int k = k0 + j * kWave;
+            const float* rec = a.scratch + op.scratch_off + ((size_t)k * op.max_tokens + b) * 2;
+            v[j] = k < t.i1 ? ld_agent(rec) : -INFINITY;
+            ix[j] = k < t.i1 ? __float_as_int(ld_agent(rec + 1)) : -1;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            if (ix[j] >= 0 && (v[j] > best || (v[j] == best && ix[j] < bi))) { best = v[j]; bi = ix[j]; }
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
@@ -1850,18 +1860,29 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
       const int rr = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
       float M = -INFINITY, L = 0.f;
       float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int s2 = 0; s2 < S; s2++) {
-        const float* rc = rec_base + (size_t)s2 * rec_floats + (size_t)rr * (D + 2);
-        const float ms = ld_agent(rc + D);
-        if (ms == -INFINITY) continue;
-        const float ls = ld_agent(rc + D + 1);
-        const float4 os = ld_agent4(rc + d4);
-        const float mn = fmaxf(M, ms);
-        const float fa = M == -INFINITY ? 0.f : exp2f(M - mn), fb = exp2f(ms - mn);
-        L = L * fa + ls * fb;
-        O.x = O.x * fa + os.x * fb; O.y = O.y * fa + os.y * fb;
-        O.z = O.z * fa + os.z * fb; O.w = O.w * fa + os.w * fb;
-        M = mn;
+      // records in split order, 4 splits' loads in flight per round trip
+      for (int s0 = 0; s0 < S; s0 += 4) {
+        float msv[4], lsv[4];
+        float4 osv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float* rc = rec_base + (size_t)(s0 + j) * rec_floats + (size_t)rr * (D + 2);
+          const bool ok = s0 + j < S;
+          msv[j] = ok ? ld_agent(rc + D) : -INFINITY;
+          lsv[j] = ok ? ld_agent(rc + D + 1) : 0.f;
+          osv[j] = ok ? ld_agent4(rc + d4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float ms = msv[j];
+          if (ms == -INFINITY) continue;
+          const float mn = fmaxf(M, ms);
+          const float fa = M == -INFINITY ? 0.f : exp2f(M - mn), fb = exp2f(ms - mn);
+          L = L * fa + lsv[j] * fb;
+          O.x = O.x * fa + osv[j].x * fb; O.y = O.y * fa + osv[j].y * fb;
+          O.z = O.z * fa + osv[j].z * fb; O.w = O.w * fa + osv[j].w * fb;
+          M = mn;
+        }
       }
       const float inv = L > 0.f ? 1.f / L : 0.f;
       const int jt = rr / G, g = rr % G;
