@@ -793,11 +793,16 @@ struct Plan {
 // 64-column tiles: every weight row segment a wave loads is one whole
 // 128-byte line (narrower tiles leave the other parts of a line to other
 // workgroups, which measured slower even with no cross-workgroup sums).
+// Units of 1024 K rows, or 512 when only that deals every workgroup the
+// same number of units (config 2a: 896 units of 1024 rows give workgroups 3
+// or 4, 1792 of 512 give all 7; measured 45.2 -> 44.9 us).
 inline Plan plan16(int K, int N, int nmat) {
   Plan p;
   p.tw = kTW;
-  p.kc = kKC;
   p.tiles = (N + p.tw - 1) / p.tw;
+  const long long u1024 = (long long)p.tiles * ((K + kKC - 1) / kKC);
+  const long long u512 = (long long)p.tiles * ((K + kKC / 2 - 1) / (kKC / 2));
+  p.kc = u1024 % kGrid != 0 && u512 % kGrid == 0 ? kKC / 2 : kKC;
   p.kch = (K + p.kc - 1) / p.kc;
   p.units = p.tiles * p.kch;
   const int rec = nmat * 16 * kTW + 16;
@@ -817,10 +822,10 @@ using namespace sk;
 static int grid_for(int units) { return units >= kGrid ? kGrid : units >= 8 ? units & ~7 : units; }
 
 template <int DT, int NMAT, int EPI>
-static void launch16(const Args& a, int tw, hipStream_t st) {
+static void launch16(const Args& a, int kc, hipStream_t st) {
   const dim3 grid(grid_for(a.units)), block(kThreads);
-  (void)tw;
-  hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC>), grid, block, 0, st, a);
+  if (kc == kKC / 2) hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC / 2>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((sk16_kernel<DT, NMAT, EPI, kTW, kKC>), grid, block, 0, st, a);
 }
 
 // Batches of 17..128 rows run in sk128_kernel (direct-to-LDS) except
@@ -903,7 +908,7 @@ int skinny_kn(const uint16_t* x, const uint16_t* gamma, const uint16_t* w0, cons
     a.kch = p.kch;
     a.units = p.units;
     a.tw = p.tw;
-#define YR_SK(DTV, NM, EP) (big ? launch128<DTV, NM, EP>(a, st) : launch16<DTV, NM, EP>(a, p.tw, st))
+#define YR_SK(DTV, NM, EP) (big ? launch128<DTV, NM, EP>(a, st) : launch16<DTV, NM, EP>(a, p.kc, st))
     if (nmat == 2) {
       if (bf) YR_SK(DT_BF16, 2, EPI_GATED); else YR_SK(DT_F16, 2, EPI_GATED);
     } else if (epi == EPI_RMSNORM) {
