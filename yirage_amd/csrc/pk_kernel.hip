@@ -320,7 +320,7 @@ enum { EPI_LIN = 0, EPI_NORM = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 constexpr int CW = PK_WAVES - 1;           // compute waves
 constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
 #ifndef YR_PK_RING
-#define YR_PK_RING 16
+#define YR_PK_RING 12
 #endif
 constexpr int RING = YR_PK_RING;           // weight loads in flight per compute lane (RING * 7 KiB per CU)
 constexpr int kCpolSC1 = 16;               // buffer cache policy: agent-coherent (sc1)
