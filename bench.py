@@ -199,8 +199,9 @@ def main():
                     help="only copy a 1 GiB device buffer 3 times (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only (the hip backend's persistent kernel is single-GPU; "
-              "see DESIGN.md for how the path would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the hip backend's persistent kernel runs on one "
+              "GPU; a multi-GPU step would shard the weights column-/row-parallel per layer); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     import torch
 
