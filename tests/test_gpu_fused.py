@@ -109,6 +109,39 @@ def test_gated_mlp_batch128_all_columns():
     _close(out, ref, "gated_mlp_b128")
 
 
+@pytest.mark.parametrize("B,K,N,layout,kind", [(17, 1000, 12296, 1, "linear"), (100, 1000, 12296, 0, "linear"),
+                                               (33, 1000, 12296, 0, "gated"), (64, 2048, 12296, 1, "rmsnorm"),
+                                               (128, 1000, 12296, 0, "rmsnorm")])
+def test_batch128_wide_tiles_and_edges(B, K, N, layout, kind):
+    """Batches of 17..128 rows with N >= 12288: the direct-to-LDS kernel's
+    128-column tiles with two K splits (linear, N x K gated), the last tile 8
+    columns wide (N = 96 * 128 + 8) and a partial 64-row chunk in each split
+    (K = 1000: splits of 512 and 488 rows); RMSNorm runs in the
+    register-staged kernel."""
+    import yirage_amd.fused as F
+
+    print(f"case batch128 {kind} B={B} K={K} N={N} layout={layout}", flush=True)
+    g = torch.Generator().manual_seed(1)
+    x = _randn((B, K), 1.0, torch.bfloat16, g)
+    wshape = (K, N) if layout == 1 else (N, K)
+    w = _randn(wshape, 0.02, torch.bfloat16, g)
+    lay = O.W_KN if layout == 1 else O.W_NK
+    O.set_num_threads(16)
+    if kind == "linear":
+        out = F.linear(x.cuda(), w.cuda(), w_layout=layout)
+        ref = O.linear(_f(x), _bits(w), "bf16", lay, None)
+    elif kind == "gated":
+        w3 = _randn(wshape, 0.02, torch.bfloat16, g)
+        out = F.gated_mlp(x.cuda(), w.cuda(), w3.cuda(), w_layout=layout)
+        ref = O.gated_mlp(_f(x), _bits(w), _bits(w3), "bf16", layout)
+    else:
+        gamma = (1.0 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+        out = F.rmsnorm_linear(x.cuda(), gamma.cuda(), w.cuda(), eps=1e-6, w_layout=layout)
+        ref = O.rmsnorm_linear(_f(x), _f(gamma), _bits(w), "bf16", layout, 1e-6)
+    torch.cuda.synchronize()
+    _close(out, ref, f"batch128 {kind}")
+
+
 @pytest.mark.parametrize("dtype,layout,B", [(torch.float16, 0, 4), (torch.bfloat16, 0, 4), (torch.bfloat16, 1, 4),
                                             (torch.float16, 1, 4), (torch.bfloat16, 1, 40), (torch.bfloat16, 0, 64),
                                             (torch.float16, 0, 150), (torch.bfloat16, 0, 256)])
