@@ -1,0 +1,106 @@
+"""GPU parity of the candidates the reference's search saved
+(tests/golden/saved_mugraphs/: benchmark/saved_mugraphs/{cuda,mps}/*.json and
+tests/ci-tests/qwen2.5/mirage_cached_mugraphs_*.json as shipped), loaded with
+yirage_amd.mugraph_json and run on the hip backend.  Each file's graphs are
+different factorizations of one computation; the first, a middle and the
+last plannable candidate of each file are checked against the CPU oracle
+(RMSNorm + linear, gated MLP, linear, silu-mul) or a float64 torch softmax
+attention, within rtol/atol 1e-2 (the tolerance of the reference's
+tests/python/test_tensor_program.py; atol 1e-3 for attention, whose outputs
+are averages of order 0.1)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from yirage_amd import YirageHipError
+from yirage_amd import mugraph_json as MJ
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "saved_mugraphs")
+RTOL, ATOL = 1e-2, 1e-2
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _inputs(g, stds, seed):
+    """Device tensors with each input's dims and strides (a column-major
+    weight is the transpose of a contiguous [N, K] tensor)."""
+    gen = torch.Generator().manual_seed(seed)
+    out = []
+    for t, std in zip(g.inputs, stds):
+        n = sum((d - 1) * s for d, s in zip(t.dims, t.strides)) + 1
+        base = (torch.randn(n, generator=gen) * std).to(t.dtype.torch)
+        out.append(torch.as_strided(base, t.dims, t.strides))
+    return out
+
+
+def _reference(kind, g, ins):
+    dt = "f16" if g.inputs[0].dtype.torch == torch.float16 else "bf16"
+    if kind == "attention":
+        q, k, v = (x.double() for x in ins)
+        return (torch.softmax(q @ k, -1) @ v).numpy()
+    if kind == "linear":
+        x, W = ins
+        return O.linear(x.float().numpy(), _bits(W), dt, O.W_KN)
+    if kind == "rmsnorm":
+        x, W = ins
+        return O.rmsnorm_linear(x.float().numpy(), None, _bits(W), dt, O.W_KN)
+    if kind == "rmsnorm_gamma_nk":
+        x, gm, W = ins
+        return O.rmsnorm_linear(x.float().numpy(), gm.float().numpy().reshape(-1), _bits(W.t()), dt, O.W_NK)
+    if kind == "gated":
+        x, W1, W3 = ins
+        return O.gated_mlp(x.float().numpy(), _bits(W1), _bits(W3), dt, O.W_KN)
+    if kind == "silu_mul_linear_nk":
+        a, u, W = ins
+        h = O.silu_mul(a.float().numpy(), u.float().numpy(), dt)
+        return O.linear(h, _bits(W.t()), dt, O.W_NK)
+    raise AssertionError(kind)
+
+
+CASES = [
+    # file, reference, input stds
+    ("rmsnorm_bs1.json", "rmsnorm", (1.0, 0.02)),
+    ("mirage_cached_mugraphs_647dd41aeaf656b4.json", "rmsnorm_gamma_nk", (1.0, 1.0, 0.02)),
+    ("mirage_cached_mugraphs_64644b2e7bbffb94.json", "silu_mul_linear_nk", (1.0, 1.0, 0.01)),
+    ("single_gated_mlp.json", "gated", (1.0, 0.02, 0.02)),
+    ("mps_yirage_cached_mugraphs_7310eff92c865e30.json", "linear", (1.0, 0.1)),
+    ("gqa_bs8.json", "attention", (0.5, 0.5, 1.0)),
+    ("single_mqa_bs1.json", "attention", (0.5, 0.5, 1.0)),
+    ("mha_bs1.json", "attention", (0.5, 0.5, 1.0)),
+]
+
+
+@pytest.mark.parametrize("name,kind,stds", CASES, ids=[c[0] for c in CASES])
+def test_saved_candidates_match_the_oracle(name, kind, stds):
+    gs = MJ.load(os.path.join(GOLDEN, name))
+    plannable = []
+    for i, g in enumerate(gs):
+        try:
+            g.plan(fuse=True)
+        except YirageHipError:
+            continue
+        plannable.append(i)
+    assert plannable
+    pick = sorted({plannable[0], plannable[len(plannable) // 2], plannable[-1]})
+    ins = _inputs(gs[pick[0]], stds, seed=len(name))
+    ref = _reference(kind, gs[pick[0]], ins)
+    dev = [x.cuda() for x in ins]  # dense views keep their strides
+    assert all(d.stride() == t.strides for d, t in zip(dev, gs[pick[0]].inputs))
+    for i in pick:
+        g = gs[i]
+        print(f"case {name} candidate {i} plan {g.plan(fuse=True).describe()}", flush=True)
+        got = g(inputs=dev)[0]
+        torch.cuda.synchronize()
+        err = np.abs(got.float().cpu().numpy() - ref)
+        # attention outputs average thousands of V rows (|o| ~ 0.1): a tighter atol
+        atol = 1e-3 if kind == "attention" else ATOL
+        bad = err > atol + RTOL * np.abs(ref)
+        print(f"[{name} #{i}] max abs err {err.max():.3e}, mismatches {bad.sum()}/{bad.size}", flush=True)
+        assert not bad.any(), f"{name} candidate {i}: {bad.sum()} elements outside rtol/atol"

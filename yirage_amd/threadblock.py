@@ -151,10 +151,19 @@ class TBGraph:
     def sub(self, A, B):
         return self._binary("sub", A, B)
 
+    def pow(self, A, B):
+        return self._binary("pow", A, B)
+
     def reduction(self, A, dim: int):
         dims = list(A.dims)
         dims[dim] = 1
         return self._op("reduction", [A], dims, A.dtype, A.after_accum, dim=dim)
+
+    def reduction_to_dimx(self, A, dim: int):
+        # src/threadblock/reduction.cc:49-58,112: dim `dim` reduced to reduction_dimx
+        dims = list(A.dims)
+        dims[dim] = self.reduction_dimx
+        return self._op("reduction_to_dimx", [A], dims, A.dtype, A.after_accum, dim=dim)
 
     def reduction_max(self, A, dim: int):
         dims = list(A.dims)
