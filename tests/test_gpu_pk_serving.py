@@ -58,7 +58,8 @@ def _compare_meta(dev, bm, MR, what):
 
 def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
     """CPU-only run of the schedule until `request` produces its first
-    generated token (the schedule up to there does not depend on eos)."""
+    generated token (the schedule up to there does not depend on eos).
+    Returns the token and the gap between its logit and the runner-up's."""
     tokens = np.zeros((len(prompts), max_seq), np.int64)
     for i, p in enumerate(prompts):
         tokens[i, :len(p)] = p
@@ -67,26 +68,34 @@ def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
     bm.prepare_next()
     for _ in range(200):
         T = int(bm["qo_indptr"][MR])
-        _, ids = orc.step(bm["input_tokens"][:T], bm["qo_indptr"], bm["kv_indptr"], bm["kv_indices"],
-                          bm["last_page_len"])
+        logits, ids = orc.step(bm["input_tokens"][:T], bm["qo_indptr"], bm["kv_indptr"], bm["kv_indices"],
+                               bm["last_page_len"])
+        slot = [s for s in range(MR) if bm["request_ids"][s] == request]
+        row = int(bm["qo_indptr"][slot[0] + 1]) - 1 if slot else -1
         bm["output_tokens"][:T] = ids
         bm.prepare_next()
         if bm["step"][request] >= len(prompts[request]):
-            return int(bm["tokens"][request, len(prompts[request])])
+            top = np.sort(logits[row])[-2:]
+            return int(bm["tokens"][request, len(prompts[request])]), float(top[1] - top[0])
     raise AssertionError("request never produced a token")
 
 
 @pytest.mark.parametrize("MR,MT,lens", [(2, 8, (50, 37, 5)), (3, 8, (9, 70, 3, 20))])
 def test_serving_prefill_decode_eos(MR, MT, lens):
-    seed, page, max_seq = 5, 64, 80
-    rng = np.random.default_rng(seed)
-    prompts = [rng.integers(0, CFG.vocab, n).tolist() for n in lens]
+    page, max_seq = 64, 80
     npg = (max_seq + page - 1) // page
     pool = MR * npg
     print(f"case serving MR={MR} MT={MT} prompts {list(lens)}", flush=True)
-    # eos = the first token request 1 generates, so that request ends by EOS
-    eos = _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, 1)
-    print(f"  eos token {eos}", flush=True)
+    # eos = the first token request 1 generates, so that request ends by EOS;
+    # the first seed from 5 on whose token wins by a clear margin (a near tie
+    # may go either way on the GPU, and the EOS case would not be exercised)
+    for seed in range(5, 25):
+        rng = np.random.default_rng(seed)
+        prompts = [rng.integers(0, CFG.vocab, n).tolist() for n in lens]
+        eos, gap = _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, 1)
+        if gap > 0.1:
+            break
+    print(f"  seed {seed} eos token {eos} (logit gap {gap:.3f})", flush=True)
     model = LlamaDecodeModel(CFG, batch=MR, page_size=page, seed=seed, with_prepare=True, prompts=prompts,
                              max_tokens=MT, max_requests=MR, max_seq=max_seq, eos_token_id=eos)
     torch.cuda.synchronize()

@@ -597,7 +597,7 @@ __device__ bool poll_event_sync(const KernelArgs& a, const TaskDesc& t, int task
       long long spins = 0;
       for (;;) {
         const uint32_t v = __hip_atomic_load(gptr(&a.events[t.wait_event]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (spins == 0 && a.profile) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns() | ((uint64_t)((need - v) & 0xfffffu) << 44);
+        if (spins == 0 && a.profile) gptr(a.profile)[(size_t)task_id * 8 + 7] = now_10ns();  // first poll
         if ((int32_t)(v - need) >= 0) break;
         if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
         if (++spins > a.spin_limit) {

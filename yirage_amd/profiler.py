@@ -49,10 +49,10 @@ def trace_events(profile: np.ndarray, task_table: np.ndarray) -> list:
         base = TASK_NAMES.get(ty, f"TASK_{ty}")
         n = counts.get(op, 0)
         counts[op] = n + 1
-        start, ready, end = int(rec[0]), int(rec[1]) & ((1 << 44) - 1), int(rec[2])
+        start, ready, end = int(rec[0]), int(rec[1]), int(rec[2])
         args = {"task": int(t), "op": op, "wait_us": max(0, ready - start) / 100.0 if ready else None}
         for k, name in enumerate(STAGES):
-            v = int(rec[4 + k]) & ((1 << 44) - 1)
+            v = int(rec[4 + k])
             if v:
                 args[name + "_us"] = (v - start) / 100.0
         ev.append({"name": f"{base}_{op}", "cat": base, "ph": "X", "pid": 0, "tid": int(rec[3]),
