@@ -162,3 +162,24 @@ def test_superoptimize_reads_a_previous_checkpoint():
     lora = _load("single_lora.json")[0]  # interface differs from every candidate in ckpt
     with pytest.raises(YirageHipError):
         lora.superoptimize(backend="hip", profile_iters=0, use_graph_dataset=False, previous_checkpoint=ckpt)
+
+
+def test_forloop_sum_planned_only_over_the_contraction():
+    """A `none` accumulator sums the forloop's tiles: around a matmul whose
+    forloop runs over K it is the whole matmul (planned as a linear step);
+    when the forloop runs over W's columns instead, the sum is not a matmul
+    of the whole tensors (its output is one tile wide) and the graph must
+    not be planned as one."""
+    def graph(w_forloop_dim, x_forloop_dim):
+        g = yr.new_kernel_graph()
+        X = g.new_input(dims=(8, 256), dtype=yr.float16)
+        W = g.new_input(dims=(256, 256), dtype=yr.float16)
+        tb = yr.new_threadblock_graph(grid_dim=(4, 1, 1), block_dim=(128, 1, 1), forloop_range=4, reduction_dimx=64)
+        tX = tb.new_input(dtensor=X, input_map=(-1, -1, -1), forloop_dim=x_forloop_dim)
+        tW = tb.new_input(dtensor=W, input_map=(1, -1, -1), forloop_dim=w_forloop_dim)
+        tb.new_output(stensor=tb.forloop_accum(tb.matmul(tX, tW)), output_map=(1, -1, -1))
+        g.mark_output(g.customized([X, W], tb)[0])
+        return g
+    assert graph(0, 1).plan(fuse=True).describe() == ["linear"]
+    with pytest.raises(YirageHipError):
+        graph(1, -1).plan(fuse=True)

@@ -49,20 +49,32 @@ _UNARY = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "clamp": 4, "sqrt": 5, "squ
 _BINARY = {"add": 0, "mul": 1, "div": 2, "pow": 3}
 
 
-def _strip_accum(e, forloop_range: int):
-    """A threadblock expression read over whole tensors: a `none`
-    accumulator lays the forloop's tiles side by side and a `sum`
-    accumulator of a matmul adds its K-chunk partial products, so both equal
-    the expression on whole tensors; a `sum` of anything else is the
-    identity only when the forloop runs once."""
+def _leaves(e):
+    return [e] if e[0] == "in" else [x for y in e[1:] if isinstance(y, tuple) for x in _leaves(y)]
+
+
+def _strip_accum(e, forloop_range: int, fl):
+    """A threadblock expression read over whole tensors.  A `none` or `sum`
+    forloop accumulator adds the tiles of the forloop's iterations
+    (src/threadblock/forloop_accum.cc:131-150: the output has the tile's
+    shape).  Around a matmul whose contraction the forloop splits (every
+    input under its left operand iterated along its last dim, every input
+    under its right operand along its second-to-last; fl[i] = (forloop_dim,
+    rank) of input i), that sum is the matmul of the whole tensors; when the
+    forloop runs once it is the identity.  Any other accumulator is kept, so
+    the expression matches no whole-tensor pattern."""
     if e[0] == "in":
         return e
     if e[0] == "accum":
-        inner = _strip_accum(e[2], forloop_range)
-        if e[1] == "none" or (e[1] == "sum" and (forloop_range == 1 or inner[0] == "matmul")):
-            return inner
+        inner = _strip_accum(e[2], forloop_range, fl)
+        if e[1] in ("none", "sum"):
+            if forloop_range == 1:
+                return inner
+            if e[2][0] == "matmul" and all(fl[x[1]][0] == fl[x[1]][1] - 1 for x in _leaves(e[2][1])) \
+                    and all(fl[x[1]][0] == fl[x[1]][1] - 2 for x in _leaves(e[2][2])):
+                return inner
         return ("accum", e[1], inner)
-    return (e[0],) + tuple(_strip_accum(x, forloop_range) for x in e[1:])
+    return (e[0],) + tuple(_strip_accum(x, forloop_range, fl) for x in e[1:])
 
 
 def _fbits(x: float) -> int:
@@ -796,7 +808,8 @@ class _Lowering:
         ex = bg.expressions()
         i0, i1, i2 = ("in", 0), ("in", 1), ("in", 2)
         ins = root.inputs
-        stripped = [_strip_accum(e, bg.forloop_range) for e in ex]
+        fl = [(t.op.attrs["forloop_dim"], len(t.dims)) for _, t in bg.inputs]
+        stripped = [_strip_accum(e, bg.forloop_range, fl) for e in ex]
         if all(e[0] == "in" and ins[e[1]].dims == o.dims and ins[e[1]].dtype == o.dtype
                for e, o in zip(stripped, root.outputs)):
             # copies of whole inputs (tiles loaded and stored back): alias them
