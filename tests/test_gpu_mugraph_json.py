@@ -2,10 +2,12 @@
 (tests/golden/saved_mugraphs/: benchmark/saved_mugraphs/{cuda,mps}/*.json and
 tests/ci-tests/qwen2.5/mirage_cached_mugraphs_*.json as shipped), loaded with
 yirage_amd.mugraph_json and run on the hip backend.  Each file's graphs are
-different factorizations of one computation; the first, a middle and the
-last plannable candidate of each file are checked against the CPU oracle
-(RMSNorm + linear, gated MLP, linear, silu-mul) or a float64 torch softmax
-attention, within rtol/atol 1e-2 (the tolerance of the reference's
+different factorizations of one computation; every plannable candidate
+(the first, a middle and the last of files with more than 8) is checked
+against the CPU oracle (RMSNorm + linear, gated MLP, linear, silu-mul) or a
+float64 torch restatement of the benchmark's graph (softmax attention,
+LoRA, the norm-transformer block: candidates the fused patterns do not cover
+run as generic steps), within rtol/atol 1e-2 (the tolerance of the reference's
 tests/python/test_tensor_program.py; atol 1e-3 for attention, whose outputs
 are averages of order 0.1)."""
 import os
@@ -61,6 +63,17 @@ def _reference(kind, g, ins):
         a, u, W = ins
         h = O.silu_mul(a.float().numpy(), u.float().numpy(), dt)
         return O.linear(h, _bits(W.t()), dt, O.W_NK)
+    if kind == "lora":
+        # benchmark/lora.py: O = X W + (X A) B
+        x, W, A, B = (t.double() for t in ins)
+        return (x @ W + (x @ A) @ B).numpy()
+    if kind == "ntrans":
+        # benchmark/norm_transformer.py: O = rms_norm(X + alpha (rms_norm(H) + X))
+        H, x, alpha = (t.double() for t in ins)
+
+        def rms(t):
+            return t / torch.sqrt((t * t).mean(-1, keepdim=True) + 1e-6)
+        return rms(x + alpha * (rms(H) + x)).numpy()
     raise AssertionError(kind)
 
 
@@ -73,7 +86,11 @@ CASES = [
     ("mps_yirage_cached_mugraphs_7310eff92c865e30.json", "linear", (1.0, 0.1)),
     ("gqa_bs8.json", "attention", (0.5, 0.5, 1.0)),
     ("single_mqa_bs1.json", "attention", (0.5, 0.5, 1.0)),
-    ("mha_bs1.json", "attention", (0.5, 0.5, 1.0)),
+    # one MHA candidate runs the graph literally (generic steps: exp without
+    # max subtraction, fp16 row sums), so scores stay small enough for fp16
+    ("mha_bs1.json", "attention", (0.25, 0.25, 1.0)),
+    ("single_lora.json", "lora", (1.0, 0.05, 0.05, 0.25)),
+    ("ntrans_bs1.json", "ntrans", (1.0, 1.0, 1.0)),
 ]
 
 
@@ -88,7 +105,7 @@ def test_saved_candidates_match_the_oracle(name, kind, stds):
             continue
         plannable.append(i)
     assert plannable
-    pick = sorted({plannable[0], plannable[len(plannable) // 2], plannable[-1]})
+    pick = plannable if len(plannable) <= 8 else sorted({plannable[0], plannable[len(plannable) // 2], plannable[-1]})
     ins = _inputs(gs[pick[0]], stds, seed=len(name))
     ref = _reference(kind, gs[pick[0]], ins)
     dev = [x.cuda() for x in ins]  # dense views keep their strides
@@ -104,3 +121,24 @@ def test_saved_candidates_match_the_oracle(name, kind, stds):
         bad = err > atol + RTOL * np.abs(ref)
         print(f"[{name} #{i}] max abs err {err.max():.3e}, mismatches {bad.sum()}/{bad.size}", flush=True)
         assert not bad.any(), f"{name} candidate {i}: {bad.sum()} elements outside rtol/atol"
+
+
+def test_customized_whole_tensor_expression_matches_torch():
+    """A customized op that no fused pattern covers, lowered to generic
+    steps: exp over a 2 x 2 grid of tiles, placed back where they came from,
+    equals torch.exp of the whole tensor (fp16 rounding)."""
+    import yirage_amd as yr
+
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(64, 64), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 2, 1), block_dim=(128, 1, 1), forloop_range=1, reduction_dimx=64)
+    tX = tb.new_input(dtensor=X, input_map=(0, 1, -1), forloop_dim=-1)
+    tb.new_output(stensor=tb.forloop_accum(tb.exp(tX)), output_map=(0, 1, -1))
+    g.mark_output(g.customized([X], tb)[0])
+    x = (torch.randn((64, 64), generator=torch.Generator().manual_seed(1))).half()
+    got = g(inputs=[x.cuda()])[0]
+    torch.cuda.synchronize()
+    assert g._plan.describe() == ["exp"]
+    ref = torch.exp(x.double()).numpy()
+    err = np.abs(got.float().cpu().numpy() - ref)
+    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"

@@ -49,32 +49,142 @@ _UNARY = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "clamp": 4, "sqrt": 5, "squ
 _BINARY = {"add": 0, "mul": 1, "div": 2, "pow": 3}
 
 
-def _leaves(e):
-    return [e] if e[0] == "in" else [x for y in e[1:] if isinstance(y, tuple) for x in _leaves(y)]
+_TB_UNARY = ("exp", "silu", "gelu", "relu", "sqrt", "square")
+_TB_BINARY = ("add", "mul", "div", "pow")
 
 
-def _strip_accum(e, forloop_range: int, fl):
-    """A threadblock expression read over whole tensors.  A `none` or `sum`
-    forloop accumulator adds the tiles of the forloop's iterations
-    (src/threadblock/forloop_accum.cc:131-150: the output has the tile's
-    shape).  Around a matmul whose contraction the forloop splits (every
-    input under its left operand iterated along its last dim, every input
-    under its right operand along its second-to-last; fl[i] = (forloop_dim,
-    rank) of input i), that sum is the matmul of the whole tensors; when the
-    forloop runs once it is the identity.  Any other accumulator is kept, so
-    the expression matches no whole-tensor pattern."""
-    if e[0] == "in":
-        return e
-    if e[0] == "accum":
-        inner = _strip_accum(e[2], forloop_range, fl)
-        if e[1] in ("none", "sum"):
-            if forloop_range == 1:
-                return inner
-            if e[2][0] == "matmul" and all(fl[x[1]][0] == fl[x[1]][1] - 1 for x in _leaves(e[2][1])) \
-                    and all(fl[x[1]][0] == fl[x[1]][1] - 2 for x in _leaves(e[2][2])):
-                return inner
-        return ("accum", e[1], inner)
-    return (e[0],) + tuple(_strip_accum(x, forloop_range, fl) for x in e[1:])
+def _whole_exprs(bg, in_dims):
+    """Each output of a threadblock graph as an expression over whole
+    tensors, or None where the tiles' arithmetic is not such an expression.
+
+    Tiles of an input are the device tensor cut along input_map by the grid
+    and along forloop_dim by the forloop.  Elementwise ops, matmuls over
+    contractions the grid does not cut, and row operations (rms_norm,
+    reductions) over uncut dims commute with that cutting, so the op applied
+    to the whole tensors gives the tiles of the result -- provided every
+    grid axis cuts the operands of an op along the same dim of the result
+    (or an operand is broadcast along it) and the output map puts each tile
+    back where that dim says.  A forloop accumulator adds its input over the
+    iterations (src/threadblock/forloop_accum.cc:131-150); `sum` first
+    reduces the tile's last dim.  Around a matmul whose contraction the
+    forloop splits, the `none` accumulation (or `sum` of a one-wide tile) is
+    the whole matmul; a forloop that runs once makes it the identity (`sum`:
+    a reduction over the last dim).  Other accumulators (rms, sum_todimx,
+    ...) are kept as ("accum", kind, x) for the fused patterns to recognise.
+    An output stored per iteration (forloop_dim >= 0) must be cut by the
+    forloop along that dim only; any other output must not depend on the
+    iteration.  `in_dims` are the whole input dims; each result is (expr,
+    whole dims)."""
+    R = bg.forloop_range
+    axes = [a for a in range(3) if bg.grid_dim[a] > 1]
+    # id(STensor) -> (expr, whole dims, forloop-cut dims, K-split pending,
+    # grid cut: dim per axis, -1 = not cut), or None
+    val = {}
+    for i, (_, t) in enumerate(bg.inputs):
+        fd = t.op.attrs["forloop_dim"]
+        im = tuple(t.op.attrs["input_map"]) + (-1,) * 3
+        gm = tuple(im[a] if a in axes else -1 for a in range(3))
+        val[id(t)] = (("in", i), tuple(in_dims[i]), frozenset([fd]) if fd >= 0 and R > 1 else frozenset(), False, gm)
+
+    def bcast(a, b):
+        if len(a) != len(b) or any(x != y and x > 1 and y > 1 for x, y in zip(a, b)):
+            return None
+        return tuple(max(x, y) for x, y in zip(a, b))
+
+    def join_cut(ga, gb, wa, wb):
+        """Grid cut of an elementwise result, or None: an operand the axis
+        does not cut must be broadcast (whole dim 1) along the other's dim."""
+        out = []
+        for a in range(3):
+            x, y = ga[a], gb[a]
+            if x == y or (x >= 0 and y < 0 and wb[x] == 1):
+                out.append(x)
+            elif x < 0 and y >= 0 and wa[y] == 1:
+                out.append(y)
+            else:
+                return None
+        return tuple(out)
+
+    for op in bg.ops:
+        if op.kind == "input":
+            continue
+        out = op.outputs[0]
+        ins = [val.get(id(x)) for x in op.inputs]
+        r = None
+        if all(v is not None for v in ins) and not any(v[3] for v in ins if op.kind != "accum"):
+            k = op.kind
+            if k in _TB_UNARY:
+                e, wd, fp, _, gm = ins[0]
+                r = ((k, e), wd, fp, False, gm)
+            elif k == "rms_norm":
+                e, wd, fp, _, gm = ins[0]
+                if op.inputs[0].dims[-1] == wd[-1]:  # whole rows in every tile
+                    r = (("rms_norm", e), wd, fp, False, gm)
+            elif k in _TB_BINARY:
+                (ea, wa, fa, _, ga), (eb, wb, fb, _, gb) = ins
+                A, B = op.inputs
+                wd = bcast(wa, wb)
+                # a dim broadcast within the tiles must be broadcast in the whole
+                # tensors (equal tile dims: cut alike, or a one-row operand
+                # that every block reads whole, i.e. a whole-tensor broadcast)
+                if wd is not None and all(A.dims[d] == B.dims[d] or (wa[d] if A.dims[d] == 1 else wb[d]) == 1
+                                          for d in range(len(wd))):
+                    gm = join_cut(ga, gb, wa, wb)
+                    if gm is not None:
+                        r = ((k, ea, eb), wd, fa | fb, False, gm)
+            elif k == "reduction":
+                e, wd, fp, _, gm = ins[0]
+                d = op.attrs["dim"]
+                if op.inputs[0].dims[d] == wd[d]:
+                    w2 = list(wd)
+                    w2[d] = 1
+                    r = (("reduction", e, d), tuple(w2), fp, False, gm)
+            elif k == "matmul":
+                (ea, wa, fa, _, ga), (eb, wb, fb, _, gb) = ins
+                A, B = op.inputs
+                n = len(wa)
+                gm = []
+                for a in range(3):
+                    x, y = ga[a], gb[a]
+                    if x == n - 1 or y == n - 2 or (x >= 0 and y >= 0 and x != y):
+                        gm = None  # a grid-cut contraction, or two different cuts on one axis
+                        break
+                    if (x >= 0 and x < n - 2 and y != x) or (y >= 0 and y < n - 2 and x != y):
+                        gm = None  # a batch dim cut in one operand only
+                        break
+                    gm.append(x if x >= 0 else y)
+                if gm is not None and len(wb) == n and wa[-1] == wb[-2] and wa[:-2] == wb[:-2]:
+                    ks = (n - 1) in fa
+                    if ks == ((n - 2) in fb) and A.dims[-1] * (R if ks else 1) == wa[-1]:
+                        fp = frozenset(d for d in fa if d < n - 1) | frozenset(d for d in fb if d != n - 2)
+                        r = (("matmul", ea, eb), wa[:-1] + (wb[-1],), fp, ks, tuple(gm))
+            elif k == "accum":
+                e, wd, fp, ks, gm = ins[0]
+                acc = op.attrs["acc"]
+                x = op.inputs[0]
+                one_wide = x.dims[-1] == 1
+                if ks and not (fp - {len(wd) - 1}) and (acc == "none" or (acc == "sum" and one_wide)):
+                    r = (e, wd, frozenset(), False, gm)
+                elif not ks and R == 1 and acc == "none":
+                    r = (e, wd, frozenset(), False, gm)
+                elif not ks and R == 1 and acc == "sum":
+                    if one_wide:
+                        r = (e, wd, frozenset(), False, gm)
+                    elif x.dims[-1] == wd[-1]:
+                        r = (("reduction", e, len(wd) - 1), wd[:-1] + (1,), frozenset(), False, gm)
+                elif not ks and acc == "rms" and fp <= {len(wd) - 1} and x.dims[-1] * (R if fp else 1) == wd[-1]:
+                    r = (("accum", "rms", e), wd[:-1] + (1,), frozenset(), False, gm)
+        val[id(out)] = r
+    res = []
+    for st, omap, ofd in bg.outputs:
+        v = val.get(id(st))
+        om = tuple(omap) + (-1,) * 3
+        if v is None or v[3] or v[2] != (frozenset([ofd]) if ofd >= 0 and R > 1 else frozenset()) \
+                or any(om[a] != v[4][a] for a in axes):
+            res.append(None)
+        else:
+            res.append((v[0], v[1]))
+    return res
 
 
 def _fbits(x: float) -> int:
@@ -808,16 +918,16 @@ class _Lowering:
         ex = bg.expressions()
         i0, i1, i2 = ("in", 0), ("in", 1), ("in", 2)
         ins = root.inputs
-        fl = [(t.op.attrs["forloop_dim"], len(t.dims)) for _, t in bg.inputs]
-        stripped = [_strip_accum(e, bg.forloop_range, fl) for e in ex]
-        if all(e[0] == "in" and ins[e[1]].dims == o.dims and ins[e[1]].dtype == o.dtype
+        whole = _whole_exprs(bg, [t.dims for t in ins])
+        stripped = [w[0] if w is not None and w[1] == o.dims else None for w, o in zip(whole, root.outputs)]
+        if all(e is not None and e[0] == "in" and ins[e[1]].dims == o.dims and ins[e[1]].dtype == o.dtype
                for e, o in zip(stripped, root.outputs)):
             # copies of whole inputs (tiles loaded and stored back): alias them
             def emit():
                 for e, o in zip(stripped, root.outputs):
                     self.ref[o.guid] = self.dense(ins[e[1]])
             return [], emit
-        if len(ex) == 1:
+        if len(ex) == 1 and stripped[0] is not None:
             r = self._customized_single(root, stripped[0])
             if r is not None:
                 return r
@@ -1026,10 +1136,102 @@ class _Lowering:
             self.emit(_lib.OP_RMSNORM, [self.dense(A)], [self.out_ref(out)],
                       [rows // n, n, A.dtype.code, _fbits(_EPS)], "rms_norm")
         elif k == "customized":
-            raise YirageHipError("hip backend: this customized threadblock graph matches no fused kernel "
-                                 "(supported: RMSNorm+linear, gated MLP, the two-op GQA of the reference demos)")
+            if not self._lower_customized(op):
+                raise YirageHipError("hip backend: this customized threadblock graph matches no fused kernel "
+                                     "(RMSNorm+linear, gated MLP, GQA, linear) and is not an expression over "
+                                     "whole tensors the generic operators can run")
         else:
             raise YirageHipError(f"hip backend: no kernel for op {k}")
+
+    def _lower_customized(self, op: KNOp) -> bool:
+        """A customized op whose threadblock graph is, output by output, an
+        expression over whole tensors (elementwise ops, matmul, rms_norm,
+        reductions; see _whole_exprs) runs as generic operator steps, one per
+        distinct subexpression.  False (nothing emitted) otherwise."""
+        bg = op.attrs["bgraph"]
+        ins = op.inputs
+        whole = _whole_exprs(bg, [t.dims for t in ins])
+        if any(w is None or w[1] != o.dims for w, o in zip(whole, op.outputs)):
+            return False
+        lowerable = ("in", "matmul", "rms_norm", "reduction") + _TB_UNARY + _TB_BINARY
+
+        def ok(e):
+            return e[0] in lowerable and all(ok(x) for x in e[1:] if isinstance(x, tuple))
+        if not all(ok(w[0]) for w in whole):
+            return False
+        dt = ins[0].dtype
+        if any(t.dtype != dt for t in ins) or dt not in (float16, bfloat16):
+            return False
+        steps = []  # (kind, operand refs, out ref, params, name), emitted only if every output lowers
+        memo = {}
+
+        def lower(e, dest=None):
+            """(ref, dims) of expression e; dest: where the last step writes."""
+            if e in memo:
+                return memo[e]
+            if e[0] == "in":
+                t = ins[e[1]]
+                r = (self.dense(t), t.dims)
+            elif e[0] == "matmul":
+                (ra, da), (rb, db) = lower(e[1]), lower(e[2])
+                dims = da[:-1] + (db[-1],)
+                batch = 1
+                for d in da[:-2]:
+                    batch *= d
+                o = dest or self.plan.tmp(dims, dt)
+                steps.append((_lib.OP_MATMUL, [ra, rb], o, [batch, da[-2], db[-1], da[-1], dt.code], "matmul"))
+                r = (o, dims)
+            elif e[0] in _TB_BINARY:
+                (ra, da), (rb, db) = lower(e[1]), lower(e[2])
+                dims = tuple(max(x, y) for x, y in zip(da, db))
+                o = dest or self.plan.tmp(dims, dt)
+                steps.append((_lib.OP_BINARY, [ra, rb], o, [len(da), _BINARY[e[0]], dt.code, *da, *db], e[0]))
+                r = (o, dims)
+            elif e[0] == "rms_norm":
+                ra, da = lower(e[1])
+                n = da[-1]
+                rows = 1
+                for d in da[:-1]:
+                    rows *= d
+                o = dest or self.plan.tmp(da, dt)
+                steps.append((_lib.OP_RMSNORM, [ra], o, [rows, n, dt.code, _fbits(_EPS)], "rms_norm"))
+                r = (o, da)
+            elif e[0] == "reduction":
+                ra, da = lower(e[1])
+                d = e[2]
+                outer = inner = 1
+                for x in da[:d]:
+                    outer *= x
+                for x in da[d + 1:]:
+                    inner *= x
+                dims = da[:d] + (1,) + da[d + 1:]
+                o = dest or self.plan.tmp(dims, dt)
+                steps.append((_lib.OP_REDUCTION, [ra], o, [outer, da[d], inner, dt.code], "reduction"))
+                r = (o, dims)
+            else:  # unary
+                ra, da = lower(e[1])
+                n = 1
+                for x in da:
+                    n *= x
+                o = dest or self.plan.tmp(da, dt)
+                steps.append((_lib.OP_UNARY, [ra], o, [n, _UNARY[e[0]], dt.code, 0, 0], e[0]))
+                r = (o, da)
+            memo[e] = r
+            return r
+
+        results = []
+        for w, out in zip(whole, op.outputs):
+            e = w[0]
+            if e[0] == "in" or e in memo:
+                results.append((out, lower(e)[0], False))
+            else:
+                results.append((out, lower(e, self.out_ref(out))[0], True))
+        for kind, a, o, params, name in steps:
+            self.emit(kind, a, [o], params, name)
+        for out, ref, written in results:
+            if not written:
+                self.ref[out.guid] = ref
+        return True
 
     # -------------------------------------------------------- driver
     def run(self) -> Plan:
