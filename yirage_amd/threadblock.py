@@ -6,10 +6,10 @@ reduction}.cc: an input tile is the device tensor divided along the
 input_map dims by the grid and along forloop_dim by forloop_range; an output
 multiplies back along output_map / forloop_dim; forloop_accum keeps, reduces
 to 1 or to reduction_dimx the last dim.  The hip backend does not generate
-code from a threadblock graph: `KNGraph.superoptimize(backend='hip')`
-recognises the customized ops the reference's own demos and tests build
-(fused RMSNorm+linear, gated MLP, the two-op GQA) by their expression and
-runs the matching fused kernel.
+per-graph code from a threadblock graph: the kernel-graph planner reads its
+outputs as expressions (`expressions()`, and over whole tensors where the
+tiling allows), runs the fused kernel of a recognised pattern (RMSNorm +
+linear, gated MLP, GQA, linear) and otherwise the generic operators.
 """
 from __future__ import annotations
 
