@@ -170,9 +170,18 @@ int yr_hip_graph_attention(const void* q, const void* k, const void* v, void* ou
  * (e.g. column-major, kernel.py:196-210) graph inputs dense. */
 int yr_hip_graph_pack(const void* src, void* dst, int g, int rows, int cols, int dst_cols, const int64_t* strides6,
                       int dtype, void* stream);
+/* dst[sum_d c_d dst_strides[d]] = src[sum_d c_d src_strides[d]] for every
+ * coordinate c of dims (ndim <= 8; element strides, 0 broadcasts).  The tile
+ * gathers and scatters of a customized op's input / output maps
+ * (src/kernel/customized.cc, src/threadblock/input_loader.cc, output.cc) when
+ * the op's threadblock graph runs operator by operator over all its tiles. */
+int yr_hip_graph_copy_nd(const void* src, void* dst, int ndim, const int64_t* dims, const int64_t* src_strides,
+                         const int64_t* dst_strides, int dtype, void* stream);
 /* y = f(x) elementwise; kind 0 exp, 1 silu, 2 gelu (erf form), 3 relu,
  * 4 clamp(lo, hi), 5 sqrt, 6 square
- * (include/yirage/transpiler/runtime/kernel/element_unary.h:22-40). */
+ * (include/yirage/transpiler/runtime/kernel/element_unary.h:22-40), 7 x * lo
+ * (the threadblock mul_scalar the reference's transpiler inserts for rms
+ * accumulators, src/transpiler/transpile.cc:681-693). */
 int yr_hip_graph_unary(const void* x, void* y, int64_t n, int kind, float lo, float hi, int dtype, void* stream);
 /* out = a (op) b with size-1 broadcasting over ndim <= 6 dims (output dims
  * = elementwise max); kind 0 add, 1 mul, 2 div, 3 pow
@@ -213,7 +222,8 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
  *   YR_OP_BINARY:         in {a, b}, out {c}; params {ndim, kind, dtype, dims_a[ndim], dims_b[ndim]}
  *   YR_OP_REDUCTION:      in {x}, out {y}; params {outer, red, inner, dtype}
  *   YR_OP_RMSNORM:        in {x}, out {y}; params {rows, n, dtype, eps_bits}
- *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...} */
+ *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...}
+ *   YR_OP_COPY_ND:        in {src}, out {dst}; params {ndim, dtype, dims[8], src_strides[8], dst_strides[8]} */
 #define YR_OP_RMSNORM_LINEAR 1
 #define YR_OP_GATED_MLP 2
 #define YR_OP_GQA_PREFILL 3
@@ -226,6 +236,7 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
 #define YR_OP_REDUCTION 10
 #define YR_OP_RMSNORM 11
 #define YR_OP_PACK 12
+#define YR_OP_COPY_ND 13
 int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);

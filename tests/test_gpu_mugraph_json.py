@@ -3,11 +3,14 @@
 tests/ci-tests/qwen2.5/mirage_cached_mugraphs_*.json as shipped), loaded with
 yirage_amd.mugraph_json and run on the hip backend.  Each file's graphs are
 different factorizations of one computation; every plannable candidate
-(the first, a middle and the last of files with more than 8) is checked
+(in files with more than 8: the first, a middle, the last and the first of
+each distinct plan) is checked
 against the CPU oracle (RMSNorm + linear, gated MLP, linear, silu-mul) or a
 float64 torch restatement of the benchmark's graph (softmax attention,
-LoRA, the norm-transformer block: candidates the fused patterns do not cover
-run as generic steps), within rtol/atol 1e-2 (the tolerance of the reference's
+LoRA, the norm-transformer block: candidates the fused patterns do not
+cover run as generic steps, or literally, tile by tile) or, for the saved
+qk-norm candidates, a block-by-block numpy emulation of their own
+threadblock graphs, within rtol/atol 1e-2 (the tolerance of the reference's
 tests/python/test_tensor_program.py; atol 1e-3 for attention, whose outputs
 are averages of order 0.1)."""
 import os
@@ -67,6 +70,10 @@ def _reference(kind, g, ins):
         # benchmark/lora.py: O = X W + (X A) B
         x, W, A, B = (t.double() for t in ins)
         return (x @ W + (x @ A) @ B).numpy()
+    if kind == "emulate":
+        # the graph's own threadblock semantics, block by block (tests/tb_numpy.py)
+        from tb_numpy import run_graph
+        return run_graph(g, [t.double().numpy() for t in ins])[0]
     if kind == "ntrans":
         # benchmark/norm_transformer.py: O = rms_norm(X + alpha (rms_norm(H) + X))
         H, x, alpha = (t.double() for t in ins)
@@ -91,6 +98,10 @@ CASES = [
     ("mha_bs1.json", "attention", (0.25, 0.25, 1.0)),
     ("single_lora.json", "lora", (1.0, 0.05, 0.05, 0.25)),
     ("ntrans_bs1.json", "ntrans", (1.0, 1.0, 1.0)),
+    # the saved qk-norm candidates that plan do not compute the benchmark's
+    # softmax(rms_norm(Q) K) rms_norm(V) (they scale K's rows by row sums of
+    # rms_norm(Q)); they are checked against their own block-by-block semantics
+    ("qknorm_gqa_bs1_subset.json", "emulate", (1.0, 0.02, 1.0)),  # K small: the literal fp16 row sums stay finite
 ]
 
 
@@ -105,9 +116,15 @@ def test_saved_candidates_match_the_oracle(name, kind, stds):
             continue
         plannable.append(i)
     assert plannable
-    pick = plannable if len(plannable) <= 8 else sorted({plannable[0], plannable[len(plannable) // 2], plannable[-1]})
+    if len(plannable) <= 8:
+        pick = plannable
+    else:  # first, middle, last, and the first of every distinct plan
+        first_of = {}
+        for i in plannable:
+            first_of.setdefault(tuple(gs[i].plan(fuse=True).describe()), i)
+        pick = sorted({plannable[0], plannable[len(plannable) // 2], plannable[-1], *first_of.values()})
     ins = _inputs(gs[pick[0]], stds, seed=len(name))
-    ref = _reference(kind, gs[pick[0]], ins)
+    ref = _reference(kind, gs[pick[0]], ins) if kind != "emulate" else None
     dev = [x.cuda() for x in ins]  # dense views keep their strides
     assert all(d.stride() == t.strides for d, t in zip(dev, gs[pick[0]].inputs))
     for i in pick:
@@ -115,6 +132,8 @@ def test_saved_candidates_match_the_oracle(name, kind, stds):
         print(f"case {name} candidate {i} plan {g.plan(fuse=True).describe()}", flush=True)
         got = g(inputs=dev)[0]
         torch.cuda.synchronize()
+        if kind == "emulate":
+            ref = _reference(kind, g, ins)
         err = np.abs(got.float().cpu().numpy() - ref)
         # attention outputs average thousands of V rows (|o| ~ 0.1): a tighter atol
         atol = 1e-3 if kind == "attention" else ATOL
@@ -140,5 +159,28 @@ def test_customized_whole_tensor_expression_matches_torch():
     torch.cuda.synchronize()
     assert g._plan.describe() == ["exp"]
     ref = torch.exp(x.double()).numpy()
+    err = np.abs(got.float().cpu().numpy() - ref)
+    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+
+
+def test_customized_block_transpose_runs_literally():
+    """A customized op whose output map puts each block's tile at the
+    transposed block position is no whole-tensor expression: it runs tile by
+    tile (gather, exp, scatter) and must equal exp of X with its 32 x 32
+    blocks swapped across the diagonal."""
+    import yirage_amd as yr
+
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(64, 64), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 2, 1), block_dim=(128, 1, 1), forloop_range=1, reduction_dimx=64)
+    tX = tb.new_input(dtensor=X, input_map=(0, 1, -1), forloop_dim=-1)
+    tb.new_output(stensor=tb.forloop_accum(tb.exp(tX)), output_map=(1, 0, -1))
+    g.mark_output(g.customized([X], tb)[0])
+    x = (torch.randn((64, 64), generator=torch.Generator().manual_seed(2))).half()
+    got = g(inputs=[x.cuda()])[0]
+    torch.cuda.synchronize()
+    assert g._plan.describe() == ["copy_nd", "exp", "copy_nd"]
+    e = torch.exp(x.double())
+    ref = e.view(2, 32, 2, 32).permute(2, 1, 0, 3).reshape(64, 64).numpy()  # block (i, j) -> (j, i)
     err = np.abs(got.float().cpu().numpy() - ref)
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"

@@ -77,7 +77,7 @@ static int pack(const char* nm, const void* src, void* dst, int G, int R, int C,
 }
 
 // ------------------------------------------------------------------ elementwise
-enum UnaryKind { U_EXP = 0, U_SILU = 1, U_GELU = 2, U_RELU = 3, U_CLAMP = 4, U_SQRT = 5, U_SQUARE = 6 };
+enum UnaryKind { U_EXP = 0, U_SILU = 1, U_GELU = 2, U_RELU = 3, U_CLAMP = 4, U_SQRT = 5, U_SQUARE = 6, U_SCALE = 7 };
 enum BinaryKind { B_ADD = 0, B_MUL = 1, B_DIV = 2, B_POW = 3 };
 
 template <int DT>
@@ -93,6 +93,7 @@ __global__ __launch_bounds__(256) void unary_kernel(const uint16_t* x, uint16_t*
       case U_RELU: r = fmaxf(a, 0.f); break;
       case U_CLAMP: r = fminf(fmaxf(a, lo), hi); break;
       case U_SQRT: r = sqrtf(a); break;
+      case U_SCALE: r = a * lo; break;
       default: r = a * a; break;
     }
     y[i] = (uint16_t)st_elem<DT>(r);
@@ -109,6 +110,32 @@ struct BinaryArgs {
   long long dims[kMaxDims];  // output dims
   long long sa[kMaxDims], sb[kMaxDims];  // element strides of a / b per output dim (0: broadcast)
 };
+
+// Strided copy over up to 8 dims (16-bit elements): the tile gathers and
+// scatters of a customized op run literally, one block tensor per tile
+// tensor (src/kernel/customized.cc input / output maps).
+constexpr int kCopyDims = 8;
+struct CopyArgs {
+  const uint16_t* src;
+  uint16_t* dst;
+  long long n;
+  int nd;
+  long long dims[kCopyDims], ss[kCopyDims], ds[kCopyDims];
+};
+
+__global__ __launch_bounds__(256) void copy_nd_kernel(CopyArgs p) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n;
+       i += (long long)gridDim.x * blockDim.x) {
+    long long rem = i, os = 0, od = 0;
+    for (int d = p.nd - 1; d >= 0; d--) {
+      const long long c = rem % p.dims[d];
+      rem /= p.dims[d];
+      os += c * p.ss[d];
+      od += c * p.ds[d];
+    }
+    p.dst[od] = p.src[os];
+  }
+}
 
 template <int DT>
 __global__ __launch_bounds__(256) void binary_kernel(BinaryArgs p) {
@@ -372,10 +399,37 @@ int yr_hip_graph_pack(const void* src, void* dst, int g, int rows, int cols, int
   return pack(nm, src, dst, g, rows, cols, dst_cols, s[0], s[1], s[2], s[3], s[4], s[5], (hipStream_t)stream);
 }
 
+int yr_hip_graph_copy_nd(const void* src, void* dst, int ndim, const int64_t* dims, const int64_t* src_strides,
+                         const int64_t* dst_strides, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_copy_nd";
+  if (!src || !dst || !dims || !src_strides || !dst_strides) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (ndim <= 0 || ndim > kCopyDims) return fail(YR_E_INVALID, "%s: %d dims (1..%d)", nm, ndim, kCopyDims);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  CopyArgs p;
+  p.src = (const uint16_t*)src;
+  p.dst = (uint16_t*)dst;
+  p.nd = ndim;
+  long long n = 1;
+  for (int d = 0; d < ndim; d++) {
+    if (dims[d] <= 0 || src_strides[d] < 0 || dst_strides[d] < 0)
+      return fail(YR_E_INVALID, "%s: axis %d: dim %lld, strides %lld / %lld", nm, d, (long long)dims[d],
+                  (long long)src_strides[d], (long long)dst_strides[d]);
+    p.dims[d] = dims[d];
+    p.ss[d] = src_strides[d];
+    p.ds[d] = dst_strides[d];
+    n *= dims[d];
+  }
+  p.n = n;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(copy_nd_kernel, dim3(grid_for(n)), dim3(256), 0, st, p);
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
 int yr_hip_graph_unary(const void* x, void* y, int64_t n, int kind, float lo, float hi, int dtype, void* stream) {
   const char* nm = "yr_hip_graph_unary";
   if (!x || !y || n <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
-  if (kind < U_EXP || kind > U_SQUARE) return fail(YR_E_INVALID, "%s: unknown kind %d", nm, kind);
+  if (kind < U_EXP || kind > U_SCALE) return fail(YR_E_INVALID, "%s: unknown kind %d", nm, kind);
   hipStream_t st = (hipStream_t)stream;
   return by_dtype(dtype, [&](auto dt) {
     hipLaunchKernelGGL((unary_kernel<decltype(dt)::value>), dim3(grid_for(n)), dim3(256), 0, st, (const uint16_t*)x,

@@ -45,7 +45,7 @@ from .threadblock import TBGraph
 _guid = itertools.count(1)
 _EPS = 1e-6  # rms_norm epsilon of the fused RMSNorm+linear contract (also used by the generic rms_norm)
 
-_UNARY = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "clamp": 4, "sqrt": 5, "square": 6}
+_UNARY = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "clamp": 4, "sqrt": 5, "square": 6, "mul_scalar": 7}
 _BINARY = {"add": 0, "mul": 1, "div": 2, "pow": 3}
 
 
@@ -185,6 +185,10 @@ def _whole_exprs(bg, in_dims):
         else:
             res.append((v[0], v[1]))
     return res
+
+
+class _NoForm(Exception):
+    """A threadblock op the literal interpreter has no generic form for."""
 
 
 def _fbits(x: float) -> int:
@@ -1136,7 +1140,7 @@ class _Lowering:
             self.emit(_lib.OP_RMSNORM, [self.dense(A)], [self.out_ref(out)],
                       [rows // n, n, A.dtype.code, _fbits(_EPS)], "rms_norm")
         elif k == "customized":
-            if not self._lower_customized(op):
+            if not self._lower_customized(op) and not self._interpret_customized(op):
                 raise YirageHipError("hip backend: this customized threadblock graph matches no fused kernel "
                                      "(RMSNorm+linear, gated MLP, GQA, linear) and is not an expression over "
                                      "whole tensors the generic operators can run")
@@ -1231,6 +1235,204 @@ class _Lowering:
         for out, ref, written in results:
             if not written:
                 self.ref[out.guid] = ref
+        return True
+
+    def _interpret_customized(self, op: KNOp) -> bool:
+        """A customized op's threadblock graph run literally, operator by
+        operator over all its tiles at once: every tile tensor is a block
+        tensor [gx, gy, gz, I, *tile] (I = forloop_range for a tensor that
+        changes with the iteration, 1 otherwise), inputs are gathered into
+        it by their input maps and forloop dims and outputs scattered out by
+        their output maps (one strided copy each), threadblock ops become
+        batched generic operators, and forloop accumulators sum over I as the
+        reference's transpiler lowers them (src/transpiler/transpile.cc:
+        660-700: none = sum over iterations, sum = that reduced over the last
+        dim, sum_todimx = reduced to reduction_dimx, rms = sqrt of the mean
+        square over the last dim and the iterations).  False (nothing emitted)
+        for ops it has no form for: max / rescale accumulators, concat, mean,
+        and matmuls whose tiles the MFMA kernel cannot take (n or k not a
+        multiple of 8)."""
+        bg = op.attrs["bgraph"]
+        gx, gy, gz = bg.grid_dim
+        grid = (gx, gy, gz)
+        R = bg.forloop_range
+        dt = op.inputs[0].dtype
+        if dt not in (float16, bfloat16) or any(t.dtype != dt for t in op.inputs):
+            return False
+        steps = []
+
+        def prod(xs):
+            n = 1
+            for x in xs:
+                n *= x
+            return n
+
+        def rm(dims):
+            return _row_major(tuple(dims))
+
+        def copy(src, dims, ss, ds, dst):
+            nd = len(dims)
+            if nd > 8:
+                raise _NoForm
+            pad = 8 - nd
+            steps.append((_lib.OP_COPY_ND, [src], dst,
+                          [nd, dt.code, *dims, *([1] * pad), *ss, *([0] * pad), *ds, *([0] * pad)], "copy_nd"))
+
+        def new(shape):
+            return self.plan.tmp(shape, dt)
+
+        vals = {}  # id(STensor) -> (ref, (G, I, *tile))
+        G = gx * gy * gz
+
+        def gather(dten, st):
+            t = tuple(st.dims)
+            D = dten.dims
+            src_st = rm(D)
+            im = tuple(st.op.attrs["input_map"]) + (-1,) * 3
+            fd = st.op.attrs["forloop_dim"]
+            I = R if fd >= 0 and R > 1 else 1
+            dims = (gx, gy, gz, I) + t
+            # a block's slice along a cut dim is dim / grid; the forloop then cuts that slice
+            ss = tuple(D[im[a]] // grid[a] * src_st[im[a]] if grid[a] > 1 and im[a] >= 0 else 0 for a in range(3))
+            ss += ((t[fd] * src_st[fd]) if I > 1 else 0,) + src_st
+            o = new(dims)
+            copy(self.dense(dten), dims, ss, rm(dims), o)
+            return o, (G, I) + t
+
+        def unary(kind, x, lo=0.0, hi=0.0):
+            ref, sh = x
+            o = new(sh)
+            steps.append((_lib.OP_UNARY, [ref], o, [prod(sh), _UNARY[kind], dt.code, _fbits(lo), _fbits(hi)], kind))
+            return o, sh
+
+        def binary(kind, a, b):
+            (ra, sa), (rb, sb) = a, b
+            if len(sa) != len(sb) or len(sa) > 6:
+                raise _NoForm
+            sh = tuple(max(x, y) for x, y in zip(sa, sb))
+            o = new(sh)
+            steps.append((_lib.OP_BINARY, [ra, rb], o, [len(sa), _BINARY[kind], dt.code, *sa, *sb], kind))
+            return o, sh
+
+        def reduce(x, axis, to=1):
+            """Sum over `axis` of the block tensor down to `to`: element j of
+            the result adds the elements j, j + to, j + 2 to, ... (the
+            reference's reduction and accumulator fingerprints,
+            include/yirage/threadblock/cuda/reduction.h:41-58)."""
+            ref, sh = x
+            L = sh[axis]
+            if L % to:
+                raise _NoForm
+            out_sh = sh[:axis] + (to,) + sh[axis + 1:]
+            o = new(out_sh)
+            steps.append((_lib.OP_REDUCTION, [ref], o, [prod(sh[:axis]), L // to, to * prod(sh[axis + 1:]), dt.code],
+                          "reduction"))
+            return o, out_sh
+
+        def expand_iters(x):
+            ref, sh = x
+            if sh[1] == R:
+                return x
+            dims = sh[:1] + (R,) + sh[2:]
+            ss = list(rm(sh))
+            ss[1] = 0
+            o = new(dims)
+            copy(ref, dims, tuple(ss), rm(dims), o)
+            return o, dims
+
+        def accumulate(x):
+            """Sum over the forloop's iterations (a loop-invariant tile adds up R times)."""
+            ref, sh = x
+            if R == 1:
+                return x
+            if sh[1] == 1:
+                return unary("mul_scalar", x, float(R))
+            return reduce(x, 1)
+
+        try:
+            for (dten, st) in bg.inputs:
+                vals[id(st)] = gather(dten, st)
+            for top in bg.ops:
+                k = top.kind
+                if k == "input":
+                    continue
+                ins = [vals[id(x)] for x in top.inputs]
+                if k in _TB_UNARY:
+                    r = unary(k, ins[0])
+                elif k == "clamp":
+                    r = unary(k, ins[0], top.attrs["min_val"], top.attrs["max_val"])
+                elif k == "mul_scalar":
+                    r = unary(k, ins[0], top.attrs["scalar"])
+                elif k in _TB_BINARY:
+                    r = binary(k, ins[0], ins[1])
+                elif k == "sub":
+                    r = binary("add", ins[0], unary("mul_scalar", ins[1], -1.0))
+                elif k == "rms_norm":
+                    ref, sh = ins[0]
+                    o = new(sh)
+                    steps.append((_lib.OP_RMSNORM, [ref], o, [prod(sh[:-1]), sh[-1], dt.code, _fbits(_EPS)], "rms_norm"))
+                    r = (o, sh)
+                elif k == "reduction":
+                    r = reduce(ins[0], 2 + top.attrs["dim"])
+                elif k == "reduction_to_dimx":
+                    r = reduce(ins[0], 2 + top.attrs["dim"], bg.reduction_dimx)
+                elif k == "matmul":
+                    a, b = ins
+                    if a[1][1] != b[1][1]:
+                        a, b = expand_iters(a), expand_iters(b)
+                    (ra, sa), (rb, sb) = a, b
+                    M, K, N = sa[-2], sa[-1], sb[-1]
+                    if sa[:-2] != sb[:-2] or sb[-2] != K or N % 8 or K % 8:
+                        raise _NoForm
+                    sh = sa[:-1] + (N,)
+                    o = new(sh)
+                    steps.append((_lib.OP_MATMUL, [ra, rb], o, [prod(sa[:-2]), M, N, K, dt.code], "matmul"))
+                    r = (o, sh)
+                elif k == "accum":
+                    acc = top.attrs["acc"]
+                    if acc == "none":
+                        r = accumulate(ins[0])
+                    elif acc == "sum":
+                        r = reduce(accumulate(ins[0]), len(ins[0][1]) - 1)
+                    elif acc == "sum_todimx":
+                        r = reduce(accumulate(ins[0]), len(ins[0][1]) - 1, bg.reduction_dimx)
+                    elif acc == "rms":
+                        x = unary("square", ins[0])
+                        x = unary("mul_scalar", x, 1.0 / (ins[0][1][-1] * R))
+                        r = unary("sqrt", reduce(accumulate(x), len(x[1]) - 1))
+                    else:
+                        raise _NoForm
+                else:
+                    raise _NoForm
+                vals[id(top.outputs[0])] = r
+            outs = []
+            for (st, omap, ofd), out in zip(bg.outputs, op.outputs):
+                ref, sh = vals[id(st)]
+                t = tuple(st.dims)
+                if sh[2:] != t:
+                    raise _NoForm
+                om = tuple(omap) + (-1,) * 3
+                O = out.dims
+                dst_st = rm(O)
+                I = R if ofd >= 0 and R > 1 else 1
+                if sh[1] not in (1, I):
+                    raise _NoForm
+                dims = (gx, gy, gz, I) + t
+                src = list(rm((gx, gy, gz, sh[1]) + t))
+                if sh[1] == 1:
+                    src[3] = 0
+                ds = tuple(O[om[a]] // grid[a] * dst_st[om[a]] if grid[a] > 1 and om[a] >= 0 else 0 for a in range(3))
+                ds += ((t[ofd] * dst_st[ofd]) if I > 1 else 0,) + dst_st
+                outs.append((ref, dims, tuple(src), ds, out))
+        except (_NoForm, KeyError):
+            return False
+        for kind, a, o, params, name in steps:
+            self.emit(kind, a, [o], params, name)
+        for ref, dims, src, ds, out in outs:
+            nd = len(dims)
+            pad = 8 - nd
+            self.emit(_lib.OP_COPY_ND, [ref], [self.out_ref(out)],
+                      [nd, dt.code, *dims, *([1] * pad), *src, *([0] * pad), *ds, *([0] * pad)], "copy_nd")
         return True
 
     # -------------------------------------------------------- driver
