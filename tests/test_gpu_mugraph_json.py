@@ -98,9 +98,10 @@ CASES = [
     ("mha_bs1.json", "attention", (0.25, 0.25, 1.0)),
     ("single_lora.json", "lora", (1.0, 0.05, 0.05, 0.25)),
     ("ntrans_bs1.json", "ntrans", (1.0, 1.0, 1.0)),
-    # the saved qk-norm candidates that plan do not compute the benchmark's
-    # softmax(rms_norm(Q) K) rms_norm(V) (they scale K's rows by row sums of
-    # rms_norm(Q)); they are checked against their own block-by-block semantics
+    # the saved qk-norm candidates do not compute the function of
+    # benchmark/qknorm_gqa.py's graph (block-by-block emulations of the two
+    # differ; the candidates agree with one another): they are checked
+    # against their own threadblock semantics
     ("qknorm_gqa_bs1_subset.json", "emulate", (1.0, 0.02, 1.0)),  # K small: the literal fp16 row sums stay finite
 ]
 

@@ -1251,7 +1251,8 @@ class _Lowering:
         square over the last dim and the iterations).  False (nothing emitted)
         for ops it has no form for: max / rescale accumulators, concat, mean,
         and matmuls whose tiles the MFMA kernel cannot take (n or k not a
-        multiple of 8)."""
+        multiple of 8, k > 1; k = 1 is an outer product, a broadcast
+        multiply)."""
         bg = op.attrs["bgraph"]
         gx, gy, gz = bg.grid_dim
         grid = (gx, gy, gz)
@@ -1382,7 +1383,12 @@ class _Lowering:
                         a, b = expand_iters(a), expand_iters(b)
                     (ra, sa), (rb, sb) = a, b
                     M, K, N = sa[-2], sa[-1], sb[-1]
-                    if sa[:-2] != sb[:-2] or sb[-2] != K or N % 8 or K % 8:
+                    if sa[:-2] != sb[:-2] or sb[-2] != K:
+                        raise _NoForm
+                    if K == 1:  # an outer product: a broadcast multiply
+                        vals[id(top.outputs[0])] = binary("mul", a, b)
+                        continue
+                    if N % 8 or K % 8:
                         raise _NoForm
                     sh = sa[:-1] + (N,)
                     o = new(sh)

@@ -104,7 +104,9 @@ class TBGraph:
     def matmul(self, A: STensor, B: STensor):
         if A.num_dims != B.num_dims or A.dims[-1] != B.dims[-2] or A.dims[:-2] != B.dims[:-2]:
             raise ValueError(f"threadblock matmul shapes {A.dims} x {B.dims}")
-        return self._op("matmul", [A, B], A.dims[:-1] + (B.dims[-1],), A.dtype)
+        # src/threadblock/matmul.cc:85: the product is after the forloop
+        # accumulation when its operands are
+        return self._op("matmul", [A, B], A.dims[:-1] + (B.dims[-1],), A.dtype, A.after_accum)
 
     def _unary(self, kind, A, **attrs):
         return self._op(kind, [A], A.dims, A.dtype, A.after_accum, **attrs)
