@@ -191,6 +191,10 @@ int yr_hip_graph_binary(const void* a, const void* b, void* out, int ndim, const
 /* y[o][i] = sum_r x[o][r][i]: reduction(x, dim) to size 1
  * (src/kernel/reduction.cc:61-77, python reduction(A, dim) = size 1). */
 int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype, void* stream);
+/* y[o][i] = max_r x[o][r][i] (threadblock reduction_max and the forloop
+ * max accumulator, src/threadblock/reduction.cc, forloop_accum.cc:102-125). */
+int yr_hip_graph_reduction_max(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype,
+                               void* stream);
 /* y[row] = x[row] * rsqrt(mean(x[row]^2) + eps) over the n trailing
  * elements (rms_norm(X, normalized_shape), src/kernel/rms_norm.cc:71-114). */
 int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream);
@@ -223,7 +227,9 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
  *   YR_OP_REDUCTION:      in {x}, out {y}; params {outer, red, inner, dtype}
  *   YR_OP_RMSNORM:        in {x}, out {y}; params {rows, n, dtype, eps_bits}
  *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...}
- *   YR_OP_COPY_ND:        in {src}, out {dst}; params {ndim, dtype, dims[8], src_strides[8], dst_strides[8]} */
+ *   YR_OP_COPY_ND:        in {src}, out {dst}; params {ndim, dtype, dims[8], src_strides[8], dst_strides[8],
+ *                                             dst_offset} (elements; 27 params)
+ *   YR_OP_REDUCTION_MAX:  in {x}, out {y}; params {outer, red, inner, dtype} */
 #define YR_OP_RMSNORM_LINEAR 1
 #define YR_OP_GATED_MLP 2
 #define YR_OP_GQA_PREFILL 3
@@ -237,6 +243,7 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
 #define YR_OP_RMSNORM 11
 #define YR_OP_PACK 12
 #define YR_OP_COPY_ND 13
+#define YR_OP_REDUCTION_MAX 14
 int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);

@@ -48,7 +48,7 @@ def run_plan(plan, inputs):
         k = st.kind
         if k == _lib.OP_COPY_ND:
             so, do = _copy_nd(src[0], p)
-            dst[do] = src[0][so]
+            dst[do + p[26]] = src[0][so]
         elif k == _lib.OP_UNARY:
             n, kind, lo, hi = p[0], p[1], _f32(p[3]), _f32(p[4])
             a = src[0][:n]
@@ -67,6 +67,9 @@ def run_plan(plan, inputs):
         elif k == _lib.OP_REDUCTION:
             outer, red, inner = p[0], p[1], p[2]
             dst[:outer * inner] = src[0][:outer * red * inner].reshape(outer, red, inner).sum(1).reshape(-1)
+        elif k == _lib.OP_REDUCTION_MAX:
+            outer, red, inner = p[0], p[1], p[2]
+            dst[:outer * inner] = src[0][:outer * red * inner].reshape(outer, red, inner).max(1).reshape(-1)
         elif k == _lib.OP_RMSNORM:
             rows, n, eps = p[0], p[1], _f32(p[3])
             x = src[0][:rows * n].reshape(rows, n)

@@ -60,7 +60,7 @@ def _customized(op, inputs):
                         v[id(st)] = x[tuple(sl)]
                     for top in bg.ops:
                         k = top.kind
-                        if k == "input" or top.outputs[0].after_accum and k != "accum":
+                        if k == "input" or top.outputs[0].after_accum and k not in ("accum", "accum_max"):
                             continue
                         a = [v[id(t)] for t in top.inputs]
                         if k == "accum":
@@ -69,13 +69,18 @@ def _customized(op, inputs):
                                 x = x * x
                             acc[id(top)] = acc.get(id(top), 0) + x
                             continue
+                        if k == "accum_max":
+                            acc[id(top)] = np.maximum(acc[id(top)], a[0]) if id(top) in acc else a[0]
+                            continue
                         v[id(top.outputs[0])] = _eval(k, top, a, bg)
                     for st, omap, ofd in bg.outputs:
                         if ofd >= 0:
                             _place(outs, bg, op, st, omap, ofd, bc, it, v[id(st)])
                 # after the loop: accumulator results, then the ops that use them
                 for top in bg.ops:
-                    if top.kind == "accum":
+                    if top.kind == "accum_max":
+                        post[id(top.outputs[0])] = acc[id(top)]
+                    elif top.kind == "accum":
                         x = acc[id(top)]
                         kind = top.attrs["acc"]
                         if kind == "sum":
@@ -112,6 +117,10 @@ def _eval(k, top, a, bg):
         return a[0].sum(top.attrs["dim"], keepdims=True)
     if k == "reduction_to_dimx":
         return _to_dimx(a[0], top.attrs["dim"], bg.reduction_dimx)
+    if k == "reduction_max":
+        return a[0].max(top.attrs["dim"], keepdims=True)
+    if k == "concat":
+        return np.concatenate(a, top.attrs["dim"])
     raise NotImplementedError(k)
 
 

@@ -185,3 +185,18 @@ def test_customized_block_transpose_runs_literally():
     ref = e.view(2, 32, 2, 32).permute(2, 1, 0, 3).reshape(64, 64).numpy()  # block (i, j) -> (j, i)
     err = np.abs(got.float().cpu().numpy() - ref)
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+
+
+def test_customized_max_and_concat_run_literally():
+    """Forloop max accumulator, reduction_max and concat on the GPU against
+    the block-by-block emulation (tests/tb_numpy.py)."""
+    from tb_numpy import run_graph
+    from test_mugraph_json import _max_concat_graph
+
+    g = _max_concat_graph()
+    x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(4))).half()
+    got = g(inputs=[x.cuda()])[0]
+    torch.cuda.synchronize()
+    ref = run_graph(g, [x.double().numpy()])[0]
+    err = np.abs(got.float().cpu().numpy() - ref)
+    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"

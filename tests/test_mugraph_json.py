@@ -178,12 +178,14 @@ def test_superoptimize_reads_a_previous_checkpoint():
     hX = h.new_input(dims=(1, 3584), dtype=yr.float16)
     hG = h.new_input(dims=(1, 3584), dtype=yr.float16)
     hW = h.new_input(dims=(3584, 37888), strides=(1, 3584), dtype=yr.float16)
+    # a rescaled accumulator (online-softmax style): no fused kernel, no
+    # whole-tensor expression and no generic form
     tb = yr.new_threadblock_graph(grid_dim=(592, 1, 1), block_dim=(128, 1, 1), forloop_range=64, reduction_dimx=64)
     tX = tb.new_input(dtensor=hX, input_map=(-1, -1, -1), forloop_dim=1)
     tG = tb.new_input(dtensor=hG, input_map=(-1, -1, -1), forloop_dim=1)
     tW = tb.new_input(dtensor=hW, input_map=(1, -1, -1), forloop_dim=0)
-    # a running max over the K chunks: no whole-tensor expression
-    tb.new_output(stensor=tb.forloop_accum_max(tb.matmul(tb.mul(tX, tG), tW)), output_map=(1, -1, -1))
+    mm = tb.matmul(tb.mul(tX, tG), tW)
+    tb.new_output(stensor=tb.forloop_accum_rescale(mm, tb.exp(tX)), output_map=(1, -1, -1))
     h.mark_output(h.customized([hX, hG, hW], tb)[0])
     with pytest.raises(YirageHipError):
         h.superoptimize(backend="hip", profile_iters=0, use_graph_dataset=False)
@@ -252,3 +254,34 @@ def test_literal_tile_interpreter_matches_block_emulation():
                 assert np.abs(got - attn).max() <= 1e-9
             checked += 1
     assert checked >= 3 + 12 + 2
+
+
+def _max_concat_graph():
+    """Tiles of X [8, 256] (grid 2 over rows, forloop 4 over columns): the
+    running max of exp over the iterations, concatenated with the summed
+    per-chunk row maxima."""
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(8, 256), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 1, 1), block_dim=(128, 1, 1), forloop_range=4, reduction_dimx=64)
+    tX = tb.new_input(dtensor=X, input_map=(0, -1, -1), forloop_dim=1)
+    m = tb.forloop_accum_max(tb.exp(tX))
+    s = tb.forloop_accum(tb.reduction_max(tX, 1))
+    tb.new_output(stensor=tb.concat(m, s, 1), output_map=(0, -1, -1))
+    g.mark_output(g.customized([X], tb)[0])
+    return g
+
+
+def test_literal_max_and_concat():
+    import numpy as np
+    from plan_numpy import run_plan
+    from tb_numpy import run_graph
+
+    g = _max_concat_graph()
+    p = g.plan(fuse=True)
+    assert "reduction_max" in p.describe() and g.outputs[0][0].dims == (8, 65)
+    x = np.random.default_rng(1).normal(0, 1, (8, 256))
+    got, ref = run_plan(p, [x])[0], run_graph(g, [x])[0]
+    assert np.abs(got - ref).max() <= 1e-12
+    # closed form: max over the row of exp(x) per column position, then the row max sums
+    xr = x.reshape(8, 4, 64)
+    assert np.allclose(ref[:, :64], np.exp(xr).max(1)) and np.allclose(ref[:, 64], xr.max(2).sum(1))

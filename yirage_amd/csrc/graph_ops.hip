@@ -162,15 +162,18 @@ __global__ __launch_bounds__(256) void binary_kernel(BinaryArgs p) {
 
 // ------------------------------------------------------------------ reductions
 // out[o][i] = sum_r x[o][r][i] (fp32), one thread per (o, i)
-template <int DT>
+template <int DT, bool MAX = false>
 __global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* x, uint16_t* y, long long outer, int red,
                                                      long long inner) {
   const long long n = outer * inner;
   for (long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (long long)gridDim.x * blockDim.x) {
     const long long o = j / inner, i = j % inner;
     const uint16_t* p = x + o * red * inner + i;
-    float s = 0.f;
-    for (int r = 0; r < red; r++) s += ld_elem<DT>(p[(long long)r * inner]);
+    float s = MAX ? -INFINITY : 0.f;
+    for (int r = 0; r < red; r++) {
+      const float v = ld_elem<DT>(p[(long long)r * inner]);
+      s = MAX ? fmaxf(s, v) : s + v;
+    }
     y[j] = (uint16_t)st_elem<DT>(s);
   }
 }
@@ -478,6 +481,19 @@ int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64
   hipStream_t st = (hipStream_t)stream;
   return by_dtype(dtype, [&](auto dt) {
     hipLaunchKernelGGL((reduce_kernel<decltype(dt)::value>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
+                       (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
+}
+
+int yr_hip_graph_reduction_max(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype,
+                               void* stream) {
+  const char* nm = "yr_hip_graph_reduction_max";
+  if (!x || !y || outer <= 0 || red <= 0 || inner <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+  hipStream_t st = (hipStream_t)stream;
+  return by_dtype(dtype, [&](auto dt) {
+    hipLaunchKernelGGL((reduce_kernel<decltype(dt)::value, true>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
                        (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
     YR_CHECK_LAUNCH(nm);
     return YR_OK;

@@ -1248,9 +1248,9 @@ class _Lowering:
         reference's transpiler lowers them (src/transpiler/transpile.cc:
         660-700: none = sum over iterations, sum = that reduced over the last
         dim, sum_todimx = reduced to reduction_dimx, rms = sqrt of the mean
-        square over the last dim and the iterations).  False (nothing emitted)
-        for ops it has no form for: max / rescale accumulators, concat, mean,
-        and matmuls whose tiles the MFMA kernel cannot take (n or k not a
+        square over the last dim and the iterations, max = the largest over
+        the iterations).  False (nothing emitted) for ops it has no form for:
+        rescale accumulators, mean, and matmuls whose tiles the MFMA kernel cannot take (n or k not a
         multiple of 8, k > 1; k = 1 is an outer product, a broadcast
         multiply)."""
         bg = op.attrs["bgraph"]
@@ -1271,13 +1271,13 @@ class _Lowering:
         def rm(dims):
             return _row_major(tuple(dims))
 
-        def copy(src, dims, ss, ds, dst):
+        def copy(src, dims, ss, ds, dst, off=0):
             nd = len(dims)
             if nd > 8:
                 raise _NoForm
             pad = 8 - nd
             steps.append((_lib.OP_COPY_ND, [src], dst,
-                          [nd, dt.code, *dims, *([1] * pad), *ss, *([0] * pad), *ds, *([0] * pad)], "copy_nd"))
+                          [nd, dt.code, *dims, *([1] * pad), *ss, *([0] * pad), *ds, *([0] * pad), off], "copy_nd"))
 
         def new(shape):
             return self.plan.tmp(shape, dt)
@@ -1314,6 +1314,14 @@ class _Lowering:
             o = new(sh)
             steps.append((_lib.OP_BINARY, [ra, rb], o, [len(sa), _BINARY[kind], dt.code, *sa, *sb], kind))
             return o, sh
+
+        def reduce_max(x, axis):
+            ref, sh = x
+            out_sh = sh[:axis] + (1,) + sh[axis + 1:]
+            o = new(out_sh)
+            steps.append((_lib.OP_REDUCTION_MAX, [ref], o, [prod(sh[:axis]), sh[axis], prod(sh[axis + 1:]), dt.code],
+                          "reduction_max"))
+            return o, out_sh
 
         def reduce(x, axis, to=1):
             """Sum over `axis` of the block tensor down to `to`: element j of
@@ -1377,6 +1385,22 @@ class _Lowering:
                     r = reduce(ins[0], 2 + top.attrs["dim"])
                 elif k == "reduction_to_dimx":
                     r = reduce(ins[0], 2 + top.attrs["dim"], bg.reduction_dimx)
+                elif k == "reduction_max":
+                    r = reduce_max(ins[0], 2 + top.attrs["dim"])
+                elif k == "accum_max":  # max over the iterations
+                    r = reduce_max(ins[0], 1) if ins[0][1][1] > 1 else ins[0]
+                elif k == "concat":
+                    a, b = ins
+                    if a[1][1] != b[1][1]:
+                        a, b = expand_iters(a), expand_iters(b)
+                    axis = 2 + top.attrs["dim"]
+                    (ra, sa), (rb, sb) = a, b
+                    sh = sa[:axis] + (sa[axis] + sb[axis],) + sa[axis + 1:]
+                    o = new(sh)
+                    dst_st = rm(sh)
+                    copy(ra, sa, rm(sa), dst_st, o)
+                    copy(rb, sb, rm(sb), dst_st, o, sa[axis] * dst_st[axis])
+                    r = (o, sh)
                 elif k == "matmul":
                     a, b = ins
                     if a[1][1] != b[1][1]:
@@ -1438,7 +1462,7 @@ class _Lowering:
             nd = len(dims)
             pad = 8 - nd
             self.emit(_lib.OP_COPY_ND, [ref], [self.out_ref(out)],
-                      [nd, dt.code, *dims, *([1] * pad), *src, *([0] * pad), *ds, *([0] * pad)], "copy_nd")
+                      [nd, dt.code, *dims, *([1] * pad), *src, *([0] * pad), *ds, *([0] * pad), 0], "copy_nd")
         return True
 
     # -------------------------------------------------------- driver

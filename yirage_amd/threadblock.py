@@ -178,7 +178,7 @@ class TBGraph:
     def concat(self, A, B, dim: int):
         dims = list(A.dims)
         dims[dim] += B.dims[dim]
-        return self._op("concat", [A, B], dims, A.dtype, dim=dim)
+        return self._op("concat", [A, B], dims, A.dtype, A.after_accum, dim=dim)  # concat.cc:83
 
     def forloop_accum(self, A: STensor, acc: str = None):
         if acc not in ACCUM_KINDS:
