@@ -1250,11 +1250,12 @@ class _Lowering:
         dim, sum_todimx = reduced to reduction_dimx, rms = sqrt of the mean
         square over the last dim and the iterations, max = the largest over
         the iterations).  False (nothing emitted) for ops it has no form
-        for: rescale and mean accumulators (which the reference's own
-        fingerprint executor, src/kernel/cuda/customized_kernel.cu, does not
-        run either), and matmuls whose tiles the MFMA kernel cannot take (n
-        or k not a multiple of 8, k > 1; k = 1 is an outer product, a
-        broadcast multiply)."""
+        for: rescale accumulators (the reference's fingerprint executor,
+        src/kernel/cuda/customized_kernel.cu:146-150, has no case for them)
+        and mean accumulators (its transpiler has no lowering,
+        transpile.cc:677-680), and matmuls whose tiles the MFMA kernel cannot
+        take (n or k not a multiple of 8, k > 1; k = 1 is an outer product,
+        a broadcast multiply)."""
         bg = op.attrs["bgraph"]
         gx, gy, gz = bg.grid_dim
         grid = (gx, gy, gz)
