@@ -195,6 +195,8 @@ def main():
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--no-coop", action="store_true",
+                    help="ordinary (non-cooperative) launch of the persistent kernel, e.g. under rocprofv3")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy a 1 GiB device buffer 3 times (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -216,6 +218,8 @@ def main():
         torch.cuda.synchronize()
         return
     model = LlamaDecodeModel(LLAMA3_8B, batch=1, kv_len=4096, seed=0)
+    if args.no_coop:
+        model.pk.set_cooperative(False)
     model.set_input_tokens([128000])
     for _ in range(args.warmup):
         model.step()
@@ -227,6 +231,12 @@ def main():
     rc, st = model.pk.status()
     if rc != 0:
         raise SystemExit(f"persistent kernel status {st}")
+    # the same steps as passes of ONE launch (the reference's offline ypk()
+    # runs a whole generation in one launch): no launch gap between steps
+    ms_in = _events_time(torch, lambda: model.pk(max_iterations=args.steps), 1) / args.steps
+    rc, st = model.pk.status()
+    if rc != 0 or model.pk.iterations() != args.steps:
+        raise SystemExit(f"persistent kernel status {st} after an in-launch run")
     step_bytes = model.weight_bytes() + model.kv_bytes()
     achieved = step_bytes / ms / 1e6
     info = model.pk.graph_info()
@@ -279,6 +289,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": PK_B1_TRAFFIC_BYTES,
                      "algorithmic_bytes": step_bytes},
         "tokens_per_s": round(1e3 / ms, 2),
+        "in_launch": {"ms_per_step": round(ms_in, 4), "steps_per_launch": args.steps,
+                      "frac_hbm": round(step_bytes / ms_in / 1e6 / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -300,9 +300,27 @@ int yr_pk_create(const yr_pk_graph* graph, const yr_pk_meta* meta, yr_pk_handle*
 /* Offline batch state (page queue, request slots) reset, as init_kernel
  * (persistent_kernel.cuh:107-132). */
 int yr_pk_init_batch(yr_pk_handle* handle, void* stream);
-/* One pass over the task graph (one decode/extend step).  Replaces
+/* Runs the task graph: up to max_iterations passes (decode / extend steps)
+ * in one launch.  When the graph has a prepare_batch task, the device starts
+ * the next pass only while that task left tokens to run, as the reference's
+ * offline scheduler does on EVENT_END_OF_TASK_GRAPH
+ * (persistent_kernel.cuh:841-857); max_iterations 0 then means "until every
+ * request finished" (at most 2^20 passes).  Without a prepare_batch task
+ * every pass runs (max_iterations >= 1 required).  Replaces
  * launch_persistent_kernel (persistent_kernel.cuh:1253-1318). */
-int yr_pk_launch(yr_pk_handle* handle, void* stream);
+int yr_pk_launch(yr_pk_handle* handle, void* stream, int max_iterations);
+/* Synchronous read of the number of passes the last launch ran. */
+int yr_pk_iterations(yr_pk_handle* handle, int* iterations);
+/* Synchronous copy of the batch state the handle owns (the reference keeps
+ * it in RuntimeConfig, persistent_kernel.cuh:107-132): request_ids
+ * [max_requests], next_request_id, page_queue [max_pages], page_queue_head,
+ * page_queue_tail, in that order (n >= max_requests + 3 + max_pages). */
+int yr_pk_read_batch(yr_pk_handle* handle, int* out, size_t n);
+/* 1 (default): cooperative launch.  0: ordinary launch of the same grid;
+ * every worker was checked co-resident at create (occupancy x CUs >=
+ * workers) and every wait stays under the watchdog.  For tools that do not
+ * follow cooperative launches (profilers).  No reference counterpart. */
+int yr_pk_set_launch_mode(yr_pk_handle* handle, int cooperative);
 /* Polls a dependency may spin before the watchdog flags an error. */
 int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
 /* Per-task timestamps (10 ns device clock) into buffer[task][8] =

@@ -9,8 +9,7 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-# YIRAGE_HIP_LIB points at another build of the same library (e.g. a tuning variant)
-LIB_PATH = os.environ.get("YIRAGE_HIP_LIB") or os.path.join(_HERE, "libyirage_hip.so")
+LIB_PATH = os.path.join(_HERE, "libyirage_hip.so")
 
 YR_OK = 0
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64 = 940, 941, 950, 955, 965
@@ -87,7 +86,10 @@ SIGNATURES = {
     "yr_pk_graph_export_json": (_I, [_P, ctypes.c_char_p, _SZ, ctypes.POINTER(_SZ)]),
     "yr_pk_create": (_I, [_P, _P, ctypes.POINTER(_P)]),
     "yr_pk_init_batch": (_I, [_P, _P]),
-    "yr_pk_launch": (_I, [_P, _P]),
+    "yr_pk_launch": (_I, [_P, _P, _I]),
+    "yr_pk_iterations": (_I, [_P, ctypes.POINTER(_I)]),
+    "yr_pk_set_launch_mode": (_I, [_P, _I]),
+    "yr_pk_read_batch": (_I, [_P, ctypes.POINTER(_I), _SZ]),
     "yr_pk_set_spin_limit": (_I, [_P, ctypes.c_longlong]),
     "yr_pk_status": (_I, [_P, ctypes.POINTER(ctypes.c_int)]),
     "yr_pk_set_profiler": (_I, [_P, _P, _SZ]),

@@ -2053,6 +2053,42 @@ __device__ __forceinline__ void run_prepare(int slot, int tid) {
   task_prepare(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
 }
 
+// Grid barrier between task-graph passes.  Every wave first releases its
+// stores at agent scope (the KV appends, the batch metadata prepare_batch
+// rewrote and the profile words are plain stores that may sit in this XCD's
+// L2); one arrival per worker; the arrival count says which barrier this is
+// (arrivals grow by num_workers per barrier), so the counter needs no epoch.
+// After the barrier every wave invalidates its non-coherent cache lines, so
+// the next pass reads the other workers' writes.  Returns false when the
+// watchdog fired or the launch aborted.
+__device__ bool grid_barrier(const KernelArgs& a, Shared& sm) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int ok = 1;
+    const uint32_t n = (uint32_t)a.num_workers;
+    const uint32_t arr = __hip_atomic_fetch_add(gptr(a.grid_bar), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t target = (arr / n + 1) * n;
+    long long spins = 0;
+    for (;;) {
+      const uint32_t v = __hip_atomic_load(gptr(a.grid_bar), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((int32_t)(v - target) >= 0) break;
+      if ((spins & 255) == 255 && aborted(a)) { ok = 0; break; }
+      if (++spins > a.spin_limit) {
+        __hip_atomic_store(gptr(a.meta.status + 2), -2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    sm.flag = ok;
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return sm.flag != 0;
+}
+
 __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) {
   Shared& sm = g_sm;
   const int w = blockIdx.x;
@@ -2067,12 +2103,15 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     }
   };
   load_descs(q0);
+  int it = 0;
+  for (;;) {  // task-graph passes (epochs a.epoch + it)
   __syncthreads();
   fill_pre(a, q1 - q0 < 256 ? q1 - q0 : 256, sm);
   if (threadIdx.x == 0) {
     sm.args = a;
+    sm.args.epoch = a.epoch + (uint32_t)it;
     sm.flag = 1;
-    sm.last_op = -1;
+    sm.last_op = -1;  // staged activations belong to the previous pass
     sm.last_T = 0;
     sm.norm_rows = 0;
     sm.coop_stage = 0;
@@ -2138,8 +2177,31 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     // task's weights in flight meanwhile
     if (!gemv) lds_sync();
     if (a.profile && threadIdx.x == 0) gptr(a.profile)[(size_t)tid * 8 + 2] = now_10ns();
-    if (!sm.flag) break;  // a dependency never arrived: leave the queue
+    if (!sm.flag) return;  // a dependency never arrived: leave the queue
   }
+  if (it + 1 >= a.max_iterations) break;
+  // every worker finished pass `it` (prepare_batch included) before any
+  // starts the next one: the next pass re-reads the batch metadata
+  if (!grid_barrier(a, sm)) return;
+  if (threadIdx.x == 0)
+    sm.flag = !a.stop_when_empty ||
+              __hip_atomic_load(gptr(a.meta.status + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  __syncthreads();
+  if (!sm.flag) {
+    // Early stop: bring every event to where max_iterations passes would
+    // have left it, so the next launch (epoch a.epoch + max_iterations, as
+    // the host counts) waits for the right values.  Nobody waits on an
+    // event in this launch any more (all workers passed the barrier).
+    const uint32_t skip = (uint32_t)(a.max_iterations - 1 - it);
+    for (int e = w * PK_THREADS + tix(); e < a.num_events; e += a.num_workers * PK_THREADS)
+      __hip_atomic_fetch_add(gptr(&a.events[e]), gptr(a.event_triggers)[e] * skip, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    break;
+  }
+  it++;
+  if (q1 - q0 > 256) load_descs(q0);  // the queue's first chunk again
+  }
+  if (w == 0 && threadIdx.x == 0) gptr(a.iterations_run)[0] = it + 1;
 }
 
 // Batch state initialisation (persistent_kernel.cuh:107-132).
@@ -2160,6 +2222,13 @@ __global__ void pk_fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 }
 
 // ------------------------------------------------------------ host handle
+// Passes one launch may run, and the epoch at which the host re-bases the
+// counters: link tags hold the epoch in 32 - kLinkOpBits = 22 bits, and a
+// wait compares counters up to num_triggers * epoch (< 2^31 for <= 512
+// triggers) with a wrap-safe difference.
+constexpr int kMaxIterations = 1 << 20;
+constexpr uint32_t kEpochRebase = 1u << 21;
+
 struct Handle {
   int device = 0;
   int num_workers = 0;
@@ -2168,14 +2237,18 @@ struct Handle {
   TaskDesc* d_tasks = nullptr;
   int* d_qoff = nullptr;
   int* d_queue = nullptr;
-  uint32_t* d_events = nullptr;
+  uint32_t* d_events = nullptr;     // [n_events] counters, then the grid-barrier counter
+  uint32_t* d_triggers = nullptr;   // [n_events] num_triggers
+  int* d_iters = nullptr;           // [1] passes the last launch ran
   uint32_t* d_tickets = nullptr;
   float* d_scratch = nullptr;
   int* d_status = nullptr;
   int* d_owned_meta = nullptr;  // request_ids, next_request_id, page_queue, head, tail, page snapshot
   BatchMeta meta;
-  uint32_t epoch = 0;
+  uint32_t epoch = 0;  // epoch of the last pass the device may have run
   long long spin_limit = 1ll << 26;
+  bool has_prepare = false;
+  bool cooperative = true;
   uint64_t* profile = nullptr;
   std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // tags restart with the epochs: cleared then
 };
@@ -2236,7 +2309,9 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   YRA(h->d_tasks, sizeof(TaskDesc) * h->n_tasks);
   YRA(h->d_qoff, sizeof(int) * qoff.size());
   YRA(h->d_queue, sizeof(int) * queue.size());
-  YRA(h->d_events, sizeof(uint32_t) * h->n_events);
+  YRA(h->d_events, sizeof(uint32_t) * (h->n_events + 1));
+  YRA(h->d_triggers, sizeof(uint32_t) * h->n_events);
+  YRA(h->d_iters, sizeof(int) * 4);
   YRA(h->d_tickets, sizeof(uint32_t) * (g->num_tickets + 1));
   YRA(h->d_scratch, sizeof(float) * (g->scratch_floats + 4));
   YRA(h->d_status, sizeof(int) * 4);
@@ -2247,7 +2322,16 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   if (rc == YR_OK) rc = hip_ok(hipMemcpy(h->d_tasks, g->tasks.data(), sizeof(TaskDesc) * h->n_tasks, hipMemcpyHostToDevice), "copy tasks");
   if (rc == YR_OK) rc = hip_ok(hipMemcpy(h->d_qoff, qoff.data(), sizeof(int) * qoff.size(), hipMemcpyHostToDevice), "copy queues");
   if (rc == YR_OK && queue.size()) rc = hip_ok(hipMemcpy(h->d_queue, queue.data(), sizeof(int) * queue.size(), hipMemcpyHostToDevice), "copy queues");
-  if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_events, 0, sizeof(uint32_t) * h->n_events), "clear events");
+  if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_events, 0, sizeof(uint32_t) * (h->n_events + 1)), "clear events");
+  if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_iters, 0, sizeof(int) * 4), "clear iterations");
+  if (rc == YR_OK && h->n_events) {
+    std::vector<uint32_t> trig(h->n_events);
+    for (size_t e = 0; e < h->n_events; e++) trig[e] = (uint32_t)g->events[e].num_triggers;
+    rc = hip_ok(hipMemcpy(h->d_triggers, trig.data(), sizeof(uint32_t) * h->n_events, hipMemcpyHostToDevice),
+                "copy event triggers");
+  }
+  for (const OpDesc& o : g->ops)
+    if (o.type == TASK_PREPARE_BATCH) h->has_prepare = true;
   if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_tickets, 0, sizeof(uint32_t) * (g->num_tickets + 1)), "clear tickets");
   if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_status, 0, sizeof(int) * 4), "clear status");
   if (rc != YR_OK) {
@@ -2297,19 +2381,27 @@ int yr_pk_init_batch(yr_pk_handle* hp, void* stream) {
   return YR_OK;
 }
 
-int yr_pk_launch(yr_pk_handle* hp, void* stream) {
+int yr_pk_launch(yr_pk_handle* hp, void* stream, int max_iterations) {
   Handle* h = reinterpret_cast<Handle*>(hp);
   if (!h) return fail(YR_E_INVALID, "yr_pk_launch: null handle");
+  if (max_iterations < 0 || max_iterations > kMaxIterations)
+    return fail(YR_E_INVALID, "yr_pk_launch: max_iterations %d outside [0, %d]", max_iterations, kMaxIterations);
+  if (max_iterations == 0) {
+    // until the batch is empty: only a graph with a prepare_batch task knows when
+    if (!h->has_prepare)
+      return fail(YR_E_INVALID, "yr_pk_launch: max_iterations 0 (run to completion) needs a prepare_batch task");
+    max_iterations = kMaxIterations;
+  }
   hipStream_t st = (hipStream_t)stream;
-  // counters are monotonic; re-base them well before 32-bit wrap
-  if (h->epoch >= (1u << 20)) {
-    hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(64), dim3(256), 0, st, h->d_events, h->n_events, 0u);
+  // counters are monotonic; re-base them well before the link tags
+  // (epoch << kLinkOpBits in 32 bits) or the counters wrap
+  if (h->epoch + (uint32_t)max_iterations >= kEpochRebase) {
+    hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(64), dim3(256), 0, st, h->d_events, h->n_events + 1, 0u);
     YR_CHECK_LAUNCH("pk_fill_u32_kernel");
     int rc = clear_links(h, st);
     if (rc != YR_OK) return rc;
     h->epoch = 0;
   }
-  h->epoch++;
   KernelArgs a;
   a.ops = h->d_ops;
   a.tasks = h->d_tasks;
@@ -2319,14 +2411,54 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream) {
   a.tickets = h->d_tickets;
   a.scratch = h->d_scratch;
   a.meta = h->meta;
-  a.epoch = h->epoch;
+  a.epoch = h->epoch + 1;
   a.num_workers = h->num_workers;
   a.spin_limit = h->spin_limit;
   a.profile = h->profile;
+  a.max_iterations = max_iterations;
+  a.stop_when_empty = h->has_prepare ? 1 : 0;
+  a.grid_bar = h->d_events + h->n_events;
+  a.event_triggers = h->d_triggers;
+  a.num_events = (int)h->n_events;
+  a.iterations_run = h->d_iters;
+  // the device ends at epoch + max_iterations whether or not it stops early
+  // (an early stop fast-forwards the counters)
+  h->epoch += (uint32_t)max_iterations;
   void* args[] = {&a};
-  hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
-                                            dim3(PK_THREADS), args, 0, st);
-  if (e != hipSuccess) return check_hip(e, "hipLaunchCooperativeKernel(pk_worker_kernel)");
+  hipError_t e;
+  if (h->cooperative)
+    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
+                                   dim3(PK_THREADS), args, 0, st);
+  else
+    e = hipLaunchKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers), dim3(PK_THREADS),
+                        args, 0, st);
+  if (e != hipSuccess) return check_hip(e, "launch of pk_worker_kernel");
+  return YR_OK;
+}
+
+int yr_pk_iterations(yr_pk_handle* hp, int* iterations) {
+  Handle* h = reinterpret_cast<Handle*>(hp);
+  if (!h || !iterations) return fail(YR_E_INVALID, "yr_pk_iterations: bad arguments");
+  hipError_t e = hipMemcpy(iterations, h->d_iters, sizeof(int), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return check_hip(e, "yr_pk_iterations");
+  return YR_OK;
+}
+
+int yr_pk_read_batch(yr_pk_handle* hp, int* out, size_t n) {
+  Handle* h = reinterpret_cast<Handle*>(hp);
+  if (!h || !out) return fail(YR_E_INVALID, "yr_pk_read_batch: bad arguments");
+  const size_t need = (size_t)h->meta.max_requests + 3 + (size_t)h->meta.max_pages;
+  if (n < need) return fail(YR_E_INVALID, "yr_pk_read_batch: needs %zu ints", need);
+  hipError_t e = hipMemcpy(out, h->d_owned_meta, sizeof(int) * need, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return check_hip(e, "yr_pk_read_batch");
+  return YR_OK;
+}
+
+int yr_pk_set_launch_mode(yr_pk_handle* hp, int cooperative) {
+  Handle* h = reinterpret_cast<Handle*>(hp);
+  if (!h) return fail(YR_E_INVALID, "yr_pk_set_launch_mode: null handle");
+  // co-residency of every worker was checked against the occupancy at create
+  h->cooperative = cooperative != 0;
   return YR_OK;
 }
 
@@ -2363,7 +2495,8 @@ int yr_pk_reset_status(yr_pk_handle* hp) {
   if (!h) return fail(YR_E_INVALID, "yr_pk_reset_status: null handle");
   // clear the flags and re-base the counters (a watchdog exit leaves them short)
   if (hipMemset(h->d_status, 0, sizeof(int) * 4) != hipSuccess) return fail(YR_E_HIP, "reset status");
-  if (hipMemset(h->d_events, 0, sizeof(uint32_t) * h->n_events) != hipSuccess) return fail(YR_E_HIP, "reset events");
+  if (hipMemset(h->d_events, 0, sizeof(uint32_t) * (h->n_events + 1)) != hipSuccess)
+    return fail(YR_E_HIP, "reset events");
   int rc = clear_links(h, nullptr);
   if (rc != YR_OK) return rc;
   if (hipDeviceSynchronize() != hipSuccess) return fail(YR_E_HIP, "reset status: synchronize");
@@ -2374,8 +2507,8 @@ int yr_pk_reset_status(yr_pk_handle* hp) {
 void yr_pk_destroy(yr_pk_handle* hp) {
   Handle* h = reinterpret_cast<Handle*>(hp);
   if (!h) return;
-  void* ptrs[] = {h->d_ops, h->d_tasks, h->d_qoff, h->d_queue, h->d_events, h->d_tickets, h->d_scratch, h->d_status,
-                  h->d_owned_meta};
+  void* ptrs[] = {h->d_ops,     h->d_tasks,   h->d_qoff,    h->d_queue,  h->d_events,     h->d_triggers,
+                  h->d_iters,   h->d_tickets, h->d_scratch, h->d_status, h->d_owned_meta};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;

@@ -117,9 +117,20 @@ struct KernelArgs {
   float* scratch;            // split records
   BatchMeta meta;
   uint64_t* profile;         // optional [num_tasks][4]: start, inputs ready, end, worker
-  uint32_t epoch;            // 1, 2, 3, ... per launch
+  uint32_t epoch;            // epoch of the launch's first task-graph pass (1, 2, 3, ...)
   int num_workers;
   long long spin_limit;      // watchdog: polls before a wait gives up
+  // In-launch iteration (the reference's offline mode runs every step of a
+  // generation in one launch, persistent_kernel.cuh:841-857): up to
+  // max_iterations passes with epochs epoch, epoch + 1, ...; with
+  // stop_when_empty the launch also ends after a pass whose prepare_batch
+  // task left no tokens to run (status[1] == 0).
+  int max_iterations;
+  int stop_when_empty;
+  uint32_t* grid_bar;        // grid barrier between passes: arrivals, +num_workers per barrier
+  const uint32_t* event_triggers;  // [num events] num_triggers (epoch fast-forward after an early stop)
+  int num_events;
+  int* iterations_run;       // [1]: passes the last launch ran (written by worker 0)
 };
 
 }  // namespace pk

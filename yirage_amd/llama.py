@@ -266,7 +266,14 @@ class LlamaDecodeModel:
         self.meta["input_tokens"][: ids.shape[0]].copy_(ids.to(self.meta["input_tokens"].device))
 
     def step(self):
-        self.pk()
+        """One decode / extend step (one task-graph pass)."""
+        self.pk(max_iterations=1)
+
+    def generate(self, max_iterations: int = 0):
+        """Serving mode: every remaining step in one launch (0: until every
+        request finished); returns the passes the device ran."""
+        self.pk(max_iterations=max_iterations)
+        return self.pk.iterations()
 
     def weight_bytes(self) -> int:
         """Bytes one decode step streams from weights (LM head and all layer

@@ -440,10 +440,19 @@ class PersistentKernel:
     def _stream(self):
         return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def __call__(self, **kwargs):
+    def __call__(self, max_iterations: int | None = None, **kwargs):
+        """Runs the task graph in one launch.  As the reference's offline
+        ypk() (persistent_kernel.cuh:841-857, demo/llama3/demo.py:864-868),
+        an offline kernel with a prepare_batch layer runs every step of the
+        generation: the device starts the next pass while requests remain.
+        Otherwise one pass (one step) per call.  `max_iterations` bounds the
+        passes (0: until the batch is empty; needs prepare_batch)."""
         if not self._is_compiled:
             raise YirageHipError("PersistentKernel: call compile() first")
-        check(lib().yr_pk_launch(self._handle, self._stream()), "persistent kernel launch")
+        if max_iterations is None:
+            has_prepare = any(o["type"] == "prepare_batch" for o in self.ops)
+            max_iterations = 0 if (self.mode == "offline" and has_prepare) else 1
+        check(lib().yr_pk_launch(self._handle, self._stream(), int(max_iterations)), "persistent kernel launch")
         if self.profiler_tensor is not None:
             # as the reference does after every launch (persistent_kernel.py:1322-1337)
             name = (self.trace_name or f"yirage_{self.mpi_rank}") + ".perfetto-trace"
@@ -490,6 +499,32 @@ class PersistentKernel:
                 out[t] = list(rec)
             self._task_table = out
         return self._task_table.copy()
+
+    def init_batch(self):
+        """Reset the offline batch manager (request slots, page queue) on the
+        device, as compile() does; the caller resets step / tokens."""
+        check(lib().yr_pk_init_batch(self._handle, self._stream()), "init batch")
+
+    def iterations(self) -> int:
+        """Passes the last launch ran (synchronizes with the device)."""
+        n = ctypes.c_int()
+        check(lib().yr_pk_iterations(self._handle, ctypes.byref(n)), "iterations")
+        return n.value
+
+    def batch_state(self) -> dict:
+        """The device batch manager's own state (synchronizes): request_ids,
+        next_request_id, page_queue, page_queue_head, page_queue_tail."""
+        import numpy as np
+        MR, MP = self.max_num_batched_requests, self.max_num_pages
+        buf = (ctypes.c_int * (MR + 3 + MP))()
+        check(lib().yr_pk_read_batch(self._handle, buf, MR + 3 + MP), "read batch")
+        a = np.array(buf, np.int32)
+        return {"request_ids": a[:MR], "next_request_id": a[MR:MR + 1], "page_queue": a[MR + 1:MR + 1 + MP],
+                "page_queue_head": a[MR + 1 + MP:MR + 2 + MP], "page_queue_tail": a[MR + 2 + MP:MR + 3 + MP]}
+
+    def set_cooperative(self, cooperative: bool = True):
+        """Cooperative (default) or ordinary launch of the worker grid."""
+        check(lib().yr_pk_set_launch_mode(self._handle, int(bool(cooperative))), "launch mode")
 
     def status(self):
         st = (ctypes.c_int * 4)()
