@@ -120,27 +120,83 @@ def bench_fused(torch):
     return out
 
 
-def cpu_baseline(sample_layers: int = 2):
-    """The CPU oracle (oracle/yr_oracle.c, double accumulation, OpenMP) timed
-    on a bounded sample of the same decode step: `sample_layers` full decoder
-    layers at batch 1 plus the LM head, scaled to 32 layers."""
+def _cpu_time(fn, warmup: int, reps: int) -> float:
+    """Mean ms per call after `warmup` untimed calls (time.perf_counter), the
+    method of the reference's CPU harness (benchmark/baselines/pytorch/
+    rms_norm.py:30-53) with repetition counts sized to the op."""
+    for _ in range(warmup):
+        fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def cpu_fused(threads: int) -> dict:
+    """The CPU oracle (oracle/yr_oracle.c: double accumulation, bf16 / f16
+    rounding at the same tensor boundaries, OpenMP over `threads`) on the
+    same shapes as BASELINE configs 1-4, seeded synthetic inputs."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(0)
+    out = {}
+
+    def rec(name, ms, warmup, reps):
+        out[name] = dict(cpu_ms=round(ms, 3), warmup=warmup, reps=reps, cores=threads)
+
+    x = O.round_to(rng.standard_normal((8, 4096)), "f16")
+    g = np.ones(4096, np.float32)
+    w = O.synth((4096, 4096), "f16", 11, 0.02)
+    rec("rmsnorm_linear_b8", _cpu_time(lambda: O.rmsnorm_linear(x, g, w, "f16", O.W_KN, 1e-6), 4, 32), 4, 32)
+    w1 = O.synth((4096, 14336), "bf16", 12, 0.02)
+    w3 = O.synth((4096, 14336), "bf16", 13, 0.02)
+    xb = O.round_to(rng.standard_normal((8, 4096)), "bf16")
+    rec("gated_mlp_b8", _cpu_time(lambda: O.gated_mlp(xb, w1, w3, "bf16"), 1, 4), 1, 4)
+    xb = O.round_to(rng.standard_normal((128, 4096)), "bf16")
+    rec("gated_mlp_b128", _cpu_time(lambda: O.gated_mlp(xb, w1, w3, "bf16"), 0, 1), 0, 1)
+    del w1, w3
+    B, Hq, Hkv, D, L, page = 8, 32, 8, 128, 4096, 64
+    P = B * L // page
+    kc = O.synth((P, page, Hkv, D), "f16", 14, 1.0)
+    vc = O.synth((P, page, Hkv, D), "f16", 15, 1.0)
+    idx = rng.permutation(P).astype(np.int32)
+    indptr = (np.arange(B + 1) * (L // page)).astype(np.int32)
+    lens = np.full(B, L, np.int32)
+    q = O.to_float(O.synth((B, Hq, D), "f16", 16, 1.0), "f16")
+    rec("gqa_decode_b8", _cpu_time(lambda: O.gqa_decode_paged(q, kc, vc, "f16", indptr, idx, lens), 1, 4), 1, 4)
+    del kc, vc
+    S = 2048
+    qq = O.to_float(O.synth((1, S, 32, 128), "bf16", 17, 1.0), "bf16")
+    kk = O.to_float(O.synth((1, S, 8, 128), "bf16", 18, 1.0), "bf16")
+    vv = O.to_float(O.synth((1, S, 8, 128), "bf16", 19, 1.0), "bf16")
+    rec("gqa_prefill_s2048", _cpu_time(lambda: O.gqa_prefill(qq, kk, vv, True), 0, 1), 0, 1)
+    return out
+
+
+def cpu_decode(batch: int, threads: int, sample_layers: int = 2, warmup: int = 1, reps: int = 2) -> dict:
+    """The CPU oracle on a bounded sample of the same decode step:
+    `sample_layers` full decoder layers (RMSNorm, QKV, RoPE + paged GQA at
+    kv 4096 with the new token appended, O-proj + residual, RMSNorm, gate /
+    up, SiLU-mul, down + residual), `warmup` untimed and `reps` timed passes
+    each, scaled to 32 layers, plus the LM head and argmax (timed the same
+    way).  Weight and cache generation are outside the timed region."""
     import numpy as np
 
     from oracle import oracle as O
     from yirage_amd.llama import LLAMA3_8B as cfg, page_table, rope_tables, tensor_seed, weight_shapes
 
-    threads = os.cpu_count() or 1
-    O.set_num_threads(threads)
     bf = "bf16"
     G, D, kv_len, page = cfg.num_q_heads // cfg.num_kv_heads, cfg.head_dim, 4096, 64
-    indptr, indices, pool = page_table(1, kv_len, page, 7)
+    indptr, indices, pool = page_table(batch, kv_len, page, 7)
     cos, sin = rope_tables(kv_len + 8, D, cfg.rope_theta)
     cos, sin = cos.float().numpy(), sin.float().numpy()
-    qo = np.array([0, 1], np.int32)
-    lpl = np.array([kv_len % page], np.int32)
+    qo = np.arange(batch + 1, dtype=np.int32)
+    lpl = np.full(batch, kv_len % page, np.int32)
     ones = np.ones(cfg.hidden, np.float32)
-    x = O.round_to(np.random.default_rng(0).standard_normal((1, cfg.hidden)), bf)
-    elapsed = 0.0
+    x0 = O.round_to(np.random.default_rng(0).standard_normal((batch, cfg.hidden)), bf)
+    per_layer = []
     for layer in range(sample_layers):
         W = {n: O.synth(s, bf, tensor_seed(0, layer, n), 0.02) for n, s in weight_shapes(cfg).items()}
         rows = []
@@ -149,30 +205,28 @@ def cpu_baseline(sample_layers: int = 2):
         wqkv = np.ascontiguousarray(np.concatenate(rows, 0))
         kc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(0, layer, "kc"), 1.0)
         vc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(0, layer, "vc"), 1.0)
-        t0 = time.perf_counter()
-        xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
-        qkv = O.round_to(O.linear(xn, wqkv, bf, O.W_NK), bf)
-        att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, kc, vc, bf, qo, indptr,
-                                           indices, lpl, cos, sin), bf)
-        h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
-        hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
-        m = O.silu_mul(O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf),
-                       O.round_to(O.linear(hn, W["wu"], bf, O.W_NK), bf), bf)
-        x = O.round_to(O.linear(m, W["wd"], bf, O.W_NK, residual=h), bf)
-        elapsed += time.perf_counter() - t0
+
+        def one_layer(x=x0):
+            xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
+            qkv = O.round_to(O.linear(xn, wqkv, bf, O.W_NK), bf)
+            att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, kc, vc, bf, qo, indptr,
+                                               indices, lpl, cos, sin), bf)
+            h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
+            hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
+            m = O.silu_mul(O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf),
+                           O.round_to(O.linear(hn, W["wu"], bf, O.W_NK), bf), bf)
+            return O.round_to(O.linear(m, W["wd"], bf, O.W_NK, residual=h), bf)
+
+        per_layer.append(_cpu_time(one_layer, warmup, reps))
         del W, kc, vc
     lm = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(0, 0, "lm_head"), 0.02)
-    t0 = time.perf_counter()
-    logits = O.round_to(O.linear(O.round_to(O.rmsnorm(x, ones, cfg.eps), bf), lm, bf, O.W_NK), bf)
-    O.argmax(logits)
-    t_lm = time.perf_counter() - t0
-    step_ms = (elapsed / sample_layers * cfg.num_layers + t_lm) * 1e3
-    import torch
-
-    return dict(value=round(step_ms, 2), unit="ms", cores=threads, kind="port",
-                sample=f"{sample_layers} of 32 decoder layers + LM head/argmax at batch 1 (kv 4096), "
-                       f"layer time scaled x32; weight generation excluded",
-                os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(), cpu_model=_cpu_model())
+    t_lm = _cpu_time(lambda: O.argmax(O.round_to(O.linear(O.round_to(O.rmsnorm(x0, ones, cfg.eps), bf), lm, bf,
+                                                                    O.W_NK), bf)), warmup, reps)
+    step_ms = sum(per_layer) / sample_layers * cfg.num_layers + t_lm
+    return dict(value=round(step_ms, 2), unit="ms", cores=threads, kind="port", warmup=warmup, reps=reps,
+                sample=f"batch {batch}: {sample_layers} of 32 decoder layers ({warmup} untimed + {reps} timed "
+                       f"passes each, mean scaled x32) + LM head/argmax ({warmup} + {reps}); kv 4096",
+                layer_ms=[round(v, 2) for v in per_layer], lm_head_ms=round(t_lm, 2))
 
 
 def _cpu_model() -> str:
@@ -249,6 +303,8 @@ def main():
     extra = {}
     if not args.no_b8:
         m8 = LlamaDecodeModel(LLAMA3_8B, batch=8, kv_len=4096, seed=0)
+        if args.no_coop:
+            m8.pk.set_cooperative(False)
         m8.set_input_tokens([128000] * 8)
         for _ in range(max(1, args.warmup)):
             m8.step()
@@ -266,7 +322,19 @@ def main():
         extra["fused_ops"] = bench_fused(torch)
         torch.cuda.synchronize()
         F._ws_cache.clear()
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        threads = os.cpu_count() or 1
+        O.set_num_threads(threads)
+        cpu = cpu_decode(1, threads)
+        cpu.update(os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(), cpu_model=_cpu_model())
+        if "decode_b8" in extra:
+            extra["decode_b8"]["cpu_baseline"] = cpu_decode(8, threads)
+        if "fused_ops" in extra:
+            for k, v in cpu_fused(threads).items():
+                extra["fused_ops"][k].update(v)
 
     line = {
         "metric": "fused-op latency (µs) & % HBM peak; 8B-shape decode step latency, batch 1",

@@ -96,3 +96,24 @@ def test_python_backend_api_lists_hip():
 
     if not torch.cuda.is_available():
         assert not yr.is_backend_available("hip")
+
+
+def test_graph_attention_plan_leaves_decode_beyond_its_tickets():
+    """Graph attention with <= 16 query rows runs on the split-KV decode
+    kernel only while every group gets an arrival ticket (64 KiB / 4 B =
+    16384 groups); beyond that the prefill kernel runs it.  The workspace
+    query shows the choice: the decode plan stages an identity page table
+    ((3 G + 1) int32, 256-byte aligned) after the 64 KiB ticket region, the
+    prefill plan over dense operands needs only the ticket region."""
+    L = _lib.lib()
+    M, Lk, d = 1, 64, 128
+
+    def ws(G):
+        # dense [G][rows][128] operands: Q / O (M rows), K^T given as [G][d][L], V [G][L][d]
+        s = (ctypes.c_int64 * 12)(M * 128, 128, 1, Lk * 128, 1, 128, Lk * 128, 128, 1, M * 128, 128, 1)
+        return L.yr_hip_graph_attention_workspace(G, M, Lk, d, s)
+
+    tickets = 64 * 1024
+    g = 16384
+    assert ws(g) == tickets + (((3 * g + 1) * 4 + 255) // 256) * 256
+    assert ws(g + 1) == tickets

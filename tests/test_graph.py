@@ -173,3 +173,24 @@ def test_graph_step_workspace_queries():
     assert L.yr_hip_fused_workspace(99, 2, bad) == 0
     rc = L.yr_hip_run_fused(_lib.OP_BINARY, 2, None, 1, None, 2, bad, None, 0, None)
     assert rc == -1
+
+
+def test_checkpoint_written_under_the_looked_up_name(tmp_path, monkeypatch):
+    """save_codes=True writes the candidate list as
+    yirage_cached_mugraphs_<hash>.json; a later superoptimize() of the same
+    structure (graph-dataset cache off) reads it back as a candidate."""
+    import json as _json
+
+    from yirage_amd import mugraph_json
+
+    monkeypatch.chdir(tmp_path)
+    g = _rms_linear()
+    name = f"yirage_cached_mugraphs_{g.get_owner_independent_hash():x}.json"
+    g.superoptimize(backend="hip", profile_iters=0, use_graph_dataset=False, save_codes=True)
+    assert (tmp_path / name).exists()
+    saved = mugraph_json.load(str(tmp_path / name))
+    assert len(saved) == 1 and g._same_interface(saved[0])
+    assert saved[0].plan(fuse=True).describe() == g.plan(fuse=True).describe()
+    assert isinstance(_json.loads((tmp_path / name).read_text())[0], list)
+    g2 = _rms_linear().superoptimize(backend="hip", profile_iters=0, use_graph_dataset=False)
+    assert g2._plan.describe() == g.plan(fuse=True).describe()

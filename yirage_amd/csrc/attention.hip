@@ -724,22 +724,37 @@ size_t yr_hip_gqa_decode_workspace(int batch, int hq, int hkv, int d, int max_kv
 
 }  // extern "C"
 
+// Shape / dtype checks of a paged decode call (everything but the workspace).
+int yr::gqa_decode_check(const char* nm, const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len, const void* out,
+                         int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype) {
+  if (!q || !k_cache || !v_cache || !kv_indptr || !kv_indices || !kv_len || !out)
+    return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (batch <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: hq must be a multiple of hkv", nm);
+  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
+  const int G = hq / hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return fail(YR_E_INVALID, "%s: group size %d", nm, G);
+  if (page_size <= 0) return fail(YR_E_INVALID, "%s: bad page size", nm);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  if (max_kv_len <= 0) return fail(YR_E_INVALID, "%s: max_kv_len must be > 0", nm);
+  if (batch * hkv > kMaxTickets) return fail(YR_E_INVALID, "%s: batch * hkv too large", nm);
+  const DecPlan dp = dec_plan(batch, hkv, max_kv_len, page_size);
+  if (dp.chunk / page_size + 2 > DEC_MAXPG)
+    return fail(YR_E_INVALID, "%s: %d pages per split exceed %d (page_size too small)", nm, dp.chunk / page_size + 2,
+                DEC_MAXPG);
+  return YR_OK;
+}
+
 // The decode launch shared by the workspace and the no-allocation entry
 // points: checks the shape, plans the splits and launches.
 int yr::gqa_decode_launch(const char* nm, const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len, void* out,
                              int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype,
                              void* workspace, size_t workspace_bytes, hipStream_t st, float scale) {
-  if (!q || !k_cache || !v_cache || !kv_indptr || !kv_indices || !kv_len || !out)
-    return fail(YR_E_INVALID, "%s: null pointer", nm);
-  if (batch <= 0 || hkv <= 0 || hq % hkv) return fail(YR_E_INVALID, "%s: hq must be a multiple of hkv", nm);
-  if (d != 128) return fail(YR_E_INVALID, "%s: head_dim %d unsupported (128)", nm, d);
-  int G = hq / hkv;
-  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return fail(YR_E_INVALID, "%s: group size %d", nm, G);
-  if (page_size <= 0) return fail(YR_E_INVALID, "%s: bad page size", nm);
-  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
-  if (max_kv_len <= 0) return fail(YR_E_INVALID, "%s: max_kv_len must be > 0", nm);
-  if (batch * hkv > kMaxTickets) return fail(YR_E_INVALID, "%s: batch * hkv too large", nm);
+  int rc = gqa_decode_check(nm, q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch, hq, hkv, d,
+                            page_size, max_kv_len, dtype);
+  if (rc != YR_OK) return rc;
+  const int G = hq / hkv;
   size_t need = yr_hip_gqa_decode_workspace(batch, hq, hkv, d, max_kv_len, page_size);
   if (need > workspace_bytes || (need && !workspace))
     return fail(YR_E_WORKSPACE, "%s: workspace %zu < %zu", nm, workspace_bytes, need);
@@ -758,9 +773,6 @@ int yr::gqa_decode_launch(const char* nm, const void* q, const void* k_cache, co
   const DecPlan dp = dec_plan(batch, hkv, max_kv_len, page_size);
   a.splits = dp.splits;
   a.chunk = dp.chunk;
-  if (dp.chunk / page_size + 2 > DEC_MAXPG)
-    return fail(YR_E_INVALID, "%s: %d pages per split exceed %d (page_size too small)", nm, dp.chunk / page_size + 2,
-                DEC_MAXPG);
   a.tickets = (uint32_t*)workspace;
   a.partial = need ? (float*)((char*)workspace + kTicketBytes) : nullptr;
   if (!(scale > 0.f)) return fail(YR_E_INVALID, "%s: scale must be positive", nm);
@@ -896,14 +908,16 @@ int yr_hip_gqa_decode_paged_noalloc(const void* q, const void* k_cache, const vo
                                     void* out, int batch, int hq, int hkv, int d, int page_size, int max_kv_len,
                                     int dtype, void* stream) {
   const char* nm = "yr_hip_gqa_decode_paged_noalloc";
-  if (batch <= 0 || hkv <= 0 || hq % hkv || page_size <= 0 || max_kv_len <= 0)
-    return fail(YR_E_INVALID, "%s: bad shape", nm);
+  // every check before the ticket fill, so a rejected call launches nothing
+  int rc = gqa_decode_check(nm, q, k_cache, v_cache, kv_indptr, kv_indices, kv_len, out, batch, hq, hkv, d,
+                            page_size, max_kv_len, dtype);
+  if (rc != YR_OK) return rc;
   const size_t need = yr_hip_gqa_decode_workspace(batch, hq, hkv, d, max_kv_len, page_size);
   if (need > kNoAllocScratchBytes)
     return fail(YR_E_WORKSPACE, "%s: needs %zu bytes of scratch, above the fixed %zu", nm, need,
                 kNoAllocScratchBytes);
   void* ws = nullptr;
-  int rc = noalloc_scratch(nm, &ws);
+  rc = noalloc_scratch(nm, &ws);
   if (rc != YR_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (need) {

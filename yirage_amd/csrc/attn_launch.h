@@ -15,6 +15,11 @@ int gqa_decode_launch(const char* nm, const void* q, const void* k_cache, const 
                       int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype, void* workspace,
                       size_t workspace_bytes, hipStream_t st, float scale);
 
+// The shape / dtype checks of gqa_decode_launch (all but the workspace).
+int gqa_decode_check(const char* nm, const void* q, const void* k_cache, const void* v_cache,
+                     const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_len, const void* out,
+                     int batch, int hq, int hkv, int d, int page_size, int max_kv_len, int dtype);
+
 // Flash-attention prefill over batch x heads with sq query rows and sk kv
 // rows per batch entry; strides in elements.
 int prefill_launch(const char* nm, const void* q, const void* k, const void* v, void* out, int batch, int sq, int sk,

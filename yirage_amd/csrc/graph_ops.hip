@@ -288,7 +288,9 @@ static bool dense_rows(const long long* s, int G, int rows, int d) {
 static AttnPlan attn_plan(int G, int M, int L, int d, const long long* sq, const long long* sk, const long long* sv,
                           const long long* so) {
   AttnPlan p;
-  p.decode = M <= 16 && (M & (M - 1)) == 0;
+  // the decode kernel takes one arrival ticket per group (G <= kMaxTickets);
+  // with one L-token page per group its page budget always fits
+  p.decode = M <= 16 && (M & (M - 1)) == 0 && G <= kMaxTickets;
   p.pack_q = !dense_rows(sq, G, M, d);
   // K as the kernel wants it is [G][L][128]: K^T's strides swapped
   const long long skt[3] = {sk[0], sk[2], sk[1]};

@@ -510,7 +510,12 @@ class KNGraph:
         (kernel.py:635-640), the plannable graphs of a saved candidate list:
         `yirage_cached_mugraphs_<hash>.json` in the working directory or the
         file `previous_checkpoint` names (e.g. benchmark/saved_mugraphs/...);
-        with more than one candidate the fastest measured one is kept."""
+        with more than one candidate the fastest measured one is kept.
+        The automatic file name is this build's structural hash of the graph
+        (the reference's get_owner_independent_hash is a C++ hash of its own
+        graph object), so a file the reference wrote is read only when given
+        as `previous_checkpoint`; with save_codes=True the candidates are
+        written under the automatic name for later calls."""
         if backend is None:
             from .backend_api import get_default_backend
             backend = get_default_backend() or "hip"
@@ -560,6 +565,19 @@ class KNGraph:
         g = self._bound(best)
         if use_graph_dataset:
             graph_dataset.store(self, g, **key)
+        auto = f"yirage_cached_mugraphs_{self.get_owner_independent_hash():x}.json"
+        if save_codes and use_cached_graphs and not os.path.exists(auto):
+            # this graph (and the saved candidates it was given) under the
+            # name a later superoptimize() looks up, so the cache round-trips
+            from .mugraph_json import graph_to_json
+
+            graphs = [graph_to_json(self)]
+            if ckpt is not None and os.path.exists(ckpt):
+                from .mugraph_json import load
+
+                graphs += [graph_to_json(c) for c in load(ckpt) if self._same_interface(c)]
+            with open(auto, "w") as f:
+                json.dump(graphs, f)
         return g
 
     def _bound(self, plan: Plan):
