@@ -56,7 +56,8 @@ def lib():
             "yo_rope": (None, [P, i32, i32, P, P, i32]),
             "yo_gqa_decode_paged": (None, [P, i32, i32, i32, i32, P, P, i32, i32, P, P, P, P]),
             "yo_gqa_prefill": (None, [P, P, P, i32, i32, i32, i32, i32, i32, P, i32, P]),
-            "yo_paged_attention": (None, [P, i32, i32, i32, P, P, i32, i32, i32, P, P, P, P, P, P, P]),
+            "yo_paged_attention": (None, [P, i32, i32, i32, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, f32,
+                                          P]),
             "yo_argmax": (None, [P, i32, i32, i32, P]),
             "yo_batch_init": (None, [P]),
             "yo_batch_prepare_next": (i32, [P]),
@@ -212,8 +213,9 @@ def gqa_prefill(q, k, v, causal=True, rows=None):
 
 
 def paged_attention(qkv, Hq, Hkv, D, kc, vc, dt, qo_indptr, kv_indptr, kv_indices, last_page_len,
-                    cos_t=None, sin_t=None):
-    """MPK attention task; kc/vc are updated in place (new tokens appended)."""
+                    cos_t=None, sin_t=None, q_norm=None, k_norm=None, qk_eps=1e-6):
+    """MPK attention task; kc/vc are updated in place (new tokens appended).
+    q_norm / k_norm: per-head RMSNorm weights [D] applied before RoPE."""
     qkv = _c(qkv, np.float32)
     assert kc.dtype == np.uint16 and kc.flags.c_contiguous and vc.flags.c_contiguous
     page = kc.shape[1]
@@ -225,7 +227,8 @@ def paged_attention(qkv, Hq, Hkv, D, kc, vc, dt, qo_indptr, kv_indptr, kv_indice
     lib().yo_paged_attention(_p(qkv), Hq, Hkv, D, _p(kc), _p(vc), dt_code(dt), page, R,
                              _p(_c(qo_indptr, np.int32)), _p(_c(kv_indptr, np.int32)),
                              _p(_c(kv_indices, np.int32)), _p(_c(last_page_len, np.int32)),
-                             _p(ct), _p(st), _p(out))
+                             _p(ct), _p(st), _p(None if q_norm is None else _c(q_norm, np.float32)),
+                             _p(None if k_norm is None else _c(k_norm, np.float32)), float(qk_eps), _p(out))
     return out
 
 

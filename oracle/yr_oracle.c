@@ -420,10 +420,22 @@ void yo_gqa_prefill(const float* q, const float* k, const float* v, int B, int S
  * seq_len = (pages - 1) * page + last_page_len, with last_page_len == 0 read as
  * a full last page (the page manager writes 0 for an exactly full page,
  * persistent_kernel.cuh:250-251).  cos/sin may be NULL (no RoPE). */
+/* Per-head RMSNorm of q / k before RoPE (qk_norm of the reference's paged
+ * attention task: multitoken_paged_attention_4_16.cuh:348-375 calling
+ * tasks/ampere/norm.cuh:21-126): x_i * rsqrt(mean(x^2) + eps) * w_i, stored
+ * back in the activation type before the rotation reads it. */
+static void qk_norm_head(float* v, int D, const float* w, double eps, int dt) {
+  double ss = 0.0;
+  for (int i = 0; i < D; i++) ss += (double)v[i] * v[i];
+  const double rcp = 1.0 / sqrt(ss / D + eps);
+  for (int i = 0; i < D; i++) v[i] = round16((float)(v[i] * rcp * w[i]), dt);
+}
+
 void yo_paged_attention(const float* qkv, int Hq, int Hkv, int D, uint16_t* kc, uint16_t* vc, int dt,
                         int page, int R, const int* qo_indptr, const int* kv_indptr,
                         const int* kv_indices, const int* last_page_len, const float* cos_t,
-                        const float* sin_t, float* out) {
+                        const float* sin_t, const float* q_norm, const float* k_norm, float qk_eps,
+                        float* out) {
   init_tables();
   int G = Hq / Hkv;
   int row = (Hq + 2 * Hkv) * D;
@@ -444,6 +456,7 @@ void yo_paged_attention(const float* qkv, int Hq, int Hkv, int D, uint16_t* kc, 
       for (int hk = 0; hk < Hkv; hk++) {
         float kb[1024];
         memcpy(kb, src + (size_t)hk * (G + 2) * D + (size_t)G * D, sizeof(float) * D);
+        if (k_norm) qk_norm_head(kb, D, k_norm, qk_eps, dt);
         if (cos_t) rope_head(kb, D, cos_t + (size_t)pos * D, sin_t + (size_t)pos * D, dt);
         const float* vb = src + (size_t)hk * (G + 2) * D + (size_t)(G + 1) * D;
         int pg = kv_indices[kv_indptr[r] + pos / page];
@@ -475,6 +488,7 @@ void yo_paged_attention(const float* qkv, int Hq, int Hkv, int D, uint16_t* kc, 
         const float* src = qkv + (size_t)(t0 + j) * row + (size_t)hk * (G + 2) * D;
         for (int g = 0; g < G; g++) {
           memcpy(qbuf, src + (size_t)g * D, sizeof(float) * D);
+          if (q_norm) qk_norm_head(qbuf, D, q_norm, qk_eps, dt);
           if (cos_t) rope_head(qbuf, D, cos_t + (size_t)pos * D, sin_t + (size_t)pos * D, dt);
           attend(qbuf, D, pos + 1, kr, vr, scale,
                  out + (size_t)(t0 + j) * Hq * D + (size_t)(hk * G + g) * D);

@@ -9,7 +9,16 @@ regenerated with the same counter-hash generator and seeds the device used.
 import numpy as np
 
 from oracle import oracle as O
-from yirage_amd.llama import page_table, rope_tables, tensor_seed, weight_shapes
+from yirage_amd.llama import QK_NORM_STD, page_table, rope_tables, tensor_seed, weight_shapes
+
+
+def qk_norm_weights(cfg, seed, layer):
+    """(q_norm, k_norm) float weights of a layer, as LlamaDecodeModel makes
+    them (1 + N(0, QK_NORM_STD) rounded to bf16), or (None, None)."""
+    if not cfg.qk_norm:
+        return None, None
+    return tuple(O.round_to(1.0 + O.to_float(O.synth((cfg.head_dim,), "bf16", tensor_seed(seed, layer, n),
+                                                     QK_NORM_STD), "bf16"), "bf16") for n in ("qn", "kn"))
 
 
 def decode_step(cfg, batch, kv_len, page, seed, tokens, return_logits=True):
@@ -40,8 +49,9 @@ def decode_step(cfg, batch, kv_len, page, seed, tokens, return_logits=True):
         shp = (pool, page, cfg.num_kv_heads, D)
         kc = O.synth(shp, bf, tensor_seed(seed, layer, "kc"), 1.0)
         vc = O.synth(shp, bf, tensor_seed(seed, layer, "vc"), 1.0)
+        qn, kn = qk_norm_weights(cfg, seed, layer)
         att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, kc, vc, bf, qo, indptr,
-                                           indices, lpl, cos, sin), bf)
+                                           indices, lpl, cos, sin, q_norm=qn, k_norm=kn), bf)
         h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
         hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
         gate = O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf)
@@ -89,9 +99,10 @@ class ServingOracle:
             for g in range(cfg.num_kv_heads):
                 rows += [W["wq"][g * G * D:(g + 1) * G * D], W["wk"][g * D:(g + 1) * D], W["wv"][g * D:(g + 1) * D]]
             qkv = O.round_to(O.linear(xn, np.concatenate(rows, 0), bf, O.W_NK), bf)
+            qn, kn = qk_norm_weights(cfg, self.seed, layer)
             att = O.round_to(O.paged_attention(qkv, cfg.num_q_heads, cfg.num_kv_heads, D, self.kc[layer],
                                                self.vc[layer], bf, qo_indptr, kv_indptr, kv_indices, last_page_len,
-                                               self.cos, self.sin), bf)
+                                               self.cos, self.sin, q_norm=qn, k_norm=kn), bf)
             h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
             hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
             gate = O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf)

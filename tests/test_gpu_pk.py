@@ -44,11 +44,14 @@ def _check(model, tokens, ref_logits, ref_ids, what, rel_l2=None, elementwise=Fa
             print(f"  near-tie at row {b}: gap {gap}", flush=True)
 
 
-@pytest.mark.parametrize("batch,kv_len", [(1, 200), (3, 130), (8, 64)])
-def test_small_llama_decode_step(batch, kv_len):
+@pytest.mark.parametrize("batch,kv_len,qk_norm", [(1, 200, False), (3, 130, False), (8, 64, False),
+                                                  (1, 200, True), (3, 130, True)])
+def test_small_llama_decode_step(batch, kv_len, qk_norm):
+    """qk_norm: per-head RMSNorm of q and the new k before RoPE
+    (paged_attention_layer(q_norm=..., k_norm=...))."""
     cfg = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, head_dim=128, intermediate=2048,
-                      vocab=4096)
-    print(f"case small llama B={batch} kv={kv_len}", flush=True)
+                      vocab=4096, qk_norm=qk_norm)
+    print(f"case small llama B={batch} kv={kv_len} qk_norm={qk_norm}", flush=True)
     model = LlamaDecodeModel(cfg, batch=batch, kv_len=kv_len, seed=3)
     tokens = (np.arange(batch) * 37 + 11) % cfg.vocab
     model.set_input_tokens(tokens)

@@ -56,7 +56,7 @@ def _compare_meta(dev, bm, MR, what):
     assert np.array_equal(dev["step"], bm["step"]), f"{what}: step differs"
 
 
-def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
+def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request, cfg=CFG):
     """CPU-only run of the schedule until `request` produces its first
     generated token (the schedule up to there does not depend on eos).
     Returns the token and the gap between its logit and the runner-up's."""
@@ -64,7 +64,7 @@ def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
     for i, p in enumerate(prompts):
         tokens[i, :len(p)] = p
     bm = O.BatchManager(MR, MT, pool, page, tokens, np.array([len(p) for p in prompts], np.int32), -1)
-    orc = ServingOracle(CFG, pool, page, seed, max_seq)
+    orc = ServingOracle(cfg, pool, page, seed, max_seq)
     bm.prepare_next()
     for _ in range(200):
         T = int(bm["qo_indptr"][MR])
@@ -80,23 +80,29 @@ def _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, request):
     raise AssertionError("request never produced a token")
 
 
-@pytest.mark.parametrize("MR,MT,lens", [(2, 8, (50, 37, 5)), (3, 8, (9, 70, 3, 20))])
-def test_serving_prefill_decode_eos(MR, MT, lens):
+QKN = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, head_dim=128, intermediate=2048,
+                  vocab=4096, qk_norm=True)
+
+
+@pytest.mark.parametrize("MR,MT,lens,cfg", [(2, 8, (50, 37, 5), CFG), (3, 8, (9, 70, 3, 20), CFG),
+                                            (2, 8, (33, 12, 6), QKN)],
+                         ids=["mr2", "mr3", "mr2-qknorm"])
+def test_serving_prefill_decode_eos(MR, MT, lens, cfg):
     page, max_seq = 64, 80
     npg = (max_seq + page - 1) // page
     pool = MR * npg
-    print(f"case serving MR={MR} MT={MT} prompts {list(lens)}", flush=True)
+    print(f"case serving MR={MR} MT={MT} prompts {list(lens)} qk_norm={cfg.qk_norm}", flush=True)
     # eos = the first token request 1 generates, so that request ends by EOS;
     # the first seed from 5 on whose token wins by a clear margin (a near tie
     # may go either way on the GPU, and the EOS case would not be exercised)
     for seed in range(5, 25):
         rng = np.random.default_rng(seed)
-        prompts = [rng.integers(0, CFG.vocab, n).tolist() for n in lens]
-        eos, gap = _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, 1)
+        prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in lens]
+        eos, gap = _simulate_first_output(prompts, MR, MT, pool, page, max_seq, seed, 1, cfg)
         if gap > 0.1:
             break
     print(f"  seed {seed} eos token {eos} (logit gap {gap:.3f})", flush=True)
-    model = LlamaDecodeModel(CFG, batch=MR, page_size=page, seed=seed, with_prepare=True, prompts=prompts,
+    model = LlamaDecodeModel(cfg, batch=MR, page_size=page, seed=seed, with_prepare=True, prompts=prompts,
                              max_tokens=MT, max_requests=MR, max_seq=max_seq, eos_token_id=eos)
     torch.cuda.synchronize()
     assert model.max_pages == pool
@@ -104,7 +110,7 @@ def test_serving_prefill_decode_eos(MR, MT, lens):
     for i, p in enumerate(prompts):
         tokens[i, :len(p)] = p
     bm = O.BatchManager(MR, MT, pool, page, tokens, np.array(lens, np.int32), eos)
-    orc = ServingOracle(CFG, pool, page, seed, max_seq)
+    orc = ServingOracle(cfg, pool, page, seed, max_seq)
     worst, near, launches, multi = 0.0, 0, 0, 0
     for launch in range(400):
         before = _meta(model)
@@ -117,7 +123,7 @@ def test_serving_prefill_decode_eos(MR, MT, lens):
         out_ids = model.meta["output_tokens"].cpu().numpy().reshape(-1)[:T]
         if T:
             qo = before["qo_indptr"]
-            multi += int(np.any(np.diff(qo) * (CFG.num_q_heads // CFG.num_kv_heads) > 16))
+            multi += int(np.any(np.diff(qo) * (cfg.num_q_heads // cfg.num_kv_heads) > 16))
             ref_logits, ref_ids = orc.step(before["input_tokens"][:T], qo, before["kv_indptr"],
                                            before["kv_indices"], before["last_page_len"])
             got = model.t["argmax_in"].tensor.float().cpu().numpy()[:T]
@@ -142,7 +148,7 @@ def test_serving_prefill_decode_eos(MR, MT, lens):
             # the K / V the device appended (every position of the batch's
             # requests) against the oracle's own cache
             kvp, kvi, lpl = before["kv_indptr"], before["kv_indices"], before["last_page_len"]
-            for layer in range(CFG.num_layers):
+            for layer in range(cfg.num_layers):
                 dk = model.kc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
                 dv = model.vc[layer].view(torch.int16).cpu().numpy().view(np.uint16)
                 for r in range(MR):

@@ -291,6 +291,81 @@ def test_paged_attention_task_rope_append_causal():
                 np.testing.assert_allclose(got, ref.numpy(), rtol=1e-5, atol=1e-6)
 
 
+def test_paged_attention_qk_norm_vs_torch_and_invariances():
+    """qk_norm of the paged-attention task (multitoken_paged_attention_4_16.cuh:
+    348-375, tasks/ampere/norm.cuh:21-126): per-head RMSNorm of q and of the
+    new k (eps 1e-6, weights [D]), stored in bf16, then RoPE.  Pinned by
+      * torch: F.rms_norm in float64 + bf16 rounding + rotate-half RoPE +
+        SDPA over the appended cache;
+      * scale invariance: q / k columns scaled by 4 (exact in bf16) give the
+        same output and cache (without the norm both would change);
+      * constant rows: a q / k head of one repeated value c normalizes to
+        sign(c) * w, so it attends exactly like an un-normalized head w."""
+    import torch.nn.functional as F
+
+    Hq, Hkv, D, page = 4, 2, 16, 4
+    G = Hq // Hkv
+    cos, sin = _rope_tables(16, D, base=10000.0)
+    qn = O.round_to(0.5 + rng.random(D), "bf16")
+    kn = O.round_to(0.5 + rng.random(D), "bf16")
+    kc = O.from_float(rng.standard_normal((3, page, Hkv, D)), "bf16")
+    vc = O.from_float(rng.standard_normal((3, page, Hkv, D)), "bf16")
+    qo, kv_indptr, kv_indices, lpl = np.int32([0, 2]), np.int32([0, 2]), np.int32([2, 0]), np.int32([3])
+    qkv = O.round_to(3.0 * rng.standard_normal((2, (Hq + 2 * Hkv) * D)), "bf16")
+
+    def run(x, kc_, vc_, **kw):
+        kc_, vc_ = kc_.copy(), vc_.copy()
+        out = O.paged_attention(x, Hq, Hkv, D, kc_, vc_, "bf16", qo, kv_indptr, kv_indices, lpl, cos, sin, **kw)
+        return out, kc_
+
+    out, kc1 = run(qkv, kc, vc, q_norm=qn, k_norm=kn)
+    # torch composition
+    def norm_rope(x, w, pos):
+        xt = torch.from_numpy(x).double()
+        y = F.rms_norm(xt, (D,), torch.from_numpy(w).double(), eps=1e-6).to(torch.bfloat16).double()
+        rot = torch.cat((-y[..., D // 2:], y[..., : D // 2]), -1)
+        c, s_ = torch.from_numpy(cos[pos]).double(), torch.from_numpy(sin[pos]).double()
+        return (y * c + rot * s_).to(torch.bfloat16).double()
+
+    seq, pages = 7, [2, 0]
+    Kall = torch.from_numpy(O.to_float(kc, "bf16")[pages].reshape(-1, Hkv, D)[:seq].copy()).double()
+    Vall = torch.from_numpy(O.to_float(vc, "bf16")[pages].reshape(-1, Hkv, D)[:seq].copy()).double()
+    for j in range(2):
+        pos = seq - 2 + j
+        row = qkv[j].reshape(Hkv, G + 2, D)
+        Kall[pos] = norm_rope(row[:, G], kn, pos)
+        Vall[pos] = torch.from_numpy(row[:, G + 1]).double()
+    np.testing.assert_array_equal(O.to_float(kc1, "bf16")[pages].reshape(-1, Hkv, D)[:seq], Kall.numpy())
+    for j in range(2):
+        pos = seq - 2 + j
+        row = qkv[j].reshape(Hkv, G + 2, D)
+        for hk in range(Hkv):
+            qh = norm_rope(row[hk, :G], qn, pos)
+            K, V = Kall[: pos + 1, hk], Vall[: pos + 1, hk]
+            ref = _sdpa(qh[:, None], K[None].expand(G, -1, -1), V[None].expand(G, -1, -1))[:, 0]
+            np.testing.assert_allclose(out[j].reshape(Hq, D)[hk * G:(hk + 1) * G], ref.numpy(), rtol=1e-5,
+                                       atol=1e-6)
+    # scale invariance of the q and k columns
+    sc = qkv.copy().reshape(2, Hkv, G + 2, D)
+    sc[:, :, : G + 1] *= 4.0
+    out4, kc4 = run(sc.reshape(2, -1), kc, vc, q_norm=qn, k_norm=kn)
+    np.testing.assert_allclose(out4, out, rtol=0, atol=1e-6)
+    np.testing.assert_array_equal(kc4, kc1)
+    plain, _ = run(sc.reshape(2, -1), kc, vc)
+    assert np.abs(plain - out).max() > 1e-2  # the check above would catch a dropped norm
+    # constant heads: normalize to sign(c) * w
+    cst = qkv.copy().reshape(2, Hkv, G + 2, D)
+    cst[:, :, :G] = -2.5
+    cst[:, :, G] = 0.75
+    a, kca = run(cst.reshape(2, -1), kc, vc, q_norm=qn, k_norm=kn)
+    ww = cst.copy()
+    ww[:, :, :G] = -qn
+    ww[:, :, G] = kn
+    b, kcb = run(ww.reshape(2, -1), kc, vc)
+    np.testing.assert_allclose(a, b, rtol=0, atol=1e-6)
+    np.testing.assert_array_equal(kca, kcb)
+
+
 # ------------------------------------------------------------- argmax
 
 def test_argmax_planted_known_answer():

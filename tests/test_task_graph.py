@@ -139,3 +139,24 @@ def test_reference_vocabulary_graph_loads_and_builds():
                      "rmsnorm_linear_argmax"]
     silu = pk.ops[4]
     assert silu["group"] == 32 and silu["weight"] == [("wgu", 0, 2 * cfg.intermediate)]
+
+
+def test_qk_norm_graph_round_trip():
+    """paged_attention_layer(q_norm=..., k_norm=...): the export lists the
+    reference's operand order (input, k_cache, v_cache, q_norm, k_norm, cos,
+    sin) and re-imports to the same tasks; the op carries the qk-norm flag."""
+    cfg = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, intermediate=2048, vocab=4096,
+                      qk_norm=True)
+    model = LlamaDecodeModel(cfg, batch=1, kv_len=100, device="meta")
+    att = [o for o in model.pk.ops if o["type"] == "attention"]
+    assert att and all(o["q_norm"] and o["k_norm"] for o in att)
+    text = model.pk.export_task_graph()
+    g = json.loads(text)
+    pa = [t for t in g["all_tasks"] if t["task_type"] == 116]
+    assert pa and [len(t["inputs"]) for t in pa[:1]] == [7]
+    assert pa[0]["inputs"][3]["dims"] == [cfg.head_dim] and pa[0]["inputs"][4]["dims"] == [cfg.head_dim]
+    pk2 = _fresh_pk(model)
+    load_task_graph(text, pk2, _binding(model.pk))
+    pk2.compile(build_only=True)
+    assert np.array_equal(pk2.task_table(), model.pk.task_table())
+    assert [o.get("q_norm") for o in pk2.ops if o["type"] == "attention"] == [o["q_norm"] for o in att]

@@ -350,6 +350,21 @@ void Graph::build(const char* text) {
       int ct = ptr_tensor(*this, o, "cos", true), st = ptr_tensor(*this, o, "sin", true);
       d.cos_t = ct >= 0 ? (const uint16_t*)tensors[ct].ptr : nullptr;
       d.sin_t = st >= 0 ? (const uint16_t*)tensors[st].ptr : nullptr;
+      // qk-norm (paged_attention_layer(q_norm=..., k_norm=...)): both or neither, [head_dim] each, eps 1e-6
+      // as the reference's task passes it (task_register.cc:294-295)
+      int qn = ptr_tensor(*this, o, "q_norm", true), kn = ptr_tensor(*this, o, "k_norm", true);
+      if ((qn >= 0) != (kn >= 0)) throw std::runtime_error("attention: q_norm and k_norm come together");
+      if (qn >= 0) {
+        for (int w : {qn, kn})
+          if (tensors[w].dims.size() != 1 || tensors[w].dims[0] != d.head_dim)
+            throw std::runtime_error("attention: q_norm / k_norm must be [head_dim]");
+        d.flags |= OPF_QK_NORM;
+        d.norm = (const uint16_t*)tensors[qn].ptr;
+        d.k_norm = (const uint16_t*)tensors[kn].ptr;
+        d.eps = 1e-6f;
+      }
+      info.norm = qn;
+      info.knorm = kn;
       d.max_tokens = cfg.max_tokens;
       d.ticket_base = ticket_next;
       ticket_next += cfg.max_requests * d.num_kv_heads;
@@ -738,6 +753,9 @@ std::string Graph::export_json() const {
           const Tensor& ct = tensors[c];
           I.add(ct, 0, ct.dims, {ct.dims[1] * ct.dims[2] * ct.dims[3], ct.dims[2] * ct.dims[3], ct.dims[3], 1});
         }
+        // the reference's operand order: input, k_cache, v_cache, q_norm, k_norm, cos, sin
+        for (int c : {inf.norm, inf.knorm})
+          if (c >= 0) I.add(tensors[c], 0, {(int64_t)D}, {1});
         for (int c : {inf.cos, inf.sin})
           if (c >= 0) I.add(tensors[c], 0, tensors[c].dims, {tensors[c].dims[1], 1});
         Ot.add(tensors[inf.out], (int64_t)h * G * D, {T, (int64_t)G * D}, {tensors[inf.out].dims[1], 1});

@@ -49,7 +49,7 @@ struct OpInfo {
   int kv_group_width = 0, kv_groups = 0, group_reads_qkv = -1;
   // operand tensors (-1: none), for the task-graph export
   int x = -1, out = -1, res = -1, norm = -1, tok = -1, table = -1, tok_out = -1, kc = -1, vc = -1, cos = -1,
-      sin = -1;
+      sin = -1, knorm = -1;
   std::vector<WSeg> wsegs;
   int group = 0, col0 = 0;
 };

@@ -1094,6 +1094,60 @@ __device__ __forceinline__ void rope_apply(const RopeVec& v, uint4 (&out)[4], Op
   }
 }
 
+// qk-norm (multitoken_paged_attention_4_16.cuh:348-375 calling
+// tasks/ampere/norm.cuh:21-126): one head row of 128 values is RMS-normalized
+// with weights w[128] (eps from the op), each value rounded to bf16 before
+// RoPE reads it.  Row layout of the q / k fragments above: four 8-element
+// chunks per lane (d = 32 q + 8 (lane / 16)), the row's other 96 values in
+// lanes lane ^ 16, ^ 32, ^ 48.  Every lane of the wave must call it.
+__device__ __forceinline__ void qk_norm4(uint4 (&x)[4], const uint16_t* w, int lane, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t v[4] = {x[q].x, x[q].y, x[q].z, x[q].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float lo = lo16<DT_BF16>(v[e]), hi = hi16<DT_BF16>(v[e]);
+      ss += lo * lo + hi * hi;
+    }
+  }
+  ss += __shfl_xor(ss, 16, kWave);
+  ss += __shfl_xor(ss, 32, kWave);
+  const float rr = rsqrtf(ss * (1.f / 128.f) + eps);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint4 wq = ldg16(w + 32 * q + (lane / 16) * 8);
+    const uint32_t v[4] = {x[q].x, x[q].y, x[q].z, x[q].w}, wv[4] = {wq.x, wq.y, wq.z, wq.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      o[e] = pack2<DT_BF16>(lo16<DT_BF16>(v[e]) * (rr * lo16<DT_BF16>(wv[e])),
+                            hi16<DT_BF16>(v[e]) * (rr * hi16<DT_BF16>(wv[e])));
+    x[q] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+// 8 values of a row given 1 / rms: x * (rr * w), rounded to bf16
+__device__ __forceinline__ uint4 qk_scale8(uint4 x, const uint16_t* w8, float rr) {
+  const uint4 wq = ldg16(w8);
+  const uint32_t v[4] = {x.x, x.y, x.z, x.w}, wv[4] = {wq.x, wq.y, wq.z, wq.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    o[e] = pack2<DT_BF16>(lo16<DT_BF16>(v[e]) * (rr * lo16<DT_BF16>(wv[e])),
+                          hi16<DT_BF16>(v[e]) * (rr * hi16<DT_BF16>(wv[e])));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+__device__ __forceinline__ float sumsq8(uint4 x) {
+  const uint32_t v[4] = {x.x, x.y, x.z, x.w};
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float lo = lo16<DT_BF16>(v[e]), hi = hi16<DT_BF16>(v[e]);
+    ss += lo * lo + hi * hi;
+  }
+  return ss;
+}
+
 template <int RMAX>
 __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const TaskDesc& t, int task_id, int slot,
                                                     Shared& sm) {
@@ -1258,6 +1312,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       rope_tab_lds(qin, tabs + (qok ? qj : 0) * 256, lane);
 #pragma unroll
       for (int q = 0; q < 4; q++) qin.x[q] = act8_data(lk, qr[q]);
+      if (op.flags & OPF_QK_NORM) qk_norm4(qin.x, op.norm, lane, op.eps);
       uint4 qo[4];
       rope_apply(qin, qo, op);
 #pragma unroll
@@ -1268,6 +1323,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
         rope_tab_lds(kin, tabs + (kok ? ik : 0) * 256, lane);
 #pragma unroll
         for (int q = 0; q < 4; q++) kin.x[q] = act8_data(lk, kr[q]);
+        if (op.flags & OPF_QK_NORM) qk_norm4(kin.x, op.k_norm, lane, op.eps);
         uint4 ko[4];
         rope_apply(kin, ko, op);
         auto tok_off = [&](int pg, int pos) __attribute__((always_inline)) -> size_t {
@@ -1649,9 +1705,20 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
     for (int idx = tix(); idx < nt * 16; idx += PK_THREADS) {
       const int i = idx / 16, c = idx % 16, cp = (c + 8) & 15;  // 8-dim chunk and its rotate-half partner
       const uint16_t* row = op.x + (size_t)(t0 + i) * op.qkv_ld + e_grp;
-      const uint4 kx = ld_agent_u128(row + (size_t)G * D + 8 * c);
-      const uint4 kp = ld_agent_u128(row + (size_t)G * D + 8 * cp);
+      uint4 kx = ld_agent_u128(row + (size_t)G * D + 8 * c);
+      uint4 kp = ld_agent_u128(row + (size_t)G * D + 8 * cp);
       const uint4 vv = ld_agent_u128(row + (size_t)(G + 1) * D + 8 * c);
+      if (op.flags & OPF_QK_NORM) {
+        // the row's 16 chunks sit in 16 consecutive lanes (idx % 16 = c)
+        float ss = sumsq8(kx);
+        ss += __shfl_xor(ss, 1, kWave);
+        ss += __shfl_xor(ss, 2, kWave);
+        ss += __shfl_xor(ss, 4, kWave);
+        ss += __shfl_xor(ss, 8, kWave);
+        const float rr = rsqrtf(ss * (1.f / 128.f) + op.eps);
+        kx = qk_scale8(kx, op.k_norm + 8 * c, rr);
+        kp = qk_scale8(kp, op.k_norm + 8 * cp, rr);
+      }
       uint4 kr = kx;
       if (op.cos_t) {
         const int pos = base + i;
@@ -1705,6 +1772,7 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
           qv.s[q] = ldg16(op.sin_t + pe);
         }
       }
+      if (op.flags & OPF_QK_NORM) qk_norm4(qv.x, op.norm, lane, op.eps);
       rope_apply(qv, qf, op);
     }
     float m_i[4], l_i[4], o_acc[16][8];

@@ -30,6 +30,7 @@ enum OpFlags : int {
   OPF_X_LL = 2,              // x (qkv for attention) is a link tensor written by op x_src
   OPF_RES_LL = 4,            // residual is a link tensor written by op res_src
   OPF_OUT_LL = 8,            // out is a link tensor
+  OPF_QK_NORM = 16,          // attention: per-head RMSNorm of q (weights `norm`) and new k (`k_norm`) before RoPE
 };
 
 // Link tensors: activations passed between CUs inside one launch are stored
@@ -67,6 +68,7 @@ struct OpDesc {
   const int64_t* tokens_in; // embed: token ids [max_tokens]
   const uint16_t* table;    // embed: [vocab][hidden]
   int64_t* tokens_out;      // argmax: output token ids [max_tokens]
+  const uint16_t* k_norm;   // attention qk-norm: k weights [head_dim] (q weights in `norm`)
 };
 
 // One per task (workgroup-sized unit of work).

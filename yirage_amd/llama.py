@@ -32,6 +32,7 @@ class LlamaConfig:
     rope_theta: float = 500000.0
     eps: float = 1e-6        # the reference MPK rmsnorm task uses 1e-6 (task_register.cc:118-122)
     weight_std: float = 0.02
+    qk_norm: bool = False    # per-head RMSNorm of q and k before RoPE (Qwen3-style; paged_attention_layer q_norm/k_norm)
 
     @property
     def qkv_out(self) -> int:
@@ -47,7 +48,8 @@ class LlamaConfig:
 LLAMA3_8B = LlamaConfig()
 
 # tensor ids for the deterministic generator: seed = base * 1000 + layer * 16 + id
-_IDS = {"wq": 1, "wk": 2, "wv": 3, "wo": 4, "wg": 5, "wu": 6, "wd": 7, "kc": 8, "vc": 9}
+_IDS = {"wq": 1, "wk": 2, "wv": 3, "wo": 4, "wg": 5, "wu": 6, "wd": 7, "kc": 8, "vc": 9, "qn": 10, "kn": 11}
+QK_NORM_STD = 0.1  # qk-norm weights: 1 + N(0, 0.1), rounded to bf16
 
 
 def tensor_seed(base: int, layer: int, name: str) -> int:
@@ -119,6 +121,11 @@ class LlamaDecodeModel:
                 t = torch.empty(shp, dtype=bf, device=dev)
                 fill(t, tensor_seed(seed, layer, name), cfg.weight_std)
                 lw[name] = t
+            if cfg.qk_norm:
+                for name in ("qn", "kn"):
+                    t = torch.empty(cfg.head_dim, dtype=bf, device=dev)
+                    fill(t, tensor_seed(seed, layer, name), QK_NORM_STD)
+                    lw[name] = t if self.graph_only else (1.0 + t.float()).to(bf)
             lw["ln1"] = torch.ones(H, dtype=bf, device=dev)
             lw["ln2"] = torch.ones(H, dtype=bf, device=dev)
             self.w.append(lw)
@@ -225,7 +232,11 @@ class LlamaDecodeModel:
                             block_dim=(128, 1, 1))
             kc = pk.attach_input(self.kc[i], name=f"layer_{i}_k_cache")
             vc = pk.attach_input(self.vc[i], name=f"layer_{i}_v_cache")
-            pk.paged_attention_layer(input=t["attn_in"], k_cache=kc, v_cache=vc, q_norm=None, k_norm=None,
+            qn = kn = None
+            if cfg.qk_norm:
+                qn = pk.attach_input(lw["qn"], name=f"layer_{i}_q_norm")
+                kn = pk.attach_input(lw["kn"], name=f"layer_{i}_k_norm")
+            pk.paged_attention_layer(input=t["attn_in"], k_cache=kc, v_cache=vc, q_norm=qn, k_norm=kn,
                                      cos_pos_embed=cos, sin_pos_embed=sin, output=t["attn_out"],
                                      grid_dim=(self.MR, cfg.num_kv_heads, 1), block_dim=(128, 1, 1))
             wo = pk.attach_input(lw["wo"], name=f"layer_{i}_o_proj")

@@ -212,12 +212,20 @@ class PersistentKernel:
     def paged_attention_layer(self, input: DTensor, k_cache: DTensor, v_cache: DTensor, q_norm: DTensor,
                               k_norm: DTensor, cos_pos_embed: DTensor, sin_pos_embed: DTensor, output: DTensor,
                               grid_dim: tuple, block_dim: tuple):
-        if q_norm is not None or k_norm is not None:
-            raise YirageHipError("hip backend: qk-norm in paged attention is not supported")
+        """python/yirage/persistent_kernel.py:532-609: RoPE (cos / sin
+        [seq, head_dim]) and, with q_norm / k_norm ([head_dim] each, both or
+        neither), per-head RMSNorm of q and the new k before it (eps 1e-6)."""
         assert k_cache.dim(0) == self.max_num_pages and k_cache.dim(1) == self.page_size
+        head_dim = k_cache.dim(3)
+        if (q_norm is None) != (k_norm is None):
+            raise YirageHipError("paged_attention_layer: q_norm and k_norm come together")
+        if q_norm is not None:
+            for w in (q_norm, k_norm):
+                if w.num_dims != 1 or w.dim(0) != head_dim:
+                    raise YirageHipError("paged_attention_layer: q_norm / k_norm must be [head_dim]")
         self._add("attention", input=input, k_cache=k_cache, v_cache=v_cache, cos=cos_pos_embed,
-                  sin=sin_pos_embed, output=output, num_q_heads=output.dim(1) // k_cache.dim(3),
-                  num_kv_heads=k_cache.dim(2), head_dim=k_cache.dim(3))
+                  sin=sin_pos_embed, q_norm=q_norm, k_norm=k_norm, output=output,
+                  num_q_heads=output.dim(1) // head_dim, num_kv_heads=k_cache.dim(2), head_dim=head_dim)
 
     def argmax_partial_layer(self, input: DTensor, output: tuple, grid_dim: tuple, block_dim: tuple):
         self._add("argmax_partial", input=input, output=output)
@@ -350,7 +358,10 @@ class PersistentKernel:
                 splits = max(1, min(256, W // (self.ATTN_SPLIT_DIVISOR * per)))
                 ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
                                 v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
-                                sin=l["sin"].name if l["sin"] is not None else None, out=l["output"].name,
+                                sin=l["sin"].name if l["sin"] is not None else None,
+                                q_norm=l["q_norm"].name if l["q_norm"] is not None else None,
+                                k_norm=l["k_norm"].name if l["k_norm"] is not None else None,
+                                out=l["output"].name,
                                 num_q_heads=l["num_q_heads"], num_kv_heads=l["num_kv_heads"],
                                 head_dim=l["head_dim"], splits=splits))
                 i += 1

@@ -193,11 +193,17 @@ def load_task_graph(graph, pk, tensors: dict, name_prefix: str = "tg"):
             pk.silu_mul_layer(input=dt(ins[0]["base_ptr"]), output=dt(outs[0]["base_ptr"]),
                               grid_dim=(len(grp), 1, 1), block_dim=(128, 1, 1))
         elif ty == PAGED_ATTN:
+            # operands: input, k_cache, v_cache, [q_norm, k_norm (1-D)], [cos, sin]
             names = [p["base_ptr"] for p in ins]
-            cos = dt(names[3]) if len(names) > 3 else None
-            sin = dt(names[4]) if len(names) > 4 else None
-            pk.paged_attention_layer(input=dt(names[0]), k_cache=dt(names[1]), v_cache=dt(names[2]), q_norm=None,
-                                     k_norm=None, cos_pos_embed=cos, sin_pos_embed=sin,
+            rest = names[3:]
+            qn = kn = None
+            if len(rest) >= 2 and len(ins[3]["dims"]) == 1 and len(ins[4]["dims"]) == 1:
+                qn, kn = dt(rest[0]), dt(rest[1])
+                rest = rest[2:]
+            cos = dt(rest[0]) if len(rest) > 0 else None
+            sin = dt(rest[1]) if len(rest) > 1 else None
+            pk.paged_attention_layer(input=dt(names[0]), k_cache=dt(names[1]), v_cache=dt(names[2]), q_norm=qn,
+                                     k_norm=kn, cos_pos_embed=cos, sin_pos_embed=sin,
                                      output=dt(outs[0]["base_ptr"]), grid_dim=(len(grp), 1, 1), block_dim=(128, 1, 1))
         elif ty == ARGMAX_PARTIAL:
             nxt = groups[i + 1] if i + 1 < len(groups) else None
