@@ -45,7 +45,8 @@ def _check(model, tokens, ref_logits, ref_ids, what, rel_l2=None, elementwise=Fa
 
 
 @pytest.mark.parametrize("batch,kv_len,qk_norm", [(1, 200, False), (3, 130, False), (8, 64, False),
-                                                  (1, 200, True), (3, 130, True)])
+                                                  (1, 200, True), (3, 130, True), (16, 100, False),
+                                                  (12, 70, True)])
 def test_small_llama_decode_step(batch, kv_len, qk_norm):
     """qk_norm: per-head RMSNorm of q and the new k before RoPE
     (paged_attention_layer(q_norm=..., k_norm=...))."""

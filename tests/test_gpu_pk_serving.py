@@ -85,8 +85,8 @@ QKN = LlamaConfig(num_layers=2, hidden=1024, num_q_heads=8, num_kv_heads=2, head
 
 
 @pytest.mark.parametrize("MR,MT,lens,cfg", [(2, 8, (50, 37, 5), CFG), (3, 8, (9, 70, 3, 20), CFG),
-                                            (2, 8, (33, 12, 6), QKN)],
-                         ids=["mr2", "mr3", "mr2-qknorm"])
+                                            (2, 8, (33, 12, 6), QKN), (3, 16, (9, 70, 3, 20), CFG)],
+                         ids=["mr2", "mr3", "mr2-qknorm", "mr3-mt16"])
 def test_serving_prefill_decode_eos(MR, MT, lens, cfg):
     page, max_seq = 64, 80
     npg = (max_seq + page - 1) // page
@@ -111,7 +111,7 @@ def test_serving_prefill_decode_eos(MR, MT, lens, cfg):
         tokens[i, :len(p)] = p
     bm = O.BatchManager(MR, MT, pool, page, tokens, np.array(lens, np.int32), eos)
     orc = ServingOracle(cfg, pool, page, seed, max_seq)
-    worst, near, launches, multi = 0.0, 0, 0, 0
+    worst, near, launches, multi, wide = 0.0, 0, 0, 0, 0
     for launch in range(400):
         before = _meta(model)
         T = int(before["qo_indptr"][MR])
@@ -124,6 +124,7 @@ def test_serving_prefill_decode_eos(MR, MT, lens, cfg):
         if T:
             qo = before["qo_indptr"]
             multi += int(np.any(np.diff(qo) * (cfg.num_q_heads // cfg.num_kv_heads) > 16))
+            wide += int(np.any(np.diff(qo) * (cfg.num_q_heads // cfg.num_kv_heads) > 32))
             ref_logits, ref_ids = orc.step(before["input_tokens"][:T], qo, before["kv_indptr"],
                                            before["kv_indices"], before["last_page_len"])
             got = model.t["argmax_in"].tensor.float().cpu().numpy()[:T]
@@ -182,9 +183,12 @@ def test_serving_prefill_decode_eos(MR, MT, lens, cfg):
             break
     else:
         raise AssertionError("requests did not finish")
-    print(f"  {launches} launches ({multi} with > 16 query rows per kv head), max logit err {worst:.4f}, "
+    print(f"  {launches} launches ({multi} with > 16, {wide} with > 32 query rows per kv head), "
+          f"max logit err {worst:.4f}, "
           f"{near} near-ties", flush=True)
     assert bm["next_request_id"][0] == len(prompts) and (bm["request_ids"] == -1).all()
     assert multi > 0, "no launch exercised the multi-token attention task"
+    if MT > 8:  # 9..16 tokens of one request: more than 32 query rows per kv head (the _32_64 regime)
+        assert wide > 0, "no launch ran more than 32 query rows per kv head"
     # request 1 ended on EOS right after its prompt; the others ran to max length or EOS
     assert bm["step"][1] == lens[1] and bm["tokens"][1, lens[1]] == eos

@@ -255,9 +255,21 @@ void Graph::build(const char* text) {
       }
       int rpt = (int)o["rows_per_task"].i64(16);
       if (rpt <= 0 || rpt % 2) throw std::runtime_error("rows_per_task must be even and > 0");
-      if (rpt * cfg.max_tokens > 4096) throw std::runtime_error("rows_per_task x max_tokens must be <= 4096");
+      if (cfg.max_tokens > 16) throw std::runtime_error("max_tokens must be <= 16");
+      {
+        // per-wave partial-sum slots of a task in LDS (8192 floats): [rows + 7]
+        // at one token, [16-row tiles + 7] x 16 x (8 or 16) tokens; the argmax
+        // epilogue keeps [tokens][rows] floats
+        const int rt = silu ? 2 * rpt : rpt;
+        const int tm = cfg.max_tokens == 1 ? 1 : (cfg.max_tokens <= 8 ? 8 : 16);
+        const int64_t slots = tm == 1 ? (int64_t)rt + 7 : ((int64_t)(rt + 15) / 16 + 7) * 16 * tm;
+        if (slots > 8192) throw std::runtime_error("rows_per_task too large for the partial-sum slots");
+        if (amax && (int64_t)tm * rpt > 8192) throw std::runtime_error("argmax: rows_per_task x tokens > 8192");
+      }
       if (col0 % 2 || d.out_ld % 2) throw std::runtime_error("linear output columns must be even-aligned");
-      if (norm && (cfg.max_tokens == 1 ? d.K > 32768 : d.K > 4096))
+      // the staged activation block holds all of K at <= 8 tokens (RMSNorm
+      // needs the whole row there); 16-token batches normalize while staging
+      if (norm && (cfg.max_tokens == 1 ? d.K > 32768 : (cfg.max_tokens <= 8 && d.K > 4096)))
         throw std::runtime_error("rmsnorm input too wide for the staged activation block");
       if (cfg.max_tokens > 1 && d.K > 4096 && rpt > 7 * 3 * (silu ? 1 : 1))
         throw std::runtime_error("batch > 1 with K > 4096: rows_per_task must be <= 21");

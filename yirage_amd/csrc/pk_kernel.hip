@@ -343,7 +343,10 @@ __device__ __forceinline__ int xs_swz(int b, int e) { return (((e >> 3) ^ b) << 
 
 // Sync wave: rows [0, TM) of elements [k0, k0 + KB) of op.x into xs[b][KB];
 // rows b >= T are zero.  16 loads per lane in flight.
-template <int TM>
+// NRM (16-token batches, where K no longer fits one staged block): each
+// value is normalized on the way in, x * (r_b * gamma) rounded to bf16, with
+// the row factors r_b = rsqrt(mean(x_b^2) + eps) from row_rms (in attn_ml).
+template <int TM, bool NRM = false>
 __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared& sm, int lane, int xoff = 0) {
   // groups of 64 chunks (one 16-byte load per lane): group m is row m / k,
   // chunks (m % k) * 64 + lane.  Row and group offsets are wave-uniform, so
@@ -376,6 +379,17 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
 #pragma unroll
     for (int u = 0; u < NB; u++) {
       uint16_t* dst = g + u < total ? sm.xs + xoff + xr * KB + xs_swz(xr, xc * 512 + lane * 8) : junk + lane * 8;
+      if constexpr (NRM) {
+        const float rb = sm.attn_ml[0][xr & 15][0];
+        const uint4 gq = ldg16(op.norm + k0 + xc * 512 + lane * 8);
+        const uint32_t xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w}, gv[4] = {gq.x, gq.y, gq.z, gq.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          o[e] = pack2<DT_BF16>(lo16<DT_BF16>(xv[e]) * (rb * lo16<DT_BF16>(gv[e])),
+                                hi16<DT_BF16>(xv[e]) * (rb * hi16<DT_BF16>(gv[e])));
+        v[u] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
       *reinterpret_cast<uint4*>(dst) = v[u];
       if (++xc == k) { xc = 0; xr++; }
     }
@@ -410,6 +424,47 @@ __device__ __forceinline__ void stage_x_coop(OpRef op, int T, int KB, Shared& sm
     const int mb = g / k, mc = g - mb * k;
     uint16_t* dst = g < total ? sm.xs + mb * KB + xs_swz(mb, mc * 512 + lane * 8) : junk + lane * 8;
     *reinterpret_cast<uint4*>(dst) = v[u];
+  }
+}
+
+// Sync wave, 16-token batches: r_b = rsqrt(mean(x_b^2) + eps) of every
+// active row over all of K, read from the input (rows past T give 0), into
+// attn_ml[0][b][0] -- RMSNorm's row factor before any block is staged.
+__device__ __forceinline__ void row_rms(OpRef op, int T, Shared& sm, int lane) {
+  const int K = op.K;
+  const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
+  const int row_bytes = op.x_ld * 2;
+  for (int b0 = 0; b0 < 16; b0 += 4) {
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < K; c += 8 * kWave * 4) {
+      uint4 v[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int col = c + (u * kWave + lane) * 8;
+          const int off = col < K ? (b0 + i) * row_bytes + col * 2 : 0x7ffffff0;
+          v[i][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, 0, off, kCpolSC1));
+        }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const uint32_t w4[4] = {v[i][u].x, v[i][u].y, v[i][u].z, v[i][u].w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
+            ss[i] += lo * lo + hi * hi;
+          }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float t = wave_sum(ss[i]);
+      if (lane == 0) sm.attn_ml[0][b0 + i][0] = rsqrtf(t / (float)K + op.eps);
+    }
   }
 }
 
@@ -684,8 +739,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM);
   const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
   // A unit is one 16-byte weight load per lane.  TM == 1: 512 elements of
-  // one row (dot products on VALU); TM == 8: a 16-row x 32-column MFMA A
-  // fragment (rows = a 16-row tile of the weight, columns = 8 tokens x 2).
+  // one row (dot products on VALU); TM == 8 / 16: a 16-row x 32-column MFMA A
+  // fragment (rows = a 16-row tile of the weight); the B operand is the
+  // staged activations, one token per MFMA column (8 or 16 valid).
   constexpr bool MF = TM > 1;
   constexpr int USH = MF ? 5 : 9;                  // log2 columns per unit
   const int NT = MF ? (RT + 15) / 16 : RT;         // rows (TM == 1) or 16-row tiles
@@ -744,7 +800,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     int T = sm.last_T;
     if (!same_op) {
       NormRegs nr;
-      const bool pre = NORM && K <= 4096;
+      // (16-token batches: K does not fit one staged block; rows are
+      // normalized while they are staged, see row_rms / stage_x<.., true>)
+      const bool pre = NORM && TM != 16 && K <= 4096;
       if (pre) load_norm(nr, op, lane);
       // a link input is validated word by word: no event poll (measured
       // faster than polling the producers' counter first)
@@ -755,6 +813,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
           if (a.profile && lane == 0) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
         } else if (TM > 1 && !(NORM && !pre)) {
           if (lane == 0) sm.coop_stage = 1;  // block 0 staged by all waves after [X]
+        } else if constexpr (NORM && TM == 16) {
+          row_rms(op, T, sm, lane);
+          stage_x<TM, true>(op, T, KB, 0, sm, lane);
         } else {
           stage_x<TM>(op, T, KB, 0, sm, lane);
         }
@@ -778,7 +839,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
           // normalized by all 8 waves after [X] (one wave alone spends ~1.5 us
           // issuing the row's arithmetic while the others wait)
           if (lane == 0) sm.norm_rows = T > 0 ? -1 : 0;
-        } else if (NORM) {
+        } else if (NORM && TM != 16) {
           norm_x(op, T, KB, sm, nr, pre, lane);
         }
       }
@@ -786,7 +847,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     }
     for (int i = lane; i < (MF ? (NT + CW) * 16 : RT + CW) * TM; i += kWave) slots[i] = 0.f;
-    if (lane == 0 && (same_op || !(NORM && K <= 4096))) sm.norm_rows = 0;
+    if (lane == 0 && (same_op || !(NORM && TM != 16 && K <= 4096))) sm.norm_rows = 0;
     if (lane == 0) {
       sm.last_T = T;
       sm.last_op = nkb == 1 ? t.op : -1;
@@ -818,7 +879,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     // compute waves consume block kb - 1 from the other half; barrier [Bkb]
     // = block kb staged and block kb - 1 consumed
     for (int kb = 1; kb < nkb; kb++) {
-      stage_x<TM>(op, T, KB, kb * KB, sm, lane, (kb & 1) * XS_HALF);
+      stage_x<TM, NORM && TM == 16>(op, T, KB, kb * KB, sm, lane, (kb & 1) * XS_HALF);
       lds_sync();  // [Bkb]
     }
   } else if (n == 0) {
@@ -2096,6 +2157,13 @@ __device__ __forceinline__ void run_gemv(int slot, int tid) {
   const TaskDesc t = task_at(slot);
   task_gemv<TM, EPI>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
 }
+// batches of 9..16 tokens (chunked prefill): out of line, so the decode
+// paths keep their code layout
+template <int EPI>
+__device__ __attribute__((noinline)) void run_gemv16(int slot, int tid) {
+  const TaskDesc t = task_at(slot);
+  task_gemv<16, EPI>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+}
 template <int RMAX>
 __device__ __forceinline__ void run_attention(int slot, int tid) {
   const TaskDesc t = task_at(slot);
@@ -2201,23 +2269,31 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       gptr(a.profile)[(size_t)tid * 8 + 3] = (uint64_t)w;
     }
     const int type = op.type;
-    const bool tm8 = op.max_tokens > 1;
+    const bool tm8 = op.max_tokens > 1, tm16 = op.max_tokens > 8;
     const bool gemv = type == TASK_LINEAR || type == TASK_RMSNORM_LINEAR || type == TASK_RMSNORM_LINEAR_SILU ||
                       type == TASK_RMSNORM_LINEAR_ARGMAX;
     if (!gemv && threadIdx.x == 0) sm.last_op = -1;  // attention / embed / batch tasks reuse xs
     switch (type) {
       case TASK_EMBED: run_embed(slot, tid); break;
       case TASK_LINEAR:
-        if (tm8) run_gemv<8, EPI_LIN>(slot, tid); else run_gemv<1, EPI_LIN>(slot, tid);
+        if (tm16) run_gemv16<EPI_LIN>(slot, tid);
+        else if (tm8) run_gemv<8, EPI_LIN>(slot, tid);
+        else run_gemv<1, EPI_LIN>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR:
-        if (tm8) run_gemv<8, EPI_NORM>(slot, tid); else run_gemv<1, EPI_NORM>(slot, tid);
+        if (tm16) run_gemv16<EPI_NORM>(slot, tid);
+        else if (tm8) run_gemv<8, EPI_NORM>(slot, tid);
+        else run_gemv<1, EPI_NORM>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_SILU:
-        if (tm8) run_gemv<8, EPI_SILU>(slot, tid); else run_gemv<1, EPI_SILU>(slot, tid);
+        if (tm16) run_gemv16<EPI_SILU>(slot, tid);
+        else if (tm8) run_gemv<8, EPI_SILU>(slot, tid);
+        else run_gemv<1, EPI_SILU>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_ARGMAX:
-        if (tm8) run_gemv<8, EPI_ARGMAX>(slot, tid); else run_gemv<1, EPI_ARGMAX>(slot, tid);
+        if (tm16) run_gemv16<EPI_ARGMAX>(slot, tid);
+        else if (tm8) run_gemv<8, EPI_ARGMAX>(slot, tid);
+        else run_gemv<1, EPI_ARGMAX>(slot, tid);
         break;
       case TASK_ATTENTION: {
         // query rows per kv head: nt * G (one MFMA row block of 4 or 16)

@@ -78,8 +78,8 @@ class PersistentKernel:
             raise YirageHipError("hip backend: the persistent kernel runs on one GPU (world_size must be 1)")
         if spec_decode_config is not None:
             raise YirageHipError("hip backend: speculative decoding is not supported")
-        if max_num_batched_tokens > 8:
-            raise YirageHipError("hip backend: max_num_batched_tokens must be <= 8")
+        if max_num_batched_tokens > 16:
+            raise YirageHipError("hip backend: max_num_batched_tokens must be <= 16")
         self.mode = mode
         self.world_size = world_size
         self.mpi_rank = mpi_rank
@@ -252,7 +252,8 @@ class PersistentKernel:
     @staticmethod
     def _rows_per_task(n_rows: int, num_workers: int, gran: int, max_rows: int | None = None) -> int:
         """Even rows per task dividing `gran`, minimising the per-worker
-        makespan ceil(tasks / workers) * rows (ties -> fewer tasks)."""
+        makespan ceil(tasks / workers) * (rows + 8): a task costs about
+        eight rows of streaming in fixed work (ties -> fewer tasks)."""
         best = None
         cands = [r for r in range(2, gran + 1, 2) if gran % r == 0] if gran else \
             list(range(2, n_rows + 2, 2))
@@ -260,7 +261,7 @@ class PersistentKernel:
             if max_rows and r > max_rows:
                 continue
             tasks = -(-n_rows // r)
-            span = -(-tasks // num_workers) * r
+            span = -(-tasks // num_workers) * (r + 8)
             key = (span, tasks)
             if best is None or key < best[0]:
                 best = (key, r)
@@ -321,6 +322,11 @@ class PersistentKernel:
                     gran, max_seg = 0, None
                 tm8 = self.max_num_batched_tokens > 1
                 max_rows = 16 if (tm8 and K > 4096) else None
+                if self.max_num_batched_tokens > 8 and max_rows is None:
+                    # 16-token tiles: a task's partial-sum slots hold (16-row
+                    # tiles + 7) x 16 x 16 floats of 8192 (400 rows; 192 rows
+                    # of [gate | up] pairs)
+                    max_rows = 192 if nxt and nxt["kind"] == "silu_mul" else 400
                 if nxt and nxt["kind"] == "silu_mul" and nxt["input"] is l["output"]:
                     two_src = w.segments and len(set(s.name for s, _, _ in w.segments)) == 2
                     one_shuffled = w.segments and len(w.segments) == 1 and w.group > 0  # pre-shuffled [gate | up]
