@@ -2197,7 +2197,7 @@ __device__ __forceinline__ void run_prepare(int slot, int tid) {
 // After the barrier every wave invalidates its non-coherent cache lines, so
 // the next pass reads the other workers' writes.  Returns false when the
 // watchdog fired or the launch aborted.
-__device__ bool grid_barrier(const KernelArgs& a, Shared& sm) {
+__device__ __attribute__((noinline)) bool grid_barrier(const KernelArgs& a, Shared& sm) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -2225,6 +2225,24 @@ __device__ bool grid_barrier(const KernelArgs& a, Shared& sm) {
   return sm.flag != 0;
 }
 
+// Linear task of a graph whose batches hold up to MT tokens (1, 8 or 16):
+// one token-tile width per kernel instance, so each instance carries only
+// its own GEMV code (the worker loop is sensitive to its code footprint).
+template <int MT, int EPI>
+__device__ __forceinline__ void run_linear(int slot, int tid) {
+  if constexpr (MT == 16) run_gemv16<EPI>(slot, tid);
+  else run_gemv<MT, EPI>(slot, tid);
+}
+
+// After an early stop: every event counter advanced by num_triggers x the
+// passes that did not run (worker w takes events w, w + workers, ...).
+__device__ __attribute__((noinline)) void fast_forward(const KernelArgs& a, int w, uint32_t skip) {
+  for (int e = w * PK_THREADS + tix(); e < a.num_events; e += a.num_workers * PK_THREADS)
+    __hip_atomic_fetch_add(gptr(&a.events[e]), gptr(a.event_triggers)[e] * skip, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MT>
 __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) {
   Shared& sm = g_sm;
   const int w = blockIdx.x;
@@ -2269,31 +2287,22 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       gptr(a.profile)[(size_t)tid * 8 + 3] = (uint64_t)w;
     }
     const int type = op.type;
-    const bool tm8 = op.max_tokens > 1, tm16 = op.max_tokens > 8;
     const bool gemv = type == TASK_LINEAR || type == TASK_RMSNORM_LINEAR || type == TASK_RMSNORM_LINEAR_SILU ||
                       type == TASK_RMSNORM_LINEAR_ARGMAX;
     if (!gemv && threadIdx.x == 0) sm.last_op = -1;  // attention / embed / batch tasks reuse xs
     switch (type) {
       case TASK_EMBED: run_embed(slot, tid); break;
       case TASK_LINEAR:
-        if (tm16) run_gemv16<EPI_LIN>(slot, tid);
-        else if (tm8) run_gemv<8, EPI_LIN>(slot, tid);
-        else run_gemv<1, EPI_LIN>(slot, tid);
+        run_linear<MT, EPI_LIN>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR:
-        if (tm16) run_gemv16<EPI_NORM>(slot, tid);
-        else if (tm8) run_gemv<8, EPI_NORM>(slot, tid);
-        else run_gemv<1, EPI_NORM>(slot, tid);
+        run_linear<MT, EPI_NORM>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_SILU:
-        if (tm16) run_gemv16<EPI_SILU>(slot, tid);
-        else if (tm8) run_gemv<8, EPI_SILU>(slot, tid);
-        else run_gemv<1, EPI_SILU>(slot, tid);
+        run_linear<MT, EPI_SILU>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_ARGMAX:
-        if (tm16) run_gemv16<EPI_ARGMAX>(slot, tid);
-        else if (tm8) run_gemv<8, EPI_ARGMAX>(slot, tid);
-        else run_gemv<1, EPI_ARGMAX>(slot, tid);
+        run_linear<MT, EPI_ARGMAX>(slot, tid);
         break;
       case TASK_ATTENTION: {
         // query rows per kv head: nt * G (one MFMA row block of 4 or 16)
@@ -2336,10 +2345,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     // have left it, so the next launch (epoch a.epoch + max_iterations, as
     // the host counts) waits for the right values.  Nobody waits on an
     // event in this launch any more (all workers passed the barrier).
-    const uint32_t skip = (uint32_t)(a.max_iterations - 1 - it);
-    for (int e = w * PK_THREADS + tix(); e < a.num_events; e += a.num_workers * PK_THREADS)
-      __hip_atomic_fetch_add(gptr(&a.events[e]), gptr(a.event_triggers)[e] * skip, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    fast_forward(a, w, (uint32_t)(a.max_iterations - 1 - it));
     break;
   }
   it++;
@@ -2392,6 +2398,7 @@ struct Handle {
   uint32_t epoch = 0;  // epoch of the last pass the device may have run
   long long spin_limit = 1ll << 26;
   bool has_prepare = false;
+  const void* kfn = nullptr;  // pk_worker_kernel<1 / 8 / 16>
   bool cooperative = true;
   uint64_t* profile = nullptr;
   std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // tags restart with the epochs: cleared then
@@ -2425,14 +2432,19 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   if (hipGetDevice(&dev) != hipSuccess) return fail(YR_E_NODEVICE, "yr_pk_create: no HIP device");
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(YR_E_NODEVICE, "yr_pk_create: device query");
+  // the kernel instance for the graph's token-tile width
+  const int mt = g->cfg.max_tokens;
+  const void* kfn = mt <= 1 ? reinterpret_cast<const void*>(pk_worker_kernel<1>)
+                    : mt <= 8 ? reinterpret_cast<const void*>(pk_worker_kernel<8>)
+                              : reinterpret_cast<const void*>(pk_worker_kernel<16>);
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(pk_worker_kernel), PK_THREADS,
-                                                   0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, PK_THREADS, 0) != hipSuccess)
     return fail(YR_E_HIP, "yr_pk_create: occupancy query failed");
   if (g->num_workers > occ * prop.multiProcessorCount)
     return fail(YR_E_INVALID, "yr_pk_create: %d workers cannot be co-resident (%d CUs x %d)", g->num_workers,
                 prop.multiProcessorCount, occ);
   Handle* h = new Handle();
+  h->kfn = kfn;
   h->device = dev;
   h->num_workers = g->num_workers;
   h->n_ops = g->ops.size();
@@ -2571,10 +2583,10 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream, int max_iterations) {
   void* args[] = {&a};
   hipError_t e;
   if (h->cooperative)
-    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers),
+    e = hipLaunchCooperativeKernel(h->kfn, dim3(h->num_workers),
                                    dim3(PK_THREADS), args, 0, st);
   else
-    e = hipLaunchKernel(reinterpret_cast<const void*>(pk_worker_kernel), dim3(h->num_workers), dim3(PK_THREADS),
+    e = hipLaunchKernel(h->kfn, dim3(h->num_workers), dim3(PK_THREADS),
                         args, 0, st);
   if (e != hipSuccess) return check_hip(e, "launch of pk_worker_kernel");
   return YR_OK;
