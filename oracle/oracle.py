@@ -61,6 +61,7 @@ def lib():
             "yo_argmax": (None, [P, i32, i32, i32, P]),
             "yo_batch_init": (None, [P]),
             "yo_batch_prepare_next": (i32, [P]),
+            "yo_batch_prepare_online": (i32, [P, P]),
             "yo_num_threads": (i32, []),
             "yo_set_num_threads": (None, [i32]),
         }
@@ -285,6 +286,12 @@ class BatchManager:
 
     def prepare_next(self) -> bool:
         return bool(lib().yo_batch_prepare_next(ctypes.byref(self.s)))
+
+    def prepare_online(self, new_token_nums) -> bool:
+        """Online mode (persistent_kernel.cuh:325-351): step[0] advances by
+        new_token_nums[0]; False once the sequence ends."""
+        n = np.ascontiguousarray(new_token_nums, np.int32)
+        return bool(lib().yo_batch_prepare_online(ctypes.byref(self.s), _p(n)))
 
     def __getitem__(self, k):
         return self.a[k]

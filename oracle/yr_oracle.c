@@ -633,6 +633,18 @@ int yo_batch_prepare_next(yo_batch_state* s) {
   return ntok != 0;
 }
 
+/* Online-mode prepare_next_batch (persistent_kernel.cuh:325-351): one
+ * request whose host feeds the number of tokens it accepted this step
+ * (new_token_nums[0], the meta tensor num_new_tokens); the step advances by
+ * it, and the run continues unless the old step + 2 reaches max_seq_length or
+ * the token after the old step is eos.  Returns 1 to continue. */
+int yo_batch_prepare_online(yo_batch_state* s, const int* new_token_nums) {
+  const int step = s->step[0];
+  s->step[0] = step + new_token_nums[0];
+  if (step + 2 >= s->max_seq_length || s->tokens[step + 1] == s->eos_token_id) return 0;
+  return 1;
+}
+
 int yo_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -474,3 +474,23 @@ def test_logit_noise_floor_of_a_two_layer_model():
     assert err.max() > 1e-2                                  # below the noise floor: not a usable bound
     assert err.max() <= 2e-2 * max(1.0, np.abs(a).max())    # the bound the GPU tests use
     assert np.linalg.norm(a - b) / np.linalg.norm(a) <= 1e-2
+
+
+def test_batch_prepare_online_known_answers():
+    """Online prepare_next_batch (persistent_kernel.cuh:325-351): step[0]
+    advances by new_token_nums[0]; the run stops when the old step + 2
+    reaches max_seq_length or the token after the old step is eos."""
+    MSL = 10
+    tokens = np.zeros((1, MSL), np.int64)
+    tokens[0, :4] = [5, 6, 7, 8]
+    bm = O.BatchManager(1, 4, 4, 64, tokens, np.int32([4]), 99)
+    bm["step"][0] = 3
+    assert bm.prepare_online([2]) and bm["step"][0] == 5          # tokens[4] = 0 != eos
+    bm["tokens"][0, 6] = 99
+    assert not bm.prepare_online([1]) and bm["step"][0] == 6      # tokens[6] is eos
+    bm["step"][0] = 7
+    assert bm.prepare_online([1]) and bm["step"][0] == 8          # 7 + 2 < 10
+    assert not bm.prepare_online([1]) and bm["step"][0] == 9      # 8 + 2 >= 10
+    bm["step"][0] = 6
+    bm["tokens"][0, 7] = 1
+    assert bm.prepare_online([0]) and bm["step"][0] == 6          # no new token: step stays

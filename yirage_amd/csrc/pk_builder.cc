@@ -123,6 +123,7 @@ void Graph::build(const char* text) {
   cfg.max_seq_len = (int)root["max_seq_len"].i64(0);
   cfg.total_requests = (int)root["total_requests"].i64(cfg.max_requests);
   cfg.eos_token_id = root["eos_token_id"].i64(-1);
+  cfg.online = (int)root["online"].i64(0);
 
   const json::Value& tv = root["tensors"];
   if (tv.kind != json::Value::Obj) throw std::runtime_error("'tensors' must be an object");

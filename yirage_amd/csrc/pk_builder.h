@@ -62,6 +62,7 @@ struct EventInfo {
 struct BuildConfig {
   int max_tokens = 1, max_requests = 1, page_size = 64, max_pages = 0, max_seq_len = 0, total_requests = 1;
   int64_t eos_token_id = -1;
+  int online = 0;  // PersistentKernel(mode="online")
 };
 
 struct Graph {

@@ -2029,7 +2029,14 @@ __device__ __forceinline__ void task_attention_mt(const KernelArgs& a, const Tas
 // thread; integer logic identical to the CPU restatement in the oracle.
 __device__ __forceinline__ void task_prepare(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   if (!wait_event(a, t, task_id, sm)) return;
-  if (tix() == 0) {
+  if (tix() == 0 && a.meta.online) {
+    // online mode (persistent_kernel.cuh:325-351): one request; the host
+    // feeds how many tokens this step produced
+    const BatchMeta& s = a.meta;
+    const int step = gptr(s.step)[0];
+    gptr(s.step)[0] = step + gptr(s.num_new_tokens)[0];
+    gptr(s.status)[1] = !(step + 2 >= s.max_seq_len || gptr(s.tokens)[step + 1] == s.eos_token_id);
+  } else if (tix() == 0) {
     const BatchMeta& s = a.meta;
     const int MR = s.max_requests, MT = s.max_tokens, MP = s.max_pages, PS = s.page_size, MSL = s.max_seq_len;
     int head = *s.page_queue_head, tail = *s.page_queue_tail;
@@ -2519,6 +2526,11 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   m.max_seq_len = g->cfg.max_seq_len;
   m.total_requests = g->cfg.total_requests;
   m.eos_token_id = g->cfg.eos_token_id;
+  m.online = g->cfg.online;
+  if (m.online && h->has_prepare && (!m.num_new_tokens || !m.step || !m.tokens)) {
+    yr_pk_destroy(reinterpret_cast<yr_pk_handle*>(h));
+    return fail(YR_E_INVALID, "yr_pk_create: online mode needs step, tokens and num_new_tokens");
+  }
   if (!m.qo_indptr || !m.kv_indptr || !m.kv_indices || !m.last_page_len) {
     yr_pk_destroy(reinterpret_cast<yr_pk_handle*>(h));
     return fail(YR_E_INVALID, "yr_pk_create: qo_indptr / paged_kv_* meta tensors are required");

@@ -106,6 +106,7 @@ struct BatchMeta {
   int* page_snap;         // [max_pages]: copy of kv_indices while prepare_batch rebuilds it
   int* status;            // [4]: [0] watchdog flag, [1] batch non-empty, [2] failing task, [3] spare
   int max_requests, max_tokens, max_pages, page_size, max_seq_len, total_requests;
+  int online;             // online mode: prepare_batch advances step[0] by num_new_tokens[0] (host-fed)
   int64_t eos_token_id;
 };
 

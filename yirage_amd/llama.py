@@ -101,11 +101,12 @@ class LlamaDecodeModel:
     def __init__(self, cfg: LlamaConfig, batch: int, kv_len: int = 0, page_size: int = 64, seed: int = 0,
                  num_workers: int | None = None, with_prepare: bool = False, device="cuda", prompts=None,
                  max_tokens: int | None = None, max_requests: int | None = None, max_seq: int | None = None,
-                 eos_token_id: int = -1):
+                 eos_token_id: int = -1, mode: str = "offline"):
         self.cfg, self.batch, self.kv_len, self.page, self.seed = cfg, batch, kv_len, page_size, seed
         self.MR = max_requests or batch
         self.MT = max_tokens or batch
         self.eos = eos_token_id
+        self.mode = mode
         serving = prompts is not None
         if serving and not with_prepare:
             raise ValueError("serving mode needs the batch manager (with_prepare=True)")
@@ -187,13 +188,19 @@ class LlamaDecodeModel:
                 "paged_kv_last_page_len_buffer": torch.full((batch,), lpl, dtype=i32, device=dev),
             }
         self.page_indptr, self.page_indices = indptr, indices
+        keep = {k: v.clone() for k, v in self.meta.items()} if (mode == "online" and not serving) else None
         self.pk = self._build(num_workers, with_prepare)
+        if keep is not None and not self.graph_only:
+            # the batch reset at compile (init_kernel of the reference) clears
+            # the page table; in online mode the host owns it: restore it
+            for k, v in keep.items():
+                self.meta[k].copy_(v)
 
     def _build(self, num_workers, with_prepare):
         cfg, B = self.cfg, self.MT  # activation rows = tokens per launch
         if num_workers is None:
             num_workers = 256 if self.graph_only else torch.cuda.get_device_properties(0).multi_processor_count
-        pk = PersistentKernel(mode="offline", world_size=1, mpi_rank=0, num_workers=num_workers,
+        pk = PersistentKernel(mode=self.mode, world_size=1, mpi_rank=0, num_workers=num_workers,
                               num_local_schedulers=0, num_remote_schedulers=0, max_seq_length=self.max_seq,
                               max_num_batched_requests=self.MR, max_num_batched_tokens=self.MT,
                               max_num_pages=self.max_pages, page_size=self.page, eos_token_id=self.eos,

@@ -239,7 +239,8 @@ class PersistentKernel:
 
     def prepare_batch_layer(self):
         """The on-device batch/page manager (prepare_next_batch of
-        persistent_kernel.cuh:169-322).  It must be the last layer recorded:
+        persistent_kernel.cuh:169-322; in mode="online", the single-request
+        step advance of :325-351).  It must be the last layer recorded:
         every attention task reads the batch metadata once at launch start,
         and prepare_batch rewrites it for the next launch (compile() refuses
         any other placement)."""
@@ -416,7 +417,7 @@ class PersistentKernel:
             num_workers=self.num_workers, max_tokens=self.max_num_batched_tokens,
             max_requests=self.max_num_batched_requests, page_size=self.page_size, max_pages=self.max_num_pages,
             max_seq_len=self.max_seq_length, total_requests=self.total_num_requests,
-            eos_token_id=int(self.eos_token_id), tensors=tensors, ops=self.ops))
+            eos_token_id=int(self.eos_token_id), online=int(self.mode == "online"), tensors=tensors, ops=self.ops))
 
     # ------------------------------------------------------------ compile / run
     def compile(self, **kwargs):
@@ -467,6 +468,9 @@ class PersistentKernel:
         if not self._is_compiled:
             raise YirageHipError("PersistentKernel: call compile() first")
         if max_iterations is None:
+            # offline: the whole generation; online (the host feeds each
+            # step's accepted tokens through num_new_tokens) and onepass: one
+            # pass per call, status()[1][1] says whether the sequence goes on
             has_prepare = any(o["type"] == "prepare_batch" for o in self.ops)
             max_iterations = 0 if (self.mode == "offline" and has_prepare) else 1
         check(lib().yr_pk_launch(self._handle, self._stream(), int(max_iterations)), "persistent kernel launch")
