@@ -24,10 +24,17 @@ def _check(model, tokens, ref_logits, ref_ids, what, rel_l2=None, elementwise=Fa
           f"ref {ref_ids.tolist()}", flush=True)
     if elementwise:
         # the north-star tolerance, element by element (only where the
-        # model's own rounding noise stays below it: one layer)
+        # model's own rounding noise stays below it: one layer).  At batch 8
+        # the oracle's own noise floor (tests/test_oracle.py::
+        # test_logit_noise_floor_llama3_8b_one_layer_batch8) puts up to 0.1 %
+        # of the logits outside it, none by more than 2^-5
         bad = err > 1e-2 + 1e-2 * np.abs(ref_logits)
         print(f"  element-wise rtol/atol 1e-2: {bad.sum()} of {bad.size} outside", flush=True)
-        assert not bad.any(), f"{what}: logits outside rtol/atol 1e-2"
+        if model.batch == 1:
+            assert not bad.any(), f"{what}: logits outside rtol/atol 1e-2"
+        else:
+            assert bad.mean() <= 1e-3, f"{what}: {bad.sum()} logits outside rtol/atol 1e-2"
+            assert err.max() <= 2.0 ** -5 + 1e-6, f"{what}: a logit moved by {err.max()}"
     if rel_l2 is None:
         assert err.max() <= 2e-2 * max(1.0, scale), f"{what}: logits differ"
     else:
@@ -69,14 +76,15 @@ def test_small_llama_decode_step(batch, kv_len, qk_norm):
     assert torch.equal(first, model.t["argmax_in"].tensor)
 
 
-@pytest.mark.parametrize("batch", [1])
+@pytest.mark.parametrize("batch", [1, 8])
 def test_llama3_8b_dims_one_layer_elementwise(batch):
     """One layer at full Llama-3-8B dims: logits element-wise within rtol /
-    atol 1e-2 of the oracle.  (From two layers on, +-1 ulp of rounding noise
-    in the activations alone moves some logits by more than that -- measured
-    oracle against perturbed oracle in tests/test_oracle.py -- so deeper
-    stacks are bounded by magnitude and relative L2 instead; at batch 8
-    even one layer leaves 25 of 1,026,048 logits just outside.)"""
+    atol 1e-2 of the oracle at batch 1; at batch 8 within it for all but
+    0.1 % of the logits and within 2^-5 everywhere, the oracle's own noise
+    floor for this layer (tests/test_oracle.py).  (From two layers on, +-1
+    ulp of rounding noise in the activations alone moves some logits by
+    more than that, so deeper stacks are bounded by magnitude and relative
+    L2 instead.)"""
     cfg = LlamaConfig(num_layers=1)
     print(f"case llama3-8b dims, 1 layer, B={batch} kv=4096", flush=True)
     model = LlamaDecodeModel(cfg, batch=batch, kv_len=4096, seed=0)

@@ -476,6 +476,59 @@ def test_logit_noise_floor_of_a_two_layer_model():
     assert np.linalg.norm(a - b) / np.linalg.norm(a) <= 1e-2
 
 
+def test_logit_noise_floor_llama3_8b_one_layer_batch8():
+    """Pins the bound of the GPU's one-layer, full Llama-3-8B-dims, batch-8
+    decode test.  The oracle against itself with +-1 ulp of noise in 30 % of
+    the layer's bf16 output (rounding-order differences of that size are what
+    two implementations of the same fp32-accumulated layer produce) moves
+    some of the 1,026,048 logits outside rtol/atol 1e-2 -- so that bound,
+    applied to every element, tests rounding order -- but fewer than 0.1 %,
+    and none by more than 2^-5 (two bf16 ulps at |logit| in [2, 4)).  That
+    pair is the GPU test's bound."""
+    from yirage_amd.llama import LlamaConfig, page_table, rope_tables, tensor_seed, weight_shapes
+
+    cfg = LlamaConfig(num_layers=1)
+    B, kv_len, page, seed, bf, G, D = 8, 4096, 64, 0, "bf16", 4, 128
+    O.set_num_threads(8)
+    indptr, indices, pool = page_table(B, kv_len, page, seed + 7)
+    cos, sin = rope_tables(kv_len + 8, D, cfg.rope_theta)
+    cos, sin = cos.float().numpy(), sin.float().numpy()
+    qo, lpl = np.arange(B + 1, dtype=np.int32), np.full(B, kv_len % page, np.int32)
+    tokens = (np.arange(B) * 15013 + 128000) % cfg.vocab
+    x = O.to_float(O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(seed, 0, "embed"), 0.02)[tokens], bf)
+    ones = np.ones(cfg.hidden, np.float32)
+    W = {n: O.synth(s_, bf, tensor_seed(seed, 0, n), 0.02) for n, s_ in weight_shapes(cfg).items()}
+    rows = []
+    for g in range(cfg.num_kv_heads):
+        rows += [W["wq"][g * G * D:(g + 1) * G * D], W["wk"][g * D:(g + 1) * D], W["wv"][g * D:(g + 1) * D]]
+    kc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(seed, 0, "kc"), 1.0)
+    vc = O.synth((pool, page, cfg.num_kv_heads, D), bf, tensor_seed(seed, 0, "vc"), 1.0)
+    xn = O.round_to(O.rmsnorm(x, ones, cfg.eps), bf)
+    qkv = O.round_to(O.linear(xn, np.concatenate(rows, 0), bf, O.W_NK), bf)
+    att = O.round_to(O.paged_attention(qkv, 32, 8, D, kc, vc, bf, qo, indptr, indices, lpl, cos, sin), bf)
+    h = O.round_to(O.linear(att, W["wo"], bf, O.W_NK, residual=x), bf)
+    hn = O.round_to(O.rmsnorm(h, ones, cfg.eps), bf)
+    m = O.silu_mul(O.round_to(O.linear(hn, W["wg"], bf, O.W_NK), bf),
+                   O.round_to(O.linear(hn, W["wu"], bf, O.W_NK), bf), bf)
+    xo = O.round_to(O.linear(m, W["wd"], bf, O.W_NK, residual=h), bf)
+    del W, kc, vc
+    lm = O.synth((cfg.vocab, cfg.hidden), bf, tensor_seed(seed, 0, "lm_head"), 0.02)
+
+    def logits(v):
+        return O.round_to(O.linear(O.round_to(O.rmsnorm(v, ones, cfg.eps), bf), lm, bf, O.W_NK), bf)
+
+    a = logits(xo)
+    r = np.random.default_rng(1)
+    bits = O.from_float(xo, bf)
+    noisy = bits + (r.integers(-1, 2, bits.shape) * (r.random(bits.shape) < 0.3)).astype(np.uint16)
+    b = logits(O.to_float(noisy, bf))
+    err = np.abs(a - b)
+    outside = err > 1e-2 + 1e-2 * np.abs(a)
+    assert outside.any()                        # rtol/atol 1e-2 on every element is below the noise floor
+    assert outside.mean() <= 1e-3               # ... but holds for all but 0.1 % of the logits
+    assert err.max() <= 2.0 ** -5 + 1e-6        # and no logit moves by more than 2^-5
+
+
 def test_batch_prepare_online_known_answers():
     """Online prepare_next_batch (persistent_kernel.cuh:325-351): step[0]
     advances by new_token_nums[0]; the run stops when the old step + 2
