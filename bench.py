@@ -120,6 +120,50 @@ def bench_fused(torch):
     return out
 
 
+def bench_mugraph_plans(torch) -> dict:
+    """Device time (HIP-graph replay, launch overhead removed) of the saved
+    muGraph candidates that run as generic steps or literally, tile by tile
+    (customized ops no fused kernel covers): each distinct plan of the LoRA,
+    qk-norm GQA, norm-transformer and MHA files (tests/golden/saved_mugraphs),
+    one launch per operator against the same plan with its elementwise trees
+    fused (fused elementwise launches)."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+    from yirage_amd import YirageHipError
+    from yirage_amd import mugraph_json as MJ
+
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden", "saved_mugraphs")
+    files = [("single_lora.json", (1.0, 0.05, 0.05, 0.25)), ("qknorm_gqa_bs1_subset.json", (1.0, 0.02, 1.0)),
+             ("ntrans_bs1.json", (1.0, 1.0, 1.0)), ("mha_bs1.json", (0.25, 0.25, 1.0))]
+    out = {}
+    for name, stds in files:
+        gs = MJ.load(os.path.join(golden, name))
+        seen = set()
+        for i, g in enumerate(gs):
+            try:
+                p0 = g.plan(fuse=True, fuse_elementwise=False)
+                p1 = g.plan(fuse=True)
+            except YirageHipError:
+                continue
+            key = tuple(p0.describe())
+            if key in seen:
+                continue
+            seen.add(key)
+            gen = torch.Generator().manual_seed(i)
+            ins = []
+            for t, sd in zip(g.inputs, stds):
+                n = sum((d - 1) * s_ for d, s_ in zip(t.dims, t.strides)) + 1
+                base = (torch.randn(n, generator=gen) * sd).to(t.dtype.torch)
+                ins.append(torch.as_strided(base, t.dims, t.strides).cuda())
+            rec = {"steps": len(p0.steps)}
+            for tag, p in (("one_launch_per_op", p0), ("elementwise_fused", p1)):
+                if tag == "elementwise_fused" and p1.describe() == p0.describe():
+                    continue
+                ms = _graph_time(torch, lambda p=p: g._execute(p, ins, None), per_graph=10, replays=5)
+                rec[tag] = dict(us=round(ms * 1e3, 2), launches=len(p.steps))
+            out[f"{name}#{i}"] = rec
+    return out
+
+
 def _cpu_time(fn, warmup: int, reps: int) -> float:
     """Mean ms per call after `warmup` untimed calls (time.perf_counter), the
     method of the reference's CPU harness (benchmark/baselines/pytorch/
@@ -249,6 +293,8 @@ def main():
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--mugraph-plans", action="store_true",
+                    help="only time the saved muGraph candidates' generic / literal plans (JSON line)")
     ap.add_argument("--no-coop", action="store_true",
                     help="ordinary (non-cooperative) launch of the persistent kernel, e.g. under rocprofv3")
     ap.add_argument("--copy-calib", action="store_true",
@@ -264,6 +310,9 @@ def main():
     from yirage_amd.llama import LLAMA3_8B, LlamaDecodeModel
 
     torch.cuda.set_device(0)
+    if args.mugraph_plans:
+        print(json.dumps({"mugraph_plans": bench_mugraph_plans(torch)}))
+        return
     if args.copy_calib:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)

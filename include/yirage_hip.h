@@ -195,6 +195,20 @@ int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64
  * max accumulator, src/threadblock/reduction.cc, forloop_accum.cc:102-125). */
 int yr_hip_graph_reduction_max(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype,
                                void* stream);
+/* A tree of elementwise operators in one launch: y = program(x0..x_{n-1})
+ * over the output dims (ndim <= 6; input k has dims in_dims[k][ndim], each 1
+ * (broadcast) or the output's; all row-major dense).  prog[j] = {op, dst,
+ * a, b, kind}: op 0 loads input a into register dst, 1 applies unary `kind`
+ * (the yr_hip_graph_unary kinds; imm[2 j], imm[2 j + 1] = lo, hi) to
+ * register a, 2 applies binary `kind` (yr_hip_graph_binary's) to registers
+ * a, b; 16 registers, <= 32 instructions; y = the last instruction's
+ * register.  Every result is rounded to dtype, so y is bit-identical to the
+ * same operators run one launch each.  The fusion of single-consumer
+ * elementwise chains of the reference's transpiler
+ * (src/transpiler/resolve_tb_fusion.cc:35-66). */
+int yr_hip_graph_ewise(const void* const* ins, int n, void* y, int ndim, const int64_t* out_dims,
+                       const int64_t* in_dims, int n_prog, const int32_t* prog, const float* imm, int dtype,
+                       void* stream);
 /* y[row] = x[row] * rsqrt(mean(x[row]^2) + eps) over the n trailing
  * elements (rms_norm(X, normalized_shape), src/kernel/rms_norm.cc:71-114). */
 int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream);
@@ -229,7 +243,10 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
  *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...}
  *   YR_OP_COPY_ND:        in {src}, out {dst}; params {ndim, dtype, dims[8], src_strides[8], dst_strides[8],
  *                                             dst_offset} (elements; 27 params)
- *   YR_OP_REDUCTION_MAX:  in {x}, out {y}; params {outer, red, inner, dtype} */
+ *   YR_OP_REDUCTION_MAX:  in {x}, out {y}; params {outer, red, inner, dtype}
+ *   YR_OP_EWISE:          in {x0..x_{n-1}} (1..8), out {y}; params {ndim, n, n_prog, dtype,
+ *                         out_dims[ndim], in_dims[n][ndim], prog[n_prog][5], imm_bits[n_prog][2]}
+ *                         (see yr_hip_graph_ewise) */
 #define YR_OP_RMSNORM_LINEAR 1
 #define YR_OP_GATED_MLP 2
 #define YR_OP_GQA_PREFILL 3
@@ -244,6 +261,7 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
 #define YR_OP_PACK 12
 #define YR_OP_COPY_ND 13
 #define YR_OP_REDUCTION_MAX 14
+#define YR_OP_EWISE 15
 int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);

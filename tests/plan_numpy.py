@@ -64,6 +64,27 @@ def run_plan(plan, inputs):
             a, b = src[0][:int(np.prod(da))].reshape(da), src[1][:int(np.prod(db))].reshape(db)
             r = {0: np.add, 1: np.multiply, 2: np.divide, 3: np.power}[kind](a, b)
             dst[:r.size] = r.reshape(-1)
+        elif k == _lib.OP_EWISE:
+            nd, nin, npg = p[0], p[1], p[2]
+            od = tuple(p[4:4 + nd])
+            ind = [tuple(p[4 + nd + i * nd:4 + nd + (i + 1) * nd]) for i in range(nin)]
+            prog = p[4 + nd + nin * nd:4 + nd + nin * nd + 5 * npg]
+            imm = p[4 + nd + nin * nd + 5 * npg:]
+            reg = {}
+            last = 0
+            for j in range(npg):
+                op, d, a, b, kind = prog[5 * j:5 * j + 5]
+                if op == 0:
+                    v = src[a][:int(np.prod(ind[a]))].reshape(ind[a])
+                elif op == 1:
+                    x, lo, hi = reg[a], _f32(imm[2 * j]), _f32(imm[2 * j + 1])
+                    v = x * lo if kind == 7 else np.clip(x, lo, hi) if kind == 4 else _UNARY[kind](x)
+                else:
+                    v = {0: np.add, 1: np.multiply, 2: np.divide, 3: np.power}[kind](reg[a], reg[b])
+                reg[d] = v
+                last = d
+            r = np.broadcast_to(reg[last], od)
+            dst[:r.size] = r.reshape(-1)
         elif k == _lib.OP_REDUCTION:
             outer, red, inner = p[0], p[1], p[2]
             dst[:outer * inner] = src[0][:outer * red * inner].reshape(outer, red, inner).sum(1).reshape(-1)

@@ -200,3 +200,56 @@ def test_customized_max_and_concat_run_literally():
     ref = run_graph(g, [x.double().numpy()])[0]
     err = np.abs(got.float().cpu().numpy() - ref)
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+
+
+def test_fused_elementwise_bit_identical_to_unfused_steps():
+    """Plans whose elementwise trees were fused into single launches
+    (yr_hip_graph_ewise) give bit-identical outputs to the same plans run one
+    operator per launch, on the saved candidates (every plan that changes)
+    and on a broadcasting tree over four inputs in f16 and bf16."""
+    import yirage_amd as yr
+
+    checked = 0
+    for name, kind, stds in CASES:
+        gs = MJ.load(os.path.join(GOLDEN, name))
+        seen = set()
+        for i, g in enumerate(gs):
+            try:
+                p1 = g.plan(fuse=True)
+                p0 = g.plan(fuse=True, fuse_elementwise=False)
+            except YirageHipError:
+                continue
+            d1 = tuple(p1.describe())
+            if d1 == tuple(p0.describe()) or d1 in seen:
+                continue
+            seen.add(d1)
+            print(f"case {name} candidate {i}: {list(d1)}", flush=True)
+            dev = [x.cuda() for x in _inputs(g, stds, seed=i)]
+            a = g._execute(p0, dev, None)
+            b = g._execute(p1, dev, None)
+            torch.cuda.synchronize()
+            for x, y in zip(a, b):
+                assert torch.equal(x, y), f"{name} candidate {i}: fused elementwise differs"
+            checked += 1
+    for dt in (yr.float16, yr.bfloat16):
+        G = yr.new_kernel_graph()
+        A = G.new_input(dims=(4, 33, 64), dtype=dt)
+        B = G.new_input(dims=(4, 1, 64), dtype=dt)
+        C = G.new_input(dims=(1, 33, 1), dtype=dt)
+        D = G.new_input(dims=(4, 33, 64), dtype=dt)
+        G.mark_output(G.div(G.mul(G.silu(G.add(A, B)), G.exp(C)), G.add(G.square(D), G.exp(G.relu(B)))))
+        p1 = G.plan(fuse=True)
+        p0 = G.plan(fuse=True, fuse_elementwise=False)
+        assert len(p1.describe()) == 1 and p1.describe()[0].startswith("ewise("), p1.describe()
+        gen = torch.Generator().manual_seed(7)
+        ins = [torch.randn(t.dims, generator=gen).to(dt.torch).cuda() for t in G.inputs]
+        a = G._execute(p0, ins, None)[0]
+        b = G._execute(p1, ins, None)[0]
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{dt}: fused elementwise differs"
+        x = [t.double() for t in ins]
+        ref = (torch.nn.functional.silu(x[0] + x[1]) * torch.exp(x[2])) / (x[3] ** 2 + torch.exp(torch.relu(x[1])))
+        err = (b.double() - ref).abs()
+        assert (err <= 3e-2 + 3e-2 * ref.abs()).all(), f"{dt}: max err {err.max()}"
+        checked += 1
+    assert checked >= 4

@@ -62,7 +62,7 @@ def test_saved_candidates_load_and_plan(name):
     for g in gs:
         assert g.outputs, "every saved graph marks an output"
         if plan is not None:
-            assert g.plan(fuse=True).describe() == plan
+            assert g.plan(fuse=True, fuse_elementwise=False).describe() == plan
 
 
 def test_mha_candidates_that_plan():
@@ -82,7 +82,7 @@ def test_norm_transformer_candidates_run_as_generic_steps():
     customized op is one whole-tensor expression run as generic rms_norm /
     elementwise steps; the three that divide by an rms accumulator in a
     separate kernel-level div run their threadblock graphs literally."""
-    plans = [g.plan(fuse=True).describe() for g in _load("ntrans_bs1.json")]
+    plans = [g.plan(fuse=True, fuse_elementwise=False).describe() for g in _load("ntrans_bs1.json")]
     assert plans.count(["rms_norm", "add", "mul", "add", "rms_norm"]) == 6
     assert sum("copy_nd" in p for p in plans) == 3
 
@@ -242,7 +242,7 @@ def test_literal_tile_interpreter_matches_block_emulation():
     for name, ins, n in cases:
         for g in _load(name)[:n]:
             try:
-                p = g.plan(fuse=True)
+                p = g.plan(fuse=True, fuse_elementwise=False)
             except YirageHipError:
                 continue
             if "copy_nd" not in p.describe():
@@ -250,6 +250,10 @@ def test_literal_tile_interpreter_matches_block_emulation():
             got = run_plan(p, ins)[0]
             ref = run_graph(g, ins)[0]
             assert np.abs(got - ref).max() <= 1e-9 * max(1.0, np.abs(ref).max())
+            # the same plan with its elementwise trees fused: same values
+            pf = g.plan(fuse=True)
+            got_f = run_plan(pf, ins)[0]
+            assert np.abs(got_f - got).max() <= 1e-12 * max(1.0, np.abs(got).max())
             if name == "mha_bs1.json":
                 assert np.abs(got - attn).max() <= 1e-9
             checked += 1
@@ -285,3 +289,34 @@ def test_literal_max_and_concat():
     # closed form: max over the row of exp(x) per column position, then the row max sums
     xr = x.reshape(8, 4, 64)
     assert np.allclose(ref[:, :64], np.exp(xr).max(1)) and np.allclose(ref[:, 64], xr.max(2).sum(1))
+
+
+def test_elementwise_trees_fuse_into_one_launch():
+    """Single-consumer trees of elementwise steps become one fused
+    elementwise launch (the reference's transpiler fusion rule,
+    src/transpiler/resolve_tb_fusion.cc:35-66): the Qwen2 candidate's
+    silu * mul, the norm-transformer's add-mul-add; a value read twice or a
+    graph output is not folded.  Values (numpy executor, float64) equal the
+    unfused plan's."""
+    import numpy as np
+    from plan_numpy import run_plan
+
+    g = _load("mirage_cached_mugraphs_64644b2e7bbffb94.json")[0]
+    assert g.plan(fuse=True).describe() == ["ewise(silu+mul)", "linear"]
+    plans = [g.plan(fuse=True).describe() for g in _load("ntrans_bs1.json")]
+    assert plans.count(["rms_norm", "ewise(add+mul+add)", "rms_norm"]) == 6
+    rng = np.random.default_rng(3)
+    for g in _load("ntrans_bs1.json"):
+        ins = [rng.normal(0, 1, t.dims) for t in g.inputs]
+        a = run_plan(g.plan(fuse=True, fuse_elementwise=False), ins)
+        b = run_plan(g.plan(fuse=True), ins)
+        for x, y in zip(a, b):
+            assert np.abs(x - y).max() <= 1e-12 * max(1.0, np.abs(x).max())
+    # a graph-level chain: exp(x) used twice stays materialized
+    G = yr.new_kernel_graph()
+    X = G.new_input(dims=(16, 64), dtype=yr.float16)
+    Y = G.new_input(dims=(16, 1), dtype=yr.float16)
+    E = G.exp(X)
+    G.mark_output(G.mul(G.add(E, Y), E))
+    d = G.plan(fuse=True).describe()
+    assert d == ["exp", "ewise(add+mul)"], d

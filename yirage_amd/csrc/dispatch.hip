@@ -38,6 +38,7 @@ bool arity_of(int kind, Arity* a) {
     case YR_OP_PACK: *a = {1, 1, 11}; return true;
     case YR_OP_COPY_ND: *a = {1, 1, 27}; return true;
     case YR_OP_REDUCTION_MAX: *a = {1, 1, 4}; return true;
+    case YR_OP_EWISE: *a = {-1, 1, -4}; return true;  // 1..8 inputs
     default: return false;
   }
 }
@@ -72,10 +73,10 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, vo
   if ((n_in && !in) || (n_out && !out) || (n_params && !p)) return fail(YR_E_INVALID, "%s: null array", nm);
   Arity ar;
   if (!arity_of(op_kind, &ar)) return fail(YR_E_INVALID, "%s: unknown op kind %d", nm, op_kind);
-  if (n_in != ar.n_in || n_out != ar.n_out ||
+  if ((ar.n_in >= 0 ? n_in != ar.n_in : n_in < 1) || n_out != ar.n_out ||
       (ar.n_params >= 0 ? n_params != ar.n_params : n_params < -ar.n_params))
-    return fail(YR_E_INVALID, "%s: op kind %d takes %d inputs, %d outputs and %s%d params (got %d, %d, %d)", nm,
-                op_kind, ar.n_in, ar.n_out, ar.n_params < 0 ? ">= " : "", ar.n_params < 0 ? -ar.n_params : ar.n_params,
+    return fail(YR_E_INVALID, "%s: op kind %d takes %s%d inputs, %d outputs and %s%d params (got %d, %d, %d)", nm,
+                op_kind, ar.n_in < 0 ? ">= " : "", ar.n_in < 0 ? 1 : ar.n_in, ar.n_out, ar.n_params < 0 ? ">= " : "", ar.n_params < 0 ? -ar.n_params : ar.n_params,
                 n_in, n_out, n_params);
   switch (op_kind) {
     case YR_OP_RMSNORM_LINEAR:
@@ -117,6 +118,19 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, vo
                                   p + 18, (int)p[1], stream);
     case YR_OP_REDUCTION_MAX:
       return yr_hip_graph_reduction_max(in[0], out[0], p[0], (int)p[1], p[2], (int)p[3], stream);
+    case YR_OP_EWISE: {
+      // {ndim, n_in, n_prog, dtype, out_dims[ndim], in_dims[n_in][ndim], prog[n_prog][5], imm_bits[n_prog][2]}
+      const int nd = (int)p[0], ni = (int)p[1], np = (int)p[2];
+      if (nd < 1 || nd > 6 || ni < 1 || ni > 8 || np < 1 || np > 32 || ni != n_in ||
+          n_params != 4 + nd + ni * nd + 7 * np)
+        return fail(YR_E_INVALID, "%s: fused elementwise params do not match their counts", nm);
+      int32_t prog[32 * 5];
+      float imm[32 * 2];
+      const int64_t* pp = p + 4 + nd + ni * nd;
+      for (int i = 0; i < 5 * np; i++) prog[i] = (int32_t)pp[i];
+      for (int i = 0; i < 2 * np; i++) imm[i] = f32_of(pp[5 * np + i]);
+      return yr_hip_graph_ewise(in, ni, out[0], nd, p + 4, p + 4 + nd, np, prog, imm, (int)p[3], stream);
+    }
     default:
       return fail(YR_E_INVALID, "%s: unknown op kind %d", nm, op_kind);
   }

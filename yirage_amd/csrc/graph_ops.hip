@@ -20,6 +20,23 @@
 namespace yr {
 namespace graph {
 
+// 32-bit unsigned division by a run-time constant, n < 2^31: q = (umulhi(n,
+// m) + n) >> l with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Figure 4.1).
+struct FastDiv {
+  uint32_t d, m, l;
+};
+static FastDiv fast_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) l++;
+  const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return {d, (uint32_t)m, l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.l;
+}
+
 // ------------------------------------------------------------------ pack
 // dst[g][r][c] = c < C ? src[g s0 + r s1 + c s2] : 0 for c < Cd (destination
 // strides d0 d1 d2).  One workgroup moves a 64 x 64 (r, c) tile through LDS:
@@ -109,6 +126,7 @@ struct BinaryArgs {
   int nd, kind;
   long long dims[kMaxDims];  // output dims
   long long sa[kMaxDims], sb[kMaxDims];  // element strides of a / b per output dim (0: broadcast)
+  FastDiv div[kMaxDims];     // output dims as divisors (n < 2^31)
 };
 
 // Strided copy over up to 8 dims (16-bit elements): the tile gathers and
@@ -122,6 +140,32 @@ struct CopyArgs {
   int nd;
   long long dims[kCopyDims], ss[kCopyDims], ds[kCopyDims];
 };
+
+
+// The same copy with collapsed dims and n < 2^31: division by multiplication.
+struct CopyArgs32 {
+  const uint16_t* src;
+  uint16_t* dst;
+  uint32_t n;
+  int nd;
+  FastDiv div[kCopyDims];
+  long long ss[kCopyDims], ds[kCopyDims];
+};
+
+__global__ __launch_bounds__(256) void copy_nd32_kernel(CopyArgs32 p) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < p.n; i += gridDim.x * blockDim.x) {
+    uint32_t rem = i;
+    long long os = 0, od = 0;
+    for (int d = p.nd - 1; d >= 0; d--) {
+      const uint32_t q = fdiv(rem, p.div[d]);
+      const uint32_t c = rem - q * p.div[d].d;
+      rem = q;
+      os += (long long)c * p.ss[d];
+      od += (long long)c * p.ds[d];
+    }
+    p.dst[od] = p.src[os];
+  }
+}
 
 __global__ __launch_bounds__(256) void copy_nd_kernel(CopyArgs p) {
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n;
@@ -141,12 +185,24 @@ template <int DT>
 __global__ __launch_bounds__(256) void binary_kernel(BinaryArgs p) {
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < p.n;
        i += (long long)gridDim.x * blockDim.x) {
-    long long rem = i, oa = 0, ob = 0;
-    for (int d = p.nd - 1; d >= 0; d--) {
-      const long long c = rem % p.dims[d];
-      rem /= p.dims[d];
-      oa += c * p.sa[d];
-      ob += c * p.sb[d];
+    long long oa = 0, ob = 0;
+    if (p.n < (1ll << 31)) {  // 32-bit index math, division by multiplication
+      uint32_t rem = (uint32_t)i;
+      for (int d = p.nd - 1; d >= 0; d--) {
+        const uint32_t q = fdiv(rem, p.div[d]);
+        const uint32_t c = rem - q * p.div[d].d;
+        rem = q;
+        oa += (long long)c * p.sa[d];
+        ob += (long long)c * p.sb[d];
+      }
+    } else {
+      long long rem = i;
+      for (int d = p.nd - 1; d >= 0; d--) {
+        const long long c = rem % p.dims[d];
+        rem /= p.dims[d];
+        oa += c * p.sa[d];
+        ob += c * p.sb[d];
+      }
     }
     const float x = ld_elem<DT>(p.a[oa]), y = ld_elem<DT>(p.b[ob]);
     float r;
@@ -160,7 +216,176 @@ __global__ __launch_bounds__(256) void binary_kernel(BinaryArgs p) {
   }
 }
 
+// ------------------------------------------------------------------ fused elementwise
+// A tree of unary / binary elementwise operators evaluated in one pass, one
+// thread per output element: the fusion of single-consumer elementwise
+// chains the reference's transpiler applies to threadblock graphs
+// (src/transpiler/resolve_tb_fusion.cc:35-66), here over binary trees too.
+// The program runs on a small register file; every operator's result is
+// rounded to the element type, as the unfused chain stores it, so the
+// output is bit-identical to running the operators one by one.
+constexpr int kEwIn = 8, kEwProg = 32, kEwRegs = 16;
+enum EwOp { EW_LOAD = 0, EW_UNARY = 1, EW_BINARY = 2 };
+struct EwiseArgs {
+  const uint16_t* in[kEwIn];
+  uint16_t* out;
+  uint32_t n;                    // < 2^31 (larger outputs are split by the host)
+  int nd, nin, nprog;
+  FastDiv div[kMaxDims];         // output dims
+  uint32_t s[kEwIn][kMaxDims];   // element strides of each input per output dim (0: broadcast)
+  int32_t op[kEwProg], dst[kEwProg], a[kEwProg], b[kEwProg], kind[kEwProg];  // dwords: scalar loads
+  float lo[kEwProg], hi[kEwProg];
+};
+
+__device__ __forceinline__ float ew_unary(int kind, float a, float lo, float hi) {
+  switch (kind) {
+    case U_EXP: return expf(a);
+    case U_SILU: return a / (1.f + expf(-a));
+    case U_GELU: return 0.5f * a * (1.f + erff(a * 0.70710678118654752f));
+    case U_RELU: return fmaxf(a, 0.f);
+    case U_CLAMP: return fminf(fmaxf(a, lo), hi);
+    case U_SQRT: return sqrtf(a);
+    case U_SCALE: return a * lo;
+    default: return a * a;
+  }
+}
+__device__ __forceinline__ float ew_binary(int kind, float x, float y) {
+  switch (kind) {
+    case B_ADD: return x + y;
+    case B_MUL: return x * y;
+    case B_DIV: return x / y;
+    default: return powf(x, y);
+  }
+}
+
+// Each thread takes EPT elements (e, e + 256, ...), and the program is
+// decoded once per instruction for all of them (its words are scalar loads
+// whose latency would otherwise be paid per element).
+template <int DT, int NR, int EPT>
+__global__ __launch_bounds__(256) void ewise_kernel(EwiseArgs p) {
+  for (uint32_t i0 = blockIdx.x * (256u * EPT) + threadIdx.x; i0 < p.n; i0 += gridDim.x * (256u * EPT)) {
+    uint32_t c[EPT][kMaxDims];  // coordinates of the thread's elements
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      uint32_t rem = i0 + 256u * e;
+      if (rem >= p.n) rem = p.n - 1;  // (finite data for the lanes past the end; not stored)
+#pragma unroll
+      for (int d = kMaxDims - 1; d >= 0; d--) {
+        if (d < p.nd) {
+          const uint32_t q = fdiv(rem, p.div[d]);
+          c[e][d] = rem - q * p.div[d].d;
+          rem = q;
+        } else {
+          c[e][d] = 0;
+        }
+      }
+    }
+    // every input element first, all loads in flight at once (a load per
+    // LOAD instruction would expose one memory latency per instruction)
+    float lv[kEwIn][EPT];
+#pragma unroll
+    for (int q = 0; q < kEwIn; q++) {
+      if (q < p.nin) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) {
+          uint32_t o = 0;
+#pragma unroll
+          for (int d = 0; d < kMaxDims; d++) o += c[e][d] * p.s[q][d];
+          lv[q][e] = ld_elem<DT>(p.in[q][o]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) lv[q][e] = 0.f;
+      }
+    }
+    // registers are addressed with static indices only (a dynamically
+    // indexed array would live in scratch memory)
+    float r[NR][EPT];
+#pragma unroll
+    for (int k = 0; k < NR; k++)
+#pragma unroll
+      for (int e = 0; e < EPT; e++) r[k][e] = 0.f;
+    float v[EPT];
+    for (int j = 0; j < p.nprog; j++) {
+      const int op = p.op[j], a = p.a[j], b = p.b[j], kind = p.kind[j], dst = p.dst[j];
+      if (op == EW_LOAD) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) v[e] = lv[0][e];
+#pragma unroll
+        for (int q = 1; q < kEwIn; q++)
+          if (a == q) {
+#pragma unroll
+            for (int e = 0; e < EPT; e++) v[e] = lv[q][e];
+          }
+      } else {
+        float x[EPT], y[EPT];
+#pragma unroll
+        for (int e = 0; e < EPT; e++) { x[e] = r[0][e]; y[e] = r[0][e]; }
+#pragma unroll
+        for (int k = 1; k < NR; k++) {
+          if (a == k) {
+#pragma unroll
+            for (int e = 0; e < EPT; e++) x[e] = r[k][e];
+          }
+          if (b == k) {
+#pragma unroll
+            for (int e = 0; e < EPT; e++) y[e] = r[k][e];
+          }
+        }
+        if (op == EW_UNARY) {
+          const float lo = p.lo[j], hi = p.hi[j];
+#pragma unroll
+          for (int e = 0; e < EPT; e++) v[e] = ld_elem<DT>((uint16_t)st_elem<DT>(ew_unary(kind, x[e], lo, hi)));
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPT; e++) v[e] = ld_elem<DT>((uint16_t)st_elem<DT>(ew_binary(kind, x[e], y[e])));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < NR; k++)
+        if (dst == k) {
+#pragma unroll
+          for (int e = 0; e < EPT; e++) r[k][e] = v[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; e++)
+      if (i0 + 256u * e < p.n) p.out[i0 + 256u * e] = (uint16_t)st_elem<DT>(v[e]);  // the last instruction's result
+  }
+}
+
 // ------------------------------------------------------------------ reductions
+// out[o][i] = sum_r x[o][r][i] (fp32) for long reductions: a workgroup takes
+// one outer index and TX consecutive i (coalesced loads along i), its 256 /
+// TX thread rows split r (thread row ty takes r = ty, ty + TY, ...), and the
+// partial sums meet in LDS in thread-row order (deterministic).
+template <int DT, bool MAX>
+__global__ __launch_bounds__(256) void reduce_rows_kernel(const uint16_t* x, uint16_t* y, long long outer, int red,
+                                                          long long inner, int lg_tx) {
+  __shared__ float part[256];
+  const int TX = 1 << lg_tx, TY = 256 >> lg_tx;
+  const int tx = threadIdx.x & (TX - 1), ty = threadIdx.x >> lg_tx;
+  const long long i = (long long)blockIdx.x * TX + tx;
+  for (long long o = blockIdx.y; o < outer; o += gridDim.y) {
+    float s = MAX ? -INFINITY : 0.f;
+    if (i < inner) {
+      const uint16_t* p = x + o * red * inner + i;
+      for (int r = ty; r < red; r += TY) {
+        const float v = ld_elem<DT>(p[(long long)r * inner]);
+        s = MAX ? fmaxf(s, v) : s + v;
+      }
+    }
+    part[threadIdx.x] = s;
+    __syncthreads();
+    if (ty == 0 && i < inner) {
+      float t = part[tx];
+      for (int k = 1; k < TY; k++) t = MAX ? fmaxf(t, part[k * TX + tx]) : t + part[k * TX + tx];
+      y[o * inner + i] = (uint16_t)st_elem<DT>(t);
+    }
+    __syncthreads();
+  }
+}
+
 // out[o][i] = sum_r x[o][r][i] (fp32), one thread per (o, i)
 template <int DT, bool MAX = false>
 __global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* x, uint16_t* y, long long outer, int red,
@@ -325,6 +550,11 @@ using namespace yr::graph;
 
 namespace {
 
+int grid_for(long long n) {
+  long long g = (n + 255) / 256;
+  return (int)(g < 1 ? 1 : g > 8192 ? 8192 : g);
+}
+
 template <class F>
 int by_dtype(int dtype, F f) {
   if (dtype == YR_DTYPE_F16) return f(std::integral_constant<int, DT_F16>{});
@@ -332,10 +562,30 @@ int by_dtype(int dtype, F f) {
   return fail(YR_E_INVALID, "graph op: dtype %d unsupported (f16 / bf16)", dtype);
 }
 
-int grid_for(long long n) {
-  long long g = (n + 255) / 256;
-  return (int)(g < 1 ? 1 : g > 8192 ? 8192 : g);
+// Short reductions (r <= 8, or enough outputs to fill the chip on their
+// own) keep one thread per output; longer ones split r across a workgroup.
+template <bool MAX>
+int reduce_launch(const char* nm, const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype,
+                  hipStream_t st) {
+  return by_dtype(dtype, [&](auto dt) {
+    constexpr int D = decltype(dt)::value;
+    if (red <= 8 || outer * inner >= (1 << 20)) {
+      hipLaunchKernelGGL((reduce_kernel<D, MAX>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
+                         (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
+    } else {
+      int lg = 0;
+      while ((1 << lg) < inner && lg < 6) lg++;
+      const long long gx = (inner + (1 << lg) - 1) >> lg;
+      if (gx > 0x7fffffffLL) return fail(YR_E_INVALID, "%s: inner dim too large", nm);
+      const unsigned gy = (unsigned)(outer < 65535 ? outer : 65535);
+      hipLaunchKernelGGL((reduce_rows_kernel<D, MAX>), dim3((unsigned)gx, gy), dim3(256), 0, st, (const uint16_t*)x,
+                         (uint16_t*)y, (long long)outer, red, (long long)inner, lg);
+    }
+    YR_CHECK_LAUNCH(nm);
+    return YR_OK;
+  });
 }
+
 
 }  // namespace
 
@@ -426,7 +676,43 @@ int yr_hip_graph_copy_nd(const void* src, void* dst, int ndim, const int64_t* di
   }
   p.n = n;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(copy_nd_kernel, dim3(grid_for(n)), dim3(256), 0, st, p);
+  // collapse: drop unit dims, merge a dim into the next one when both
+  // sides step through them contiguously
+  long long cd[kCopyDims], cs[kCopyDims], cdst[kCopyDims];
+  int m = 0;
+  for (int d = 0; d < ndim; d++) {
+    if (p.dims[d] == 1) continue;
+    if (m > 0 && cs[m - 1] == p.ss[d] * p.dims[d] && cdst[m - 1] == p.ds[d] * p.dims[d]) {
+      cd[m - 1] *= p.dims[d];
+      cs[m - 1] = p.ss[d];
+      cdst[m - 1] = p.ds[d];
+      continue;
+    }
+    cd[m] = p.dims[d];
+    cs[m] = p.ss[d];
+    cdst[m] = p.ds[d];
+    m++;
+  }
+  if (m == 0) {
+    cd[0] = 1;
+    cs[0] = cdst[0] = 0;
+    m = 1;
+  }
+  if (n < (1ll << 31)) {
+    CopyArgs32 q;
+    q.src = p.src;
+    q.dst = p.dst;
+    q.n = (uint32_t)n;
+    q.nd = m;
+    for (int d = 0; d < m; d++) {
+      q.div[d] = fast_div((uint32_t)cd[d]);
+      q.ss[d] = cs[d];
+      q.ds[d] = cdst[d];
+    }
+    hipLaunchKernelGGL(copy_nd32_kernel, dim3(grid_for(n)), dim3(256), 0, st, q);
+  } else {
+    hipLaunchKernelGGL(copy_nd_kernel, dim3(grid_for(n)), dim3(256), 0, st, p);
+  }
   YR_CHECK_LAUNCH(nm);
   return YR_OK;
 }
@@ -462,6 +748,7 @@ int yr_hip_graph_binary(const void* a, const void* b, void* out, int ndim, const
     if (da <= 0 || db <= 0 || (da != db && da != 1 && db != 1))
       return fail(YR_E_INVALID, "%s: dims %lld and %lld of axis %d do not broadcast", nm, da, db, d);
     p.dims[d] = da > db ? da : db;
+    p.div[d] = fast_div((uint32_t)(p.dims[d] < (1ll << 31) ? p.dims[d] : 1));
     p.sa[d] = da == 1 && p.dims[d] > 1 ? 0 : sa;
     p.sb[d] = db == 1 && p.dims[d] > 1 ? 0 : sb;
     sa *= da;
@@ -477,29 +764,105 @@ int yr_hip_graph_binary(const void* a, const void* b, void* out, int ndim, const
   });
 }
 
-int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype, void* stream) {
-  const char* nm = "yr_hip_graph_reduction";
-  if (!x || !y || outer <= 0 || red <= 0 || inner <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+int yr_hip_graph_ewise(const void* const* ins, int nin, void* out, int ndim, const int64_t* out_dims,
+                       const int64_t* in_dims, int nprog, const int32_t* prog, const float* imm, int dtype,
+                       void* stream) {
+  const char* nm = "yr_hip_graph_ewise";
+  if (!ins || !out || !out_dims || !in_dims || !prog || !imm) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (ndim <= 0 || ndim > kMaxDims) return fail(YR_E_INVALID, "%s: %d dims (1..%d)", nm, ndim, kMaxDims);
+  if (nin <= 0 || nin > kEwIn) return fail(YR_E_INVALID, "%s: %d inputs (1..%d)", nm, nin, kEwIn);
+  if (nprog <= 0 || nprog > kEwProg) return fail(YR_E_INVALID, "%s: %d instructions (1..%d)", nm, nprog, kEwProg);
+  EwiseArgs p;
+  memset(&p, 0, sizeof(p));
+  long long n = 1;
+  for (int d = 0; d < ndim; d++) {
+    if (out_dims[d] <= 0) return fail(YR_E_INVALID, "%s: output dim %d", nm, d);
+    p.div[d] = fast_div((uint32_t)out_dims[d]);
+    n *= out_dims[d];
+  }
+  if (n >= (1ll << 31)) return fail(YR_E_INVALID, "%s: %lld elements (< 2^31)", nm, n);
+  for (int k = 0; k < nin; k++) {
+    if (!ins[k]) return fail(YR_E_INVALID, "%s: input %d is null", nm, k);
+    p.in[k] = (const uint16_t*)ins[k];
+    long long st = 1;
+    for (int d = ndim - 1; d >= 0; d--) {
+      const long long dk = in_dims[k * ndim + d];
+      if (dk != 1 && dk != out_dims[d])
+        return fail(YR_E_INVALID, "%s: input %d dim %d (%lld) does not broadcast to %lld", nm, k, d, dk,
+                    (long long)out_dims[d]);
+      p.s[k][d] = dk == 1 ? 0u : (uint32_t)st;
+      st *= dk;
+    }
+  }
+  for (int k = nin; k < kEwIn; k++) p.in[k] = p.in[0];
+  bool defined[kEwRegs] = {};
+  int nreg = 0;
+  for (int j = 0; j < nprog; j++) {
+    const int32_t* w = prog + 5 * j;  // {op, dst, a, b, kind}
+    const int op = w[0], dst = w[1], a = w[2], b = w[3], kind = w[4];
+    if (dst < 0 || dst >= kEwRegs) return fail(YR_E_INVALID, "%s: instruction %d: register %d", nm, j, dst);
+    if (op == EW_LOAD) {
+      if (a < 0 || a >= nin) return fail(YR_E_INVALID, "%s: instruction %d loads input %d", nm, j, a);
+    } else if (op == EW_UNARY) {
+      if (a < 0 || a >= kEwRegs || !defined[a] || kind < U_EXP || kind > U_SCALE)
+        return fail(YR_E_INVALID, "%s: instruction %d: bad unary", nm, j);
+    } else if (op == EW_BINARY) {
+      if (a < 0 || a >= kEwRegs || b < 0 || b >= kEwRegs || !defined[a] || !defined[b] || kind < B_ADD ||
+          kind > B_POW)
+        return fail(YR_E_INVALID, "%s: instruction %d: bad binary", nm, j);
+    } else {
+      return fail(YR_E_INVALID, "%s: instruction %d: op %d", nm, j, op);
+    }
+    defined[dst] = true;
+    if (dst + 1 > nreg) nreg = dst + 1;
+    p.op[j] = op;
+    p.dst[j] = dst;
+    p.a[j] = a;
+    p.b[j] = b;
+    p.kind[j] = kind;
+    p.lo[j] = imm[2 * j];
+    p.hi[j] = imm[2 * j + 1];
+  }
+  p.out = (uint16_t*)out;
+  p.n = (uint32_t)n;
+  p.nd = ndim;
+  p.nin = nin;
+  p.nprog = nprog;
   hipStream_t st = (hipStream_t)stream;
+  // the register file is selected by compares: the smallest that holds the program
   return by_dtype(dtype, [&](auto dt) {
-    hipLaunchKernelGGL((reduce_kernel<decltype(dt)::value>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
-                       (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
+    constexpr int D = decltype(dt)::value;
+    // four elements per thread once the chip is full (amortizes the program
+    // decode), one below that (latency-bound sizes want the waves)
+    const bool big = n >= (1ll << 18);
+    const int grid = grid_for(big ? (n + 3) / 4 : n);
+#define YR_EW(NR_)                                                                               \
+  if (big) hipLaunchKernelGGL((ewise_kernel<D, NR_, 4>), dim3(grid), dim3(256), 0, st, p);      \
+  else hipLaunchKernelGGL((ewise_kernel<D, NR_, 1>), dim3(grid), dim3(256), 0, st, p);
+    if (nreg <= 4) {
+      YR_EW(4)
+    } else if (nreg <= 8) {
+      YR_EW(8)
+    } else {
+      YR_EW(kEwRegs)
+    }
+#undef YR_EW
     YR_CHECK_LAUNCH(nm);
     return YR_OK;
   });
+}
+
+int yr_hip_graph_reduction(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype, void* stream) {
+  const char* nm = "yr_hip_graph_reduction";
+  if (!x || !y || outer <= 0 || red <= 0 || inner <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
+  return reduce_launch<false>(nm, x, y, outer, red, inner, dtype, (hipStream_t)stream);
 }
 
 int yr_hip_graph_reduction_max(const void* x, void* y, int64_t outer, int red, int64_t inner, int dtype,
                                void* stream) {
   const char* nm = "yr_hip_graph_reduction_max";
   if (!x || !y || outer <= 0 || red <= 0 || inner <= 0) return fail(YR_E_INVALID, "%s: bad arguments", nm);
-  hipStream_t st = (hipStream_t)stream;
-  return by_dtype(dtype, [&](auto dt) {
-    hipLaunchKernelGGL((reduce_kernel<decltype(dt)::value, true>), dim3(grid_for(outer * inner)), dim3(256), 0, st,
-                       (const uint16_t*)x, (uint16_t*)y, (long long)outer, red, (long long)inner);
-    YR_CHECK_LAUNCH(nm);
-    return YR_OK;
-  });
+  return reduce_launch<true>(nm, x, y, outer, red, inner, dtype, (hipStream_t)stream);
 }
 
 int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream) {

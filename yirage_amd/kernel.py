@@ -493,9 +493,14 @@ class KNGraph:
         return self._error_message
 
     # ------------------------------------------------------------ planning
-    def plan(self, fuse: bool = True) -> Plan:
-        """Lower the graph to yr_hip_run_fused steps (host only, no GPU)."""
-        return _Lowering(self, fuse).run()
+    def plan(self, fuse: bool = True, fuse_elementwise: bool = True) -> Plan:
+        """Lower the graph to yr_hip_run_fused steps (host only, no GPU).
+        fuse: the fused-operator patterns; fuse_elementwise: single-consumer
+        trees of elementwise steps become one fused elementwise launch."""
+        plan = _Lowering(self, fuse).run()
+        if fuse_elementwise:
+            _fuse_elementwise(plan)
+        return plan
 
     def superoptimize(self, imaps: list = None, omaps: list = None, griddims: list = None, blockdims: list = None,
                       fmaps: list = None, franges: list = None, verbose: bool = False, config: str = None,
@@ -1524,6 +1529,166 @@ class _Lowering:
             self.emit(_lib.OP_PACK, [r], [("out", k)], [dims3[0], dims3[1], dims3[2], dims3[2], dt.code, *s3, *d3],
                       "pack_output")
         return self.plan
+
+
+_EW_MAX_IN, _EW_MAX_PROG, _EW_MAX_REGS = 8, 32, 16
+
+
+def _fuse_elementwise(plan: Plan) -> None:
+    """Collapse trees of elementwise steps (unary / binary) into single
+    OP_EWISE launches, in place.  A step's output folds into its consumer
+    when it is a temporary read by that one step only (the reference's
+    transpiler fuses a threadblock elementwise op with its producer under the
+    same single-consumer rule, src/transpiler/resolve_tb_fusion.cc:35-66; it
+    chains unary ops, this pass takes binary trees too) and its dims
+    broadcast to the consumer tree's output dims.  Every operator still
+    rounds to the element type, so results are bit-identical to the unfused
+    steps."""
+    steps = plan.steps
+    EW = (_lib.OP_UNARY, _lib.OP_BINARY)
+    # dims of every ref an elementwise step touches: binary steps carry their
+    # operands' dims; a unary step's output has its input's dims
+    dims, bad = {}, set()  # bad: refs seen with two different dims (left out of fusion)
+
+    def put(r, d):
+        if r in dims and dims[r] != d:
+            bad.add(r)
+        dims.setdefault(r, d)
+
+    for st in steps:
+        if st.kind == _lib.OP_BINARY:
+            nd = st.params[0]
+            da, db = tuple(st.params[3:3 + nd]), tuple(st.params[3 + nd:3 + 2 * nd])
+            put(st.ins[0], da)
+            put(st.ins[1], db)
+            put(st.outs[0], tuple(max(x, y) for x, y in zip(da, db)))
+    changed = True
+    while changed:
+        changed = False
+        for st in steps:
+            if st.kind == _lib.OP_UNARY:
+                a, o = st.ins[0], st.outs[0]
+                if a in dims and o not in dims:
+                    dims[o] = dims[a]
+                    changed = True
+                elif o in dims and a not in dims:
+                    dims[a] = dims[o]
+                    changed = True
+    for st in steps:
+        if st.kind == _lib.OP_UNARY:
+            a, o = st.ins[0], st.outs[0]
+            dims.setdefault(a, (st.params[0],))
+            dims.setdefault(o, (st.params[0],))
+            if dims[a] != dims[o]:
+                bad.update((a, o))
+    uses = {}
+    for st in steps:
+        for r in st.ins:
+            uses[r] = uses.get(r, 0) + 1
+    producer = {st.outs[0]: i for i, st in enumerate(steps) if st.kind in EW}
+
+    def fits(d, root):
+        return len(d) == len(root) and all(x == 1 or x == y for x, y in zip(d, root))
+
+    absorbed = set()
+    groups = {}  # root index -> (leaves, program)
+    for ri in range(len(steps) - 1, -1, -1):
+        root = steps[ri]
+        if root.kind not in EW or ri in absorbed or any(r in bad for r in root.ins + root.outs):
+            continue
+        rd = dims[root.outs[0]]
+        dtc = root.params[2]
+        leaves, prog, members = [], [], []
+        reg = [0]
+
+        def build(i):
+            """Instructions computing step i's output; returns its register."""
+            st = steps[i]
+            regs = []
+            for r in st.ins:
+                j = producer.get(r)
+                if (j is not None and j < i and j not in absorbed and r[0] == "tmp" and uses.get(r) == 1
+                        and fits(dims[r], rd) and steps[j].params[2] == dtc
+                        and not any(x in bad for x in steps[j].ins + steps[j].outs)):
+                    members.append(j)
+                    regs.append(build(j))
+                else:
+                    if r in bad or not fits(dims[r], rd):
+                        raise _NoForm
+                    if r in [lf for lf, _ in leaves]:
+                        k = [lf for lf, _ in leaves].index(r)
+                    else:
+                        k = len(leaves)
+                        leaves.append((r, dims[r]))
+                    d = reg[0]
+                    reg[0] += 1
+                    prog.append((0, d, k, 0, 0, 0, 0))
+                    regs.append(d)
+            d = reg[0]
+            reg[0] += 1
+            if st.kind == _lib.OP_UNARY:
+                prog.append((1, d, regs[0], 0, st.params[1], st.params[3], st.params[4]))
+            else:
+                prog.append((2, d, regs[0], regs[1], st.params[1], 0, 0))
+            return d
+
+        try:
+            build(ri)
+        except _NoForm:
+            continue
+        prog, nreg = _ew_alloc(prog)
+        if not members or len(leaves) > _EW_MAX_IN or len(prog) > _EW_MAX_PROG or nreg > _EW_MAX_REGS:
+            continue
+        absorbed.update(members)
+        groups[ri] = (leaves, prog, rd, dtc, [steps[j].name for j in sorted(members)] + [root.name])
+    if not groups:
+        return
+    out = []
+    for i, st in enumerate(steps):
+        if i in absorbed:
+            continue
+        if i in groups:
+            leaves, prog, rd, dtc, names = groups[i]
+            nd = len(rd)
+            params = [nd, len(leaves), len(prog), dtc, *rd]
+            for _, d in leaves:
+                params += list(d)
+            for (op, d, a, b, kind, lo, hi) in prog:
+                params += [op, d, a, b, kind]
+            for (op, d, a, b, kind, lo, hi) in prog:
+                params += [lo, hi]
+            out.append(Step(_lib.OP_EWISE, [r for r, _ in leaves], st.outs, params, "ewise(" + "+".join(names) + ")"))
+        else:
+            out.append(st)
+    plan.steps = out
+
+
+def _ew_alloc(prog):
+    """Register allocation of a fused elementwise program: a value's
+    register is reused once its last reader has run (the kernel selects
+    registers with compares, so fewer registers is fewer instructions).
+    Returns (program, registers used)."""
+    last = {}
+    for j, (op, d, a, b, kind, lo, hi) in enumerate(prog):
+        if op >= 1:
+            last[a] = j
+        if op == 2:
+            last[b] = j
+    free, where, out, top = [], {}, [], 0
+    for j, (op, d, a, b, kind, lo, hi) in enumerate(prog):
+        ra = where.get(a, 0) if op >= 1 else a
+        rb = where.get(b, 0) if op == 2 else b
+        for v in ((a,) if op == 1 else (a, b) if op == 2 else ()):
+            if last.get(v) == j and v in where:
+                free.append(where.pop(v))
+        if free:
+            r = min(free)
+            free.remove(r)
+        else:
+            r, top = top, top + 1
+        where[d] = r
+        out.append((op, r, ra, rb, kind, lo, hi))
+    return out, top
 
 
 def new_kernel_graph() -> KNGraph:
