@@ -320,3 +320,28 @@ def test_elementwise_trees_fuse_into_one_launch():
     G.mark_output(G.mul(G.add(E, Y), E))
     d = G.plan(fuse=True).describe()
     assert d == ["exp", "ewise(add+mul)"], d
+
+
+def test_reference_graph_crosses_over_in_mugraph_json(tmp_path):
+    """The hip branch of the reference's superoptimize: a graph object that
+    only offers the reference's to_json(filename) (here a stand-in writing
+    one of the reference's saved files) becomes a graph of this backend,
+    with the same interface and plan as loading the file directly."""
+    import shutil
+
+    src = os.path.join(GOLDEN, "mirage_cached_mugraphs_647dd41aeaf656b4.json")
+    with open(src) as f:
+        first = json.dumps(json.load(f)[0])
+
+    class RefGraph:  # the reference's KNGraph surface used by the branch
+        def to_json(self, filename):
+            with open(filename, "w") as f:
+                f.write(first)
+
+    g = yr.from_reference_graph(RefGraph())
+    direct = yr.from_reference_graph(first)
+    assert g._same_interface(direct)
+    assert g.plan(fuse=True).describe() == direct.plan(fuse=True).describe()
+    opt = g.superoptimize(backend="hip", profile_iters=0, use_graph_dataset=False)
+    assert opt.backend == "hip" and opt._plan.describe() == direct.plan(fuse=True).describe()
+    shutil.rmtree(tmp_path, ignore_errors=True)

@@ -28,7 +28,7 @@ from .dtypes import (
     uint8,
 )
 from .graph_dataset import graph_dataset
-from .kernel import DTensor, KNGraph, check_stride, new_kernel_graph
+from .kernel import DTensor, KNGraph, check_stride, from_reference_graph, new_kernel_graph
 from .threadblock import STensor, TBGraph, new_threadblock_graph
 
 __version__ = "0.2.0"

@@ -1691,6 +1691,29 @@ def _ew_alloc(prog):
     return out, top
 
 
+def from_reference_graph(graph) -> KNGraph:
+    """A kernel graph built with the reference's own KNGraph (any object
+    with its to_json(filename), python/yirage/kernel.py:1254-1255), or that
+    JSON as a path or text, as a graph of this backend.  This is the body of
+    the hip branch of the reference's superoptimize (kernel.py:584-601,
+    337-343): carry the graph across in the reference's muGraph JSON, then
+    superoptimize(backend='hip') here."""
+    import tempfile
+
+    from .mugraph_json import load
+
+    if hasattr(graph, "to_json"):
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "graph.json")
+            graph.to_json(path)
+            gs = load(path)
+    else:
+        gs = load(graph)
+    if len(gs) != 1:
+        raise YirageHipError(f"from_reference_graph: expected one graph, got {len(gs)}")
+    return gs[0]
+
+
 def new_kernel_graph() -> KNGraph:
     """python/yirage/__init__.py:76-78."""
     return KNGraph()
