@@ -339,7 +339,9 @@ int yr_pk_read_batch(yr_pk_handle* handle, int* out, size_t n);
  * workers) and every wait stays under the watchdog.  For tools that do not
  * follow cooperative launches (profilers).  No reference counterpart. */
 int yr_pk_set_launch_mode(yr_pk_handle* handle, int cooperative);
-/* Polls a dependency may spin before the watchdog flags an error. */
+/* Polls a dependency may spin before the watchdog flags an error (default
+ * 2^26); the kernel then drains: every later wait gives up at once.  No
+ * reference counterpart (its waits are unbounded). */
 int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
 /* Per-task timestamps (10 ns device clock) into buffer[task][8] =
  * {start, inputs ready, end, worker, s4, s5, s6, s7}; NULL disables.
@@ -352,6 +354,9 @@ int yr_pk_set_spin_limit(yr_pk_handle* handle, long long polls);
 int yr_pk_set_profiler(yr_pk_handle* handle, uint64_t* buffer, size_t entries);
 /* Synchronous read of the status words; YR_E_TIMEOUT after a watchdog exit. */
 int yr_pk_status(yr_pk_handle* handle, int* status4);
+/* After a watchdog exit (synchronizes): zero the status words, the event and
+ * grid-barrier counters, the arrival tickets and every epoch-tagged word (link
+ * tensors, split records), and restart the epochs. */
 int yr_pk_reset_status(yr_pk_handle* handle);
 /* Replaces finalize_persistent_kernel (persistent_kernel.cuh:1320-1363). */
 void yr_pk_destroy(yr_pk_handle* handle);

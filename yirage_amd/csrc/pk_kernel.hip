@@ -2389,7 +2389,7 @@ constexpr uint32_t kEpochRebase = 1u << 21;
 struct Handle {
   int device = 0;
   int num_workers = 0;
-  size_t n_ops = 0, n_tasks = 0, n_events = 0;
+  size_t n_ops = 0, n_tasks = 0, n_events = 0, n_tickets = 0;
   OpDesc* d_ops = nullptr;
   TaskDesc* d_tasks = nullptr;
   int* d_qoff = nullptr;
@@ -2409,15 +2409,22 @@ struct Handle {
   bool cooperative = true;
   uint64_t* profile = nullptr;
   std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // tags restart with the epochs: cleared then
+  size_t scratch_words = 0;                                  // d_scratch, in 32-bit words
 };
 
-// Zero every link tensor (their tags embed the epoch, which restarts at 0).
-static int clear_links(Handle* h, hipStream_t st) {
+// Zero every word that carries an epoch tag: the link tensors and the
+// scratch area (the attention split records), since the tags restart with
+// the epochs.  A record slot that some pass left behind (a request mix that
+// no longer uses it) would otherwise match a restarted epoch's tag.
+static int clear_tagged(Handle* h, hipStream_t st) {
   for (auto& lb : h->link_buffers) {
     hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(lb.first),
                        (size_t)(lb.second / 4), 0u);
     YR_CHECK_LAUNCH("pk_fill_u32_kernel (link tensors)");
   }
+  hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(h->d_scratch),
+                     h->scratch_words, 0u);
+  YR_CHECK_LAUNCH("pk_fill_u32_kernel (scratch)");
   return YR_OK;
 }
 
@@ -2477,6 +2484,8 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   YRA(h->d_iters, sizeof(int) * 4);
   YRA(h->d_tickets, sizeof(uint32_t) * (g->num_tickets + 1));
   YRA(h->d_scratch, sizeof(float) * (g->scratch_floats + 4));
+  h->scratch_words = g->scratch_floats + 4;
+  h->n_tickets = g->num_tickets;
   YRA(h->d_status, sizeof(int) * 4);
   const int MR = g->cfg.max_requests, MP = g->cfg.max_pages;
   YRA(h->d_owned_meta, sizeof(int) * (MR + 1 + MP + 2 + MP));
@@ -2497,6 +2506,7 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
     if (o.type == TASK_PREPARE_BATCH) h->has_prepare = true;
   if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_tickets, 0, sizeof(uint32_t) * (g->num_tickets + 1)), "clear tickets");
   if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_status, 0, sizeof(int) * 4), "clear status");
+  if (rc == YR_OK) rc = hip_ok(hipMemset(h->d_scratch, 0, sizeof(float) * h->scratch_words), "clear scratch");
   if (rc != YR_OK) {
     yr_pk_destroy(reinterpret_cast<yr_pk_handle*>(h));
     return rc;
@@ -2566,7 +2576,7 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream, int max_iterations) {
   if (h->epoch + (uint32_t)max_iterations >= kEpochRebase) {
     hipLaunchKernelGGL(pk_fill_u32_kernel, dim3(64), dim3(256), 0, st, h->d_events, h->n_events + 1, 0u);
     YR_CHECK_LAUNCH("pk_fill_u32_kernel");
-    int rc = clear_links(h, st);
+    int rc = clear_tagged(h, st);
     if (rc != YR_OK) return rc;
     h->epoch = 0;
   }
@@ -2661,11 +2671,15 @@ int yr_pk_status(yr_pk_handle* hp, int* status4) {
 int yr_pk_reset_status(yr_pk_handle* hp) {
   Handle* h = reinterpret_cast<Handle*>(hp);
   if (!h) return fail(YR_E_INVALID, "yr_pk_reset_status: null handle");
-  // clear the flags and re-base the counters (a watchdog exit leaves them short)
+  // clear the flags and re-base the counters (a watchdog exit leaves them
+  // short, the grid-barrier counter and split-K / multi-token attention
+  // arrival tickets part-way)
   if (hipMemset(h->d_status, 0, sizeof(int) * 4) != hipSuccess) return fail(YR_E_HIP, "reset status");
   if (hipMemset(h->d_events, 0, sizeof(uint32_t) * (h->n_events + 1)) != hipSuccess)
     return fail(YR_E_HIP, "reset events");
-  int rc = clear_links(h, nullptr);
+  if (hipMemset(h->d_tickets, 0, sizeof(uint32_t) * (h->n_tickets + 1)) != hipSuccess)
+    return fail(YR_E_HIP, "reset tickets");
+  int rc = clear_tagged(h, nullptr);
   if (rc != YR_OK) return rc;
   if (hipDeviceSynchronize() != hipSuccess) return fail(YR_E_HIP, "reset status: synchronize");
   h->epoch = 0;

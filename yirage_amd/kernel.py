@@ -29,7 +29,6 @@ from __future__ import annotations
 
 import ctypes
 import hashlib
-import itertools
 import json
 import os
 import struct
@@ -41,8 +40,7 @@ from ._lib import YirageHipError
 from .dtypes import as_dtype, bfloat16, float16, float32  # noqa: F401  (re-exported API)
 from .graph_dataset import graph_dataset
 from .threadblock import TBGraph
-
-_guid = itertools.count(1)
+from .threadblock import _guid  # one guid space for device and threadblock tensors, as in saved graphs
 _EPS = 1e-6  # rms_norm epsilon of the fused RMSNorm+linear contract (also used by the generic rms_norm)
 
 _UNARY = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "clamp": 4, "sqrt": 5, "square": 6, "mul_scalar": 7}

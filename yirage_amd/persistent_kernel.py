@@ -547,6 +547,16 @@ class PersistentKernel:
         """Cooperative (default) or ordinary launch of the worker grid."""
         check(lib().yr_pk_set_launch_mode(self._handle, int(bool(cooperative))), "launch mode")
 
+    def set_spin_limit(self, polls: int):
+        """Watchdog: polls of one wait before the kernel gives up, flags
+        status()[1][0] and drains (every later wait gives up at once)."""
+        check(lib().yr_pk_set_spin_limit(self._handle, int(polls)), "spin limit")
+
+    def reset_status(self):
+        """After a watchdog exit: clear the status flags and re-base the
+        event counters, arrival tickets and tagged words (synchronizes)."""
+        check(lib().yr_pk_reset_status(self._handle), "reset status")
+
     def status(self):
         st = (ctypes.c_int * 4)()
         rc = lib().yr_pk_status(self._handle, st)

@@ -17,7 +17,7 @@ import itertools
 
 from .dtypes import as_dtype
 
-_guid = itertools.count(1)
+_guid = itertools.count(1)  # shared with kernel.py: device and threadblock tensors never share a guid
 
 # forloop_accum kinds (python/yirage/_cython/core.pyx forloop_accum)
 ACCUM_KINDS = {None: "none", "sum": "sum", "mean": "mean", "rms": "rms", "sum_todimx": "sum_todimx"}
