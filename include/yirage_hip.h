@@ -339,6 +339,15 @@ int yr_pk_read_batch(yr_pk_handle* handle, int* out, size_t n);
  * workers) and every wait stays under the watchdog.  For tools that do not
  * follow cooperative launches (profilers).  No reference counterpart. */
 int yr_pk_set_launch_mode(yr_pk_handle* handle, int cooperative);
+/* Batch > 1 graphs (max_num_batched_tokens > 1): copy every linear task's
+ * weights into handle-owned memory in the order the task streams them
+ * (16-row x 32-column MFMA fragments, 1 KiB per load instruction), so the
+ * weight stream reads sequential 1 KiB units instead of 16 rows x 64 bytes.
+ * enable 0 frees the copy and restores the original weight pointers.
+ * `bytes` (optional) receives the size of the copy (about the linear
+ * weights' size).  Synchronizes; not during a launch.  No reference
+ * counterpart (a layout choice of this backend). */
+int yr_pk_pack_weights(yr_pk_handle* handle, int enable, size_t* bytes);
 /* Polls a dependency may spin before the watchdog flags an error (default
  * 2^26); the kernel then drains: every later wait gives up at once.  No
  * reference counterpart (its waits are unbounded). */

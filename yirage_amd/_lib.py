@@ -91,6 +91,7 @@ SIGNATURES = {
     "yr_pk_iterations": (_I, [_P, ctypes.POINTER(_I)]),
     "yr_pk_set_launch_mode": (_I, [_P, _I]),
     "yr_pk_read_batch": (_I, [_P, ctypes.POINTER(_I), _SZ]),
+    "yr_pk_pack_weights": (_I, [_P, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
     "yr_pk_set_spin_limit": (_I, [_P, ctypes.c_longlong]),
     "yr_pk_status": (_I, [_P, ctypes.POINTER(ctypes.c_int)]),
     "yr_pk_set_profiler": (_I, [_P, _P, _SZ]),

@@ -361,6 +361,14 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
   const int row_bytes = op.x_ld * 2;
   uint16_t* const junk = reinterpret_cast<uint16_t*>(sm.red);
   constexpr int NB = TM == 1 ? 16 : 32;  // loads per lane in flight
+  // NRM: this lane's gamma chunks of the block (k <= 4: KB <= XS_ELEMS / 16),
+  // loaded once up front -- a gamma load per staged chunk would cost one
+  // round trip through the CU's memory queue each
+  uint4 gam[4];
+  if constexpr (NRM) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) gam[j] = j < k ? ldg16(op.norm + k0 + j * 512 + lane * 8) : make_uint4(0, 0, 0, 0);
+  }
   for (int g = 0; g < total; g += NB) {
     const int mb0 = g / k, mc0 = g - mb0 * k;
     uint4 v[NB];
@@ -381,7 +389,7 @@ __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared&
       uint16_t* dst = g + u < total ? sm.xs + xoff + xr * KB + xs_swz(xr, xc * 512 + lane * 8) : junk + lane * 8;
       if constexpr (NRM) {
         const float rb = sm.attn_ml[0][xr & 15][0];
-        const uint4 gq = ldg16(op.norm + k0 + xc * 512 + lane * 8);
+        const uint4 gq = xc == 0 ? gam[0] : xc == 1 ? gam[1] : xc == 2 ? gam[2] : gam[3];
         const uint32_t xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w}, gv[4] = {gq.x, gq.y, gq.z, gq.w};
         uint32_t o[4];
 #pragma unroll
@@ -440,13 +448,17 @@ __device__ __forceinline__ void row_rms(OpRef op, int T, Shared& sm, int lane) {
     float ss[4] = {0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c < K; c += 8 * kWave * 4) {
       uint4 v[4][4];
+      // lane part of the offset in the vector operand, the rest scalar (a
+      // lane-dependent scalar operand would make the compiler loop over lanes)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int u = 0; u < 4; u++) {
           const int col = c + (u * kWave + lane) * 8;
-          const int off = col < K ? (b0 + i) * row_bytes + col * 2 : 0x7ffffff0;
-          v[i][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, 0, off, kCpolSC1));
+          const uint32_t vo = col < K ? (uint32_t)(lane * 16) : 0x7ffffff0u;
+          v[i][u] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, (b0 + i) * row_bytes + (c + u * kWave * 8) * 2,
+                                                           kCpolSC1));
         }
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -717,7 +729,7 @@ __device__ __forceinline__ void flush_acc(float (&acc)[TM], float* slot, int lan
 // chunks whose activations fit the staging buffer -- or, when one block does
 // not hold all of K, half of it: blocks then alternate between the two
 // halves, and block kb + 1 is staged while block kb is consumed.
-__device__ __forceinline__ int gemv_blocks(int NC, int TM) {
+__host__ __device__ __forceinline__ int gemv_blocks(int NC, int TM) {
   int maxc = (XS_ELEMS / TM) >> 9;
   if (NC > maxc) maxc >>= 1;
   int nkb = (NC + maxc - 1) / maxc;
@@ -726,7 +738,7 @@ __device__ __forceinline__ int gemv_blocks(int NC, int TM) {
 }
 constexpr int XS_HALF = XS_ELEMS / 2;  // second staging buffer (multi-block K)
 
-template <int TM, int EPI>
+template <int TM, int EPI, bool PK = false>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   constexpr bool SILU = EPI == EPI_SILU;
   constexpr bool NORM = EPI != EPI_LIN;
@@ -771,8 +783,38 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   };
   int l_i = 0, l_ib = 0, l_kb = 0, l_row = row0, l_c = c00;
   const uint16_t* lrow = row_ptr(row0, 0);
+  // packed weights (batch > 1): the host laid this task's weights out in
+  // stream order, unit (block kb, unit u) at w0 + (kb U + u) 512 with lane
+  // l's 16 bytes at + 8 l, so every load instruction reads 1 KiB contiguous
+  // and a wave walks one sequential range per block.  The last tile's rows
+  // past RT are padding: those lanes load nothing (out-of-range offset).
+  constexpr bool packed = MF && PK;
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(t.w0), 0, packed ? nkb * U * 1024 : 0, 0x00020000);
+  const bool last_ok = (NT - 1) * 16 + lane % 16 < RT;  // this lane's row of the last tile exists
+  uint32_t poff = (uint32_t)u0 * 1024u + lane * 16;
+  int p_tile = row0, p_c = c00;
   uint4 ring[RING];
   auto issue = [&](uint4& dst) __attribute__((always_inline)) {
+    if constexpr (packed) {
+      if (l_i < total) {
+        dst = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, p_tile < NT - 1 || last_ok ? poff : 0xfffffff0u, 0, 0));
+        l_i++;
+        poff += 1024u;
+        if (++p_c == UPR) {
+          p_c = 0;
+          p_tile++;
+        }
+        if (++l_ib == n) {
+          l_ib = 0;
+          poff += (uint32_t)(U - n) * 1024u;
+          p_tile = row0;
+          p_c = c00;
+        }
+      }
+      return;
+    }
     if (l_i < total) {
       dst = ldg16(lrow + (l_c << USH));
       l_i++;
@@ -2159,17 +2201,17 @@ __device__ __forceinline__ TaskDesc task_at(int slot) {
   return t;
 }
 
-template <int TM, int EPI>
+template <int TM, int EPI, bool PK>
 __device__ __forceinline__ void run_gemv(int slot, int tid) {
   const TaskDesc t = task_at(slot);
-  task_gemv<TM, EPI>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+  task_gemv<TM, EPI, PK>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
 }
 // batches of 9..16 tokens (chunked prefill): out of line, so the decode
 // paths keep their code layout
-template <int EPI>
+template <int EPI, bool PK>
 __device__ __attribute__((noinline)) void run_gemv16(int slot, int tid) {
   const TaskDesc t = task_at(slot);
-  task_gemv<16, EPI>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
+  task_gemv<16, EPI, PK>(g_sm.args, t, __builtin_amdgcn_readfirstlane(tid), g_sm);
 }
 template <int RMAX>
 __device__ __forceinline__ void run_attention(int slot, int tid) {
@@ -2235,10 +2277,10 @@ __device__ __attribute__((noinline)) bool grid_barrier(const KernelArgs& a, Shar
 // Linear task of a graph whose batches hold up to MT tokens (1, 8 or 16):
 // one token-tile width per kernel instance, so each instance carries only
 // its own GEMV code (the worker loop is sensitive to its code footprint).
-template <int MT, int EPI>
+template <int MT, bool PK, int EPI>
 __device__ __forceinline__ void run_linear(int slot, int tid) {
-  if constexpr (MT == 16) run_gemv16<EPI>(slot, tid);
-  else run_gemv<MT, EPI>(slot, tid);
+  if constexpr (MT == 16) run_gemv16<EPI, PK>(slot, tid);
+  else run_gemv<MT, EPI, PK>(slot, tid);
 }
 
 // After an early stop: every event counter advanced by num_triggers x the
@@ -2249,7 +2291,10 @@ __device__ __attribute__((noinline)) void fast_forward(const KernelArgs& a, int 
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int MT>
+// MT: token-tile width (1, 8, 16); PK: batch > 1 linear tasks read weights
+// packed in stream order (yr_pk_pack_weights).  One instance per pair, so
+// each carries only its own linear-task code.
+template <int MT, bool PK>
 __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) {
   Shared& sm = g_sm;
   const int w = blockIdx.x;
@@ -2300,16 +2345,16 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     switch (type) {
       case TASK_EMBED: run_embed(slot, tid); break;
       case TASK_LINEAR:
-        run_linear<MT, EPI_LIN>(slot, tid);
+        run_linear<MT, PK, EPI_LIN>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR:
-        run_linear<MT, EPI_NORM>(slot, tid);
+        run_linear<MT, PK, EPI_NORM>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_SILU:
-        run_linear<MT, EPI_SILU>(slot, tid);
+        run_linear<MT, PK, EPI_SILU>(slot, tid);
         break;
       case TASK_RMSNORM_LINEAR_ARGMAX:
-        run_linear<MT, EPI_ARGMAX>(slot, tid);
+        run_linear<MT, PK, EPI_ARGMAX>(slot, tid);
         break;
       case TASK_ATTENTION: {
         // query rows per kv head: nt * G (one MFMA row block of 4 or 16)
@@ -2374,6 +2419,25 @@ __global__ void pk_init_batch_kernel(BatchMeta s) {
   }
 }
 
+// One linear task's weights in the order its batch > 1 stream reads them:
+// unit p = (block kb, 16-row tile, 32-column chunk c), 64 lanes x 16 bytes,
+// lane l = row 16 tile + l % 16 (clamped to the last row), columns
+// kb KB + 32 c + 8 (l / 16) .. + 8 -- the MFMA A fragment task_gemv loads.
+__global__ void pk_pack_kernel(const uint16_t* w0, const uint16_t* w1, int seg, int RT, int K, int KB, int NT,
+                               int UPR, size_t units, uint16_t* dst) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < units * kWave;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t p = i / kWave;
+    const int l = (int)(i % kWave);
+    const int kb = (int)(p / ((size_t)NT * UPR)), rem = (int)(p % ((size_t)NT * UPR));
+    const int tile = rem / UPR, c = rem % UPR;
+    const int r = min(tile * 16 + l % 16, RT - 1);
+    const uint16_t* src = (r < seg ? w0 + (size_t)r * K : w1 + (size_t)(r - seg) * K) + (size_t)kb * KB + c * 32 +
+                          (l / 16) * 8;
+    *reinterpret_cast<uint4*>(dst + p * 512 + l * 8) = *reinterpret_cast<const uint4*>(src);
+  }
+}
+
 __global__ void pk_fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
 }
@@ -2405,11 +2469,16 @@ struct Handle {
   uint32_t epoch = 0;  // epoch of the last pass the device may have run
   long long spin_limit = 1ll << 26;
   bool has_prepare = false;
-  const void* kfn = nullptr;  // pk_worker_kernel<1 / 8 / 16>
+  const void* kfn = nullptr;         // pk_worker_kernel<1 / 8 / 16, false>
+  const void* kfn_packed = nullptr;  // pk_worker_kernel<8 / 16, true> (weights packed)
   bool cooperative = true;
   uint64_t* profile = nullptr;
   std::vector<std::pair<uint64_t, uint64_t>> link_buffers;  // tags restart with the epochs: cleared then
   size_t scratch_words = 0;                                  // d_scratch, in 32-bit words
+  int tm = 1;                                                // token-tile width of the kernel instance
+  std::vector<TaskDesc> tasks;                               // host copy (weight pointers as built)
+  std::vector<OpDesc> ops;
+  uint16_t* d_packed = nullptr;                              // packed linear weights (yr_pk_pack_weights)
 };
 
 // Zero every word that carries an epoch tag: the link tensors and the
@@ -2448,17 +2517,27 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(YR_E_NODEVICE, "yr_pk_create: device query");
   // the kernel instance for the graph's token-tile width
   const int mt = g->cfg.max_tokens;
-  const void* kfn = mt <= 1 ? reinterpret_cast<const void*>(pk_worker_kernel<1>)
-                    : mt <= 8 ? reinterpret_cast<const void*>(pk_worker_kernel<8>)
-                              : reinterpret_cast<const void*>(pk_worker_kernel<16>);
+  const void* kfn = mt <= 1 ? reinterpret_cast<const void*>(pk_worker_kernel<1, false>)
+                    : mt <= 8 ? reinterpret_cast<const void*>(pk_worker_kernel<8, false>)
+                              : reinterpret_cast<const void*>(pk_worker_kernel<16, false>);
+  const void* kfn_packed = mt <= 1 ? nullptr
+                           : mt <= 8 ? reinterpret_cast<const void*>(pk_worker_kernel<8, true>)
+                                     : reinterpret_cast<const void*>(pk_worker_kernel<16, true>);
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kfn, PK_THREADS, 0) != hipSuccess)
     return fail(YR_E_HIP, "yr_pk_create: occupancy query failed");
+  if (kfn_packed) {
+    int occ2 = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ2, kfn_packed, PK_THREADS, 0) != hipSuccess)
+      return fail(YR_E_HIP, "yr_pk_create: occupancy query failed");
+    occ = std::min(occ, occ2);
+  }
   if (g->num_workers > occ * prop.multiProcessorCount)
     return fail(YR_E_INVALID, "yr_pk_create: %d workers cannot be co-resident (%d CUs x %d)", g->num_workers,
                 prop.multiProcessorCount, occ);
   Handle* h = new Handle();
   h->kfn = kfn;
+  h->kfn_packed = kfn_packed;
   h->device = dev;
   h->num_workers = g->num_workers;
   h->n_ops = g->ops.size();
@@ -2485,6 +2564,9 @@ int yr_pk_create(const yr_pk_graph* gp, const yr_pk_meta* mp, yr_pk_handle** out
   YRA(h->d_tickets, sizeof(uint32_t) * (g->num_tickets + 1));
   YRA(h->d_scratch, sizeof(float) * (g->scratch_floats + 4));
   h->scratch_words = g->scratch_floats + 4;
+  h->tm = mt <= 1 ? 1 : mt <= 8 ? 8 : 16;
+  h->tasks = g->tasks;
+  h->ops = g->ops;
   h->n_tickets = g->num_tickets;
   YRA(h->d_status, sizeof(int) * 4);
   const int MR = g->cfg.max_requests, MP = g->cfg.max_pages;
@@ -2603,12 +2685,13 @@ int yr_pk_launch(yr_pk_handle* hp, void* stream, int max_iterations) {
   // (an early stop fast-forwards the counters)
   h->epoch += (uint32_t)max_iterations;
   void* args[] = {&a};
+  const void* fn = h->d_packed ? h->kfn_packed : h->kfn;
   hipError_t e;
   if (h->cooperative)
-    e = hipLaunchCooperativeKernel(h->kfn, dim3(h->num_workers),
+    e = hipLaunchCooperativeKernel(fn, dim3(h->num_workers),
                                    dim3(PK_THREADS), args, 0, st);
   else
-    e = hipLaunchKernel(h->kfn, dim3(h->num_workers), dim3(PK_THREADS),
+    e = hipLaunchKernel(fn, dim3(h->num_workers), dim3(PK_THREADS),
                         args, 0, st);
   if (e != hipSuccess) return check_hip(e, "launch of pk_worker_kernel");
   return YR_OK;
@@ -2637,6 +2720,66 @@ int yr_pk_set_launch_mode(yr_pk_handle* hp, int cooperative) {
   if (!h) return fail(YR_E_INVALID, "yr_pk_set_launch_mode: null handle");
   // co-residency of every worker was checked against the occupancy at create
   h->cooperative = cooperative != 0;
+  return YR_OK;
+}
+
+int yr_pk_pack_weights(yr_pk_handle* hp, int enable, size_t* bytes) {
+  Handle* h = reinterpret_cast<Handle*>(hp);
+  if (!h) return fail(YR_E_INVALID, "yr_pk_pack_weights: null handle");
+  if (bytes) *bytes = 0;
+  std::vector<TaskDesc> tasks = h->tasks;
+  if (h->d_packed) {
+    (void)hipDeviceSynchronize();  // no launch may still read them
+    (void)hipFree(h->d_packed);
+    h->d_packed = nullptr;
+  }
+  if (enable && h->tm > 1) {
+    // geometry of each batch > 1 linear task, as task_gemv derives it
+    struct Job { size_t task, off, units; int RT, seg, K, KB, NT, UPR; };
+    std::vector<Job> jobs;
+    size_t total = 0;
+    for (size_t i = 0; i < tasks.size(); i++) {
+      const TaskDesc& t = tasks[i];
+      const OpDesc& o = h->ops[t.op];
+      const bool silu = o.type == TASK_RMSNORM_LINEAR_SILU;
+      if (o.type != TASK_LINEAR && o.type != TASK_RMSNORM_LINEAR && !silu && o.type != TASK_RMSNORM_LINEAR_ARGMAX)
+        continue;
+      if (t.rows <= 0) continue;
+      Job j;
+      j.task = i;
+      j.K = o.K;
+      j.RT = silu ? 2 * t.rows : t.rows;
+      j.seg = silu ? t.rows : t.split_row;
+      const int NC = o.K >> 9, nkb = gemv_blocks(NC, h->tm);
+      j.KB = (NC / nkb) << 9;
+      j.NT = (j.RT + 15) / 16;
+      j.UPR = j.KB >> 5;
+      j.units = (size_t)nkb * j.NT * j.UPR;
+      j.off = total;
+      total += j.units * 512;
+      jobs.push_back(j);
+    }
+    if (total) {
+      if (hipMalloc((void**)&h->d_packed, total * 2) != hipSuccess) {
+        h->d_packed = nullptr;
+        return fail(YR_E_HIP, "yr_pk_pack_weights: cannot allocate %zu bytes", total * 2);
+      }
+      for (const Job& j : jobs) {
+        TaskDesc& t = tasks[j.task];
+        const int blocks = (int)std::min<size_t>((j.units * kWave + 255) / 256, 1024);
+        hipLaunchKernelGGL(pk_pack_kernel, dim3(blocks), dim3(256), 0, 0, t.w0, t.w1, j.seg, j.RT, j.K, j.KB, j.NT,
+                           j.UPR, j.units, h->d_packed + j.off);
+        YR_CHECK_LAUNCH("pk_pack_kernel");
+        t.w0 = h->d_packed + j.off;
+        t.w1 = nullptr;
+        t.packed = 1;
+      }
+      if (bytes) *bytes = total * 2;
+    }
+  }
+  if (hipMemcpy(h->d_tasks, tasks.data(), sizeof(TaskDesc) * tasks.size(), hipMemcpyHostToDevice) != hipSuccess)
+    return fail(YR_E_HIP, "yr_pk_pack_weights: task copy");
+  if (hipDeviceSynchronize() != hipSuccess) return fail(YR_E_HIP, "yr_pk_pack_weights: synchronize");
   return YR_OK;
 }
 
@@ -2690,7 +2833,7 @@ void yr_pk_destroy(yr_pk_handle* hp) {
   Handle* h = reinterpret_cast<Handle*>(hp);
   if (!h) return;
   void* ptrs[] = {h->d_ops,     h->d_tasks,   h->d_qoff,    h->d_queue,  h->d_events,     h->d_triggers,
-                  h->d_iters,   h->d_tickets, h->d_scratch, h->d_status, h->d_owned_meta};
+                  h->d_iters,   h->d_tickets, h->d_scratch, h->d_status, h->d_owned_meta, h->d_packed};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;

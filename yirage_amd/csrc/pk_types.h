@@ -81,7 +81,7 @@ struct TaskDesc {
   int i0, i1;         // attention: request, kv head; argmax: task ordinal
   int i2, i3;         // attention: split index; argmax: number of tasks
   int split_row;      // linear: rows [0, split_row) come from w0, the rest from w1
-  int pad1;
+  int packed;         // linear, batch > 1: w0 holds this task's weights in stream order (yr_pk_pack_weights)
   const uint16_t* w0; // weight rows of this task (gate rows for the SiLU op)
   const uint16_t* w1; // up rows for the SiLU op; second weight segment of a linear task
 };

@@ -449,6 +449,12 @@ class PersistentKernel:
         h = ctypes.c_void_p()
         check(lib().yr_pk_create(g, ctypes.byref(m), ctypes.byref(h)), "persistent kernel create")
         self._handle = h
+        if self.max_num_batched_tokens > 1 and kwargs.get("pack_weights", True):
+            # batch > 1: the linear tasks stream a copy of their weights laid
+            # out in load order (about the linear weights' size again, in
+            # HBM); pack_weights(False) frees it, pack_weights() after a
+            # weight update refreshes it
+            self.pack_weights(True)
         if any(o["type"] == "prepare_batch" for o in self.ops):
             check(lib().yr_pk_init_batch(h, self._stream()), "init batch")
         self._is_compiled = True
@@ -546,6 +552,16 @@ class PersistentKernel:
     def set_cooperative(self, cooperative: bool = True):
         """Cooperative (default) or ordinary launch of the worker grid."""
         check(lib().yr_pk_set_launch_mode(self._handle, int(bool(cooperative))), "launch mode")
+
+    def pack_weights(self, enable: bool = True) -> int:
+        """Batch > 1 graphs: give the linear tasks a copy of their weights in
+        the order they stream them (sequential 1 KiB MFMA fragments instead
+        of 16 rows x 64 bytes per load); False frees it.  Returns the bytes
+        the copy holds (0 at batch 1, where rows already stream
+        contiguously).  Results are bit-identical either way."""
+        n = ctypes.c_size_t()
+        check(lib().yr_pk_pack_weights(self._handle, int(bool(enable)), ctypes.byref(n)), "pack weights")
+        return n.value
 
     def set_spin_limit(self, polls: int):
         """Watchdog: polls of one wait before the kernel gives up, flags
