@@ -727,16 +727,69 @@ __device__ __forceinline__ void flush_acc(float (&acc)[TM], float* slot, int lan
 
 // Number of staged K blocks: the fewest equal blocks of whole 512-element
 // chunks whose activations fit the staging buffer -- or, when one block does
-// not hold all of K, half of it: blocks then alternate between the two
-// halves, and block kb + 1 is staged while block kb is consumed.
-__host__ __device__ __forceinline__ int gemv_blocks(int NC, int TM) {
+// not hold all of K, a quarter of it (QUAD: blocks rotate through four
+// buffers, loaded straight into LDS up to three blocks ahead) or half of it
+// (the 16-token RMSNorm ops, which scale rows on their way in: blocks
+// alternate between two halves, block kb + 1 staged while kb is consumed).
+__host__ __device__ __forceinline__ int gemv_blocks(int NC, int TM, bool quad) {
   int maxc = (XS_ELEMS / TM) >> 9;
-  if (NC > maxc) maxc >>= 1;
+  if (NC > maxc) maxc = quad ? maxc >> 2 : maxc >> 1;
+  if (maxc < 1) maxc = 1;
   int nkb = (NC + maxc - 1) / maxc;
   while (NC % nkb) nkb++;
   return nkb;
 }
-constexpr int XS_HALF = XS_ELEMS / 2;  // second staging buffer (multi-block K)
+constexpr int XS_HALF = XS_ELEMS / 2;     // second staging buffer (multi-block K)
+constexpr int XS_QUARTER = XS_ELEMS / 4;  // QUAD staging buffers
+
+// 16 bytes per lane from a buffer straight into LDS (lane l's data lands at
+// lds_block + 16 l, lds_block wave-uniform), agent-coherent (sc1); an offset
+// past the buffer writes zeros.  Inline assembly, so the compiler inserts no
+// waits of its own for these loads: the sync wave orders them itself
+// (s_waitcnt vmcnt, then the barrier that publishes the block).
+__device__ __forceinline__ void bload_lds16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, void* lds_block) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(lds_block));
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen sc1 lds"
+               :
+               : "v"(off), "s"(lds), "s"(r)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// s_waitcnt vmcnt(n) for a wave-uniform n in {0, 8, 16, 24, 32, 40, 48}
+// (blocks still allowed in flight x loads per block); other values round down
+__device__ __forceinline__ void wait_dma(int n) {
+  if (n >= 48) wait_vmcnt_le<48>();
+  else if (n >= 40) wait_vmcnt_le<40>();
+  else if (n >= 32) wait_vmcnt_le<32>();
+  else if (n >= 24) wait_vmcnt_le<24>();
+  else if (n >= 16) wait_vmcnt_le<16>();
+  else if (n >= 8) wait_vmcnt_le<8>();
+  else wait_vmcnt_le<0>();
+}
+
+// Sync wave, QUAD multi-block input: block [k0, k0 + KB) of rows [0, TM)
+// into the staging buffer at xs + xoff by direct-to-LDS loads, one
+// instruction per row and 512 columns (TM KB / 512 <= 16 in all).  LDS chunk
+// p of row b receives global chunk p ^ b (the xs_swz layout); rows >= T
+// read as zero.
+template <int TM>
+__device__ __forceinline__ void stage_x_dma(OpRef op, int T, int KB, int k0, Shared& sm, int lane, int xoff) {
+  const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
+  const int G = KB >> 9;  // 512-column groups per row (1 or 2)
+#pragma unroll
+  for (int b = 0; b < TM; b++)
+    for (int g = 0; g < G; g++) {
+      const uint32_t off = (uint32_t)((b * op.x_ld + k0 + (g * 64 + (lane ^ b)) * 8) * 2);
+      bload_lds16_sc1(r, off, sm.xs + xoff + b * KB + g * 512);
+    }
+}
 
 template <int TM, int EPI, bool PK = false>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
@@ -748,7 +801,11 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int RT = SILU ? 2 * R : R;                 // weight rows streamed
   const int seg = SILU ? R : t.split_row;          // rows [0, seg) from w0, the rest from w1
   const int NC = K >> 9;                           // 512-element chunks per row
-  const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM);
+  // QUAD: multi-block inputs staged by direct loads into four buffers (all
+  // but the 16-token RMSNorm ops, which scale rows while staging)
+  constexpr bool QUAD = TM > 1 && !(NORM && TM == 16);
+  const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM, QUAD);
+  const bool dma = QUAD && nkb > 1;
   const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
   // A unit is one 16-byte weight load per lane.  TM == 1: 512 elements of
   // one row (dot products on VALU); TM == 8 / 16: a 16-row x 32-column MFMA A
@@ -853,6 +910,11 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         if (TM == 1 && (op.flags & OPF_X_LL)) {
           stage_x_link(a, op, KB, 0, sm, lane);
           if (a.profile && lane == 0) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();  // inputs valid
+        } else if (dma) {
+          // blocks 0..3 straight into the four buffers; block 0 lands before [X]
+          const int ahead = nkb - 1 < 3 ? nkb - 1 : 3;
+          for (int j = 0; j <= ahead; j++) stage_x_dma<TM>(op, T, KB, j * KB, sm, lane, j * XS_QUARTER);
+          wait_dma(ahead * TM * (KB >> 9));
         } else if (TM > 1 && !(NORM && !pre)) {
           if (lane == 0) sm.coop_stage = 1;  // block 0 staged by all waves after [X]
         } else if constexpr (NORM && TM == 16) {
@@ -917,12 +979,26 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   }
 
   if (is_sync) {
-    // multi-block K (batch > 1 only): block kb goes to half kb & 1 while the
-    // compute waves consume block kb - 1 from the other half; barrier [Bkb]
-    // = block kb staged and block kb - 1 consumed
-    for (int kb = 1; kb < nkb; kb++) {
-      stage_x<TM, NORM && TM == 16>(op, T, KB, kb * KB, sm, lane, (kb & 1) * XS_HALF);
-      lds_sync();  // [Bkb]
+    if (dma) {
+      // QUAD: block kb sits in buffer kb & 3; up to three blocks are in
+      // flight ahead of the one the compute waves consume.  [Bkb] = block kb
+      // landed (this wave's loads of it complete) and block kb - 1 consumed,
+      // whose buffer then takes block kb + 3.
+      const int L = TM * (KB >> 9);
+      for (int kb = 1; kb < nkb; kb++) {
+        const int after = (nkb - 1 < kb + 2 ? nkb - 1 : kb + 2) - kb;  // blocks issued after kb
+        wait_dma(after * L);
+        lds_sync();  // [Bkb]
+        if (kb + 3 < nkb) stage_x_dma<TM>(op, T, KB, (kb + 3) * KB, sm, lane, ((kb + 3) & 3) * XS_QUARTER);
+      }
+    } else {
+      // multi-block K (16-token RMSNorm ops): block kb goes to half kb & 1
+      // while the compute waves consume block kb - 1 from the other half;
+      // barrier [Bkb] = block kb staged and block kb - 1 consumed
+      for (int kb = 1; kb < nkb; kb++) {
+        stage_x<TM, NORM && TM == 16>(op, T, KB, kb * KB, sm, lane, (kb & 1) * XS_HALF);
+        lds_sync();  // [Bkb]
+      }
     }
   } else if (n == 0) {
     for (int kb = 1; kb < nkb; kb++) lds_sync();
@@ -946,7 +1022,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
               tl = row0;
               c = c00;
               kb++;
-              xrow = sm.xs + (kb & 1) * XS_HALF + bt * KB;
+              xrow = sm.xs + (dma ? (kb & 3) * XS_QUARTER : (kb & 1) * XS_HALF) + bt * KB;
               lds_sync();  // [Bkb]
             }
             const uint4 w = ring[s];
@@ -2750,7 +2826,8 @@ int yr_pk_pack_weights(yr_pk_handle* hp, int enable, size_t* bytes) {
       j.K = o.K;
       j.RT = silu ? 2 * t.rows : t.rows;
       j.seg = silu ? t.rows : t.split_row;
-      const int NC = o.K >> 9, nkb = gemv_blocks(NC, h->tm);
+      const bool norm = o.type != TASK_LINEAR;
+      const int NC = o.K >> 9, nkb = gemv_blocks(NC, h->tm, !(norm && h->tm == 16));
       j.KB = (NC / nkb) << 9;
       j.NT = (j.RT + 15) / 16;
       j.UPR = j.KB >> 5;
