@@ -51,6 +51,7 @@ struct Shared {
   float attn_p[PK_WAVES][16][64]; // attention probabilities per wave
   float attn_ml[PK_WAVES][16][2];
   TaskDesc tq[256];               // this worker's first 256 task descriptors
+  int tq_id[256];                 // their task ids
   AttnPre pre[kPreMax];           // attention geometry / page ids, read when descriptors load
   uint8_t pre_of[256];            // descriptor slot -> pre entry (kPreNone: none)
   int pre_n;
@@ -2381,7 +2382,9 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     const int words = (int)(sizeof(TaskDesc) / 4);
     for (int i = tix(); i < n * words; i += PK_THREADS) {
       int k = i / words, e = i % words;
-      reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = gptr(reinterpret_cast<const uint32_t*>(&a.tasks[gptr(a.queue)[first + k]]))[e];
+      const int id = gptr(a.queue)[first + k];
+      reinterpret_cast<uint32_t*>(&sm.tq[k])[e] = gptr(reinterpret_cast<const uint32_t*>(&a.tasks[id]))[e];
+      if (e == 0) sm.tq_id[k] = id;
     }
   };
   load_descs(q0);
@@ -2407,8 +2410,10 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
       for (int i = tix(); i < 256; i += PK_THREADS) sm.pre_of[i] = kPreNone;
       __syncthreads();
     }
-    const int tid = __builtin_amdgcn_readfirstlane(gptr(a.queue)[q]);
     const int slot = (q - q0) % 256;
+    // (task ids come from LDS: a global read here would put a dependent
+    // memory round trip at the start of every task)
+    const int tid = __builtin_amdgcn_readfirstlane(sm.tq_id[slot]);
     OpRef op = op_of(a, sm.tq[slot].op);
     if (a.profile && threadIdx.x == 0) {
       gptr(a.profile)[(size_t)tid * 8] = now_10ns();
@@ -2463,7 +2468,10 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
   if (it + 1 >= a.max_iterations) break;
   // every worker finished pass `it` (prepare_batch included) before any
   // starts the next one: the next pass re-reads the batch metadata
-  if (!grid_barrier(a, sm)) return;
+  // (the LDS copy of the arguments: passing the kernel argument itself by
+  // reference to an out-of-line function would put it in scratch memory, and
+  // every later field read would become a memory round trip)
+  if (!grid_barrier(sm.args, sm)) return;
   if (threadIdx.x == 0)
     sm.flag = !a.stop_when_empty ||
               __hip_atomic_load(gptr(a.meta.status + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -2473,7 +2481,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void pk_worker_kernel(KernelArgs a) 
     // have left it, so the next launch (epoch a.epoch + max_iterations, as
     // the host counts) waits for the right values.  Nobody waits on an
     // event in this launch any more (all workers passed the barrier).
-    fast_forward(a, w, (uint32_t)(a.max_iterations - 1 - it));
+    fast_forward(sm.args, w, (uint32_t)(a.max_iterations - 1 - it));
     break;
   }
   it++;
