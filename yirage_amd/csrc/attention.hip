@@ -59,8 +59,11 @@ __device__ uint64_t g_dec_prof[4096 * 8];
 #define DPROF(i)
 #endif
 
-// D = 128, G <= 16
-template <int DT, int G>
+// D = 128, G <= 16.  PG32 (page size a multiple of 32): a 32-token block
+// lies in one page, whose id each wave reads with one scalar load when it
+// issues the block (no page-table staging before the first K/V load);
+// otherwise the split's page ids are staged in LDS first.
+template <int DT, int G, bool PG32>
 __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = 128;
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
@@ -83,7 +86,8 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
   const int pg0 = c0 / a.page;
   const int npg = c1 > c0 ? (c1 - 1) / a.page - pg0 + 1 : 0;
   const int pbase = a.kv_indptr[b];
-  for (int i = tid; i < npg; i += DEC_THREADS) s_pg[i] = a.kv_indices[pbase + pg0 + i];
+  if constexpr (!PG32)
+    for (int i = tid; i < npg; i += DEC_THREADS) s_pg[i] = a.kv_indices[pbase + pg0 + i];
   // ---- Q as the MFMA A operand: row = head (lane%16 < G), k = d
   uint4 qf[4];
   {
@@ -109,16 +113,36 @@ __global__ __launch_bounds__(DEC_THREADS) void gqa_decode_kernel(DecodeArgs a) {
     uint4 k[2][4];  // [16-token tile j][k step s]: token 16 j + lane % 16, d = 32 s + 8 (lane / 16)
     uint4 v[8];     // token lane / 16 + 4 i, d = 8 (lane % 16)
   };
+  // the page table through the scalar path (read-only for the launch)
+  const __attribute__((address_space(4))) int32_t* kvi =
+      reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(a.kv_indices));
   auto issue = [&](Blk& bk, int blk) __attribute__((always_inline)) {
-    const int tb = c0 + blk * DEC_BLK;
+    const int tb = __builtin_amdgcn_readfirstlane(c0 + blk * DEC_BLK);
+    if constexpr (PG32) {
+      // tokens tb .. tb + 31 (clamped to c1 - 1, the same block) share a page
+      const int pg = kvi[pbase + tb / a.page];
+      auto off32 = [&](int t) __attribute__((always_inline)) -> size_t {
+        t = min(t, c1 - 1);
+        return ((size_t)pg * a.page + t % a.page) * tok_stride + (size_t)hk * D;
+      };
 #pragma unroll
-    for (int n = 0; n < 2; n++) {
-      const size_t off = tok_off(tb + 16 * n + lane % 16) + (lane / 16) * 8;
+      for (int n = 0; n < 2; n++) {
+        const size_t off = off32(tb + 16 * n + lane % 16) + (lane / 16) * 8;
 #pragma unroll
-      for (int s = 0; s < 4; s++) bk.k[n][s] = ldg16(a.kc + off + 32 * s);
+        for (int s = 0; s < 4; s++) bk.k[n][s] = ldg16(a.kc + off + 32 * s);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) bk.v[i] = ldg16(a.vc + off32(tb + lane / 16 + 4 * i) + (lane % 16) * 8);
+    } else {
+#pragma unroll
+      for (int n = 0; n < 2; n++) {
+        const size_t off = tok_off(tb + 16 * n + lane % 16) + (lane / 16) * 8;
+#pragma unroll
+        for (int s = 0; s < 4; s++) bk.k[n][s] = ldg16(a.kc + off + 32 * s);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) bk.v[i] = ldg16(a.vc + tok_off(tb + lane / 16 + 4 * i) + (lane % 16) * 8);
     }
-#pragma unroll
-    for (int i = 0; i < 8; i++) bk.v[i] = ldg16(a.vc + tok_off(tb + lane / 16 + 4 * i) + (lane % 16) * 8);
   };
 
   // online softmax state of rows 4 (lane / 16) + i; O in the MFMA C layout:
@@ -780,8 +804,13 @@ int yr::gqa_decode_launch(const char* nm, const void* q, const void* k_cache, co
   dim3 grid(a.splits, hkv, batch);
 #define YR_DEC(G_)                                                                                        \
   if (G == G_) {                                                                                          \
-    if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL((gqa_decode_kernel<DT_F16, G_>), grid, dim3(DEC_THREADS), 0, st, a); \
-    else hipLaunchKernelGGL((gqa_decode_kernel<DT_BF16, G_>), grid, dim3(DEC_THREADS), 0, st, a);         \
+    if (page_size % DEC_BLK == 0) {                                                                       \
+      if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL((gqa_decode_kernel<DT_F16, G_, true>), grid, dim3(DEC_THREADS), 0, st, a); \
+      else hipLaunchKernelGGL((gqa_decode_kernel<DT_BF16, G_, true>), grid, dim3(DEC_THREADS), 0, st, a);   \
+    } else {                                                                                              \
+      if (dtype == YR_DTYPE_F16) hipLaunchKernelGGL((gqa_decode_kernel<DT_F16, G_, false>), grid, dim3(DEC_THREADS), 0, st, a); \
+      else hipLaunchKernelGGL((gqa_decode_kernel<DT_BF16, G_, false>), grid, dim3(DEC_THREADS), 0, st, a);  \
+    }                                                                                                     \
   }
   YR_DEC(1) YR_DEC(2) YR_DEC(4) YR_DEC(8) YR_DEC(16)
 #undef YR_DEC
