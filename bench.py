@@ -294,6 +294,7 @@ def main():
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--no-b16", action="store_true")
     ap.add_argument("--mugraph-plans", action="store_true",
                     help="only time the saved muGraph candidates' generic / literal plans (JSON line)")
     ap.add_argument("--no-coop", action="store_true",
@@ -362,9 +363,28 @@ def main():
         b8 = m8.weight_bytes() + m8.kv_bytes()
         extra["decode_b8"] = dict(ms=round(ms8, 4), gbs=round(b8 / ms8 / 1e6, 1),
                                   frac_hbm=round(b8 / ms8 / 1e6 / HBM_PEAK_GBS, 4),
-                                  tokens_per_s=round(8 / ms8 * 1e3, 1))
+                                  tokens_per_s=round(8 / ms8 * 1e3, 1),
+                                  weights="packed in stream order at compile (yr_pk_pack_weights)")
         m8.pk.finalize()
         del m8
+        torch.cuda.empty_cache()
+    if not args.no_b16:
+        # 16 tokens per launch (the largest max_num_batched_tokens): 16
+        # requests of one token each, 16-token MFMA tiles
+        m16 = LlamaDecodeModel(LLAMA3_8B, batch=16, kv_len=4096, seed=0)
+        if args.no_coop:
+            m16.pk.set_cooperative(False)
+        m16.set_input_tokens(list(range(128000, 128016)))
+        for _ in range(max(1, args.warmup)):
+            m16.step()
+        ms16 = _events_time(torch, m16.step, max(5, args.steps // 2))
+        b16 = m16.weight_bytes() + m16.kv_bytes()
+        extra["decode_b16"] = dict(ms=round(ms16, 4), gbs=round(b16 / ms16 / 1e6, 1),
+                                   frac_hbm=round(b16 / ms16 / 1e6 / HBM_PEAK_GBS, 4),
+                                   tokens_per_s=round(16 / ms16 * 1e3, 1),
+                                   weights="packed in stream order at compile (yr_pk_pack_weights)")
+        m16.pk.finalize()
+        del m16
         torch.cuda.empty_cache()
     if not args.no_fused:
         import yirage_amd.fused as F
