@@ -2507,18 +2507,33 @@ __global__ void pk_init_batch_kernel(BatchMeta s) {
 // unit p = (block kb, 16-row tile, 32-column chunk c), 64 lanes x 16 bytes,
 // lane l = row 16 tile + l % 16 (clamped to the last row), columns
 // kb KB + 32 c + 8 (l / 16) .. + 8 -- the MFMA A fragment task_gemv loads.
-__global__ void pk_pack_kernel(const uint16_t* w0, const uint16_t* w1, int seg, int RT, int K, int KB, int NT,
-                               int UPR, size_t units, uint16_t* dst) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < units * kWave;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const size_t p = i / kWave;
+struct PackJob {
+  const uint16_t* w0;
+  const uint16_t* w1;
+  uint16_t* dst;
+  unsigned long long unit0;  // first global unit of this task's stream
+  int seg, RT, K, KB, NT, UPR;
+};
+// Every task's stream in one launch: global unit u belongs to the job whose
+// [unit0, next unit0) holds it (binary search over the sorted job table).
+__global__ void pk_pack_kernel(const PackJob* jobs, int njobs, unsigned long long units) {
+  for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < units * kWave;
+       i += (unsigned long long)gridDim.x * blockDim.x) {
+    const unsigned long long u = i / kWave;
     const int l = (int)(i % kWave);
-    const int kb = (int)(p / ((size_t)NT * UPR)), rem = (int)(p % ((size_t)NT * UPR));
-    const int tile = rem / UPR, c = rem % UPR;
-    const int r = min(tile * 16 + l % 16, RT - 1);
-    const uint16_t* src = (r < seg ? w0 + (size_t)r * K : w1 + (size_t)(r - seg) * K) + (size_t)kb * KB + c * 32 +
-                          (l / 16) * 8;
-    *reinterpret_cast<uint4*>(dst + p * 512 + l * 8) = *reinterpret_cast<const uint4*>(src);
+    int lo = 0, hi = njobs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (jobs[mid].unit0 <= u) lo = mid; else hi = mid - 1;
+    }
+    const PackJob& j = jobs[lo];
+    const size_t p = (size_t)(u - j.unit0);
+    const int kb = (int)(p / ((size_t)j.NT * j.UPR)), rem = (int)(p % ((size_t)j.NT * j.UPR));
+    const int tile = rem / j.UPR, c = rem % j.UPR;
+    const int r = min(tile * 16 + l % 16, j.RT - 1);
+    const uint16_t* src = (r < j.seg ? j.w0 + (size_t)r * j.K : j.w1 + (size_t)(r - j.seg) * j.K) +
+                          (size_t)kb * j.KB + c * 32 + (l / 16) * 8;
+    *reinterpret_cast<uint4*>(j.dst + p * 512 + l * 8) = *reinterpret_cast<const uint4*>(src);
   }
 }
 
@@ -2849,15 +2864,38 @@ int yr_pk_pack_weights(yr_pk_handle* hp, int enable, size_t* bytes) {
         h->d_packed = nullptr;
         return fail(YR_E_HIP, "yr_pk_pack_weights: cannot allocate %zu bytes", total * 2);
       }
-      for (const Job& j : jobs) {
+      // one launch over every task's stream (the job table in a temporary
+      // device buffer)
+      std::vector<PackJob> pj(jobs.size());
+      for (size_t i = 0; i < jobs.size(); i++) {
+        const Job& j = jobs[i];
         TaskDesc& t = tasks[j.task];
-        const int blocks = (int)std::min<size_t>((j.units * kWave + 255) / 256, 1024);
-        hipLaunchKernelGGL(pk_pack_kernel, dim3(blocks), dim3(256), 0, 0, t.w0, t.w1, j.seg, j.RT, j.K, j.KB, j.NT,
-                           j.UPR, j.units, h->d_packed + j.off);
-        YR_CHECK_LAUNCH("pk_pack_kernel");
+        pj[i] = PackJob{t.w0, t.w1, h->d_packed + j.off, (unsigned long long)(j.off / 512), j.seg, j.RT, j.K, j.KB,
+                        j.NT, j.UPR};
         t.w0 = h->d_packed + j.off;
         t.w1 = nullptr;
         t.packed = 1;
+      }
+      PackJob* d_jobs = nullptr;
+      if (hipMalloc((void**)&d_jobs, sizeof(PackJob) * pj.size()) != hipSuccess) {
+        (void)hipFree(h->d_packed);
+        h->d_packed = nullptr;
+        return fail(YR_E_HIP, "yr_pk_pack_weights: job table");
+      }
+      int rc = YR_OK;
+      if (hipMemcpy(d_jobs, pj.data(), sizeof(PackJob) * pj.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        rc = fail(YR_E_HIP, "yr_pk_pack_weights: job table copy");
+      } else {
+        hipLaunchKernelGGL(pk_pack_kernel, dim3(4096), dim3(256), 0, 0, d_jobs, (int)pj.size(),
+                           (unsigned long long)(total / 512));
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+          rc = fail(YR_E_HIP, "yr_pk_pack_weights: pack launch");
+      }
+      (void)hipFree(d_jobs);
+      if (rc != YR_OK) {  // the launch keeps using the original weights
+        (void)hipFree(h->d_packed);
+        h->d_packed = nullptr;
+        return rc;
       }
       if (bytes) *bytes = total * 2;
     }
