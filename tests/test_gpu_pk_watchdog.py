@@ -74,3 +74,51 @@ def test_watchdog_fires_drains_and_recovers(batch):
     assert torch.equal(got, want), "logits after recovery differ"
     assert torch.equal(model.meta["output_tokens"], want_tok)
     model.pk.finalize()
+
+
+def test_watchdog_in_a_whole_generation_launch():
+    """A multi-pass launch (a serving graph run until the batch is empty)
+    whose first dependency wait gives up: the workers still inside the pass
+    leave it, the rest give up at the grid barrier, the launch returns with
+    YR_E_TIMEOUT; after reset_status, init_batch and restored caches the
+    same generation gives the tokens a clean run gave."""
+    from tests.test_gpu_pk_serving import CFG as SCFG
+    MR, MT, page, max_seq = 3, 8, 64, 40
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, SCFG.vocab, n).tolist() for n in (9, 17, 3, 12)]
+    print("case watchdog whole-generation launch", flush=True)
+    model = LlamaDecodeModel(SCFG, batch=MR, page_size=page, seed=5, with_prepare=True, prompts=prompts,
+                             max_tokens=MT, max_requests=MR, max_seq=max_seq, eos_token_id=-1)
+    tokens0 = model.meta["tokens"].clone()
+    kc0 = [k.clone() for k in model.kc]
+    vc0 = [v.clone() for v in model.vc]
+
+    def restore():
+        model.meta["step"].zero_()
+        model.meta["tokens"].copy_(tokens0)
+        for i in range(SCFG.num_layers):
+            model.kc[i].copy_(kc0[i])
+            model.vc[i].copy_(vc0[i])
+        model.pk.init_batch()
+
+    passes = model.generate(0)
+    torch.cuda.synchronize()
+    assert model.pk.status()[0] == 0
+    want = model.meta["tokens"].clone()
+
+    restore()
+    model.pk.set_spin_limit(1)
+    model.pk(max_iterations=0)
+    torch.cuda.synchronize()  # every worker left the launch
+    rc, st = model.pk.status()
+    print(f"  after the forced timeout: rc {rc} status {st}", flush=True)
+    assert rc == YR_E_TIMEOUT and st[0] == 1
+
+    model.pk.set_spin_limit(1 << 26)
+    model.pk.reset_status()
+    restore()
+    assert model.generate(0) == passes
+    torch.cuda.synchronize()
+    assert model.pk.status()[0] == 0
+    assert torch.equal(model.meta["tokens"], want), "generation after recovery differs"
+    model.pk.finalize()
