@@ -393,6 +393,8 @@ class PersistentKernel:
         if self.max_num_batched_tokens > 1:
             # every task re-reads all token rows of its input: at batch > 1
             # the doubled bytes cost more than the confirmation they replace
+            # (measured at 8 tokens with only the residual stream linked, the
+            # rows staged by all waves with tag checks: 5.46 against 5.18 ms)
             return
         owned = {id(t) for t in self._owned}
         for op in self.ops:
