@@ -323,6 +323,9 @@ constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
 #ifndef YR_PK_RING
 #define YR_PK_RING 12
 #endif
+#ifndef YR_PK_RING1
+#define YR_PK_RING1 14  // batch 1 (sweep 10 / 12 / 14 / 16: 3.629 / 3.636 / 3.611 / 3.632 ms)
+#endif
 constexpr int RING = YR_PK_RING;           // weight loads in flight per compute lane (RING * 7 KiB per CU)
 constexpr int kCpolSC1 = 16;               // buffer cache policy: agent-coherent (sc1)
 
@@ -794,6 +797,7 @@ __device__ __forceinline__ void stage_x_dma(OpRef op, int T, int KB, int k0, Sha
 
 template <int TM, int EPI, bool PK = false>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
+  constexpr int RG = TM == 1 ? YR_PK_RING1 : RING;  // weight loads in flight per compute lane
   constexpr bool SILU = EPI == EPI_SILU;
   constexpr bool NORM = EPI != EPI_LIN;
   OpRef op = op_of(a, t.op);
@@ -852,7 +856,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const bool last_ok = (NT - 1) * 16 + lane % 16 < RT;  // this lane's row of the last tile exists
   uint32_t poff = (uint32_t)u0 * 1024u + lane * 16;
   int p_tile = row0, p_c = c00;
-  uint4 ring[RING];
+  uint4 ring[RG];
   auto issue = [&](uint4& dst) __attribute__((always_inline)) {
     if constexpr (packed) {
       if (l_i < total) {
@@ -892,7 +896,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     }
   };
 #pragma unroll
-  for (int s = 0; s < RING; s++) issue(ring[s]);
+  for (int s = 0; s < RG; s++) issue(ring[s]);
 
   if (is_sync) {
     // ---------------- sync wave: inputs
@@ -1014,9 +1018,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       const uint16_t* xrow = sm.xs + bt * KB;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       int tl = row0, c = c00, ib = 0, kb = 0;
-      for (int g0 = 0; g0 < total; g0 += RING) {
+      for (int g0 = 0; g0 < total; g0 += RG) {
 #pragma unroll
-        for (int s = 0; s < RING; s++) {
+        for (int s = 0; s < RG; s++) {
           if (g0 + s < total) {
             if (ib == n) {  // next staged block, in the other half
               ib = 0;
@@ -1052,9 +1056,9 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
 #pragma unroll
     for (int b = 0; b < TM; b++) acc[b] = 0.f;
     int row = row0, c = c00, ib = 0;
-    for (int g0 = 0; g0 < total; g0 += RING) {
+    for (int g0 = 0; g0 < total; g0 += RG) {
 #pragma unroll
-      for (int s = 0; s < RING; s++) {
+      for (int s = 0; s < RG; s++) {
         if (g0 + s < total) {
           if (TM > 1 && ib == n) {  // (batch 1 stages all of K at once)
             ib = 0;
