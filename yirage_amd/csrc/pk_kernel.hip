@@ -99,6 +99,12 @@ __device__ __forceinline__ void lds_sync() {
   asm volatile("" ::: "memory");
 }
 
+#ifndef YR_PK_LINK_SLEEP
+#define YR_PK_LINK_SLEEP 2  // s_sleep between re-reads of stale link words (x 64 clocks)
+#endif
+#ifndef YR_PK_LINK_NB
+#define YR_PK_LINK_NB 24    // link-word loads per lane in flight when staging a batch-1 input
+#endif
 // ------------------------------------------------------------ protocol
 __device__ __forceinline__ bool aborted(const KernelArgs& a) {
   return __hip_atomic_load(gptr(a.meta.status), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -190,7 +196,7 @@ __device__ __forceinline__ bool link_spin(const KernelArgs& a, const uint64_t* w
       __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(YR_PK_LINK_SLEEP);
   }
 }
 // the bf16 pair at (even) element e, waiting for this launch's producer
@@ -225,7 +231,7 @@ __device__ __forceinline__ bool link_retry(const KernelArgs& a, long long& spins
     __hip_atomic_store(gptr(a.meta.status), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return false;
   }
-  __builtin_amdgcn_s_sleep(2);
+  __builtin_amdgcn_s_sleep(YR_PK_LINK_SLEEP);
   return true;
 }
 // eight elements of either kind of tensor (plain: one agent-coherent load)
@@ -494,7 +500,7 @@ __device__ __forceinline__ void stage_x_link(const KernelArgs& a, OpRef op, int 
   const int total = KB >> 2;
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x) + 2 * k0, 0, total * 16, 0x00020000);
-  constexpr int NB = 24;
+  constexpr int NB = YR_PK_LINK_NB;
   for (int g0 = 0; g0 < total; g0 += kWave * NB) {
     uint4 v[NB];
     long long spins = 0;
