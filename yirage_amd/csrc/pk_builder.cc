@@ -333,9 +333,16 @@ void Graph::build(const char* text) {
       d.splits = (int)o["splits"].i64(1);
       // a split holds at most 7 compute waves x kAttnBlocksPerWave x 64
       // cached positions
+      // empty_merger: one more split than the cached positions need, which
+      // reads none of them and only appends and merges -- kept only while
+      // every attention task still gets a worker of its own
+      bool empty_merger = o.has("empty_merger") && o["empty_merger"].i64(0) != 0 && d.splits > 1;
       const int per_split = 7 * kAttnBlocksPerWave * 64;
-      int min_splits = (cfg.max_seq_len + per_split - 1) / per_split;
-      if (d.splits < min_splits) d.splits = min_splits;
+      const int min_cached = (cfg.max_seq_len + per_split - 1) / per_split;
+      int cached = empty_merger ? d.splits - 1 : d.splits;
+      if (cached < min_cached) cached = min_cached;
+      if (empty_merger && (int64_t)(cached + 1) * cfg.max_requests * d.num_kv_heads > num_workers) empty_merger = false;
+      d.splits = empty_merger ? cached + 1 : cached;
       d.page_size = cfg.page_size;
       if (d.head_dim != 128) throw std::runtime_error("attention: head_dim must be 128");
       if (d.num_kv_heads <= 0 || d.num_q_heads % d.num_kv_heads) throw std::runtime_error("attention: bad heads");
@@ -354,6 +361,7 @@ void Graph::build(const char* text) {
         d.flags |= OPF_OUT_LL;
         link_writer[out] = (int)ops.size();
       }
+      if (empty_merger) d.flags |= OPF_EMPTY_MERGER;
       const Tensor& KC = tensors[kc];
       if (cfg.page_size != 64) throw std::runtime_error("attention: page_size must be 64");
       if (KC.dims.size() != 4 || KC.dims[1] != cfg.page_size || KC.dims[2] != d.num_kv_heads || KC.dims[3] != d.head_dim)

@@ -280,7 +280,10 @@ __device__ __forceinline__ void task_embed(const KernelArgs& a, const TaskDesc& 
 
 // Geometry of attention task (request r, split s): new tokens [t0, t0+nt),
 // pages [pb, pb+np) of the page table, cached positions [0, base), of which
-// this split reads [c0, c1).
+// this split reads [c0, c1).  With OPF_EMPTY_MERGER the cached positions go
+// to splits 0 .. S-2 and the last split -- which appends the new tokens,
+// attends to them and merges the others' records -- reads none, so it is
+// ready to merge as soon as the others' records arrive.
 constexpr int kPage = 64;  // KV page size in positions (the builder accepts only this)
 
 struct AttnGeom {
@@ -297,7 +300,8 @@ __device__ __forceinline__ AttnGeom attn_geom(const BatchMeta& m, OpRef op, int 
   const int lpl = gptr(m.last_page_len)[r];
   const int seq = g.nt > 0 ? (g.np - 1) * kPage + (lpl == 0 ? kPage : lpl) : 0;
   g.base = seq - g.nt;
-  int chunk = (g.base + S - 1) / S;
+  const int SC = S > 1 && (op.flags & OPF_EMPTY_MERGER) ? S - 1 : S;  // splits that read cached positions
+  int chunk = (g.base + SC - 1) / SC;
   chunk = (chunk + 15) & ~15;
   g.c0 = s * chunk < g.base ? s * chunk : g.base;
   g.c1 = (s + 1) * chunk < g.base ? (s + 1) * chunk : g.base;

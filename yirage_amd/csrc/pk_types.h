@@ -31,6 +31,7 @@ enum OpFlags : int {
   OPF_RES_LL = 4,            // residual is a link tensor written by op res_src
   OPF_OUT_LL = 8,            // out is a link tensor
   OPF_QK_NORM = 16,          // attention: per-head RMSNorm of q (weights `norm`) and new k (`k_norm`) before RoPE
+  OPF_EMPTY_MERGER = 32,     // attention: the last split reads no cached positions (it appends and merges)
 };
 
 // Link tensors: activations passed between CUs inside one launch are stored

@@ -358,11 +358,18 @@ class PersistentKernel:
                 continue
             if k == "attention":
                 per = self.max_num_batched_requests * l["num_kv_heads"]
-                # about half the workers: fewer, larger splits merge faster
-                # (measured at batch 1: 16 splits per kv head 3.82 ms, 32:
-                # 3.88 ms, 8: 3.90 ms); the builder raises it to what the
-                # per-task block budget needs
-                splits = max(1, min(256, W // (self.ATTN_SPLIT_DIVISOR * per)))
+                # about half the workers read the cached positions: fewer,
+                # larger splits merge faster (measured at batch 1: 16 splits
+                # per kv head 3.82 ms, 32: 3.88 ms, 8: 3.90 ms), plus the
+                # last split, which reads none and merges (17 at batch 1:
+                # 3.582 against 3.611 ms for 16 with the merger reading its
+                # share); the builder raises it to what the per-task block
+                # budget needs and drops the extra split when the tasks would
+                # outnumber the workers (batch 8: 5 splits x 64 > 256 workers
+                # measured 5.92 against 5.05 ms for 4)
+                splits = max(1, min(255, int(W // (self.ATTN_SPLIT_DIVISOR * per))))
+                empty_merger = splits > 1
+                splits = splits + 1 if empty_merger else 1
                 ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
                                 v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
                                 sin=l["sin"].name if l["sin"] is not None else None,
@@ -370,7 +377,7 @@ class PersistentKernel:
                                 k_norm=l["k_norm"].name if l["k_norm"] is not None else None,
                                 out=l["output"].name,
                                 num_q_heads=l["num_q_heads"], num_kv_heads=l["num_kv_heads"],
-                                head_dim=l["head_dim"], splits=splits))
+                                head_dim=l["head_dim"], splits=splits, empty_merger=int(empty_merger)))
                 i += 1
                 continue
             if k == "prepare_batch":
