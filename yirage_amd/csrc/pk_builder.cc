@@ -400,18 +400,22 @@ void Graph::build(const char* text) {
       // records of tagged 8-byte words {f32, tag}: 2 floats per value
       scratch_next += (int64_t)cfg.max_requests * d.num_kv_heads * d.splits * d.rec_rows * (d.head_dim + 2) * 2;
       if (scratch_next >= (1ll << 31)) throw std::runtime_error("attention: split records exceed 2^31 floats");
-      for (int r = 0; r < cfg.max_requests; r++)
-        for (int h = 0; h < d.num_kv_heads; h++)
-          for (int s = 0; s < d.splits; s++) {
-            TaskDesc td;
-            memset(&td, 0, sizeof(td));
-            td.i0 = r;
-            td.i1 = h;
-            td.i2 = s;
-            td.row0 = h * (G + 2) * d.head_dim;
-            td.rows = (G + 2) * d.head_dim;
-            add_task(td);
-          }
+      // with an empty merger the merging splits come last, so they land on
+      // consecutive workers (which the next linear op can leave free)
+      const int S = d.splits, S0 = empty_merger ? S - 1 : S;
+      for (int pass = 0; pass < (empty_merger ? 2 : 1); pass++)
+        for (int r = 0; r < cfg.max_requests; r++)
+          for (int h = 0; h < d.num_kv_heads; h++)
+            for (int s = pass ? S0 : 0; s < (pass ? S : S0); s++) {
+              TaskDesc td;
+              memset(&td, 0, sizeof(td));
+              td.i0 = r;
+              td.i1 = h;
+              td.i2 = s;
+              td.row0 = h * (G + 2) * d.head_dim;
+              td.rows = (G + 2) * d.head_dim;
+              add_task(td);
+            }
       info.reads.push_back({qkv, 0, d.qkv_ld, 2});
       info.writes.push_back({out, 0, d.num_q_heads * d.head_dim, 2});
       info.x = qkv;

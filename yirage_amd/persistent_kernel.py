@@ -285,6 +285,7 @@ class PersistentKernel:
         ops = []
         i = 0
         W = self.num_workers
+        attn_free = {}  # attention output -> workers its mergers occupy (left free by the next linear op)
         while i < len(L):
             l = L[i]
             k = l["kind"]
@@ -304,6 +305,10 @@ class PersistentKernel:
                 k = "rmsnorm_linear"
             if k in ("rmsnorm_linear", "linear"):
                 w = l["weight"]
+                # a linear op right after an attention op with merger splits
+                # leaves the mergers' workers free: they finish the attention
+                # last, and a task there would start its weight stream late
+                Wl = W - attn_free.get(l["input"].name, 0)
                 K = w.dim(1)
                 op = dict(x=l["input"].name, weight=self._segments(w), out=l["output"].name)
                 if k == "rmsnorm_linear":
@@ -352,7 +357,7 @@ class PersistentKernel:
                     i += 3
                 else:
                     lim = min(x for x in (max_rows, max_seg) if x) if (max_rows or max_seg) else None
-                    op["rows_per_task"] = self._rows_per_task(w.dim(0), W, gran, lim)
+                    op["rows_per_task"] = self._rows_per_task(w.dim(0), Wl, gran, lim)
                     i += 1
                 ops.append(op)
                 continue
@@ -368,8 +373,16 @@ class PersistentKernel:
                 # outnumber the workers (batch 8: 5 splits x 64 > 256 workers
                 # measured 5.92 against 5.05 ms for 4)
                 splits = max(1, min(255, int(W // (self.ATTN_SPLIT_DIVISOR * per))))
-                empty_merger = splits > 1
-                splits = splits + 1 if empty_merger else 1
+                # (as the builder does: the cached-position splits the per-task
+                # block budget needs, and the extra split only while every
+                # attention task still gets a worker)
+                per_split = 7 * 3 * 64
+                cached = max(splits, -(-self.max_seq_length // per_split))
+                empty_merger = splits > 1 and (cached + 1) * per <= W
+                splits = cached + 1 if empty_merger else cached
+                # the mergers come last in the op's task list, so they sit on
+                # consecutive workers, which the next linear op leaves free
+                attn_free[l["output"].name] = per if empty_merger else 0
                 ops.append(dict(type="attention", qkv=l["input"].name, k_cache=l["k_cache"].name,
                                 v_cache=l["v_cache"].name, cos=l["cos"].name if l["cos"] is not None else None,
                                 sin=l["sin"].name if l["sin"] is not None else None,
