@@ -359,7 +359,7 @@ __device__ __forceinline__ int xs_swz(int b, int e) { return (((e >> 3) ^ b) << 
 // rows b >= T are zero.  16 loads per lane in flight.
 // NRM (16-token batches, where K no longer fits one staged block): each
 // value is normalized on the way in, x * (r_b * gamma) rounded to bf16, with
-// the row factors r_b = rsqrt(mean(x_b^2) + eps) from row_rms (in attn_ml).
+// the row factors r_b = rsqrt(mean(x_b^2) + eps) from row_rms_coop (in attn_ml).
 template <int TM, bool NRM = false>
 __device__ __forceinline__ void stage_x(OpRef op, int T, int KB, int k0, Shared& sm, int lane, int xoff = 0) {
   // groups of 64 chunks (one 16-byte load per lane): group m is row m / k,
@@ -449,50 +449,91 @@ __device__ __forceinline__ void stage_x_coop(OpRef op, int T, int KB, Shared& sm
   }
 }
 
-// Sync wave, 16-token batches: r_b = rsqrt(mean(x_b^2) + eps) of every
-// active row over all of K, read from the input (rows past T give 0), into
-// attn_ml[0][b][0] -- RMSNorm's row factor before any block is staged.
-__device__ __forceinline__ void row_rms(OpRef op, int T, Shared& sm, int lane) {
+// 16-token batches, all 8 waves after [X]: r_b = rsqrt(mean(x_b^2) + eps)
+// of every row (wave w takes rows w, w + 8), all of a wave's loads of a
+// 2048-column stretch in flight at once, into attn_ml[0][b][0]; rows past T
+// read as zero.  (The sync wave alone needed one trip through the CU's
+// memory queue, behind the weight prefetch, per 2048 columns and 4 rows.)
+template <int TM>
+__device__ __forceinline__ void row_rms_coop(OpRef op, int T, Shared& sm, int wave, int lane) {
   const int K = op.K;
   const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
   const int row_bytes = op.x_ld * 2;
-  for (int b0 = 0; b0 < 16; b0 += 4) {
-    float ss[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < K; c += 8 * kWave * 4) {
-      uint4 v[4][4];
-      // lane part of the offset in the vector operand, the rest scalar (a
-      // lane-dependent scalar operand would make the compiler loop over lanes)
+  constexpr int RPW = TM / PK_WAVES;  // rows per wave (2)
+  float ss[RPW];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+  for (int i = 0; i < RPW; i++) ss[i] = 0.f;
+  for (int c = 0; c < K; c += 8 * kWave * 4) {
+    uint4 v[RPW][4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int col = c + (u * kWave + lane) * 8;
-          const uint32_t vo = col < K ? (uint32_t)(lane * 16) : 0x7ffffff0u;
-          v[i][u] = __builtin_bit_cast(
-              uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, (b0 + i) * row_bytes + (c + u * kWave * 8) * 2,
-                                                           kCpolSC1));
+    for (int i = 0; i < RPW; i++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int col = c + (u * kWave + lane) * 8;
+        const uint32_t vo = col < K ? (uint32_t)(lane * 16) : 0x7ffffff0u;
+        v[i][u] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, (wave + PK_WAVES * i) * row_bytes + (c + u * kWave * 8) * 2,
+                                                         kCpolSC1));
+      }
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint32_t w4[4] = {v[i][u].x, v[i][u].y, v[i][u].z, v[i][u].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
+          ss[i] += lo * lo + hi * hi;
         }
+      }
+  }
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+  for (int i = 0; i < RPW; i++) {
+    const float t = wave_sum(ss[i]);
+    if (lane == 0) sm.attn_ml[0][wave + PK_WAVES * i][0] = rsqrtf(t / (float)K + op.eps);
+  }
+}
+
+// 16-token batches, all 8 waves after the row factors: block 0 of the input
+// staged normalized, x * (r_b * gamma) rounded to bf16 (the values stage_x<16,
+// true> writes), 512-column groups to waves by g % 8, one batch of loads.
+template <int TM>
+__device__ __forceinline__ void stage_x_coop_nrm(OpRef op, int T, int KB, Shared& sm, int wave, int lane) {
+  const int k = KB >> 9, total = TM * k;  // <= 64 groups
+  const int nrec = __builtin_amdgcn_readfirstlane((int)((size_t)T * op.x_ld * 2));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(op.x), 0, nrec, 0x00020000);
+  const uint32_t vo = lane * 16;
+  const int row_bytes = op.x_ld * 2;
+  constexpr int NB = 8;
+  uint4 v[NB], gq[NB];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const uint32_t w4[4] = {v[i][u].x, v[i][u].y, v[i][u].z, v[i][u].w};
+  for (int u = 0; u < NB; u++) {
+    const int g = wave + PK_WAVES * u;
+    const int mb = g / k, mc = g - mb * k;
+    const int off = g < total ? mb * row_bytes + mc * 1024 : 0x7ffffff0;
+    v[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, off, kCpolSC1));
+    gq[u] = g < total ? ldg16(op.norm + mc * 512 + lane * 8) : make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const float lo = lo16<DT_BF16>(w4[e]), hi = hi16<DT_BF16>(w4[e]);
-            ss[i] += lo * lo + hi * hi;
-          }
-        }
-    }
+  for (int u = 0; u < NB; u++) {
+    const int g = wave + PK_WAVES * u;
+    if (g < total) {
+      const int mb = g / k, mc = g - mb * k;
+      const float rb = sm.attn_ml[0][mb & 15][0];
+      const uint32_t xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w}, gv[4] = {gq[u].x, gq[u].y, gq[u].z, gq[u].w};
+      uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float t = wave_sum(ss[i]);
-      if (lane == 0) sm.attn_ml[0][b0 + i][0] = rsqrtf(t / (float)K + op.eps);
+      for (int e = 0; e < 4; e++)
+        o[e] = pack2<DT_BF16>(lo16<DT_BF16>(xv[e]) * (rb * lo16<DT_BF16>(gv[e])),
+                              hi16<DT_BF16>(xv[e]) * (rb * hi16<DT_BF16>(gv[e])));
+      *reinterpret_cast<uint4*>(sm.xs + mb * KB + xs_swz(mb, mc * 512 + lane * 8)) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
+
 
 // Sync wave, link-tensor input (batch-1 graphs only): elements [k0, k0 + KB)
 // of row 0 of op.x into xs[0][KB].  A lane loads chunks of four elements (one
@@ -915,7 +956,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
     if (!same_op) {
       NormRegs nr;
       // (16-token batches: K does not fit one staged block; rows are
-      // normalized while they are staged, see row_rms / stage_x<.., true>)
+      // normalized while they are staged, see row_rms_coop / stage_x_coop_nrm / stage_x<.., true>)
       const bool pre = NORM && TM != 16 && K <= 4096;
       if (pre) load_norm(nr, op, lane);
       // a link input is validated word by word: no event poll (measured
@@ -933,8 +974,8 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         } else if (TM > 1 && !(NORM && !pre)) {
           if (lane == 0) sm.coop_stage = 1;  // block 0 staged by all waves after [X]
         } else if constexpr (NORM && TM == 16) {
-          row_rms(op, T, sm, lane);
-          stage_x<TM, true>(op, T, KB, 0, sm, lane);
+          // row factors and block 0 by all waves after [X]
+          if (lane == 0) sm.coop_stage = 2;
         } else {
           stage_x<TM>(op, T, KB, 0, sm, lane);
         }
@@ -976,7 +1017,17 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   if (!sm.flag) return;
   const int T = sm.last_T;
   if constexpr (TM > 1) {
-    if (__builtin_amdgcn_readfirstlane(sm.coop_stage)) {  // workgroup-uniform
+    const int cs = __builtin_amdgcn_readfirstlane(sm.coop_stage);  // workgroup-uniform
+    if constexpr (NORM && TM == 16) {
+      if (cs == 2) {
+        row_rms_coop<TM>(op, T, sm, wave, lane);
+        lds_sync();  // row factors in attn_ml
+        stage_x_coop_nrm<TM>(op, T, KB, sm, wave, lane);
+        lds_sync();  // block 0 staged
+        if (tix() == 0) sm.coop_stage = 0;
+      }
+    }
+    if (cs == 1) {
       stage_x_coop<TM>(op, T, KB, sm, wave, lane);
       lds_sync();  // block 0 staged
       if (tix() == 0) sm.coop_stage = 0;
