@@ -270,7 +270,7 @@ void Graph::build(const char* text) {
       if (col0 % 2 || d.out_ld % 2) throw std::runtime_error("linear output columns must be even-aligned");
       // the staged activation block holds all of K at <= 8 tokens (RMSNorm
       // needs the whole row there); 16-token batches normalize while staging
-      if (norm && (cfg.max_tokens == 1 ? d.K > 32768 : (cfg.max_tokens <= 8 && d.K > 4096)))
+      if (norm && (cfg.max_tokens == 1 ? d.K > 32768 : cfg.max_tokens <= 8 ? d.K > 4096 : d.K > 16384))
         throw std::runtime_error("rmsnorm input too wide for the staged activation block");
       if (cfg.max_tokens > 1 && d.K > 4096 && rpt > 7 * 3 * (silu ? 1 : 1))
         throw std::runtime_error("batch > 1 with K > 4096: rows_per_task must be <= 21");

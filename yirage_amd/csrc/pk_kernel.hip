@@ -846,6 +846,37 @@ __device__ __forceinline__ void stage_x_dma(OpRef op, int T, int KB, int k0, Sha
     }
 }
 
+// 16-token RMSNorm ops, all 8 waves: block [k0, k0 + KB) of rows [0, TM),
+// landed raw in the staging buffer at xs + xoff, scaled in place to
+// x * (r_b * gamma) rounded to bf16 (the values stage_x<16, true> writes),
+// with r_b from row_rms_coop (attn_ml) and gamma staged in attn_p.  Chunk
+// position p of row b holds the row's chunk p ^ b (the xs_swz layout).
+template <int TM>
+__device__ __forceinline__ void norm_block_lds(Shared& sm, int KB, int k0, int xoff) {
+  const uint16_t* const gam = reinterpret_cast<const uint16_t*>(&sm.attn_p[0][0][0]);
+  const int cpr = KB >> 3;  // 8-element chunks per row
+  for (int c = tix(); c < TM * cpr; c += PK_THREADS) {
+    const int b = c / cpr, p = c - b * cpr;
+    uint4* const ptr = reinterpret_cast<uint4*>(sm.xs + xoff + b * KB + p * 8);
+    const uint4 x = *ptr;
+    const uint4 g = *reinterpret_cast<const uint4*>(gam + k0 + ((p ^ b) << 3));
+    const float rb = sm.attn_ml[0][b][0];
+    const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, gv[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      o[e] = pack2<DT_BF16>(lo16<DT_BF16>(xv[e]) * (rb * lo16<DT_BF16>(gv[e])),
+                            hi16<DT_BF16>(xv[e]) * (rb * hi16<DT_BF16>(gv[e])));
+    *ptr = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// gamma (K <= 16384 elements) into attn_p, all 8 waves
+__device__ __forceinline__ void stage_gamma_lds(OpRef op, Shared& sm) {
+  uint16_t* const gam = reinterpret_cast<uint16_t*>(&sm.attn_p[0][0][0]);
+  for (int e = tix() * 8; e < op.K; e += PK_THREADS * 8) *reinterpret_cast<uint4*>(gam + e) = ldg16(op.norm + e);
+}
+
 template <int TM, int EPI, bool PK = false>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
   constexpr int RG = TM == 1 ? YR_PK_RING1 : RING;  // weight loads in flight per compute lane
@@ -857,9 +888,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int RT = SILU ? 2 * R : R;                 // weight rows streamed
   const int seg = SILU ? R : t.split_row;          // rows [0, seg) from w0, the rest from w1
   const int NC = K >> 9;                           // 512-element chunks per row
-  // QUAD: multi-block inputs staged by direct loads into four buffers (all
-  // but the 16-token RMSNorm ops, which scale rows while staging)
-  constexpr bool QUAD = TM > 1 && !(NORM && TM == 16);
+  // QUAD: multi-block inputs staged by direct loads into four buffers (the
+  // 16-token RMSNorm ops then scale each block in LDS, see norm_block_lds)
+  constexpr bool QUAD = TM > 1;
+  constexpr bool NBLK = NORM && TM == 16;  // blocks normalized in LDS after they land
   const int nkb = TM == 1 ? 1 : gemv_blocks(NC, TM, QUAD);
   const bool dma = QUAD && nkb > 1;
   const int NCB = NC / nkb, KB = NCB << 9;         // chunks / elements per staged block
@@ -971,6 +1003,7 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
           const int ahead = nkb - 1 < 3 ? nkb - 1 : 3;
           for (int j = 0; j <= ahead; j++) stage_x_dma<TM>(op, T, KB, j * KB, sm, lane, j * XS_QUARTER);
           wait_dma(ahead * TM * (KB >> 9));
+          if (NBLK && lane == 0) sm.coop_stage = 3;  // row factors, then block 0 scaled, by all waves
         } else if (TM > 1 && !(NORM && !pre)) {
           if (lane == 0) sm.coop_stage = 1;  // block 0 staged by all waves after [X]
         } else if constexpr (NORM && TM == 16) {
@@ -1018,6 +1051,16 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
   const int T = sm.last_T;
   if constexpr (TM > 1) {
     const int cs = __builtin_amdgcn_readfirstlane(sm.coop_stage);  // workgroup-uniform
+    if constexpr (NBLK) {
+      if (cs == 3) {
+        stage_gamma_lds(op, sm);
+        row_rms_coop<TM>(op, T, sm, wave, lane);
+        lds_sync();  // row factors in attn_ml, gamma in attn_p
+        norm_block_lds<TM>(sm, KB, 0, 0);
+        lds_sync();  // block 0 normalized
+        if (tix() == 0) sm.coop_stage = 0;
+      }
+    }
     if constexpr (NORM && TM == 16) {
       if (cs == 2) {
         row_rms_coop<TM>(op, T, sm, wave, lane);
@@ -1055,6 +1098,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
         const int after = (nkb - 1 < kb + 2 ? nkb - 1 : kb + 2) - kb;  // blocks issued after kb
         wait_dma(after * L);
         lds_sync();  // [Bkb]
+        if constexpr (NBLK) {
+          norm_block_lds<TM>(sm, KB, kb * KB, (kb & 3) * XS_QUARTER);
+          lds_sync();  // [Nkb]: block kb normalized
+        }
         if (kb + 3 < nkb) stage_x_dma<TM>(op, T, KB, (kb + 3) * KB, sm, lane, ((kb + 3) & 3) * XS_QUARTER);
       }
     } else {
@@ -1067,7 +1114,13 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
       }
     }
   } else if (n == 0) {
-    for (int kb = 1; kb < nkb; kb++) lds_sync();
+    for (int kb = 1; kb < nkb; kb++) {
+      lds_sync();  // [Bkb]
+      if (NBLK && dma) {
+        norm_block_lds<TM>(sm, KB, kb * KB, (kb & 3) * XS_QUARTER);
+        lds_sync();  // [Nkb]
+      }
+    }
   } else {
     // ---------------- compute waves: stream the unit range
     if constexpr (MF) {
@@ -1090,6 +1143,10 @@ __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t
               kb++;
               xrow = sm.xs + (dma ? (kb & 3) * XS_QUARTER : (kb & 1) * XS_HALF) + bt * KB;
               lds_sync();  // [Bkb]
+              if (NBLK && dma) {
+                norm_block_lds<TM>(sm, KB, kb * KB, (kb & 3) * XS_QUARTER);
+                lds_sync();  // [Nkb]
+              }
             }
             const uint4 w = ring[s];
             issue(ring[s]);
@@ -2914,8 +2971,7 @@ int yr_pk_pack_weights(yr_pk_handle* hp, int enable, size_t* bytes) {
       j.K = o.K;
       j.RT = silu ? 2 * t.rows : t.rows;
       j.seg = silu ? t.rows : t.split_row;
-      const bool norm = o.type != TASK_LINEAR;
-      const int NC = o.K >> 9, nkb = gemv_blocks(NC, h->tm, !(norm && h->tm == 16));
+      const int NC = o.K >> 9, nkb = gemv_blocks(NC, h->tm, true);
       j.KB = (NC / nkb) << 9;
       j.NT = (j.RT + 15) / 16;
       j.UPR = j.KB >> 5;
