@@ -331,13 +331,16 @@ void Graph::build(const char* text) {
       d.num_kv_heads = (int)o["num_kv_heads"].i64();
       d.head_dim = (int)o["head_dim"].i64(128);
       d.splits = (int)o["splits"].i64(1);
-      // a split holds at most 7 compute waves x kAttnBlocksPerWave x 64
+      // a split holds at most 7 compute waves x blocks_per_wave x 64
       // cached positions
       // empty_merger: one more split than the cached positions need, which
       // reads none of them and only appends and merges -- kept only while
       // every attention task still gets a worker of its own
       bool empty_merger = o.has("empty_merger") && o["empty_merger"].i64(0) != 0 && d.splits > 1;
-      const int per_split = 7 * kAttnBlocksPerWave * 64;
+      const int bpw = (int)o["blocks_per_wave"].i64(kAttnBlocksPerWave);
+      if (bpw < 1 || bpw > 64) throw std::runtime_error("attention: blocks_per_wave must be 1..64");
+      d.attn_blocks = 7 * bpw;
+      const int per_split = 7 * bpw * 64;
       const int min_cached = (cfg.max_seq_len + per_split - 1) / per_split;
       int cached = empty_merger ? d.splits - 1 : d.splits;
       if (cached < min_cached) cached = min_cached;

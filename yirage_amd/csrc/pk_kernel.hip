@@ -1483,7 +1483,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
   const float scale = 1.4426950408889634f / sqrtf((float)D);
 
   // cached positions: blocks of 64; compute wave w takes blocks w, w + CW, ...
-  // (at most kAttnBlocksPerWave each)
+  // (at most op.attn_blocks / CW each)
   const int nblk = (c1 - c0 + 63) / 64;
   uint4 kf[4][4], vf[16];
   // a 64-position block spans at most two pages (the builder fixes the page
@@ -1532,7 +1532,7 @@ __device__ __forceinline__ void task_attention_body(const KernelArgs& a, const T
       vf[i] = ldg16((o >= kPage ? ba.vB : ba.vA) + (uint32_t)((o & (kPage - 1)) * (int)tok_stride) + (lane % 16) * 8);
     }
   };
-  const bool fits = nt > 0 && nt * G <= 16 && nblk <= CW * kAttnBlocksPerWave;
+  const bool fits = nt > 0 && nt * G <= 16 && nblk <= op.attn_blocks;
   if (!fits) {  // nothing to do / beyond one MFMA row block or the block budget
     if (!(op.flags & OPF_X_LL) && !wait_event(a, t, task_id, sm)) return;
     if (nt > 0 && tix() == 0)

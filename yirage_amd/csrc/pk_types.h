@@ -70,6 +70,8 @@ struct OpDesc {
   const uint16_t* table;    // embed: [vocab][hidden]
   int64_t* tokens_out;      // argmax: output token ids [max_tokens]
   const uint16_t* k_norm;   // attention qk-norm: k weights [head_dim] (q weights in `norm`)
+  int attn_blocks;          // attention: cached 64-position blocks a split may read (7 waves x blocks per wave)
+  int pad0;
 };
 
 // One per task (workgroup-sized unit of work).

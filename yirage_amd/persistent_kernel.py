@@ -376,7 +376,14 @@ class PersistentKernel:
                 # (as the builder does: the cached-position splits the per-task
                 # block budget needs, and the extra split only while every
                 # attention task still gets a worker)
-                per_split = 7 * 3 * 64
+                # blocks per wave: 3, or more when the splits the cached
+                # positions need would outnumber the workers (16 requests:
+                # 2 splits of 5 blocks per wave on 256 workers instead of
+                # 4 x 128 tasks, two per worker)
+                bpw = 3
+                while bpw < 16 and -(-self.max_seq_length // (7 * bpw * 64)) * per > W:
+                    bpw += 1
+                per_split = 7 * bpw * 64
                 cached = max(splits, -(-self.max_seq_length // per_split))
                 empty_merger = splits > 1 and (cached + 1) * per <= W
                 splits = cached + 1 if empty_merger else cached
@@ -390,7 +397,8 @@ class PersistentKernel:
                                 k_norm=l["k_norm"].name if l["k_norm"] is not None else None,
                                 out=l["output"].name,
                                 num_q_heads=l["num_q_heads"], num_kv_heads=l["num_kv_heads"],
-                                head_dim=l["head_dim"], splits=splits, empty_merger=int(empty_merger)))
+                                head_dim=l["head_dim"], splits=splits, empty_merger=int(empty_merger),
+                                blocks_per_wave=bpw))
                 i += 1
                 continue
             if k == "prepare_batch":
