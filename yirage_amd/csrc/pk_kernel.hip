@@ -99,6 +99,9 @@ __device__ __forceinline__ void lds_sync() {
   asm volatile("" ::: "memory");
 }
 
+#ifndef YR_PK_EVENT_SLEEP
+#define YR_PK_EVENT_SLEEP 16  // s_sleep between event-counter polls of a whole-workgroup wait (x 64 clocks)
+#endif
 #ifndef YR_PK_LINK_SLEEP
 #define YR_PK_LINK_SLEEP 2  // s_sleep between re-reads of stale link words (x 64 clocks)
 #endif
@@ -135,7 +138,7 @@ __device__ bool wait_event(const KernelArgs& a, const TaskDesc& t, int task_id, 
         ok = 0;
         break;
       }
-      __builtin_amdgcn_s_sleep(16);
+      __builtin_amdgcn_s_sleep(YR_PK_EVENT_SLEEP);
     }
     if (a.profile) gptr(a.profile)[(size_t)task_id * 8 + 1] = now_10ns();
     sm.flag = ok;
@@ -332,6 +335,9 @@ constexpr int CW = PK_WAVES - 1;           // compute waves
 constexpr int SYNC_T0 = CW * kWave;        // first thread of the sync wave
 #ifndef YR_PK_RING
 #define YR_PK_RING 12
+#endif
+#ifndef YR_PK_RING8
+#define YR_PK_RING8 16  // batch 2..8 (packed; 12 / 16: 5.251 / 5.136 ms, 16 tokens 6.95 / 7.16 ms at 16)
 #endif
 #ifndef YR_PK_RING1
 #define YR_PK_RING1 14  // batch 1 (sweep 10 / 12 / 14 / 16: 3.629 / 3.636 / 3.611 / 3.632 ms)
@@ -879,7 +885,7 @@ __device__ __forceinline__ void stage_gamma_lds(OpRef op, Shared& sm) {
 
 template <int TM, int EPI, bool PK = false>
 __device__ __forceinline__ void task_gemv(const KernelArgs& a, const TaskDesc& t, int task_id, Shared& sm) {
-  constexpr int RG = TM == 1 ? YR_PK_RING1 : RING;  // weight loads in flight per compute lane
+  constexpr int RG = TM == 1 ? YR_PK_RING1 : TM == 8 ? YR_PK_RING8 : RING;  // weight loads in flight per compute lane
   constexpr bool SILU = EPI == EPI_SILU;
   constexpr bool NORM = EPI != EPI_LIN;
   OpRef op = op_of(a, t.op);
