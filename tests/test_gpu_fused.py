@@ -208,6 +208,13 @@ def test_gqa_decode_paged(B, Hq, Hkv, L, page, dtype):
     (77, False, torch.float16, 2, 4, 1),
     (64, False, torch.bfloat16, 1, 4, 1),    # one full tile, no masked positions
     (1, True, torch.float16, 1, 4, 2),       # single token: output is V
+    # more group sizes and ragged lengths: odd block counts, partial last
+    # blocks and tiles, a single block, group size 8
+    (97, True, torch.bfloat16, 1, 8, 2),
+    (33, True, torch.float16, 2, 4, 1),
+    (32, True, torch.bfloat16, 1, 4, 1),
+    (160, False, torch.bfloat16, 1, 16, 2),  # group size 8, odd block count, one block split
+    (1000, True, torch.float16, 1, 8, 1),    # group size 8, causal
 ])
 def test_gqa_prefill(S, causal, dtype, B, Hq, Hkv):
     import yirage_amd.fused as F
