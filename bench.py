@@ -23,10 +23,10 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 # HBM bytes per pk_worker_kernel launch of the batch-1 headline step, from
 # rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a 1 GiB copy kernel: x2.0 /
 # x1.0), measured on the current kernel with ordinary launches (FETCH
-# 7,835,527 KiB, WRITE 61,967 KiB per dispatch); the profile summary of the
+# 7,650,294 KiB, WRITE 52,553 KiB per dispatch); the profile summary of the
 # decode step has the runs.  The bytes a step moves do not depend on the task
 # schedule.
-PK_B1_TRAFFIC_BYTES = 16_110_262_005
+PK_B1_TRAFFIC_BYTES = 15_721_272_310
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 
 
