@@ -3,11 +3,12 @@ by block and iteration by iteration (test infrastructure).  It follows the
 threadblock semantics of the reference's fingerprint executor: tiles are the
 device tensor cut along input_map by the grid and along forloop_dim by the
 forloop (src/threadblock/input_loader.cc); a forloop accumulator adds its
-input over the iterations, `sum` / `sum_todimx` / `rms` reducing the last
-dim with element j adding j, j + dimx, j + 2 dimx, ...
+input over the iterations, `sum` / `sum_todimx` / `rms` / `mean` reducing
+the last dim with element j adding j, j + dimx, j + 2 dimx, ...
 (include/yirage/threadblock/cuda/reduction.h:41-58, src/threadblock/
 graph.cc:460-485, rms as the transpiler lowers it, src/transpiler/
-transpile.cc:681-693); ops after an accumulator run once after the loop;
+transpile.cc:681-693, mean divided by the count of the summed elements as
+include/yirage/threadblock/cuda/forloop_accum.h:89-97 does); ops after an accumulator run once after the loop;
 outputs are placed by output_map and forloop_dim (output.cc).  float64
 throughout.  It is a second, independent reading of the same semantics as
 the planner's tile interpreter, which runs every block at once as batched
@@ -89,6 +90,8 @@ def _customized(op, inputs):
                             x = _to_dimx(x, x.ndim - 1, bg.reduction_dimx)
                         elif kind == "rms":
                             x = np.sqrt(x.sum(-1, keepdims=True) / (top.inputs[0].dims[-1] * R))
+                        elif kind == "mean":
+                            x = x.sum(-1, keepdims=True) / (top.inputs[0].dims[-1] * R)
                         elif kind != "none":
                             raise NotImplementedError(kind)
                         post[id(top.outputs[0])] = x

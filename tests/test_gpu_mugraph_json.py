@@ -202,6 +202,23 @@ def test_customized_max_and_concat_run_literally():
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
 
 
+def test_customized_mean_accumulator_runs_literally():
+    """The mean forloop accumulator on the GPU against its closed form, the
+    row mean of exp(X) (float64), and the sum accumulator of the same tiles
+    divided by the 256 summed elements."""
+    from test_mugraph_json import _mean_graph
+
+    g = _mean_graph()
+    x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(5))).half()
+    mean, total = g(inputs=[x.cuda()])
+    torch.cuda.synchronize()
+    ref = torch.exp(x.double()).mean(1, keepdim=True).numpy()
+    err = np.abs(mean.float().cpu().numpy() - ref)
+    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+    err2 = np.abs(mean.float().cpu().numpy() - total.float().cpu().numpy() / 256)
+    assert not (err2 > ATOL + RTOL * np.abs(ref)).any(), f"mean vs sum / 256: {err2.max()}"
+
+
 def test_fused_elementwise_bit_identical_to_unfused_steps():
     """Plans whose elementwise trees were fused into single launches
     (yr_hip_graph_ewise) give bit-identical outputs to the same plans run one

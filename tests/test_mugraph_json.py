@@ -291,6 +291,43 @@ def test_literal_max_and_concat():
     assert np.allclose(ref[:, :64], np.exp(xr).max(1)) and np.allclose(ref[:, 64], xr.max(2).sum(1))
 
 
+def _mean_graph():
+    """Tiles of X [8, 256] (grid 2 over rows, forloop 4 over columns): the
+    mean accumulator of exp over the 256 columns of each row, plus a sum
+    accumulator of the same tiles for the ratio check."""
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(8, 256), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 1, 1), block_dim=(128, 1, 1), forloop_range=4, reduction_dimx=64)
+    tX = tb.new_input(dtensor=X, input_map=(0, -1, -1), forloop_dim=1)
+    e = tb.exp(tX)
+    tb.new_output(stensor=tb.forloop_accum(e, "mean"), output_map=(0, -1, -1))
+    tb.new_output(stensor=tb.forloop_accum(e, "sum"), output_map=(0, -1, -1))
+    outs = g.customized([X], tb)
+    g.mark_output(outs[0])
+    g.mark_output(outs[1])
+    return g
+
+
+def test_literal_mean_accumulator():
+    """The mean forloop accumulator (the fingerprint executor's: the sum over
+    the last dim and the iterations over their count) against its closed
+    form, the row mean of exp(X), and against sum / 256 of the same tiles;
+    also the block-by-block emulation."""
+    import numpy as np
+    from plan_numpy import run_plan
+    from tb_numpy import run_graph
+
+    g = _mean_graph()
+    p = g.plan(fuse=True)
+    assert g.outputs[0][0].dims == (8, 1)
+    x = np.random.default_rng(3).normal(0, 1, (8, 256))
+    got = run_plan(p, [x])
+    assert np.allclose(got[0][:, 0], np.exp(x).mean(1), rtol=1e-12, atol=0)
+    assert np.allclose(got[0], got[1] / 256, rtol=1e-12, atol=0)
+    ref = run_graph(g, [x])
+    assert np.abs(got[0] - ref[0]).max() <= 1e-12
+
+
 def test_elementwise_trees_fuse_into_one_launch():
     """Single-consumer trees of elementwise steps become one fused
     elementwise launch (the reference's transpiler fusion rule,

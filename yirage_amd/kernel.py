@@ -1270,13 +1270,16 @@ class _Lowering:
         660-700: none = sum over iterations, sum = that reduced over the last
         dim, sum_todimx = reduced to reduction_dimx, rms = sqrt of the mean
         square over the last dim and the iterations, max = the largest over
-        the iterations).  False (nothing emitted) for ops it has no form
-        for: rescale accumulators (the reference's fingerprint executor,
-        src/kernel/cuda/customized_kernel.cu:146-150, has no case for them)
-        and mean accumulators (its transpiler has no lowering,
-        transpile.cc:677-680), and matmuls whose tiles the MFMA kernel cannot
-        take (n or k not a multiple of 8, k > 1; k = 1 is an outer product,
-        a broadcast multiply)."""
+        the iterations) and, where the transpiler has no lowering
+        (transpile.cc:677-680), mean as the reference's fingerprint executor
+        computes it: the sum over the last dim and the iterations divided by
+        their count (include/yirage/threadblock/cuda/forloop_accum.h:66-97).
+        False (nothing emitted) for ops it has no form for: rescale
+        accumulators (the fingerprint executor, src/kernel/cuda/
+        customized_kernel.cu:146-150, has no case for them, and
+        forloop_accum.cc:131-150 rejects them), and matmuls whose tiles the
+        MFMA kernel cannot take (n or k not a multiple of 8, k > 1; k = 1 is
+        an outer product, a broadcast multiply)."""
         bg = op.attrs["bgraph"]
         gx, gy, gz = bg.grid_dim
         grid = (gx, gy, gz)
@@ -1454,6 +1457,12 @@ class _Lowering:
                         x = unary("square", ins[0])
                         x = unary("mul_scalar", x, 1.0 / (ins[0][1][-1] * R))
                         r = unary("sqrt", reduce(accumulate(x), len(x[1]) - 1))
+                    elif acc == "mean":
+                        # the fingerprint executor's order: sum over the last
+                        # dim and the iterations, then divide by their count
+                        # (include/yirage/threadblock/cuda/forloop_accum.h:66-97)
+                        x = reduce(accumulate(ins[0]), len(ins[0][1]) - 1)
+                        r = unary("mul_scalar", x, 1.0 / (ins[0][1][-1] * R))
                     else:
                         raise _NoForm
                 else:
