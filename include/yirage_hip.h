@@ -242,7 +242,7 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
  *   YR_OP_RMSNORM:        in {x}, out {y}; params {rows, n, dtype, eps_bits}
  *   YR_OP_PACK:           in {src}, out {dst}; params {g, rows, cols, dst_cols, dtype, strides6...}
  *   YR_OP_COPY_ND:        in {src}, out {dst}; params {ndim, dtype, dims[8], src_strides[8], dst_strides[8],
- *                                             dst_offset} (elements; 27 params)
+ *                                             dst_offset[, src_offset]} (elements; 27 or 28 params)
  *   YR_OP_REDUCTION_MAX:  in {x}, out {y}; params {outer, red, inner, dtype}
  *   YR_OP_EWISE:          in {x0..x_{n-1}} (1..8), out {y}; params {ndim, n, n_prog, dtype,
  *                         out_dims[ndim], in_dims[n][ndim], prog[n_prog][5], imm_bits[n_prog][2]}

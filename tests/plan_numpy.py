@@ -48,7 +48,7 @@ def run_plan(plan, inputs):
         k = st.kind
         if k == _lib.OP_COPY_ND:
             so, do = _copy_nd(src[0], p)
-            dst[do + p[26]] = src[0][so]
+            dst[do + p[26]] = src[0][so + (p[27] if len(p) > 27 else 0)]
         elif k == _lib.OP_UNARY:
             n, kind, lo, hi = p[0], p[1], _f32(p[3]), _f32(p[4])
             a = src[0][:n]

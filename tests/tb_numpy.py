@@ -8,7 +8,10 @@ the last dim with element j adding j, j + dimx, j + 2 dimx, ...
 (include/yirage/threadblock/cuda/reduction.h:41-58, src/threadblock/
 graph.cc:460-485, rms as the transpiler lowers it, src/transpiler/
 transpile.cc:681-693, mean divided by the count of the summed elements as
-include/yirage/threadblock/cuda/forloop_accum.h:89-97 does); ops after an accumulator run once after the loop;
+include/yirage/threadblock/cuda/forloop_accum.h:89-97 does); a rescale
+accumulator multiplies its running value by the rescale tile and adds the
+input each iteration, as the transpiler's kernel does
+(include/yirage/transpiler/runtime/threadblock/forloop_accum.h:67-93); ops after an accumulator run once after the loop;
 outputs are placed by output_map and forloop_dim (output.cc).  float64
 throughout.  It is a second, independent reading of the same semantics as
 the planner's tile interpreter, which runs every block at once as batched
@@ -61,7 +64,7 @@ def _customized(op, inputs):
                         v[id(st)] = x[tuple(sl)]
                     for top in bg.ops:
                         k = top.kind
-                        if k == "input" or top.outputs[0].after_accum and k not in ("accum", "accum_max"):
+                        if k == "input" or top.outputs[0].after_accum and k not in ("accum", "accum_max", "accum_rescale"):
                             continue
                         a = [v[id(t)] for t in top.inputs]
                         if k == "accum":
@@ -69,6 +72,9 @@ def _customized(op, inputs):
                             if top.attrs["acc"] == "rms":
                                 x = x * x
                             acc[id(top)] = acc.get(id(top), 0) + x
+                            continue
+                        if k == "accum_rescale":  # acc * rescale + input, from zero
+                            acc[id(top)] = acc.get(id(top), 0) * a[1] + a[0]
                             continue
                         if k == "accum_max":
                             acc[id(top)] = np.maximum(acc[id(top)], a[0]) if id(top) in acc else a[0]
@@ -81,6 +87,9 @@ def _customized(op, inputs):
                 for top in bg.ops:
                     if top.kind == "accum_max":
                         post[id(top.outputs[0])] = acc[id(top)]
+                    elif top.kind == "accum_rescale":
+                        x = acc[id(top)]
+                        post[id(top.outputs[0])] = x.sum(-1, keepdims=True) if top.attrs["acc"] == "sum" else x
                     elif top.kind == "accum":
                         x = acc[id(top)]
                         kind = top.attrs["acc"]

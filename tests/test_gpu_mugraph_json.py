@@ -219,6 +219,22 @@ def test_customized_mean_accumulator_runs_literally():
     assert not (err2 > ATOL + RTOL * np.abs(ref)).any(), f"mean vs sum / 256: {err2.max()}"
 
 
+def test_customized_rescale_accumulator_runs_literally():
+    """Rescale accumulators (acc = acc * rescale + input per iteration, kept
+    whole and with the last dim summed) on the GPU against the closed form
+    sum_i x_i prod_{j>i} r_j in float64."""
+    from test_mugraph_json import _rescale_closed_form, _rescale_graph
+
+    g = _rescale_graph()
+    x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(7))).half()
+    whole, summed = g(inputs=[x.cuda()])
+    torch.cuda.synchronize()
+    want, want_sum = _rescale_closed_form(x.double().numpy())
+    for got, ref in ((whole, want), (summed, want_sum)):
+        err = np.abs(got.float().cpu().numpy() - ref)
+        assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+
+
 def test_fused_elementwise_bit_identical_to_unfused_steps():
     """Plans whose elementwise trees were fused into single launches
     (yr_hip_graph_ewise) give bit-identical outputs to the same plans run one

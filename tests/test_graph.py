@@ -131,8 +131,9 @@ def test_strided_output_gets_a_pack_step():
 def test_unsupported_customized_graph_raises():
     g = yr.new_kernel_graph()
     X = g.new_input(dims=(8, 64), dtype=yr.float16)
-    # a rescaled accumulator: no fused kernel, no whole-tensor expression
-    # and no generic form
+    # a rescale tile with one factor per element instead of per row (the
+    # reference's rescale kernel rejects it too): no fused kernel, no
+    # whole-tensor expression and no generic form
     tb = yr.new_threadblock_graph(grid_dim=(1, 1, 1), block_dim=(128, 1, 1), forloop_range=2, reduction_dimx=64)
     tX = tb.new_input(dtensor=X, input_map=(-1, -1, -1), forloop_dim=1)
     tb.new_output(stensor=tb.forloop_accum_rescale(tb.exp(tX), tX), output_map=(-1, -1, -1))

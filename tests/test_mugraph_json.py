@@ -178,7 +178,8 @@ def test_superoptimize_reads_a_previous_checkpoint():
     hX = h.new_input(dims=(1, 3584), dtype=yr.float16)
     hG = h.new_input(dims=(1, 3584), dtype=yr.float16)
     hW = h.new_input(dims=(3584, 37888), strides=(1, 3584), dtype=yr.float16)
-    # a rescaled accumulator (online-softmax style): no fused kernel, no
+    # a rescaled accumulator whose rescale tile is not one factor per row
+    # (the reference's rescale kernel rejects it too): no fused kernel, no
     # whole-tensor expression and no generic form
     tb = yr.new_threadblock_graph(grid_dim=(592, 1, 1), block_dim=(128, 1, 1), forloop_range=64, reduction_dimx=64)
     tX = tb.new_input(dtensor=hX, input_map=(-1, -1, -1), forloop_dim=1)
@@ -326,6 +327,56 @@ def test_literal_mean_accumulator():
     assert np.allclose(got[0], got[1] / 256, rtol=1e-12, atol=0)
     ref = run_graph(g, [x])
     assert np.abs(got[0] - ref[0]).max() <= 1e-12
+
+
+def _rescale_graph():
+    """Tiles of X [8, 256] (grid 2 over rows, forloop 4 over columns): an
+    online-softmax style accumulation, acc = acc * exp(-rowmax) + exp(x)
+    every iteration, kept whole and with its last dim summed."""
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(8, 256), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 1, 1), block_dim=(128, 1, 1), forloop_range=4, reduction_dimx=64)
+    tX = tb.new_input(dtensor=X, input_map=(0, -1, -1), forloop_dim=1)
+    s = tb.exp(tb.mul_scalar(tb.reduction_max(tX, 1), -1.0))
+    e = tb.exp(tX)
+    tb.new_output(stensor=tb.forloop_accum_rescale(e, s), output_map=(0, -1, -1))
+    tb.new_output(stensor=tb.forloop_accum_rescale(e, s, "sum"), output_map=(0, -1, -1))
+    outs = g.customized([X], tb)
+    g.mark_output(outs[0])
+    g.mark_output(outs[1])
+    return g
+
+
+def _rescale_closed_form(x):
+    """sum_i exp(x_i) prod_{j > i} exp(-max_j) per row, x cut into 4 column
+    chunks of 64 (float64)."""
+    import numpy as np
+
+    c = x.reshape(8, 4, 64)
+    f = np.exp(-c.max(2))  # [8, 4] rescale factor of each iteration
+    acc = np.zeros((8, 64))
+    for i in range(4):
+        acc += np.exp(c[:, i]) * np.prod(f[:, i + 1:], axis=1, keepdims=True)
+    return acc, acc.sum(1, keepdims=True)
+
+
+def test_literal_rescale_accumulator():
+    """Rescale accumulators (the transpiler's acc = acc * rescale + input per
+    iteration) against the closed form sum_i x_i prod_{j>i} r_j, and against
+    the block-by-block emulation."""
+    import numpy as np
+    from plan_numpy import run_plan
+    from tb_numpy import run_graph
+
+    g = _rescale_graph()
+    p = g.plan(fuse=True)
+    assert [o[0].dims for o in g.outputs] == [(8, 64), (8, 1)]
+    x = np.random.default_rng(6).normal(0, 1, (8, 256))
+    got = run_plan(p, [x])
+    want, want_sum = _rescale_closed_form(x)
+    assert np.allclose(got[0], want, rtol=1e-12, atol=0) and np.allclose(got[1], want_sum, rtol=1e-12, atol=0)
+    ref = run_graph(g, [x])
+    assert np.abs(got[0] - ref[0]).max() <= 1e-12 and np.abs(got[1] - ref[1]).max() <= 1e-12
 
 
 def test_elementwise_trees_fuse_into_one_launch():

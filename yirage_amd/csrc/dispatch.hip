@@ -36,7 +36,7 @@ bool arity_of(int kind, Arity* a) {
     case YR_OP_REDUCTION: *a = {1, 1, 4}; return true;
     case YR_OP_RMSNORM: *a = {1, 1, 4}; return true;
     case YR_OP_PACK: *a = {1, 1, 11}; return true;
-    case YR_OP_COPY_ND: *a = {1, 1, 27}; return true;
+    case YR_OP_COPY_ND: *a = {1, 1, -27}; return true;  // 27, or 28 with a source offset
     case YR_OP_REDUCTION_MAX: *a = {1, 1, 4}; return true;
     case YR_OP_EWISE: *a = {-1, 1, -4}; return true;  // 1..8 inputs
     default: return false;
@@ -113,9 +113,11 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, vo
       return yr_hip_graph_rmsnorm(in[0], out[0], (int)p[0], (int)p[1], f32_of(p[3]), (int)p[2], stream);
     case YR_OP_PACK:
       return yr_hip_graph_pack(in[0], out[0], (int)p[0], (int)p[1], (int)p[2], (int)p[3], p + 5, (int)p[4], stream);
-    case YR_OP_COPY_ND:  // p[26]: element offset of the destination
-      return yr_hip_graph_copy_nd(in[0], out[0] ? (uint16_t*)out[0] + p[26] : nullptr, (int)p[0], p + 2, p + 10,
-                                  p + 18, (int)p[1], stream);
+    case YR_OP_COPY_ND:  // p[26]: element offset of the destination; p[27] (optional): of the source
+      if (n_params > 28) return fail(YR_E_INVALID, "%s: copy_nd takes 27 or 28 params", nm);
+      return yr_hip_graph_copy_nd(in[0] ? (const uint16_t*)in[0] + (n_params > 27 ? p[27] : 0) : nullptr,
+                                  out[0] ? (uint16_t*)out[0] + p[26] : nullptr, (int)p[0], p + 2, p + 10, p + 18,
+                                  (int)p[1], stream);
     case YR_OP_REDUCTION_MAX:
       return yr_hip_graph_reduction_max(in[0], out[0], p[0], (int)p[1], p[2], (int)p[3], stream);
     case YR_OP_EWISE: {

@@ -1274,12 +1274,13 @@ class _Lowering:
         (transpile.cc:677-680), mean as the reference's fingerprint executor
         computes it: the sum over the last dim and the iterations divided by
         their count (include/yirage/threadblock/cuda/forloop_accum.h:66-97).
-        False (nothing emitted) for ops it has no form for: rescale
-        accumulators (the fingerprint executor, src/kernel/cuda/
-        customized_kernel.cu:146-150, has no case for them, and
-        forloop_accum.cc:131-150 rejects them), and matmuls whose tiles the
-        MFMA kernel cannot take (n or k not a multiple of 8, k > 1; k = 1 is
-        an outer product, a broadcast multiply)."""
+        Rescale accumulators run as the transpiler's kernel does them
+        (acc = acc * rescale + input each iteration; forloop_accum.h:67-93;
+        the fingerprint executor has no case for them): one step per
+        iteration.  False (nothing emitted) for ops it has no form for:
+        matmuls whose tiles the MFMA kernel cannot take (n or k not a
+        multiple of 8, k > 1; k = 1 is an outer product, a broadcast
+        multiply), and rescale tiles that are not one factor per row."""
         bg = op.attrs["bgraph"]
         gx, gy, gz = bg.grid_dim
         grid = (gx, gy, gz)
@@ -1298,13 +1299,14 @@ class _Lowering:
         def rm(dims):
             return _row_major(tuple(dims))
 
-        def copy(src, dims, ss, ds, dst, off=0):
+        def copy(src, dims, ss, ds, dst, off=0, src_off=0):
             nd = len(dims)
             if nd > 8:
                 raise _NoForm
             pad = 8 - nd
             steps.append((_lib.OP_COPY_ND, [src], dst,
-                          [nd, dt.code, *dims, *([1] * pad), *ss, *([0] * pad), *ds, *([0] * pad), off], "copy_nd"))
+                          [nd, dt.code, *dims, *([1] * pad), *ss, *([0] * pad), *ds, *([0] * pad), off]
+                          + ([src_off] if src_off else []), "copy_nd"))
 
         def new(shape):
             return self.plan.tmp(shape, dt)
@@ -1374,6 +1376,17 @@ class _Lowering:
             ss[1] = 0
             o = new(dims)
             copy(ref, dims, tuple(ss), rm(dims), o)
+            return o, dims
+
+        def iteration(x, i):
+            """Iteration i of a block tensor (a loop-invariant one as is)."""
+            ref, sh = x
+            if sh[1] == 1:
+                return x
+            dims = sh[:1] + (1,) + sh[2:]
+            o = new(dims)
+            src_st = rm(sh)
+            copy(ref, dims, src_st, rm(dims), o, src_off=i * src_st[1])
             return o, dims
 
         def accumulate(x):
@@ -1465,6 +1478,27 @@ class _Lowering:
                         r = unary("mul_scalar", x, 1.0 / (ins[0][1][-1] * R))
                     else:
                         raise _NoForm
+                elif k == "accum_rescale":
+                    # acc = acc * rescale + input every iteration, from zero
+                    # (the transpiler's ForloopAccumRescaleKernel,
+                    # include/yirage/transpiler/runtime/threadblock/
+                    # forloop_accum.h:67-93; the rescale tile broadcasts over
+                    # the input tile's trailing dims); sum: then the last dim
+                    # summed (transpile.cc:714-722)
+                    acc = top.attrs["acc"]
+                    if acc not in ("none", "sum"):
+                        raise _NoForm
+                    x, s = ins
+                    # one factor per row of the tile (the kernel's static
+                    # check, forloop_accum.h:73: rescale size = the tile's
+                    # rows)
+                    if len(s[1]) != len(x[1]) or s[1][-1] != 1 or s[1][2:-1] != x[1][2:-1]:
+                        raise _NoForm
+                    r = iteration(x, 0)
+                    for i in range(1, R):
+                        r = binary("add", binary("mul", r, iteration(s, i)), iteration(x, i))
+                    if acc == "sum":
+                        r = reduce(r, len(r[1]) - 1)
                 else:
                     raise _NoForm
                 vals[id(top.outputs[0])] = r
