@@ -127,7 +127,8 @@ def bench_mugraph_plans(torch) -> dict:
     (customized ops no fused kernel covers): each distinct plan of the LoRA,
     qk-norm GQA, norm-transformer and MHA files (tests/golden/saved_mugraphs),
     one launch per operator against the same plan with its elementwise trees
-    fused (fused elementwise launches)."""
+    fused (fused elementwise launches), and against the plan whose customized
+    ops each run as one tile-program launch (yr_hip_tb_program)."""
     sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
     from yirage_amd import YirageHipError
     from yirage_amd import mugraph_json as MJ
@@ -143,6 +144,7 @@ def bench_mugraph_plans(torch) -> dict:
             try:
                 p0 = g.plan(fuse=True, fuse_elementwise=False)
                 p1 = g.plan(fuse=True)
+                p2 = g.plan(fuse=True, tb_program=True)
             except YirageHipError:
                 continue
             key = tuple(p0.describe())
@@ -156,8 +158,10 @@ def bench_mugraph_plans(torch) -> dict:
                 base = (torch.randn(n, generator=gen) * sd).to(t.dtype.torch)
                 ins.append(torch.as_strided(base, t.dims, t.strides).cuda())
             rec = {"steps": len(p0.steps)}
-            for tag, p in (("one_launch_per_op", p0), ("elementwise_fused", p1)):
+            for tag, p in (("one_launch_per_op", p0), ("elementwise_fused", p1), ("tile_program", p2)):
                 if tag == "elementwise_fused" and p1.describe() == p0.describe():
+                    continue
+                if tag == "tile_program" and "tb_program" not in p2.describe():
                     continue
                 ms = _graph_time(torch, lambda p=p: g._execute(p, ins, None), per_graph=10, replays=5)
                 rec[tag] = dict(us=round(ms * 1e3, 2), launches=len(p.steps))

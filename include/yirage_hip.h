@@ -209,6 +209,23 @@ int yr_hip_graph_reduction_max(const void* x, void* y, int64_t outer, int red, i
 int yr_hip_graph_ewise(const void* const* ins, int n, void* y, int ndim, const int64_t* out_dims,
                        const int64_t* in_dims, int n_prog, const int32_t* prog, const float* imm, int dtype,
                        void* stream);
+/* One customized operator of a kernel graph in one launch: its threadblock
+ * graph (src/threadblock/graph.cc; what the reference's transpiler turns
+ * into generated CUDA, src/transpiler/transpile.cc:370-720) run as a tile
+ * program, one workgroup per block of the grid (gx, gy, gz), every tile in
+ * LDS as fp32, each operator's result rounded to dtype, accumulators fp32
+ * over the forloop iterations.  program: int32 words (format in
+ * csrc/tb_program.hip: header, tiles, inputs cut by input_map / forloop_dim
+ * from dense row-major device tensors, operators, outputs placed by
+ * output_map / forloop_dim); at most 800 words, 8 inputs, 4 outputs and
+ * 160 KiB of tiles.  The program is checked against the launch (every tile
+ * and device access in bounds, operator shapes consistent) before anything
+ * runs; YR_E_INVALID otherwise. */
+int yr_hip_tb_program(const int32_t* program, int n_words, const void* const* ins, int n_in, void* const* outs,
+                      int n_out, int gx, int gy, int gz, int dtype, void* stream);
+/* The host-side check of yr_hip_tb_program alone (no device work): YR_OK
+ * when the program would be accepted for that launch shape. */
+int yr_hip_tb_program_check(const int32_t* program, int n_words, int n_in, int n_out, int gx, int gy, int gz);
 /* y[row] = x[row] * rsqrt(mean(x[row]^2) + eps) over the n trailing
  * elements (rms_norm(X, normalized_shape), src/kernel/rms_norm.cc:71-114). */
 int yr_hip_graph_rmsnorm(const void* x, void* y, int rows, int n, float eps, int dtype, void* stream);
@@ -246,7 +263,9 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
  *   YR_OP_REDUCTION_MAX:  in {x}, out {y}; params {outer, red, inner, dtype}
  *   YR_OP_EWISE:          in {x0..x_{n-1}} (1..8), out {y}; params {ndim, n, n_prog, dtype,
  *                         out_dims[ndim], in_dims[n][ndim], prog[n_prog][5], imm_bits[n_prog][2]}
- *                         (see yr_hip_graph_ewise) */
+ *                         (see yr_hip_graph_ewise)
+ *   YR_OP_TB_PROGRAM:     in {x0..} (1..8), out {y0..} (1..4); params {gx, gy, gz, dtype, program words...}
+ *                         (see yr_hip_tb_program) */
 #define YR_OP_RMSNORM_LINEAR 1
 #define YR_OP_GATED_MLP 2
 #define YR_OP_GQA_PREFILL 3
@@ -262,6 +281,7 @@ int yr_hip_graph_matmul(const void* a, const void* b, void* c, int batch, int m,
 #define YR_OP_COPY_ND 13
 #define YR_OP_REDUCTION_MAX 14
 #define YR_OP_EWISE 15
+#define YR_OP_TB_PROGRAM 16
 int yr_hip_run_fused(int op_kind, int n_in, const void* const* inputs, int n_out, void* const* outputs,
                      int n_params, const int64_t* params, void* workspace, size_t workspace_bytes,
                      void* stream);

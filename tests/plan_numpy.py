@@ -3,7 +3,7 @@ infrastructure: it lets CPU tests check what the planner emits -- tile
 gathers and scatters, elementwise ops, reductions, matmuls -- against a
 float64 restatement of the graph without a GPU).  Values are kept in float64
 and not rounded to 16 bits between steps; the plan must use only the
-generic operators (no fused kernels)."""
+generic operators and tile programs (no fused kernels)."""
 import numpy as np
 
 from yirage_amd import _lib
@@ -30,6 +30,139 @@ def _copy_nd(src, p):
     return so, do
 
 
+def _tb_program(words, srcs, dsts):
+    """The tile program of a customized op (yr_hip_tb_program's word format,
+    yirage_amd/csrc/tb_program.hip), block by block and iteration by
+    iteration, float64, no rounding: a third reading of the threadblock
+    semantics, checked against tests/tb_numpy.py and on the GPU against the
+    kernel.  The LDS is emulated at its byte offsets (one slot per 16 bits,
+    a wide tile's second slot holding a guard), so tiles the program lets
+    share space while both are live corrupt the values (or trip the guard)."""
+    w = list(words)
+    R, nt, ni, no, nout, lds_bytes, dimx, gx, gy, gz = w[2], w[3], w[4], w[5], w[6], w[7], w[8], w[9], w[10], w[11]
+    pos = 12
+    tiles = []  # (halfword offset, dims, wide)
+    for _ in range(nt):
+        off, nd = w[pos], w[pos + 1]
+        tiles.append((off // 2, tuple(w[pos + 2:pos + 2 + nd]), w[pos + 6]))
+        pos += 7
+    ins = [w[pos + 10 * i:pos + 10 * (i + 1)] for i in range(ni)]
+    pos += 10 * ni
+    ops = [w[pos + 9 * i:pos + 9 * (i + 1)] for i in range(no)]
+    pos += 9 * no
+    outs = [w[pos + 11 * i:pos + 11 * (i + 1)] for i in range(nout)]
+    grid = (gx, gy, gz)
+    GUARD = -7.25e300
+    mem = np.full(lds_bytes // 2 + 2, np.nan)
+
+    def get(i):
+        h, dims, wide = tiles[i]
+        n = int(np.prod(dims))
+        if wide:
+            assert (mem[h + 1:h + 2 * n:2] == GUARD).all(), f"wide tile {i} overwritten while live"
+            return mem[h:h + 2 * n:2].reshape(dims).copy()
+        return mem[h:h + n].reshape(dims).copy()
+
+    def put(i, v):
+        h, dims, wide = tiles[i]
+        n = int(np.prod(dims))
+        v = np.broadcast_to(v, dims).reshape(-1)
+        if wide:
+            mem[h:h + 2 * n:2] = v
+            mem[h + 1:h + 2 * n:2] = GUARD
+        else:
+            mem[h:h + n] = v
+
+    def sl(rec, it, b):
+        dims = tiles[rec[0]][1]
+        gd = rec[2:2 + len(dims)]
+        start = [0] * len(dims)
+        for a in range(3):
+            m = rec[6 + a]
+            if m >= 0:
+                start[m] += b[a] * (gd[m] // grid[a])
+        if rec[9] >= 0:
+            start[rec[9]] += it * dims[rec[9]]
+        return gd, tuple(slice(s, s + d) for s, d in zip(start, dims))
+
+    def run(o):
+        kind, out, a = o[0], o[1], get(o[2])
+        if kind == 1:
+            lo, hi = _f32(o[5]), _f32(o[6])
+            r = a * lo if o[4] == 7 else np.clip(a, lo, hi) if o[4] == 4 else _UNARY[o[4]](a)
+        elif kind == 2:
+            r = {0: np.add, 1: np.multiply, 2: np.divide, 3: np.power, 4: np.subtract}[o[4]](a, get(o[3]))
+        elif kind == 3:
+            r = a @ get(o[3])
+        elif kind in (4, 5):
+            dim, to = o[4], (o[5] if kind == 4 else 1)
+            sh = a.shape
+            x = a.reshape(sh[:dim] + (sh[dim] // to, to) + sh[dim + 1:])
+            r = x.sum(dim) if kind == 4 else x.max(dim)
+        elif kind == 6:
+            r = a / np.sqrt((a * a).mean(-1, keepdims=True) + _f32(o[5]))
+        elif kind == 7:
+            r = np.concatenate([a, get(o[3])], o[4])
+        else:
+            raise NotImplementedError(kind)
+        put(out, r.reshape(tiles[out][1]))
+
+    for b in np.ndindex(gx, gy, gz):
+        mem[:] = np.nan
+        for it in range(R):
+            for rec in ins:
+                if it == 0 or rec[9] >= 0:
+                    gd, s = sl(rec, it, b)
+                    put(rec[0], srcs[rec[1]].reshape(gd)[s])
+            if it == 0:
+                for o in ops:
+                    if o[0] == 8:
+                        put(o[8], np.full(tiles[o[8]][1], -np.inf if o[4] == 5 else 0.0))
+            for o in ops:
+                if o[7]:
+                    continue
+                if o[0] == 8:
+                    acc, x = get(o[8]), get(o[2])
+                    if o[4] in (6, 7):
+                        acc = acc * get(o[3]) + x
+                    elif o[4] == 5:
+                        acc = np.maximum(acc, x)
+                    else:
+                        acc = acc + (x * x if o[4] == 3 else x)
+                    put(o[8], acc)
+                else:
+                    run(o)
+            for rec in outs:
+                if rec[9] >= 0 and rec[10] == 0:
+                    gd, s = sl(rec, it, b)
+                    dsts[rec[1]].reshape(gd)[s] = get(rec[0])
+        for o in ops:
+            if o[0] != 8:
+                continue
+            acc, kind = get(o[8]), o[4]
+            n = acc.shape[-1]
+            if kind in (0, 5, 6):
+                r = acc
+            elif kind == 2:
+                r = acc.reshape(acc.shape[:-1] + (n // dimx, dimx)).sum(-2)
+            else:
+                r = acc.sum(-1, keepdims=True)
+                if kind == 4:
+                    r = r / (n * R)
+                elif kind == 3:
+                    r = np.sqrt(r / (n * R))
+            put(o[1], r.reshape(tiles[o[1]][1]))
+        for o in ops:
+            if o[7] and o[0] != 8:
+                run(o)
+        for rec in outs:
+            if rec[9] >= 0 and rec[10] == 0:
+                continue
+            for it in range(R if rec[9] >= 0 else 1):
+                gd, s = sl(rec, it, b)
+                dsts[rec[1]].reshape(gd)[s] = get(rec[0])
+
+
 def run_plan(plan, inputs):
     """inputs: float arrays with each graph input's dims (dense).  Returns
     the graph outputs as float64 arrays of their dims."""
@@ -46,7 +179,9 @@ def run_plan(plan, inputs):
         src = [buf(r) for r in st.ins]
         dst = buf(st.outs[0])
         k = st.kind
-        if k == _lib.OP_COPY_ND:
+        if k == _lib.OP_TB_PROGRAM:
+            _tb_program(p[4:], src, [buf(r) for r in st.outs])
+        elif k == _lib.OP_COPY_ND:
             so, do = _copy_nd(src[0], p)
             dst[do + p[26]] = src[0][so + (p[27] if len(p) > 27 else 0)]
         elif k == _lib.OP_UNARY:

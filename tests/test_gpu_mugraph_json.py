@@ -181,10 +181,16 @@ def test_customized_block_transpose_runs_literally():
     got = g(inputs=[x.cuda()])[0]
     torch.cuda.synchronize()
     assert g._plan.describe() == ["copy_nd", "exp", "copy_nd"]
+    prog = g.plan(fuse=True, tb_program=True)
+    assert prog.describe() == ["tb_program"]
+    got_prog = g._execute(prog, [x.cuda()], None)[0]
+    torch.cuda.synchronize()
     e = torch.exp(x.double())
     ref = e.view(2, 32, 2, 32).permute(2, 1, 0, 3).reshape(64, 64).numpy()  # block (i, j) -> (j, i)
-    err = np.abs(got.float().cpu().numpy() - ref)
-    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+    for out in (got, got_prog):
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+    assert torch.equal(got, got_prog)  # one exp, one rounding either way
 
 
 def test_customized_max_and_concat_run_literally():
@@ -233,6 +239,42 @@ def test_customized_rescale_accumulator_runs_literally():
     for got, ref in ((whole, want), (summed, want_sum)):
         err = np.abs(got.float().cpu().numpy() - ref)
         assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
+
+
+@pytest.mark.parametrize("name,kind,stds", [c for c in CASES if c[0] in ("mha_bs1.json", "ntrans_bs1.json",
+                                                                          "qknorm_gqa_bs1_subset.json")],
+                         ids=["mha", "ntrans", "qknorm"])
+def test_tile_programs_match_the_literal_plans(name, kind, stds):
+    """Every saved candidate whose customized op runs as a tile program
+    (yr_hip_tb_program, one launch) against the same graph run literally
+    (one launch per threadblock op, block tensors in HBM) and against the
+    block-by-block float64 emulation (tests/tb_numpy.py), on the GPU."""
+    from tb_numpy import run_graph
+
+    gs = MJ.load(os.path.join(GOLDEN, name))
+    checked = 0
+    for i, g in enumerate(gs):
+        try:
+            pt = g.plan(fuse=True, tb_program=True)
+            pl = g.plan(fuse=True)
+        except YirageHipError:
+            continue
+        if "tb_program" not in pt.describe():
+            continue
+        print(f"case {name} candidate {i}: {pt.describe()}", flush=True)
+        ins = _inputs(g, stds, seed=i)
+        dev = [x.cuda() for x in ins]
+        a = g._execute(pt, dev, None)[0]
+        b = g._execute(pl, dev, None)[0]
+        torch.cuda.synchronize()
+        ref = run_graph(g, [x.double().numpy() for x in ins])[0]
+        for out, what in ((a, "tile program"), (b, "literal plan")):
+            err = np.abs(out.float().cpu().numpy() - ref)
+            atol = 1e-3 if kind == "attention" else ATOL
+            bad = err > atol + RTOL * np.abs(ref)
+            assert not bad.any(), f"{name} candidate {i} ({what}): {bad.sum()} outside, max err {err.max()}"
+        checked += 1
+    assert checked >= {"mha_bs1.json": 15, "ntrans_bs1.json": 3, "qknorm_gqa_bs1_subset.json": 12}[name]
 
 
 def test_fused_elementwise_bit_identical_to_unfused_steps():

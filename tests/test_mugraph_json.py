@@ -69,22 +69,31 @@ def test_mha_candidates_that_plan():
     """Every saved MHA candidate plans: five as the two-op attention form
     (one fused attention step), one as a whole-tensor expression of generic
     steps, and the ones that split the softmax into partial results per
-    block run their threadblock graphs literally (tile copies in and out)."""
-    plans = [g.plan(fuse=True).describe() for g in _load("mha_bs1.json")]
+    block run each customized op as one tile program (or, without it,
+    literally: tile copies in and out)."""
+    gs = _load("mha_bs1.json")
+    plans = [g.plan(fuse=True, tb_program=True).describe() for g in gs]
     assert len(plans) == 21
     assert plans.count(["attention"]) == 5
     assert plans.count(["matmul", "exp", "matmul", "reduction", "div"]) == 1
-    assert all(p in (["attention"], ["matmul", "exp", "matmul", "reduction", "div"]) or "copy_nd" in p for p in plans)
+    rest = [p for p in plans if p not in (["attention"], ["matmul", "exp", "matmul", "reduction", "div"])]
+    assert len(rest) == 15 and all("tb_program" in p for p in rest)
+    lit = [g.plan(fuse=True, tb_program=False).describe() for g in gs]
+    assert sum("copy_nd" in p for p in lit) == 15
 
 
 def test_norm_transformer_candidates_run_as_generic_steps():
     """benchmark/norm_transformer.py's saved candidates: the six whose
     customized op is one whole-tensor expression run as generic rms_norm /
     elementwise steps; the three that divide by an rms accumulator in a
-    separate kernel-level div run their threadblock graphs literally."""
-    plans = [g.plan(fuse=True, fuse_elementwise=False).describe() for g in _load("ntrans_bs1.json")]
+    separate kernel-level div run their customized op as one tile program
+    (or literally)."""
+    gs = _load("ntrans_bs1.json")
+    plans = [g.plan(fuse=True, fuse_elementwise=False, tb_program=True).describe() for g in gs]
     assert plans.count(["rms_norm", "add", "mul", "add", "rms_norm"]) == 6
-    assert sum("copy_nd" in p for p in plans) == 3
+    assert sum("tb_program" in p for p in plans) == 3
+    lit = [g.plan(fuse=True, fuse_elementwise=False, tb_program=False).describe() for g in gs]
+    assert sum("copy_nd" in p for p in lit) == 3
 
 
 def test_grid_placement_must_match_the_cut():
@@ -102,9 +111,18 @@ def test_grid_placement_must_match_the_cut():
         g.mark_output(O)
         return g
     assert graph((0, 1, -1)).plan(fuse=True).describe() == ["exp"]
-    # run literally instead: tiles gathered, exp, tiles scattered to the
-    # transposed block positions
-    assert graph((1, 0, -1)).plan(fuse=True).describe() == ["copy_nd", "exp", "copy_nd"]
+    # one tile-program launch instead, or literally: tiles gathered, exp,
+    # tiles scattered to the transposed block positions
+    assert graph((1, 0, -1)).plan(fuse=True, tb_program=True).describe() == ["tb_program"]
+    assert graph((1, 0, -1)).plan(fuse=True, tb_program=False).describe() == ["copy_nd", "exp", "copy_nd"]
+    import numpy as np
+    from plan_numpy import run_plan
+
+    x = np.random.default_rng(8).normal(0, 1, (64, 64))
+    want = np.exp(x).reshape(2, 32, 2, 32).transpose(2, 1, 0, 3).reshape(64, 64)
+    for tbp in (True, False):
+        got = run_plan(graph((1, 0, -1)).plan(fuse=True, tb_program=tbp), [x])[0]
+        assert np.allclose(got, want, rtol=1e-12, atol=0)
 
 
 def _renumber(ops):
@@ -215,8 +233,19 @@ def test_forloop_sum_planned_only_over_the_contraction():
         g.mark_output(g.customized([X, W], tb)[0])
         return g
     assert graph(0, 1).plan(fuse=True).describe() == ["linear"]
-    # the tile sums run literally instead
-    assert "copy_nd" in graph(1, -1).plan(fuse=True).describe()
+    # the tile sums run as a tile program instead (or literally)
+    assert graph(1, -1).plan(fuse=True, tb_program=True).describe() == ["tb_program"]
+    assert "copy_nd" in graph(1, -1).plan(fuse=True, tb_program=False).describe()
+    import numpy as np
+    from plan_numpy import run_plan
+    from tb_numpy import run_graph
+
+    rng = np.random.default_rng(9)
+    ins = [rng.normal(0, 1, (8, 256)), rng.normal(0, 1, (256, 256))]
+    ref = run_graph(graph(1, -1), ins)[0]
+    for tbp in (True, False):
+        got = run_plan(graph(1, -1).plan(fuse=True, tb_program=tbp), ins)[0]
+        assert np.abs(got - ref).max() <= 1e-9 * max(1.0, np.abs(ref).max())
 
 
 def test_literal_tile_interpreter_matches_block_emulation():
@@ -239,11 +268,11 @@ def test_literal_tile_interpreter_matches_block_emulation():
         ("mha_bs1.json", mha, 4),
     ]
     attn = (torch.softmax(torch.tensor(mha[0]) @ torch.tensor(mha[1]), -1) @ torch.tensor(mha[2])).numpy()
-    checked = 0
+    checked = programs = 0
     for name, ins, n in cases:
         for g in _load(name)[:n]:
             try:
-                p = g.plan(fuse=True, fuse_elementwise=False)
+                p = g.plan(fuse=True, fuse_elementwise=False, tb_program=False)
             except YirageHipError:
                 continue
             if "copy_nd" not in p.describe():
@@ -252,13 +281,20 @@ def test_literal_tile_interpreter_matches_block_emulation():
             ref = run_graph(g, ins)[0]
             assert np.abs(got - ref).max() <= 1e-9 * max(1.0, np.abs(ref).max())
             # the same plan with its elementwise trees fused: same values
-            pf = g.plan(fuse=True)
+            pf = g.plan(fuse=True, tb_program=False)
             got_f = run_plan(pf, ins)[0]
             assert np.abs(got_f - got).max() <= 1e-12 * max(1.0, np.abs(got).max())
             if name == "mha_bs1.json":
                 assert np.abs(got - attn).max() <= 1e-9
             checked += 1
+            # each such customized op as one tile program
+            pt = g.plan(fuse=True, tb_program=True)
+            if "tb_program" in pt.describe():
+                got_t = run_plan(pt, ins)[0]
+                assert np.abs(got_t - ref).max() <= 1e-9 * max(1.0, np.abs(ref).max())
+                programs += 1
     assert checked >= 3 + 12 + 2
+    print("tile programs checked", programs)
 
 
 def _max_concat_graph():
@@ -282,11 +318,13 @@ def test_literal_max_and_concat():
     from tb_numpy import run_graph
 
     g = _max_concat_graph()
-    p = g.plan(fuse=True)
-    assert "reduction_max" in p.describe() and g.outputs[0][0].dims == (8, 65)
+    assert "reduction_max" in g.plan(fuse=True, tb_program=False).describe() and g.outputs[0][0].dims == (8, 65)
+    assert g.plan(fuse=True, tb_program=True).describe() == ["tb_program"]
     x = np.random.default_rng(1).normal(0, 1, (8, 256))
-    got, ref = run_plan(p, [x])[0], run_graph(g, [x])[0]
-    assert np.abs(got - ref).max() <= 1e-12
+    ref = run_graph(g, [x])[0]
+    for tbp in (True, False):
+        got = run_plan(g.plan(fuse=True, tb_program=tbp), [x])[0]
+        assert np.abs(got - ref).max() <= 1e-12
     # closed form: max over the row of exp(x) per column position, then the row max sums
     xr = x.reshape(8, 4, 64)
     assert np.allclose(ref[:, :64], np.exp(xr).max(1)) and np.allclose(ref[:, 64], xr.max(2).sum(1))
@@ -319,14 +357,14 @@ def test_literal_mean_accumulator():
     from tb_numpy import run_graph
 
     g = _mean_graph()
-    p = g.plan(fuse=True)
     assert g.outputs[0][0].dims == (8, 1)
     x = np.random.default_rng(3).normal(0, 1, (8, 256))
-    got = run_plan(p, [x])
-    assert np.allclose(got[0][:, 0], np.exp(x).mean(1), rtol=1e-12, atol=0)
-    assert np.allclose(got[0], got[1] / 256, rtol=1e-12, atol=0)
     ref = run_graph(g, [x])
-    assert np.abs(got[0] - ref[0]).max() <= 1e-12
+    for tbp in (True, False):
+        got = run_plan(g.plan(fuse=True, tb_program=tbp), [x])
+        assert np.allclose(got[0][:, 0], np.exp(x).mean(1), rtol=1e-12, atol=0)
+        assert np.allclose(got[0], got[1] / 256, rtol=1e-12, atol=0)
+        assert np.abs(got[0] - ref[0]).max() <= 1e-12
 
 
 def _rescale_graph():
@@ -369,14 +407,14 @@ def test_literal_rescale_accumulator():
     from tb_numpy import run_graph
 
     g = _rescale_graph()
-    p = g.plan(fuse=True)
     assert [o[0].dims for o in g.outputs] == [(8, 64), (8, 1)]
     x = np.random.default_rng(6).normal(0, 1, (8, 256))
-    got = run_plan(p, [x])
     want, want_sum = _rescale_closed_form(x)
-    assert np.allclose(got[0], want, rtol=1e-12, atol=0) and np.allclose(got[1], want_sum, rtol=1e-12, atol=0)
     ref = run_graph(g, [x])
-    assert np.abs(got[0] - ref[0]).max() <= 1e-12 and np.abs(got[1] - ref[1]).max() <= 1e-12
+    for tbp in (True, False):
+        got = run_plan(g.plan(fuse=True, tb_program=tbp), [x])
+        assert np.allclose(got[0], want, rtol=1e-12, atol=0) and np.allclose(got[1], want_sum, rtol=1e-12, atol=0)
+        assert np.abs(got[0] - ref[0]).max() <= 1e-12 and np.abs(got[1] - ref[1]).max() <= 1e-12
 
 
 def test_elementwise_trees_fuse_into_one_launch():

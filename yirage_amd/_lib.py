@@ -15,7 +15,7 @@ YR_OK = 0
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_I32, DTYPE_I64 = 940, 941, 950, 955, 965
 W_NK, W_KN = 0, 1
 (OP_RMSNORM_LINEAR, OP_GATED_MLP, OP_GQA_PREFILL, OP_LINEAR, OP_GQA_DECODE, OP_ATTENTION, OP_MATMUL, OP_UNARY,
- OP_BINARY, OP_REDUCTION, OP_RMSNORM, OP_PACK, OP_COPY_ND, OP_REDUCTION_MAX, OP_EWISE) = range(1, 16)
+ OP_BINARY, OP_REDUCTION, OP_RMSNORM, OP_PACK, OP_COPY_ND, OP_REDUCTION_MAX, OP_EWISE, OP_TB_PROGRAM) = range(1, 17)
 
 
 class YirageHipError(RuntimeError):
@@ -75,6 +75,8 @@ SIGNATURES = {
     "yr_hip_graph_reduction_max": (_I, [_P, _P, ctypes.c_int64, _I, ctypes.c_int64, _I, _P]),
     "yr_hip_graph_unary": (_I, [_P, _P, ctypes.c_int64, _I, _F, _F, _I, _P]),
     "yr_hip_graph_ewise": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P]),
+    "yr_hip_tb_program": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _P]),
+    "yr_hip_tb_program_check": (_I, [_P, _I, _I, _I, _I, _I, _I]),
     "yr_hip_graph_binary": (_I, [_P, _P, _P, _I, _P, _P, _I, _I, _P]),
     "yr_hip_graph_reduction": (_I, [_P, _P, ctypes.c_int64, _I, ctypes.c_int64, _I, _P]),
     "yr_hip_graph_rmsnorm": (_I, [_P, _P, _I, _I, _F, _I, _P]),

@@ -39,6 +39,7 @@ bool arity_of(int kind, Arity* a) {
     case YR_OP_COPY_ND: *a = {1, 1, -27}; return true;  // 27, or 28 with a source offset
     case YR_OP_REDUCTION_MAX: *a = {1, 1, 4}; return true;
     case YR_OP_EWISE: *a = {-1, 1, -4}; return true;  // 1..8 inputs
+    case YR_OP_TB_PROGRAM: *a = {-1, -1, -16}; return true;  // 1..8 inputs, 1..4 outputs
     default: return false;
   }
 }
@@ -73,7 +74,7 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, vo
   if ((n_in && !in) || (n_out && !out) || (n_params && !p)) return fail(YR_E_INVALID, "%s: null array", nm);
   Arity ar;
   if (!arity_of(op_kind, &ar)) return fail(YR_E_INVALID, "%s: unknown op kind %d", nm, op_kind);
-  if ((ar.n_in >= 0 ? n_in != ar.n_in : n_in < 1) || n_out != ar.n_out ||
+  if ((ar.n_in >= 0 ? n_in != ar.n_in : n_in < 1) || (ar.n_out >= 0 ? n_out != ar.n_out : n_out < 1) ||
       (ar.n_params >= 0 ? n_params != ar.n_params : n_params < -ar.n_params))
     return fail(YR_E_INVALID, "%s: op kind %d takes %s%d inputs, %d outputs and %s%d params (got %d, %d, %d)", nm,
                 op_kind, ar.n_in < 0 ? ">= " : "", ar.n_in < 0 ? 1 : ar.n_in, ar.n_out, ar.n_params < 0 ? ">= " : "", ar.n_params < 0 ? -ar.n_params : ar.n_params,
@@ -120,6 +121,13 @@ int yr_hip_run_fused(int op_kind, int n_in, const void* const* in, int n_out, vo
                                   (int)p[1], stream);
     case YR_OP_REDUCTION_MAX:
       return yr_hip_graph_reduction_max(in[0], out[0], p[0], (int)p[1], p[2], (int)p[3], stream);
+    case YR_OP_TB_PROGRAM: {
+      int32_t w[800];
+      const int nw = n_params - 4;
+      if (nw > 800) return fail(YR_E_INVALID, "%s: tile program of %d words (<= 800)", nm, nw);
+      for (int i = 0; i < nw; i++) w[i] = (int32_t)p[4 + i];
+      return yr_hip_tb_program(w, nw, in, n_in, out, n_out, (int)p[0], (int)p[1], (int)p[2], (int)p[3], stream);
+    }
     case YR_OP_EWISE: {
       // {ndim, n_in, n_prog, dtype, out_dims[ndim], in_dims[n_in][ndim], prog[n_prog][5], imm_bits[n_prog][2]}
       const int nd = (int)p[0], ni = (int)p[1], np = (int)p[2];

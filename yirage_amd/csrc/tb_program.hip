@@ -1,0 +1,561 @@
+// One launch per customized operator: a threadblock graph (the reference's
+// TB graph of a customized op, src/threadblock/graph.cc; the role its
+// transpiler gives to generated CUDA, src/transpiler/transpile.cc:370-720)
+// run by a small tile program interpreter.  A workgroup is one block of the
+// customized op's grid; every tile lives in LDS as fp32 for the whole launch
+// (no block tensor reaches HBM), inputs are cut from the device tensors by
+// input_map / forloop_dim each iteration, outputs are placed by output_map /
+// forloop_dim.  Tiles are stored in the 16-bit type, so each operator's
+// result is rounded once (as the transpiled element ops do); math is fp32,
+// and accumulators keep fp32 buffers over the iterations, rounded once when
+// they are finalised.  Tiles whose lifetimes do not overlap share LDS.
+//
+// Program words (int32), see yr_hip_tb_program in include/yirage_hip.h:
+//   header  {version, dtype, R, n_tensors, n_inputs, n_ops, n_outputs,
+//            lds_bytes, reduction_dimx, gx, gy, gz}
+//   tensors n_tensors x {lds_byte_offset, ndim, d0, d1, d2, d3, wide}
+//            (wide: an fp32 accumulator buffer; every other tile is 16-bit)
+//   inputs  n_inputs x {tensor, input_index, gdims[4], im[3], forloop_dim}
+//           (device tensors dense row-major, rank = the tile's)
+//   ops     n_ops x {kind, out, in0, in1, a0, a1, a2, phase, acc}
+//   outputs n_outputs x {tensor, output_index, gdims[4], om[3], forloop_dim,
+//            post (1: the tile is final only after the loop)}
+#include <math.h>
+#include <string.h>
+
+#include "yr_common.h"
+
+namespace yr {
+namespace tbp {
+
+constexpr int kVersion = 1;
+constexpr int kHdr = 12, kTw = 7, kIw = 10, kOw = 11, kRw = 9;
+constexpr int kMaxWords = 800, kMaxIn = 8, kMaxOut = 4, kMaxDim = 4;
+constexpr int kThreads = 256;
+constexpr int kMaxLdsBytes = 160 * 1024;
+
+enum OpKind { K_UNARY = 1, K_BINARY = 2, K_MATMUL = 3, K_REDUCE = 4, K_REDMAX = 5, K_RMSNORM = 6, K_CONCAT = 7,
+              K_ACC = 8 };
+enum UnaryKind { U_EXP = 0, U_SILU = 1, U_GELU = 2, U_RELU = 3, U_CLAMP = 4, U_SQRT = 5, U_SQUARE = 6, U_SCALE = 7 };
+enum BinaryKind { B_ADD = 0, B_MUL = 1, B_DIV = 2, B_POW = 3, B_SUB = 4 };
+enum AccKind { A_NONE = 0, A_SUM = 1, A_TODIMX = 2, A_RMS = 3, A_MEAN = 4, A_MAX = 5, A_RESCALE = 6,
+               A_RESCALE_SUM = 7 };
+
+struct Args {
+  const uint16_t* in[kMaxIn];
+  uint16_t* out[kMaxOut];
+  int32_t w[kMaxWords];
+};
+
+struct Tile {
+  int off, nd, d[kMaxDim], n, wide;  // off in bytes; wide: fp32 (accumulator buffers), else 16-bit
+};
+
+__device__ __forceinline__ Tile tile_of(const int32_t* w, int t) {
+  const int32_t* p = w + kHdr + t * kTw;
+  Tile x;
+  x.off = p[0];
+  x.nd = p[1];
+  x.wide = p[6];
+  x.n = 1;
+#pragma unroll
+  for (int i = 0; i < kMaxDim; i++) {
+    x.d[i] = i < x.nd ? p[2 + i] : 1;
+    x.n *= x.d[i];
+  }
+  return x;
+}
+
+// element i of a tile as fp32 / stored (a 16-bit tile rounds: one rounding
+// per operator)
+template <int DT>
+__device__ __forceinline__ float tld(const char* lds, const Tile& t, int i) {
+  return t.wide ? reinterpret_cast<const float*>(lds + t.off)[i]
+                : ld_elem<DT>(reinterpret_cast<const uint16_t*>(lds + t.off)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void tst(char* lds, const Tile& t, int i, float v) {
+  if (t.wide) reinterpret_cast<float*>(lds + t.off)[i] = v;
+  else reinterpret_cast<uint16_t*>(lds + t.off)[i] = (uint16_t)st_elem<DT>(v);
+}
+
+// coordinates of element e of a row-major tile
+__device__ __forceinline__ void coords(const Tile& t, int e, int (&c)[kMaxDim]) {
+#pragma unroll
+  for (int i = kMaxDim - 1; i >= 0; i--) {
+    if (i < t.nd) {
+      c[i] = e % t.d[i];
+      e /= t.d[i];
+    } else {
+      c[i] = 0;
+    }
+  }
+}
+
+// element of tile t at coordinates c (dims of size 1 broadcast)
+__device__ __forceinline__ int index_bcast(const Tile& t, const int (&c)[kMaxDim]) {
+  int idx = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxDim; i++)
+    if (i < t.nd) idx = idx * t.d[i] + (t.d[i] == 1 ? 0 : c[i]);
+  return idx;
+}
+
+__device__ __forceinline__ float unary(int kind, float a, float lo, float hi) {
+  switch (kind) {
+    case U_EXP: return expf(a);
+    case U_SILU: return a / (1.f + expf(-a));
+    case U_GELU: return 0.5f * a * (1.f + erff(a * 0.70710678118654752f));
+    case U_RELU: return fmaxf(a, 0.f);
+    case U_CLAMP: return fminf(fmaxf(a, lo), hi);
+    case U_SQRT: return sqrtf(a);
+    case U_SCALE: return a * lo;
+    default: return a * a;
+  }
+}
+__device__ __forceinline__ float binary(int kind, float x, float y) {
+  switch (kind) {
+    case B_ADD: return x + y;
+    case B_MUL: return x * y;
+    case B_DIV: return x / y;
+    case B_SUB: return x - y;
+    default: return powf(x, y);
+  }
+}
+
+// start of this block's (iteration's) tile along each dim of a device tensor
+__device__ __forceinline__ void tile_start(const int32_t* r, const Tile& t, int it, int (&s)[kMaxDim]) {
+  const int gd[kMaxDim] = {r[2], r[3], r[4], r[5]};
+  const int b[3] = {(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int g[3] = {(int)gridDim.x, (int)gridDim.y, (int)gridDim.z};
+#pragma unroll
+  for (int i = 0; i < kMaxDim; i++) s[i] = 0;
+#pragma unroll
+  for (int a = 0; a < 3; a++) {
+    const int m = r[6 + a];
+    if (m >= 0) s[m] += b[a] * (gd[m] / g[a]);
+  }
+  const int fd = r[9];
+  if (fd >= 0) s[fd] += it * t.d[fd];
+}
+
+// device element offset of tile element e
+__device__ __forceinline__ long long dev_index(const int32_t* r, const Tile& t, const int (&s)[kMaxDim], int e) {
+  int c[kMaxDim];
+  coords(t, e, c);
+  long long g = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxDim; i++)
+    if (i < t.nd) g = g * r[2 + i] + (s[i] + c[i]);
+  return g;
+}
+
+template <int DT>
+__device__ void load_input(const Args& A, const int32_t* w, const int32_t* r, int it, char* lds) {
+  const Tile t = tile_of(w, r[0]);
+  const uint16_t* src = A.in[r[1]];
+  uint16_t* dst = reinterpret_cast<uint16_t*>(lds + t.off);  // input tiles are 16-bit
+  int s[kMaxDim];
+  tile_start(r, t, it, s);
+  for (int e = threadIdx.x; e < t.n; e += kThreads) dst[e] = src[dev_index(r, t, s, e)];
+}
+
+template <int DT>
+__device__ void store_output(const Args& A, const int32_t* w, const int32_t* r, int it, const char* lds) {
+  const Tile t = tile_of(w, r[0]);
+  uint16_t* dst = A.out[r[1]];
+  int s[kMaxDim];
+  tile_start(r, t, it, s);
+  for (int e = threadIdx.x; e < t.n; e += kThreads) dst[dev_index(r, t, s, e)] = (uint16_t)st_elem<DT>(tld<DT>(lds, t, e));
+}
+
+__device__ __forceinline__ float fbits(int32_t b) { return __int_as_float(b); }
+
+// one operator over its output tile, all threads; fp32 math
+template <int DT>
+__device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
+  const int kind = o[0];
+  const Tile to = tile_of(w, o[1]);
+  const Tile ta = tile_of(w, o[2]);
+  switch (kind) {
+    case K_UNARY: {
+      const float lo = fbits(o[5]), hi = fbits(o[6]);
+      for (int e = threadIdx.x; e < to.n; e += kThreads) tst<DT>(lds, to, e, unary(o[4], tld<DT>(lds, ta, e), lo, hi));
+      break;
+    }
+    case K_BINARY: {
+      const Tile tb = tile_of(w, o[3]);
+      for (int e = threadIdx.x; e < to.n; e += kThreads) {
+        int c[kMaxDim];
+        coords(to, e, c);
+        tst<DT>(lds, to, e, binary(o[4], tld<DT>(lds, ta, index_bcast(ta, c)), tld<DT>(lds, tb, index_bcast(tb, c))));
+      }
+      break;
+    }
+    case K_MATMUL: {  // a [.., M, K] x b [.., K, N]
+      const Tile tb = tile_of(w, o[3]);
+      const int M = ta.d[ta.nd - 2], K = ta.d[ta.nd - 1], N = tb.d[tb.nd - 1];
+      for (int e = threadIdx.x; e < to.n; e += kThreads) {
+        const int n = e % N, m = (e / N) % M, bt = e / (M * N);
+        const int ar = (bt * M + m) * K, bc = bt * K * N + n;
+        float s = 0.f;
+        for (int k = 0; k < K; k++) s = fmaf(tld<DT>(lds, ta, ar + k), tld<DT>(lds, tb, bc + k * N), s);
+        tst<DT>(lds, to, e, s);
+      }
+      break;
+    }
+    case K_REDUCE:    // sum over dim a0 down to a1 elements (element j adds j, j + a1, ...)
+    case K_REDMAX: {  // max over dim a0
+      const int dim = o[4], to_n = kind == K_REDUCE ? o[5] : 1;
+      const int L = ta.d[dim];
+      int inner = 1;
+      for (int i = dim + 1; i < ta.nd; i++) inner *= ta.d[i];
+      for (int e = threadIdx.x; e < to.n; e += kThreads) {
+        const int in_ = e % inner, j = (e / inner) % to_n, ou = e / (inner * to_n);
+        const int base = ou * L * inner + in_;
+        float s = kind == K_REDMAX ? -INFINITY : 0.f;
+        for (int r = j; r < L; r += to_n) {
+          const float v = tld<DT>(lds, ta, base + r * inner);
+          s = kind == K_REDMAX ? fmaxf(s, v) : s + v;
+        }
+        tst<DT>(lds, to, e, s);
+      }
+      break;
+    }
+    case K_RMSNORM: {  // rows of the last dim: x * rsqrt(mean(x^2) + eps)
+      const int n = ta.d[ta.nd - 1];
+      const float eps = fbits(o[5]);
+      for (int e = threadIdx.x; e < to.n; e += kThreads) {
+        const int row = (e / n) * n;
+        float ss = 0.f;
+        for (int i = 0; i < n; i++) {
+          const float v = tld<DT>(lds, ta, row + i);
+          ss += v * v;
+        }
+        tst<DT>(lds, to, e, tld<DT>(lds, ta, e) * rsqrtf(ss / (float)n + eps));
+      }
+      break;
+    }
+    case K_CONCAT: {  // a then b along dim a0
+      const Tile tb = tile_of(w, o[3]);
+      const int dim = o[4];
+      for (int e = threadIdx.x; e < to.n; e += kThreads) {
+        int c[kMaxDim];
+        coords(to, e, c);
+        const bool first = c[dim] < ta.d[dim];
+        if (!first) c[dim] -= ta.d[dim];
+        const Tile& ts = first ? ta : tb;
+        int idx = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxDim; i++)
+          if (i < ts.nd) idx = idx * ts.d[i] + c[i];
+        tst<DT>(lds, to, e, tld<DT>(lds, ts, idx));
+      }
+      break;
+    }
+    default:
+      break;
+  }
+}
+
+// accumulator update (per iteration): the fp32 buffer, the input tile's shape
+template <int DT>
+__device__ void acc_update(const int32_t* w, const int32_t* o, char* lds) {
+  const Tile tx = tile_of(w, o[2]), ta = tile_of(w, o[8]);
+  float* acc = reinterpret_cast<float*>(lds + ta.off);
+  const int kind = o[4];
+  if (kind == A_RESCALE || kind == A_RESCALE_SUM) {
+    const Tile tr = tile_of(w, o[3]);
+    for (int e = threadIdx.x; e < tx.n; e += kThreads) {
+      int c[kMaxDim];
+      coords(tx, e, c);
+      acc[e] = acc[e] * tld<DT>(lds, tr, index_bcast(tr, c)) + tld<DT>(lds, tx, e);
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < tx.n; e += kThreads) {
+    const float v = tld<DT>(lds, tx, e);
+    if (kind == A_MAX) acc[e] = fmaxf(acc[e], v);
+    else acc[e] += kind == A_RMS ? v * v : v;
+  }
+}
+
+__device__ void acc_init(const int32_t* w, const int32_t* o, char* lds) {
+  const Tile ta = tile_of(w, o[8]);
+  float* acc = reinterpret_cast<float*>(lds + ta.off);
+  const float v = o[4] == A_MAX ? -INFINITY : 0.f;
+  for (int e = threadIdx.x; e < ta.n; e += kThreads) acc[e] = v;
+}
+
+// after the loop: the accumulator's value into its (16-bit) output tile
+template <int DT>
+__device__ void acc_final(const int32_t* w, const int32_t* o, char* lds, int R, int dimx) {
+  const Tile tx = tile_of(w, o[2]), ta = tile_of(w, o[8]), to = tile_of(w, o[1]);
+  const float* acc = reinterpret_cast<const float*>(lds + ta.off);
+  const int kind = o[4];
+  const int n = tx.d[tx.nd - 1];
+  for (int e = threadIdx.x; e < to.n; e += kThreads) {
+    float v;
+    if (kind == A_NONE || kind == A_MAX || kind == A_RESCALE) {
+      v = acc[e];
+    } else {
+      const int to_n = kind == A_TODIMX ? dimx : 1;
+      const int j = e % to_n, row = e / to_n;
+      const float* p = acc + (size_t)row * n;
+      float s = 0.f;
+      for (int i = j; i < n; i += to_n) s += p[i];
+      if (kind == A_MEAN) s /= (float)(n * R);
+      else if (kind == A_RMS) s = sqrtf(s / (float)(n * R));
+      v = s;
+    }
+    tst<DT>(lds, to, e, v);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void tb_program_kernel(Args A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int32_t* w = A.w;
+  const int R = w[2], nt = w[3], ni = w[4], no = w[5], nout = w[6], dimx = w[8];
+  const int32_t* ins = w + kHdr + nt * kTw;
+  const int32_t* ops = ins + ni * kIw;
+  const int32_t* outs = ops + no * kRw;
+  for (int it = 0; it < R; it++) {
+    for (int i = 0; i < ni; i++)
+      if (it == 0 || ins[i * kIw + 9] >= 0) load_input<DT>(A, w, ins + i * kIw, it, lds);
+    if (it == 0) {  // (accumulator buffers may reuse tiles that are dead by now: after the loads)
+      __syncthreads();
+      for (int i = 0; i < no; i++)
+        if (ops[i * kRw] == K_ACC) acc_init(w, ops + i * kRw, lds);
+    }
+    __syncthreads();
+    for (int i = 0; i < no; i++) {
+      const int32_t* o = ops + i * kRw;
+      if (o[7] != 0) continue;  // after the loop
+      if (o[0] == K_ACC) acc_update<DT>(w, o, lds);
+      else exec_op<DT>(w, o, lds);
+      __syncthreads();
+    }
+    // outputs placed per iteration
+    for (int i = 0; i < nout; i++) {
+      const int32_t* r = outs + i * kOw;
+      if (r[9] >= 0 && r[10] == 0) store_output<DT>(A, w, r, it, lds);
+    }
+    __syncthreads();  // the tiles are read before the next iteration's loads replace them
+  }
+  for (int i = 0; i < no; i++)
+    if (ops[i * kRw] == K_ACC) acc_final<DT>(w, ops + i * kRw, lds, R, dimx);
+  __syncthreads();
+  for (int i = 0; i < no; i++) {
+    const int32_t* o = ops + i * kRw;
+    if (o[7] == 0) continue;
+    exec_op<DT>(w, o, lds);
+    __syncthreads();
+  }
+  for (int i = 0; i < nout; i++) {
+    const int32_t* r = outs + i * kOw;
+    if (r[9] >= 0 && r[10] == 0) continue;  // stored in the loop
+    // a final tile placed along the forloop dim goes to every iteration's slot
+    const int reps = r[9] >= 0 ? R : 1;
+    for (int it = 0; it < reps; it++) store_output<DT>(A, w, r, it, lds);
+  }
+}
+
+// Host-side check of a program against the launch: every tile inside the
+// LDS budget, every tensor reference, every op's shapes and every device
+// tile access in bounds, so the kernel never indexes outside what it was
+// given.
+static int check_program(const int32_t* w, int nw, int n_in, int n_out, int gx, int gy, int gz, const char* nm) {
+  auto bad = [&](const char* what) { return fail(YR_E_INVALID, "%s: bad program (%s)", nm, what); };
+  if (nw < kHdr || nw > kMaxWords) return bad("size");
+  const int R = w[2], nt = w[3], ni = w[4], no = w[5], nout = w[6], lf = w[7], dimx = w[8];
+  if (w[0] != kVersion) return bad("version");
+  if (R < 1 || nt < 1 || ni < 1 || ni > kMaxIn || no < 0 || nout < 1 || nout > kMaxOut) return bad("counts");
+  if (kHdr + nt * kTw + ni * kIw + no * kRw + nout * kOw != nw) return bad("length");
+  if (lf < 1 || lf > kMaxLdsBytes || dimx < 1) return bad("lds / dimx");
+  if (ni != n_in || nout != n_out) return bad("input / output count");
+  if (w[9] != gx || w[10] != gy || w[11] != gz) return bad("grid");
+  Tile T[kMaxWords / kTw];
+  for (int t = 0; t < nt; t++) {
+    const int32_t* p = w + kHdr + t * kTw;
+    Tile& x = T[t];
+    x.off = p[0];
+    x.nd = p[1];
+    x.wide = p[6];
+    if (x.nd < 1 || x.nd > kMaxDim || (x.wide != 0 && x.wide != 1)) return bad("tile rank");
+    long long n = 1;
+    for (int i = 0; i < kMaxDim; i++) {
+      x.d[i] = i < x.nd ? p[2 + i] : 1;
+      if (x.d[i] < 1) return bad("tile dim");
+      n *= x.d[i];
+    }
+    const int es = x.wide ? 4 : 2;
+    if (x.off < 0 || x.off % es || x.off + n * es > lf) return bad("tile outside the LDS budget");
+    x.n = (int)n;
+  }
+  const int g[3] = {gx, gy, gz};
+  auto check_io = [&](const int32_t* r, int count, bool is_in) -> bool {
+    if (r[0] < 0 || r[0] >= nt || r[1] < 0 || r[1] >= count) return false;
+    const Tile& x = T[r[0]];
+    if (x.wide) return false;
+    const int fd = r[9];
+    if (fd >= x.nd || fd < -1) return false;
+    for (int d = 0; d < x.nd; d++) {
+      const int gd = r[2 + d];
+      if (gd < 1) return false;
+      long long block = gd;
+      int cuts = 0;
+      for (int a = 0; a < 3; a++) {
+        const int m = r[6 + a];
+        if (m < -1 || m >= x.nd) return false;
+        if (m == d) {
+          if (gd % g[a]) return false;
+          block = gd / g[a];
+          cuts++;
+        }
+      }
+      if (cuts > 1) return false;
+      const long long span = (long long)x.d[d] * (d == fd ? R : 1);
+      if (span > block) return false;
+    }
+    (void)is_in;
+    return true;
+  };
+  const int32_t* ins = w + kHdr + nt * kTw;
+  for (int i = 0; i < ni; i++)
+    if (!check_io(ins + i * kIw, n_in, true)) return bad("input tile outside its tensor");
+  const int32_t* ops = ins + ni * kIw;
+  auto same = [&](const Tile& a, const Tile& b) {
+    if (a.nd != b.nd) return false;
+    for (int i = 0; i < a.nd; i++)
+      if (a.d[i] != b.d[i]) return false;
+    return true;
+  };
+  for (int i = 0; i < no; i++) {
+    const int32_t* o = ops + i * kRw;
+    const int k = o[0];
+    auto tid_ok = [&](int t) { return t >= 0 && t < nt; };
+    if (!tid_ok(o[1]) || !tid_ok(o[2]) || (o[7] != 0 && o[7] != 1)) return bad("op tensor");
+    const Tile &to = T[o[1]], &ta = T[o[2]];
+    if (to.wide || ta.wide || (k != K_UNARY && k != K_RMSNORM && k != K_REDUCE && k != K_REDMAX && o[3] >= 0 &&
+                               tid_ok(o[3]) && T[o[3]].wide))
+      return bad("16-bit operator tiles");
+    switch (k) {
+      case K_UNARY:
+        if (!same(to, ta) || o[4] < 0 || o[4] > U_SCALE) return bad("unary");
+        break;
+      case K_BINARY: {
+        if (!tid_ok(o[3]) || o[4] < 0 || o[4] > B_SUB) return bad("binary");
+        const Tile& tb = T[o[3]];
+        if (ta.nd != to.nd || tb.nd != to.nd) return bad("binary rank");
+        for (int d = 0; d < to.nd; d++)
+          if ((ta.d[d] != to.d[d] && ta.d[d] != 1) || (tb.d[d] != to.d[d] && tb.d[d] != 1) ||
+              to.d[d] != (ta.d[d] > tb.d[d] ? ta.d[d] : tb.d[d]))
+            return bad("binary dims");
+        break;
+      }
+      case K_MATMUL: {
+        if (!tid_ok(o[3])) return bad("matmul");
+        const Tile& tb = T[o[3]];
+        if (ta.nd < 2 || tb.nd != ta.nd || to.nd != ta.nd) return bad("matmul rank");
+        for (int d = 0; d < ta.nd - 2; d++)
+          if (ta.d[d] != tb.d[d] || to.d[d] != ta.d[d]) return bad("matmul batch");
+        if (tb.d[ta.nd - 2] != ta.d[ta.nd - 1] || to.d[ta.nd - 2] != ta.d[ta.nd - 2] || to.d[ta.nd - 1] != tb.d[ta.nd - 1])
+          return bad("matmul dims");
+        break;
+      }
+      case K_REDUCE:
+      case K_REDMAX: {
+        const int dim = o[4], to_n = k == K_REDUCE ? o[5] : 1;
+        if (dim < 0 || dim >= ta.nd || to.nd != ta.nd || to_n < 1 || ta.d[dim] % to_n) return bad("reduction");
+        for (int d = 0; d < ta.nd; d++)
+          if (to.d[d] != (d == dim ? to_n : ta.d[d])) return bad("reduction dims");
+        break;
+      }
+      case K_RMSNORM:
+        if (!same(to, ta)) return bad("rms_norm");
+        break;
+      case K_CONCAT: {
+        if (!tid_ok(o[3])) return bad("concat");
+        const Tile& tb = T[o[3]];
+        const int dim = o[4];
+        if (dim < 0 || dim >= to.nd || ta.nd != to.nd || tb.nd != to.nd) return bad("concat rank");
+        for (int d = 0; d < to.nd; d++)
+          if (to.d[d] != (d == dim ? ta.d[d] + tb.d[d] : ta.d[d]) || (d != dim && tb.d[d] != ta.d[d]))
+            return bad("concat dims");
+        break;
+      }
+      case K_ACC: {
+        if (!tid_ok(o[8]) || o[7] != 0 || o[4] < A_NONE || o[4] > A_RESCALE_SUM) return bad("accumulator");
+        const Tile& tc = T[o[8]];
+        if (!same(tc, ta) || !tc.wide) return bad("accumulator buffer");
+        const int n = ta.d[ta.nd - 1];
+        for (int d = 0; d < ta.nd - 1; d++)
+          if (to.nd != ta.nd || to.d[d] != ta.d[d]) return bad("accumulator output");
+        const int kind = o[4];
+        const int last = kind == A_NONE || kind == A_MAX || kind == A_RESCALE ? n : kind == A_TODIMX ? dimx : 1;
+        if (to.d[ta.nd - 1] != last || (kind == A_TODIMX && n % dimx)) return bad("accumulator output dims");
+        if (kind == A_RESCALE || kind == A_RESCALE_SUM) {
+          if (!tid_ok(o[3])) return bad("rescale");
+          const Tile& tr = T[o[3]];
+          if (tr.nd != ta.nd || tr.d[ta.nd - 1] != 1) return bad("rescale dims");
+          for (int d = 0; d < ta.nd - 1; d++)
+            if (tr.d[d] != ta.d[d]) return bad("rescale dims");
+        }
+        break;
+      }
+      default:
+        return bad("op kind");
+    }
+  }
+  const int32_t* outs = ops + no * kRw;
+  for (int i = 0; i < nout; i++)
+    if (!check_io(outs + i * kOw, n_out, false) || (outs[i * kOw + 10] != 0 && outs[i * kOw + 10] != 1))
+      return bad("output tile outside its tensor");
+  return YR_OK;
+}
+
+}  // namespace tbp
+}  // namespace yr
+
+extern "C" int yr_hip_tb_program(const int32_t* program, int n_words, const void* const* ins, int n_in,
+                                 void* const* outs, int n_out, int gx, int gy, int gz, int dtype, void* stream) {
+  using namespace yr;
+  using namespace yr::tbp;
+  const char* nm = "yr_hip_tb_program";
+  if (!program || !ins || !outs) return fail(YR_E_INVALID, "%s: null pointer", nm);
+  if (dtype != YR_DTYPE_F16 && dtype != YR_DTYPE_BF16) return fail(YR_E_INVALID, "%s: dtype", nm);
+  if (gx < 1 || gy < 1 || gz < 1 || gy > 65535 || gz > 65535) return fail(YR_E_INVALID, "%s: grid", nm);
+  if (n_in < 1 || n_in > kMaxIn || n_out < 1 || n_out > kMaxOut) return fail(YR_E_INVALID, "%s: %d inputs, %d outputs", nm, n_in, n_out);
+  for (int i = 0; i < n_in; i++)
+    if (!ins[i]) return fail(YR_E_INVALID, "%s: null input %d", nm, i);
+  for (int i = 0; i < n_out; i++)
+    if (!outs[i]) return fail(YR_E_INVALID, "%s: null output %d", nm, i);
+  int rc = check_program(program, n_words, n_in, n_out, gx, gy, gz, nm);
+  if (rc != YR_OK) return rc;
+  if (program[1] != dtype) return fail(YR_E_INVALID, "%s: program dtype", nm);
+  Args a;
+  memset(&a, 0, sizeof(a));
+  for (int i = 0; i < n_in; i++) a.in[i] = (const uint16_t*)ins[i];
+  for (int i = 0; i < n_out; i++) a.out[i] = (uint16_t*)outs[i];
+  memcpy(a.w, program, sizeof(int32_t) * n_words);
+  const size_t lds = (size_t)program[7];
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(gx, gy, gz);
+  // more than 64 KiB of dynamic LDS needs the function's limit raised
+  const void* fn = dtype == YR_DTYPE_BF16 ? (const void*)tb_program_kernel<DT_BF16> : (const void*)tb_program_kernel<DT_F16>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(YR_E_HIP, "%s: LDS limit %zu bytes: %s", nm, lds, hipGetErrorString(e));
+  }
+  if (dtype == YR_DTYPE_BF16) hipLaunchKernelGGL(tb_program_kernel<DT_BF16>, grid, dim3(kThreads), lds, st, a);
+  else hipLaunchKernelGGL(tb_program_kernel<DT_F16>, grid, dim3(kThreads), lds, st, a);
+  YR_CHECK_LAUNCH(nm);
+  return YR_OK;
+}
+
+extern "C" int yr_hip_tb_program_check(const int32_t* program, int n_words, int n_in, int n_out, int gx, int gy,
+                                       int gz) {
+  if (!program) return yr::fail(YR_E_INVALID, "yr_hip_tb_program_check: null program");
+  return yr::tbp::check_program(program, n_words, n_in, n_out, gx, gy, gz, "yr_hip_tb_program_check");
+}

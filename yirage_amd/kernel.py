@@ -491,11 +491,17 @@ class KNGraph:
         return self._error_message
 
     # ------------------------------------------------------------ planning
-    def plan(self, fuse: bool = True, fuse_elementwise: bool = True) -> Plan:
+    def plan(self, fuse: bool = True, fuse_elementwise: bool = True, tb_program: bool = False) -> Plan:
         """Lower the graph to yr_hip_run_fused steps (host only, no GPU).
         fuse: the fused-operator patterns; fuse_elementwise: single-consumer
-        trees of elementwise steps become one fused elementwise launch."""
-        plan = _Lowering(self, fuse).run()
+        trees of elementwise steps become one fused elementwise launch;
+        tb_program: customized ops that are no whole-tensor expression run as
+        one tile-program launch each (else tile by tile, one launch per
+        threadblock op).  Off by default: on the saved candidates the tile
+        programs are correct but slower than the literal plans (the customized
+        ops' grids are 8-64 blocks, one workgroup each, against launches that
+        spread each operator over the whole chip)."""
+        plan = _Lowering(self, fuse, tb_program).run()
         if fuse_elementwise:
             _fuse_elementwise(plan)
         return plan
@@ -689,8 +695,8 @@ class _Lowering:
     """Pattern matching (from the outputs backwards) and emission of steps
     (in graph order)."""
 
-    def __init__(self, g: KNGraph, fuse: bool):
-        self.g, self.fuse = g, fuse
+    def __init__(self, g: KNGraph, fuse: bool, tb_program: bool = False):
+        self.g, self.fuse, self.tb_program = g, fuse, tb_program
         self.plan = Plan("fused" if fuse else "generic")
         self.ref: dict = {}        # tensor guid -> ref
         self.consumers: dict = {}  # tensor guid -> [op]
@@ -1161,7 +1167,8 @@ class _Lowering:
             self.emit(_lib.OP_RMSNORM, [self.dense(A)], [self.out_ref(out)],
                       [rows // n, n, A.dtype.code, _fbits(_EPS)], "rms_norm")
         elif k == "customized":
-            if not self._lower_customized(op) and not self._interpret_customized(op):
+            if not self._lower_customized(op) and not self._program_customized(op) and \
+                    not self._interpret_customized(op):
                 raise YirageHipError("hip backend: this customized threadblock graph matches no fused kernel "
                                      "(RMSNorm+linear, gated MLP, GQA, linear) and is not an expression over "
                                      "whole tensors the generic operators can run")
@@ -1256,6 +1263,172 @@ class _Lowering:
         for out, ref, written in results:
             if not written:
                 self.ref[out.guid] = ref
+        return True
+
+    def _program_customized(self, op: KNOp) -> bool:
+        """A customized op as one launch: its threadblock graph compiled to a
+        tile program (yr_hip_tb_program; the role of the reference's
+        generated CUDA, src/transpiler/transpile.cc:370-720).  One workgroup
+        per block, every tile in LDS (16-bit, fp32 accumulator buffers;
+        tiles whose lifetimes do not overlap share space), inputs cut and
+        outputs placed as _interpret_customized reads the maps, accumulators
+        as there (none / sum / sum_todimx / rms / mean / max / rescale).
+        False (nothing emitted) when the lowering was asked for without it,
+        a tile has more than 4 dims, the tiles need more than 160 KiB of LDS
+        or the program more than 800 words, or an op has no tile form; the
+        literal reading then runs."""
+        if not self.tb_program:
+            return False
+        bg = op.attrs["bgraph"]
+        gx, gy, gz = bg.grid_dim
+        R = bg.forloop_range
+        ins, outs = op.inputs, op.outputs
+        dt = ins[0].dtype
+        if dt not in (float16, bfloat16) or any(t.dtype != dt for t in ins) or any(o.dtype != dt for o in outs):
+            return False
+        if len(ins) > 8 or len(outs) > 4 or len(bg.outputs) != len(outs):
+            return False
+        tiles = []  # [dims, wide, first time, last time]
+        tid = {}
+        END = 1 << 30
+
+        def tile(dims, wide=False, at=0):
+            dims = tuple(int(d) for d in dims)
+            if not 1 <= len(dims) <= 4:
+                raise _NoForm
+            tiles.append([dims, wide, at, at])
+            return len(tiles) - 1
+
+        def use(i, at):
+            tiles[i][3] = max(tiles[i][3], at)
+
+        def pad4(ds, fill):
+            return list(ds) + [fill] * (4 - len(ds))
+
+        UN = {"exp": 0, "silu": 1, "gelu": 2, "relu": 3, "sqrt": 5, "square": 6}
+        BI = {"add": 0, "mul": 1, "div": 2, "pow": 3, "sub": 4}
+        ACC = {"none": 0, "sum": 1, "sum_todimx": 2, "rms": 3, "mean": 4}
+        body = [top for top in bg.ops if top.kind != "input"]
+        loop = [top for top in body if not (top.outputs[0].after_accum and
+                                            top.kind not in ("accum", "accum_max", "accum_rescale"))]
+        post = [top for top in body if top not in loop]
+        # timeline: 0 loads; 1..n loop ops; n + 1 per-iteration stores; n + 2
+        # accumulators finalised; then the ops after the loop; END final stores
+        n_loop = len(loop)
+        t_fin = n_loop + 2
+        when = {id(top): (1 + i if top in loop else t_fin + 1 + post.index(top)) for i, top in enumerate(body)}
+        loop_end = t_fin
+        try:
+            in_recs = []
+            for dten, st in bg.inputs:
+                k = next(i for i, t_ in enumerate(ins) if t_ is dten)
+                if len(st.dims) != len(dten.dims):
+                    raise _NoForm
+                i = tid[id(st)] = tile(st.dims)
+                fd = st.op.attrs["forloop_dim"]
+                if R > 1 and fd < 0:
+                    use(i, loop_end)  # loaded once, read by every iteration
+                im = tuple(st.op.attrs["input_map"]) + (-1,) * 3
+                in_recs.append([i, k, *pad4(dten.dims, 1), *im[:3], fd])
+            op_recs = []
+            for top in body:
+                kd, o, at = top.kind, top.outputs[0], when[id(top)]
+                a = [tid[id(x)] for x in top.inputs]
+                for x in a:
+                    use(x, at)
+                phase = 0 if top in loop else 1
+                z = 0
+                if kd in UN:
+                    rec = [1, 0, a[0], -1, UN[kd], z, z]
+                elif kd == "clamp":
+                    rec = [1, 0, a[0], -1, 4, _fbits(top.attrs["min_val"]), _fbits(top.attrs["max_val"])]
+                elif kd == "mul_scalar":
+                    rec = [1, 0, a[0], -1, 7, _fbits(top.attrs["scalar"]), z]
+                elif kd in BI:
+                    rec = [2, 0, a[0], a[1], BI[kd], z, z]
+                elif kd == "matmul":
+                    rec = [3, 0, a[0], a[1], z, z, z]
+                elif kd in ("reduction", "reduction_to_dimx"):
+                    rec = [4, 0, a[0], -1, top.attrs["dim"], 1 if kd == "reduction" else bg.reduction_dimx, z]
+                elif kd == "reduction_max":
+                    rec = [5, 0, a[0], -1, top.attrs["dim"], z, z]
+                elif kd == "rms_norm":
+                    rec = [6, 0, a[0], -1, z, _fbits(_EPS), z]
+                elif kd == "concat":
+                    rec = [7, 0, a[0], a[1], top.attrs["dim"], z, z]
+                elif kd in ("accum", "accum_max", "accum_rescale"):
+                    if kd == "accum":
+                        if top.attrs["acc"] not in ACC:
+                            raise _NoForm
+                        kind, r = ACC[top.attrs["acc"]], -1
+                    elif kd == "accum_max":
+                        kind, r = 5, -1
+                    else:
+                        if top.attrs["acc"] not in ("none", "sum"):
+                            raise _NoForm
+                        kind, r = (6 if top.attrs["acc"] == "none" else 7), a[1]
+                    buf = tile(top.inputs[0].dims, wide=True, at=0)  # fp32, the input tile's shape
+                    use(buf, t_fin)
+                    i = tid[id(o)] = tile(o.dims, at=t_fin)
+                    op_recs.append([8, i, a[0], r, kind, z, z, 0, buf])
+                    continue
+                else:
+                    raise _NoForm
+                i = tid[id(o)] = tile(o.dims, at=at)
+                rec[1] = i
+                op_recs.append(rec + [phase, 0])
+            varies = {}  # tile -> changes with the iteration
+            for dten, st in bg.inputs:
+                varies[id(st)] = st.op.attrs["forloop_dim"] >= 0 and R > 1
+            for top in body:
+                v = any(varies.get(id(x), False) for x in top.inputs)
+                varies[id(top.outputs[0])] = v and not top.outputs[0].after_accum
+            out_recs = []
+            for k, ((st, omap, ofd), out) in enumerate(zip(bg.outputs, outs)):
+                if len(st.dims) != len(out.dims):
+                    raise _NoForm
+                if ofd < 0 and varies.get(id(st), False):
+                    raise _NoForm  # a per-iteration tile with no place per iteration
+                i = tid[id(st)]
+                per_iter = ofd >= 0 and not st.after_accum
+                use(i, n_loop + 1 if per_iter else END)
+                if not per_iter and not st.after_accum:
+                    use(i, END)
+                om = tuple(omap) + (-1,) * 3
+                out_recs.append([i, k, *pad4(out.dims, 1), *om[:3], ofd, 1 if st.after_accum else 0])
+        except (_NoForm, KeyError, StopIteration):
+            return False
+        # first fit: a tile may reuse bytes of tiles whose lifetimes it does not meet
+        offs, sizes = [], []
+        for i, (dims, wide, a0, a1) in enumerate(tiles):
+            n = 1
+            for d in dims:
+                n *= d
+            size, align = n * (4 if wide else 2), 4 if wide else 2
+            busy = sorted((offs[j], offs[j] + sizes[j]) for j in range(i) if not (tiles[j][3] < a0 or a1 < tiles[j][2]))
+            off = 0
+            for lo, hi in busy:
+                if off + size <= lo:
+                    break
+                off = max(off, (hi + align - 1) // align * align)
+            offs.append(off)
+            sizes.append(size)
+        lds_bytes = max(o + s for o, s in zip(offs, sizes))
+        if lds_bytes > 160 * 1024:
+            return False
+        words = [1, dt.code, R, len(tiles), len(in_recs), len(op_recs), len(out_recs), lds_bytes, bg.reduction_dimx,
+                 gx, gy, gz]
+        for (dims, wide, _, _), off in zip(tiles, offs):
+            words += [off, len(dims), *pad4(dims, 1), 1 if wide else 0]
+        for r in in_recs + op_recs + out_recs:
+            words += r
+        if len(words) > 800:
+            return False
+        arr = (ctypes.c_int32 * len(words))(*words)
+        if _lib.lib().yr_hip_tb_program_check(arr, len(words), len(ins), len(outs), gx, gy, gz) != _lib.YR_OK:
+            return False
+        self.emit(_lib.OP_TB_PROGRAM, [self.dense(t_) for t_ in ins], [self.out_ref(o) for o in outs],
+                  [gx, gy, gz, dt.code] + words, "tb_program")
         return True
 
     def _interpret_customized(self, op: KNOp) -> bool:
