@@ -2,8 +2,8 @@
 // TB graph of a customized op, src/threadblock/graph.cc; the role its
 // transpiler gives to generated CUDA, src/transpiler/transpile.cc:370-720)
 // run by a small tile program interpreter.  A workgroup is one block of the
-// customized op's grid; every tile lives in LDS as fp32 for the whole launch
-// (no block tensor reaches HBM), inputs are cut from the device tensors by
+// customized op's grid; every tile lives in LDS for the whole launch (no
+// block tensor reaches HBM), inputs are cut from the device tensors by
 // input_map / forloop_dim each iteration, outputs are placed by output_map /
 // forloop_dim.  Tiles are stored in the 16-bit type, so each operator's
 // result is rounded once (as the transpiled element ops do); math is fp32,
@@ -64,6 +64,17 @@ __device__ __forceinline__ Tile tile_of(const int32_t* w, int t) {
     x.n *= x.d[i];
   }
   return x;
+}
+
+// a[i] for a runtime i without indexing the array (a runtime index would put
+// the array, and the tile holding it, in per-lane scratch memory)
+__device__ __forceinline__ int dsel(const int (&a)[kMaxDim], int i) {
+  return i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3];
+}
+__device__ __forceinline__ void dadd(int (&a)[kMaxDim], int i, int v) {
+#pragma unroll
+  for (int q = 0; q < kMaxDim; q++)
+    if (q == i) a[q] += v;
 }
 
 // element i of a tile as fp32 / stored (a 16-bit tile rounds: one rounding
@@ -133,10 +144,10 @@ __device__ __forceinline__ void tile_start(const int32_t* r, const Tile& t, int 
 #pragma unroll
   for (int a = 0; a < 3; a++) {
     const int m = r[6 + a];
-    if (m >= 0) s[m] += b[a] * (gd[m] / g[a]);
+    if (m >= 0) dadd(s, m, b[a] * (dsel(gd, m) / g[a]));
   }
   const int fd = r[9];
-  if (fd >= 0) s[fd] += it * t.d[fd];
+  if (fd >= 0) dadd(s, fd, it * dsel(t.d, fd));
 }
 
 // device element offset of tile element e
@@ -150,6 +161,34 @@ __device__ __forceinline__ long long dev_index(const int32_t* r, const Tile& t, 
   return g;
 }
 
+// sum / max over the 64 lanes of a wave (every lane gets the result)
+__device__ __forceinline__ float wave_red(float v, bool mx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o);
+    v = mx ? fmaxf(v, u) : v + u;
+  }
+  return v;
+}
+
+// whole 16-byte pieces: the tile's and the device tensor's rows hold whole
+// groups of 8 elements, the tile starts on one, and both base addresses are
+// 16-byte aligned
+__device__ __forceinline__ bool vec8(const Tile& t, const int32_t* r, const int (&s)[kMaxDim], const void* dev) {
+  const int l = t.nd - 1;
+  return ((dsel(t.d, l) | r[2 + l] | dsel(s, l)) & 7) == 0 && (t.off & 15) == 0 && (reinterpret_cast<uintptr_t>(dev) & 15) == 0;
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
+                                                  0, 0);
+}
+
 template <int DT>
 __device__ void load_input(const Args& A, const int32_t* w, const int32_t* r, int it, char* lds) {
   const Tile t = tile_of(w, r[0]);
@@ -157,6 +196,24 @@ __device__ void load_input(const Args& A, const int32_t* w, const int32_t* r, in
   uint16_t* dst = reinterpret_cast<uint16_t*>(lds + t.off);  // input tiles are 16-bit
   int s[kMaxDim];
   tile_start(r, t, it, s);
+  if (vec8(t, r, s, src)) {  // 16-byte row pieces, 8 loads per thread in flight
+    constexpr int U = 8;
+    const int nc = t.n >> 3;
+    for (int c0 = threadIdx.x; c0 < nc; c0 += kThreads * U) {
+      uint4 v[U];
+#pragma unroll
+      for (int j = 0; j < U; j++) {  // (unconditional loads, clamped: keeps v in registers)
+        const int c = min(c0 + j * kThreads, nc - 1);
+        v[j] = *reinterpret_cast<const uint4*>(src + dev_index(r, t, s, c << 3));
+      }
+#pragma unroll
+      for (int j = 0; j < U; j++) {
+        const int c = c0 + j * kThreads;
+        if (c < nc) *reinterpret_cast<uint4*>(dst + (c << 3)) = v[j];
+      }
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < t.n; e += kThreads) dst[e] = src[dev_index(r, t, s, e)];
 }
 
@@ -166,6 +223,22 @@ __device__ void store_output(const Args& A, const int32_t* w, const int32_t* r, 
   uint16_t* dst = A.out[r[1]];
   int s[kMaxDim];
   tile_start(r, t, it, s);
+  if (vec8(t, r, s, dst)) {
+    for (int c = threadIdx.x; c < (t.n >> 3); c += kThreads) {
+      uint4 v;
+      if (t.wide) {  // 8 fp32 values, each rounded once
+        const float* f = reinterpret_cast<const float*>(lds + t.off) + (c << 3);
+        v.x = st_elem<DT>(f[0]) | (st_elem<DT>(f[1]) << 16);
+        v.y = st_elem<DT>(f[2]) | (st_elem<DT>(f[3]) << 16);
+        v.z = st_elem<DT>(f[4]) | (st_elem<DT>(f[5]) << 16);
+        v.w = st_elem<DT>(f[6]) | (st_elem<DT>(f[7]) << 16);
+      } else {  // already 16-bit values of the type
+        v = *reinterpret_cast<const uint4*>(lds + t.off + (c << 4));
+      }
+      *reinterpret_cast<uint4*>(dst + dev_index(r, t, s, c << 3)) = v;
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < t.n; e += kThreads) dst[dev_index(r, t, s, e)] = (uint16_t)st_elem<DT>(tld<DT>(lds, t, e));
 }
 
@@ -194,7 +267,32 @@ __device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
     }
     case K_MATMUL: {  // a [.., M, K] x b [.., K, N]
       const Tile tb = tile_of(w, o[3]);
-      const int M = ta.d[ta.nd - 2], K = ta.d[ta.nd - 1], N = tb.d[tb.nd - 1];
+      const int M = dsel(ta.d, ta.nd - 2), K = dsel(ta.d, ta.nd - 1), N = dsel(tb.d, tb.nd - 1);
+      if (!ta.wide && !tb.wide && ((M | N) & 15) == 0 && (K & 31) == 0 && (ta.off & 15) == 0) {
+        // 16 x 16 output tiles on MFMA (16x16x32), one wave per tile.  Lane l:
+        // A = row l % 16, k 8 (l / 16) .. + 7 (one 16-byte LDS read); B =
+        // column l % 16, the same 8 k; result rows 4 (l / 16) + i, column l % 16
+        const int lane = threadIdx.x & 63, r16 = lane & 15, kg = (lane >> 4) * 8;
+        const int mt = M >> 4, nt = N >> 4, per = mt * nt, tiles = (to.n / (M * N)) * per;
+        const uint16_t* A_ = reinterpret_cast<const uint16_t*>(lds + ta.off);
+        const uint16_t* B_ = reinterpret_cast<const uint16_t*>(lds + tb.off);
+        for (int t = threadIdx.x >> 6; t < tiles; t += kThreads / 64) {
+          const int bt = t / per, m0 = (t % per) / nt * 16, n0 = (t % nt) * 16;
+          const uint16_t* ap = A_ + (bt * M + m0 + r16) * K + kg;
+          const uint16_t* bp = B_ + bt * K * N + kg * N + n0 + r16;
+          f32x4 c = {0.f, 0.f, 0.f, 0.f};
+          for (int k0 = 0; k0 < K; k0 += 32) {
+            const uint4 a = *reinterpret_cast<const uint4*>(ap + k0);
+            const uint16_t* q = bp + k0 * N;
+            const uint4 b = {q[0] | ((uint32_t)q[N] << 16), q[2 * N] | ((uint32_t)q[3 * N] << 16),
+                             q[4 * N] | ((uint32_t)q[5 * N] << 16), q[6 * N] | ((uint32_t)q[7 * N] << 16)};
+            c = mfma16<DT>(a, b, c);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) tst<DT>(lds, to, (bt * M + m0 + (lane >> 4) * 4 + i) * N + n0 + r16, c[i]);
+        }
+        break;
+      }
       for (int e = threadIdx.x; e < to.n; e += kThreads) {
         const int n = e % N, m = (e / N) % M, bt = e / (M * N);
         const int ar = (bt * M + m) * K, bc = bt * K * N + n;
@@ -207,32 +305,51 @@ __device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
     case K_REDUCE:    // sum over dim a0 down to a1 elements (element j adds j, j + a1, ...)
     case K_REDMAX: {  // max over dim a0
       const int dim = o[4], to_n = kind == K_REDUCE ? o[5] : 1;
-      const int L = ta.d[dim];
+      const int L = dsel(ta.d, dim);
       int inner = 1;
-      for (int i = dim + 1; i < ta.nd; i++) inner *= ta.d[i];
+#pragma unroll
+      for (int i = 0; i < kMaxDim; i++)
+        if (i > dim && i < ta.nd) inner *= ta.d[i];
+      const bool mx = kind == K_REDMAX;
+      if (L / to_n >= 64) {  // long reductions: one wave per output
+        const int lane = threadIdx.x & 63;
+        for (int e = threadIdx.x >> 6; e < to.n; e += kThreads / 64) {
+          const int in_ = e % inner, j = (e / inner) % to_n, ou = e / (inner * to_n);
+          const int base = ou * L * inner + in_;
+          float s = mx ? -INFINITY : 0.f;
+          for (int r = j + lane * to_n; r < L; r += 64 * to_n) {
+            const float v = tld<DT>(lds, ta, base + r * inner);
+            s = mx ? fmaxf(s, v) : s + v;
+          }
+          s = wave_red(s, mx);
+          if (lane == 0) tst<DT>(lds, to, e, s);
+        }
+        break;
+      }
       for (int e = threadIdx.x; e < to.n; e += kThreads) {
         const int in_ = e % inner, j = (e / inner) % to_n, ou = e / (inner * to_n);
         const int base = ou * L * inner + in_;
-        float s = kind == K_REDMAX ? -INFINITY : 0.f;
+        float s = mx ? -INFINITY : 0.f;
         for (int r = j; r < L; r += to_n) {
           const float v = tld<DT>(lds, ta, base + r * inner);
-          s = kind == K_REDMAX ? fmaxf(s, v) : s + v;
+          s = mx ? fmaxf(s, v) : s + v;
         }
         tst<DT>(lds, to, e, s);
       }
       break;
     }
-    case K_RMSNORM: {  // rows of the last dim: x * rsqrt(mean(x^2) + eps)
-      const int n = ta.d[ta.nd - 1];
+    case K_RMSNORM: {  // rows of the last dim: x * rsqrt(mean(x^2) + eps), one wave per row
+      const int n = dsel(ta.d, ta.nd - 1), rows = to.n / n, lane = threadIdx.x & 63;
       const float eps = fbits(o[5]);
-      for (int e = threadIdx.x; e < to.n; e += kThreads) {
-        const int row = (e / n) * n;
+      for (int row = threadIdx.x >> 6; row < rows; row += kThreads / 64) {
+        const int b = row * n;
         float ss = 0.f;
-        for (int i = 0; i < n; i++) {
-          const float v = tld<DT>(lds, ta, row + i);
+        for (int i = lane; i < n; i += 64) {
+          const float v = tld<DT>(lds, ta, b + i);
           ss += v * v;
         }
-        tst<DT>(lds, to, e, tld<DT>(lds, ta, e) * rsqrtf(ss / (float)n + eps));
+        const float sc = rsqrtf(wave_red(ss, false) / (float)n + eps);
+        for (int i = lane; i < n; i += 64) tst<DT>(lds, to, b + i, tld<DT>(lds, ta, b + i) * sc);
       }
       break;
     }
@@ -242,9 +359,10 @@ __device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
       for (int e = threadIdx.x; e < to.n; e += kThreads) {
         int c[kMaxDim];
         coords(to, e, c);
-        const bool first = c[dim] < ta.d[dim];
-        if (!first) c[dim] -= ta.d[dim];
-        const Tile& ts = first ? ta : tb;
+        const int ad = dsel(ta.d, dim);
+        const bool first = dsel(c, dim) < ad;
+        if (!first) dadd(c, dim, -ad);
+        const Tile ts = first ? ta : tb;
         int idx = 0;
 #pragma unroll
         for (int i = 0; i < kMaxDim; i++)
@@ -293,13 +411,27 @@ __device__ void acc_final(const int32_t* w, const int32_t* o, char* lds, int R, 
   const Tile tx = tile_of(w, o[2]), ta = tile_of(w, o[8]), to = tile_of(w, o[1]);
   const float* acc = reinterpret_cast<const float*>(lds + ta.off);
   const int kind = o[4];
-  const int n = tx.d[tx.nd - 1];
+  const int n = dsel(tx.d, tx.nd - 1);
+  const bool red = !(kind == A_NONE || kind == A_MAX || kind == A_RESCALE);
+  const int to_n = kind == A_TODIMX ? dimx : 1;
+  if (red && n / to_n >= 64) {  // long row sums: one wave per output
+    const int lane = threadIdx.x & 63;
+    for (int e = threadIdx.x >> 6; e < to.n; e += kThreads / 64) {
+      const float* p = acc + (size_t)(e / to_n) * n;
+      float s = 0.f;
+      for (int i = e % to_n + lane * to_n; i < n; i += 64 * to_n) s += p[i];
+      s = wave_red(s, false);
+      if (kind == A_MEAN) s /= (float)(n * R);
+      else if (kind == A_RMS) s = sqrtf(s / (float)(n * R));
+      if (lane == 0) tst<DT>(lds, to, e, s);
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < to.n; e += kThreads) {
     float v;
     if (kind == A_NONE || kind == A_MAX || kind == A_RESCALE) {
       v = acc[e];
     } else {
-      const int to_n = kind == A_TODIMX ? dimx : 1;
       const int j = e % to_n, row = e / to_n;
       const float* p = acc + (size_t)row * n;
       float s = 0.f;

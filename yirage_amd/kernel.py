@@ -1404,7 +1404,7 @@ class _Lowering:
             n = 1
             for d in dims:
                 n *= d
-            size, align = n * (4 if wide else 2), 4 if wide else 2
+            size, align = n * (4 if wide else 2), 16  # 16-byte aligned: whole-row vector access
             busy = sorted((offs[j], offs[j] + sizes[j]) for j in range(i) if not (tiles[j][3] < a0 or a1 < tiles[j][2]))
             off = 0
             for lo, hi in busy:
