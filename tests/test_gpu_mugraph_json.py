@@ -277,6 +277,29 @@ def test_tile_programs_match_the_literal_plans(name, kind, stds):
     assert checked >= {"mha_bs1.json": 15, "ntrans_bs1.json": 3, "qknorm_gqa_bs1_subset.json": 12}[name]
 
 
+def test_superoptimize_times_tile_program_candidates(capsys):
+    """superoptimize over a saved qk-norm candidate list times each
+    candidate's literal plan and, where it exists, its tile-program plan,
+    and keeps the fastest; whichever it keeps matches the block-by-block
+    emulation of the graph it was given."""
+    from tb_numpy import run_graph
+
+    path = os.path.join(GOLDEN, "qknorm_gqa_bs1_subset.json")
+    g = MJ.load(path)[10]
+    print("case superoptimize qk-norm #10 with its saved list", flush=True)
+    opt = g.superoptimize(backend="hip", warmup_iters=2, profile_iters=5, verbose=True, use_graph_dataset=False,
+                          use_cached_graphs=False, previous_checkpoint=path)
+    log = capsys.readouterr().out
+    timed = [l for l in log.splitlines() if l.startswith("[superoptimize hip]")]
+    assert any("tb_program" in l for l in timed) and any("tb_program" not in l for l in timed), log
+    ins = _inputs(g, (1.0, 0.02, 1.0), seed=10)
+    got = opt(inputs=[x.cuda() for x in ins])[0]
+    torch.cuda.synchronize()
+    ref = run_graph(g, [x.double().numpy() for x in ins])[0]
+    err = np.abs(got.float().cpu().numpy() - ref)
+    assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()} (kept {opt._plan.describe()})"
+
+
 def test_fused_elementwise_bit_identical_to_unfused_steps():
     """Plans whose elementwise trees were fused into single launches
     (yr_hip_graph_ewise) give bit-identical outputs to the same plans run one

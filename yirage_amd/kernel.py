@@ -518,8 +518,10 @@ class KNGraph:
         plans and, like the reference's use_cached_graphs
         (kernel.py:635-640), the plannable graphs of a saved candidate list:
         `yirage_cached_mugraphs_<hash>.json` in the working directory or the
-        file `previous_checkpoint` names (e.g. benchmark/saved_mugraphs/...);
-        with more than one candidate the fastest measured one is kept.
+        file `previous_checkpoint` names (e.g. benchmark/saved_mugraphs/...),
+        each also with its customized ops as tile programs where that form
+        exists; with more than one candidate the fastest measured one is
+        kept (without a GPU, the first: the literal fused plan).
         The automatic file name is this build's structural hash of the graph
         (the reference's get_owner_independent_hash is a C++ hash of its own
         graph object), so a file the reference wrote is read only when given
@@ -562,6 +564,17 @@ class KNGraph:
                     continue  # a customized op this backend has no kernel for
                 if all(p.describe() != c.describe() for c in candidates):
                     candidates.append(p)
+        # each plan's customized ops as tile programs, one launch each: a
+        # further candidate wherever that form exists (timed with the rest;
+        # without a GPU to time them the first candidate above is kept)
+        for src in [self] + ([c for c in load(ckpt) if self._same_interface(c)]
+                             if ckpt is not None and os.path.exists(ckpt) else []):
+            try:
+                p = src.plan(fuse=True, tb_program=True)
+            except YirageHipError:
+                continue
+            if "tb_program" in p.describe() and all(p.describe() != c.describe() for c in candidates):
+                candidates.append(p)
         if not candidates:
             raise errors[0]
         best = candidates[0]
