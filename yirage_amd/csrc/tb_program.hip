@@ -31,7 +31,7 @@ namespace tbp {
 constexpr int kVersion = 1;
 constexpr int kHdr = 12, kTw = 7, kIw = 10, kOw = 11, kRw = 9;
 constexpr int kMaxWords = 800, kMaxIn = 8, kMaxOut = 4, kMaxDim = 4;
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kMaxLdsBytes = 160 * 1024;
 
 enum OpKind { K_UNARY = 1, K_BINARY = 2, K_MATMUL = 3, K_REDUCE = 4, K_REDMAX = 5, K_RMSNORM = 6, K_CONCAT = 7,
@@ -258,6 +258,11 @@ __device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
     }
     case K_BINARY: {
       const Tile tb = tile_of(w, o[3]);
+      if (ta.n == to.n && tb.n == to.n) {  // no broadcast: the operands have the output's shape
+        for (int e = threadIdx.x; e < to.n; e += kThreads)
+          tst<DT>(lds, to, e, binary(o[4], tld<DT>(lds, ta, e), tld<DT>(lds, tb, e)));
+        break;
+      }
       for (int e = threadIdx.x; e < to.n; e += kThreads) {
         int c[kMaxDim];
         coords(to, e, c);

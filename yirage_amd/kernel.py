@@ -497,10 +497,10 @@ class KNGraph:
         trees of elementwise steps become one fused elementwise launch;
         tb_program: customized ops that are no whole-tensor expression run as
         one tile-program launch each (else tile by tile, one launch per
-        threadblock op).  Off by default: on the saved candidates the tile
-        programs are correct but slower than the literal plans (the customized
-        ops' grids are 8-64 blocks, one workgroup each, against launches that
-        spread each operator over the whole chip)."""
+        threadblock op).  Off by default: on most saved candidates the tile
+        programs are slower than the literal plans (the customized ops'
+        grids are 8-64 blocks, one workgroup each, against launches that
+        spread each operator over the whole chip); superoptimize times both."""
         plan = _Lowering(self, fuse, tb_program).run()
         if fuse_elementwise:
             _fuse_elementwise(plan)
