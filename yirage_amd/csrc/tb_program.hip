@@ -189,36 +189,44 @@ __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
                                                   0, 0);
 }
 
+// U 16-byte pieces per thread in flight, every load a distinct piece (no
+// clamped repeats of one address, which the memory path serialises); U = 8
+// repeats while whole batches remain, smaller sizes run at most once each
+template <int U>
+__device__ __forceinline__ void load_batch(const uint16_t* src, uint16_t* dst, const int32_t* r, const Tile& t,
+                                           const int (&s)[kMaxDim], int nc, int& c0) {
+  for (; c0 + (U - 1) * kThreads < nc; c0 += U * kThreads) {
+    uint4 v[U];
+#pragma unroll
+    for (int j = 0; j < U; j++)
+      v[j] = *reinterpret_cast<const uint4*>(src + dev_index(r, t, s, (c0 + j * kThreads) << 3));
+#pragma unroll
+    for (int j = 0; j < U; j++) *reinterpret_cast<uint4*>(dst + ((c0 + j * kThreads) << 3)) = v[j];
+    if (U < 8) break;
+  }
+}
+
 template <int DT>
-__device__ void load_input(const Args& A, const int32_t* w, const int32_t* r, int it, char* lds) {
+__device__ __forceinline__ void load_input(const Args& A, const int32_t* w, const int32_t* r, int it, char* lds) {
   const Tile t = tile_of(w, r[0]);
   const uint16_t* src = A.in[r[1]];
   uint16_t* dst = reinterpret_cast<uint16_t*>(lds + t.off);  // input tiles are 16-bit
   int s[kMaxDim];
   tile_start(r, t, it, s);
-  if (vec8(t, r, s, src)) {  // 16-byte row pieces, 8 loads per thread in flight
-    constexpr int U = 8;
+  if (vec8(t, r, s, src)) {  // 16-byte row pieces: batches of 8, then 4, 2, 1 loads in flight per thread
     const int nc = t.n >> 3;
-    for (int c0 = threadIdx.x; c0 < nc; c0 += kThreads * U) {
-      uint4 v[U];
-#pragma unroll
-      for (int j = 0; j < U; j++) {  // (unconditional loads, clamped: keeps v in registers)
-        const int c = min(c0 + j * kThreads, nc - 1);
-        v[j] = *reinterpret_cast<const uint4*>(src + dev_index(r, t, s, c << 3));
-      }
-#pragma unroll
-      for (int j = 0; j < U; j++) {
-        const int c = c0 + j * kThreads;
-        if (c < nc) *reinterpret_cast<uint4*>(dst + (c << 3)) = v[j];
-      }
-    }
+    int c0 = threadIdx.x;
+    load_batch<8>(src, dst, r, t, s, nc, c0);
+    load_batch<4>(src, dst, r, t, s, nc, c0);
+    load_batch<2>(src, dst, r, t, s, nc, c0);
+    load_batch<1>(src, dst, r, t, s, nc, c0);
     return;
   }
   for (int e = threadIdx.x; e < t.n; e += kThreads) dst[e] = src[dev_index(r, t, s, e)];
 }
 
 template <int DT>
-__device__ void store_output(const Args& A, const int32_t* w, const int32_t* r, int it, const char* lds) {
+__device__ __forceinline__ void store_output(const Args& A, const int32_t* w, const int32_t* r, int it, const char* lds) {
   const Tile t = tile_of(w, r[0]);
   uint16_t* dst = A.out[r[1]];
   int s[kMaxDim];
@@ -246,7 +254,7 @@ __device__ __forceinline__ float fbits(int32_t b) { return __int_as_float(b); }
 
 // one operator over its output tile, all threads; fp32 math
 template <int DT>
-__device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
+__device__ __forceinline__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
   const int kind = o[0];
   const Tile to = tile_of(w, o[1]);
   const Tile ta = tile_of(w, o[2]);
@@ -383,7 +391,7 @@ __device__ void exec_op(const int32_t* w, const int32_t* o, char* lds) {
 
 // accumulator update (per iteration): the fp32 buffer, the input tile's shape
 template <int DT>
-__device__ void acc_update(const int32_t* w, const int32_t* o, char* lds) {
+__device__ __forceinline__ void acc_update(const int32_t* w, const int32_t* o, char* lds) {
   const Tile tx = tile_of(w, o[2]), ta = tile_of(w, o[8]);
   float* acc = reinterpret_cast<float*>(lds + ta.off);
   const int kind = o[4];
@@ -403,7 +411,7 @@ __device__ void acc_update(const int32_t* w, const int32_t* o, char* lds) {
   }
 }
 
-__device__ void acc_init(const int32_t* w, const int32_t* o, char* lds) {
+__device__ __forceinline__ void acc_init(const int32_t* w, const int32_t* o, char* lds) {
   const Tile ta = tile_of(w, o[8]);
   float* acc = reinterpret_cast<float*>(lds + ta.off);
   const float v = o[4] == A_MAX ? -INFINITY : 0.f;
@@ -412,7 +420,7 @@ __device__ void acc_init(const int32_t* w, const int32_t* o, char* lds) {
 
 // after the loop: the accumulator's value into its (16-bit) output tile
 template <int DT>
-__device__ void acc_final(const int32_t* w, const int32_t* o, char* lds, int R, int dimx) {
+__device__ __forceinline__ void acc_final(const int32_t* w, const int32_t* o, char* lds, int R, int dimx) {
   const Tile tx = tile_of(w, o[2]), ta = tile_of(w, o[8]), to = tile_of(w, o[1]);
   const float* acc = reinterpret_cast<const float*>(lds + ta.off);
   const int kind = o[4];
