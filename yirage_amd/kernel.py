@@ -497,10 +497,11 @@ class KNGraph:
         trees of elementwise steps become one fused elementwise launch;
         tb_program: customized ops that are no whole-tensor expression run as
         one tile-program launch each (else tile by tile, one launch per
-        threadblock op).  Off by default: on most saved candidates the tile
-        programs are slower than the literal plans (the customized ops'
-        grids are 8-64 blocks, one workgroup each, against launches that
-        spread each operator over the whole chip); superoptimize times both."""
+        threadblock op).  Off by default: which form is faster depends on the
+        graph (the customized op's grid, 8-64 blocks of one workgroup each,
+        against literal launches that spread each operator over the chip:
+        the tile programs win on most saved qk-norm candidates and lose on
+        the MHA ones); superoptimize times both and keeps the faster."""
         plan = _Lowering(self, fuse, tb_program).run()
         if fuse_elementwise:
             _fuse_elementwise(plan)
