@@ -193,31 +193,41 @@ def test_customized_block_transpose_runs_literally():
     assert torch.equal(got, got_prog)  # one exp, one rounding either way
 
 
-def test_customized_max_and_concat_run_literally():
+def _run(g, ins, tbp):
+    """g's plan with its customized ops run literally or as tile programs."""
+    p = g.plan(fuse=True, tb_program=tbp)
+    assert ("tb_program" in p.describe()) == tbp, p.describe()
+    out = g._execute(p, [x.cuda() for x in ins], None)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("tbp", [False, True], ids=["literal", "tile_program"])
+def test_customized_max_and_concat_run_literally(tbp):
     """Forloop max accumulator, reduction_max and concat on the GPU against
-    the block-by-block emulation (tests/tb_numpy.py)."""
+    the block-by-block emulation (tests/tb_numpy.py), run literally and as a
+    tile program."""
     from tb_numpy import run_graph
     from test_mugraph_json import _max_concat_graph
 
     g = _max_concat_graph()
     x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(4))).half()
-    got = g(inputs=[x.cuda()])[0]
-    torch.cuda.synchronize()
+    got = _run(g, [x], tbp)[0]
     ref = run_graph(g, [x.double().numpy()])[0]
     err = np.abs(got.float().cpu().numpy() - ref)
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
 
 
-def test_customized_mean_accumulator_runs_literally():
+@pytest.mark.parametrize("tbp", [False, True], ids=["literal", "tile_program"])
+def test_customized_mean_accumulator_runs_literally(tbp):
     """The mean forloop accumulator on the GPU against its closed form, the
     row mean of exp(X) (float64), and the sum accumulator of the same tiles
-    divided by the 256 summed elements."""
+    divided by the 256 summed elements; literally and as a tile program."""
     from test_mugraph_json import _mean_graph
 
     g = _mean_graph()
     x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(5))).half()
-    mean, total = g(inputs=[x.cuda()])
-    torch.cuda.synchronize()
+    mean, total = _run(g, [x], tbp)
     ref = torch.exp(x.double()).mean(1, keepdim=True).numpy()
     err = np.abs(mean.float().cpu().numpy() - ref)
     assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"max err {err.max()}"
@@ -225,16 +235,16 @@ def test_customized_mean_accumulator_runs_literally():
     assert not (err2 > ATOL + RTOL * np.abs(ref)).any(), f"mean vs sum / 256: {err2.max()}"
 
 
-def test_customized_rescale_accumulator_runs_literally():
+@pytest.mark.parametrize("tbp", [False, True], ids=["literal", "tile_program"])
+def test_customized_rescale_accumulator_runs_literally(tbp):
     """Rescale accumulators (acc = acc * rescale + input per iteration, kept
     whole and with the last dim summed) on the GPU against the closed form
-    sum_i x_i prod_{j>i} r_j in float64."""
+    sum_i x_i prod_{j>i} r_j in float64; literally and as a tile program."""
     from test_mugraph_json import _rescale_closed_form, _rescale_graph
 
     g = _rescale_graph()
     x = (torch.randn((8, 256), generator=torch.Generator().manual_seed(7))).half()
-    whole, summed = g(inputs=[x.cuda()])
-    torch.cuda.synchronize()
+    whole, summed = _run(g, [x], tbp)
     want, want_sum = _rescale_closed_form(x.double().numpy())
     for got, ref in ((whole, want), (summed, want_sum)):
         err = np.abs(got.float().cpu().numpy() - ref)
