@@ -8,9 +8,12 @@ import numpy as np
 
 from yirage_amd import _lib
 
+from scipy.special import erf as _erf
+
 _UNARY = {
     0: np.exp,
     1: lambda a: a / (1.0 + np.exp(-a)),
+    2: lambda a: 0.5 * a * (1.0 + _erf(a / np.sqrt(2.0))),
     3: lambda a: np.maximum(a, 0.0),
     5: np.sqrt,
     6: np.square,

@@ -202,6 +202,36 @@ def _run(g, ins, tbp):
     return out
 
 
+def test_customized_unary_chain_as_tile_program():
+    """Every unary kind (silu, gelu, relu, clamp, square, sqrt, mul_scalar,
+    exp) and add / div in one block-transposed customized op, run as a tile
+    program and literally, against float64 torch (each operator's result is
+    rounded to fp16 in both plans, hence the tolerance)."""
+    import yirage_amd as yr
+
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(64, 64), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 2, 1), block_dim=(128, 1, 1), forloop_range=1, reduction_dimx=64)
+    t = tb.new_input(dtensor=X, input_map=(0, 1, -1), forloop_dim=-1)
+    s = tb.add(tb.silu(t), tb.gelu(t))
+    s = tb.add(s, tb.relu(t))
+    s = tb.add(s, tb.clamp(t, -0.5, 0.5))
+    s = tb.add(s, tb.sqrt(tb.square(t)))
+    s = tb.add(s, tb.mul_scalar(t, 0.5))
+    s = tb.div(s, tb.exp(t))
+    tb.new_output(stensor=tb.forloop_accum(s), output_map=(1, 0, -1))
+    g.mark_output(g.customized([X], tb)[0])
+    x = (torch.randn((64, 64), generator=torch.Generator().manual_seed(9))).half()
+    xd = x.double()
+    ref = (torch.nn.functional.silu(xd) + torch.nn.functional.gelu(xd) + torch.relu(xd) + xd.clamp(-0.5, 0.5)
+           + xd.abs() + 0.5 * xd) / torch.exp(xd)
+    ref = ref.view(2, 32, 2, 32).permute(2, 1, 0, 3).reshape(64, 64).numpy()
+    for tbp in (True, False):
+        got = _run(g, [x], tbp)[0]
+        err = np.abs(got.float().cpu().numpy() - ref)
+        assert not (err > 2 * ATOL + 2 * RTOL * np.abs(ref)).any(), f"tile program {tbp}: max err {err.max()}"
+
+
 @pytest.mark.parametrize("tbp", [False, True], ids=["literal", "tile_program"])
 def test_customized_max_and_concat_run_literally(tbp):
     """Forloop max accumulator, reduction_max and concat on the GPU against

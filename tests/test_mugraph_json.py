@@ -125,6 +125,39 @@ def test_grid_placement_must_match_the_cut():
         assert np.allclose(got, want, rtol=1e-12, atol=0)
 
 
+def test_unary_chain_tile_program_and_literal_plan():
+    """Every unary kind (silu, gelu, relu, clamp, square, sqrt, mul_scalar,
+    exp) and add / div in one block-transposed customized op: the tile
+    program (numpy VM of its words) and the literal plan against float64
+    torch."""
+    import numpy as np
+    import torch
+    from plan_numpy import run_plan
+
+    g = yr.new_kernel_graph()
+    X = g.new_input(dims=(64, 64), dtype=yr.float16)
+    tb = yr.new_threadblock_graph(grid_dim=(2, 2, 1), block_dim=(128, 1, 1), forloop_range=1, reduction_dimx=64)
+    t = tb.new_input(dtensor=X, input_map=(0, 1, -1), forloop_dim=-1)
+    s = tb.add(tb.silu(t), tb.gelu(t))
+    s = tb.add(s, tb.relu(t))
+    s = tb.add(s, tb.clamp(t, -0.5, 0.5))
+    s = tb.add(s, tb.sqrt(tb.square(t)))
+    s = tb.add(s, tb.mul_scalar(t, 0.5))
+    s = tb.div(s, tb.exp(t))
+    tb.new_output(stensor=tb.forloop_accum(s), output_map=(1, 0, -1))
+    g.mark_output(g.customized([X], tb)[0])
+    x = np.random.default_rng(9).normal(0, 1, (64, 64))
+    xd = torch.tensor(x)
+    ref = (torch.nn.functional.silu(xd) + torch.nn.functional.gelu(xd) + torch.relu(xd) + xd.clamp(-0.5, 0.5)
+           + xd.abs() + 0.5 * xd) / torch.exp(xd)
+    ref = ref.view(2, 32, 2, 32).permute(2, 1, 0, 3).reshape(64, 64).numpy()
+    for tbp in (True, False):
+        p = g.plan(fuse=True, tb_program=tbp)
+        assert ("tb_program" in p.describe()) == tbp
+        got = run_plan(p, [x])[0]
+        assert np.abs(got - ref).max() <= 1e-12
+
+
 def _renumber(ops):
     """The JSON text with guids replaced by their order of first use."""
     ids = {}
