@@ -189,21 +189,14 @@ __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
                                                   0, 0);
 }
 
-// U 16-byte pieces per thread in flight, every load a distinct piece (no
-// clamped repeats of one address, which the memory path serialises); U = 8
-// repeats while whole batches remain, smaller sizes run at most once each
-template <int U>
-__device__ __forceinline__ void load_batch(const uint16_t* src, uint16_t* dst, const int32_t* r, const Tile& t,
-                                           const int (&s)[kMaxDim], int nc, int& c0) {
-  for (; c0 + (U - 1) * kThreads < nc; c0 += U * kThreads) {
-    uint4 v[U];
-#pragma unroll
-    for (int j = 0; j < U; j++)
-      v[j] = *reinterpret_cast<const uint4*>(src + dev_index(r, t, s, (c0 + j * kThreads) << 3));
-#pragma unroll
-    for (int j = 0; j < U; j++) *reinterpret_cast<uint4*>(dst + ((c0 + j * kThreads) << 3)) = v[j];
-    if (U < 8) break;
-  }
+// 16 bytes per lane from global memory straight into LDS: lane l's data
+// lands at lds_base + 16 l (lds_base wave-uniform)
+__device__ __forceinline__ void lds_load16(const uint16_t* g, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(
+      (const __attribute__((address_space(1))) void*)(g),
+      reinterpret_cast<__attribute__((address_space(3))) void*>(
+          reinterpret_cast<__attribute__((address_space(3))) char*>(reinterpret_cast<uintptr_t>(lds_base))),
+      16, 0, 0);
 }
 
 template <int DT>
@@ -213,14 +206,13 @@ __device__ __forceinline__ void load_input(const Args& A, const int32_t* w, cons
   uint16_t* dst = reinterpret_cast<uint16_t*>(lds + t.off);  // input tiles are 16-bit
   int s[kMaxDim];
   tile_start(r, t, it, s);
-  if (vec8(t, r, s, src)) {  // 16-byte row pieces: batches of 8, then 4, 2, 1 loads in flight per thread
-    const int nc = t.n >> 3;
-    int c0 = threadIdx.x;
-    load_batch<8>(src, dst, r, t, s, nc, c0);
-    load_batch<4>(src, dst, r, t, s, nc, c0);
-    load_batch<2>(src, dst, r, t, s, nc, c0);
-    load_batch<1>(src, dst, r, t, s, nc, c0);
-    return;
+  if (vec8(t, r, s, src)) {  // 16-byte row pieces straight into LDS, 64 consecutive pieces per wave
+    const int nc = t.n >> 3, lane = threadIdx.x & 63;
+    for (int g0 = (threadIdx.x >> 6) * 64; g0 < nc; g0 += kThreads) {
+      const int c = g0 + lane;
+      if (c < nc) lds_load16(src + dev_index(r, t, s, c << 3), dst + (g0 << 3));
+    }
+    return;  // (the caller waits for the loads before its barrier)
   }
   for (int e = threadIdx.x; e < t.n; e += kThreads) dst[e] = src[dev_index(r, t, s, e)];
 }
@@ -468,6 +460,7 @@ __global__ __launch_bounds__(kThreads) void tb_program_kernel(Args A) {
   for (int it = 0; it < R; it++) {
     for (int i = 0; i < ni; i++)
       if (it == 0 || ins[i * kIw + 9] >= 0) load_input<DT>(A, w, ins + i * kIw, it, lds);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads into LDS have landed
     if (it == 0) {  // (accumulator buffers may reuse tiles that are dead by now: after the loads)
       __syncthreads();
       for (int i = 0; i < no; i++)
