@@ -218,7 +218,7 @@ int yr_hip_graph_ewise(const void* const* ins, int n, void* y, int ndim, const i
  * csrc/tb_program.hip: header, tiles, inputs cut by input_map / forloop_dim
  * from dense row-major device tensors, operators, outputs placed by
  * output_map / forloop_dim); at most 800 words, 8 inputs, 4 outputs and
- * 160 KiB of tiles.  The program is checked against the launch (every tile
+ * 160 KiB less 256 bytes of tiles.  The program is checked against the launch (every tile
  * and device access in bounds, operator shapes consistent) before anything
  * runs; YR_E_INVALID otherwise. */
 int yr_hip_tb_program(const int32_t* program, int n_words, const void* const* ins, int n_in, void* const* outs,

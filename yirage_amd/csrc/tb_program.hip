@@ -32,7 +32,7 @@ constexpr int kVersion = 1;
 constexpr int kHdr = 12, kTw = 7, kIw = 10, kOw = 11, kRw = 9;
 constexpr int kMaxWords = 800, kMaxIn = 8, kMaxOut = 4, kMaxDim = 4;
 constexpr int kThreads = 1024;
-constexpr int kMaxLdsBytes = 160 * 1024;
+constexpr int kMaxLdsBytes = 160 * 1024 - 256;  // the tiles' share (block reductions keep a few words)
 
 enum OpKind { K_UNARY = 1, K_BINARY = 2, K_MATMUL = 3, K_REDUCE = 4, K_REDMAX = 5, K_RMSNORM = 6, K_CONCAT = 7,
               K_ACC = 8 };
@@ -169,6 +169,22 @@ __device__ __forceinline__ float wave_red(float v, bool mx) {
     v = mx ? fmaxf(v, u) : v + u;
   }
   return v;
+}
+
+// one float per wave for block-wide reductions
+__shared__ float tb_red[kThreads / 64];
+
+// sum / max over the whole block (every thread gets the result; all threads
+// must call it)
+__device__ __forceinline__ float block_red(float v, bool mx) {
+  v = wave_red(v, mx);
+  if ((threadIdx.x & 63) == 0) tb_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = tb_red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / 64; i++) r = mx ? fmaxf(r, tb_red[i]) : r + tb_red[i];
+  __syncthreads();  // tb_red is reused by the next call
+  return r;
 }
 
 // whole 16-byte pieces: the tile's and the device tensor's rows hold whole
@@ -316,6 +332,20 @@ __device__ __forceinline__ void exec_op(const int32_t* w, const int32_t* o, char
       for (int i = 0; i < kMaxDim; i++)
         if (i > dim && i < ta.nd) inner *= ta.d[i];
       const bool mx = kind == K_REDMAX;
+      if (L / to_n >= kThreads && to.n < kThreads / 64) {  // few long reductions: the whole block on each
+        for (int e = 0; e < to.n; e++) {
+          const int in_ = e % inner, j = (e / inner) % to_n, ou = e / (inner * to_n);
+          const int base = ou * L * inner + in_;
+          float s = mx ? -INFINITY : 0.f;
+          for (int r = j + threadIdx.x * to_n; r < L; r += kThreads * to_n) {
+            const float v = tld<DT>(lds, ta, base + r * inner);
+            s = mx ? fmaxf(s, v) : s + v;
+          }
+          s = block_red(s, mx);
+          if (threadIdx.x == 0) tst<DT>(lds, to, e, s);
+        }
+        break;
+      }
       if (L / to_n >= 64) {  // long reductions: one wave per output
         const int lane = threadIdx.x & 63;
         for (int e = threadIdx.x >> 6; e < to.n; e += kThreads / 64) {
@@ -346,6 +376,19 @@ __device__ __forceinline__ void exec_op(const int32_t* w, const int32_t* o, char
     case K_RMSNORM: {  // rows of the last dim: x * rsqrt(mean(x^2) + eps), one wave per row
       const int n = dsel(ta.d, ta.nd - 1), rows = to.n / n, lane = threadIdx.x & 63;
       const float eps = fbits(o[5]);
+      if (rows < kThreads / 64 && n >= kThreads) {  // few long rows: the whole block on each
+        for (int row = 0; row < rows; row++) {
+          const int b = row * n;
+          float ss = 0.f;
+          for (int i = threadIdx.x; i < n; i += kThreads) {
+            const float v = tld<DT>(lds, ta, b + i);
+            ss += v * v;
+          }
+          const float sc = rsqrtf(block_red(ss, false) / (float)n + eps);
+          for (int i = threadIdx.x; i < n; i += kThreads) tst<DT>(lds, to, b + i, tld<DT>(lds, ta, b + i) * sc);
+        }
+        break;
+      }
       for (int row = threadIdx.x >> 6; row < rows; row += kThreads / 64) {
         const int b = row * n;
         float ss = 0.f;
@@ -419,6 +462,18 @@ __device__ __forceinline__ void acc_final(const int32_t* w, const int32_t* o, ch
   const int n = dsel(tx.d, tx.nd - 1);
   const bool red = !(kind == A_NONE || kind == A_MAX || kind == A_RESCALE);
   const int to_n = kind == A_TODIMX ? dimx : 1;
+  if (red && n / to_n >= kThreads && to.n < kThreads / 64) {  // few long row sums: the whole block on each
+    for (int e = 0; e < to.n; e++) {
+      const float* p = acc + (size_t)(e / to_n) * n;
+      float s = 0.f;
+      for (int i = e % to_n + threadIdx.x * to_n; i < n; i += kThreads * to_n) s += p[i];
+      s = block_red(s, false);
+      if (kind == A_MEAN) s /= (float)(n * R);
+      else if (kind == A_RMS) s = sqrtf(s / (float)(n * R));
+      if (threadIdx.x == 0) tst<DT>(lds, to, e, s);
+    }
+    return;
+  }
   if (red && n / to_n >= 64) {  // long row sums: one wave per output
     const int lane = threadIdx.x & 63;
     for (int e = threadIdx.x >> 6; e < to.n; e += kThreads / 64) {

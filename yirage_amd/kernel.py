@@ -674,10 +674,14 @@ class KNGraph:
                 raise YirageHipError("hip backend: inputs must live on the GPU")
         dev = inputs[0].device
         key = dev.index
-        temps = self._cache.get(("tmp", id(plan), key))
-        if temps is None:
+        # (the entry keeps its plan: a plan freed and another allocated at the
+        # same address must not inherit its temporaries)
+        hit = self._cache.get(("tmp", id(plan), key))
+        if hit is not None and hit[0] is plan:
+            temps = hit[1]
+        else:
             temps = [torch.empty(d, dtype=dt.torch, device=dev) for d, dt in plan.temps]
-            self._cache[("tmp", id(plan), key)] = temps
+            self._cache[("tmp", id(plan), key)] = (plan, temps)
         outs = []
         for dims, strides, dt in plan.outputs:
             n = sum((d - 1) * s for d, s in zip(dims, strides)) + 1
@@ -1288,9 +1292,9 @@ class _Lowering:
         outputs placed as _interpret_customized reads the maps, accumulators
         as there (none / sum / sum_todimx / rms / mean / max / rescale).
         False (nothing emitted) when the lowering was asked for without it,
-        a tile has more than 4 dims, the tiles need more than 160 KiB of LDS
-        or the program more than 800 words, or an op has no tile form; the
-        literal reading then runs."""
+        a tile has more than 4 dims, the tiles need more than 160 KiB less
+        256 bytes of LDS or the program more than 800 words, or an op has no
+        tile form; the literal reading then runs."""
         if not self.tb_program:
             return False
         bg = op.attrs["bgraph"]
@@ -1428,7 +1432,7 @@ class _Lowering:
             offs.append(off)
             sizes.append(size)
         lds_bytes = max(o + s for o, s in zip(offs, sizes))
-        if lds_bytes > 160 * 1024:
+        if lds_bytes > 160 * 1024 - 256:  # the kernel keeps a few words of its own
             return False
         words = [1, dt.code, R, len(tiles), len(in_recs), len(op_recs), len(out_recs), lds_bytes, bg.reduction_dimx,
                  gx, gy, gz]
